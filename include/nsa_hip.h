@@ -1,0 +1,168 @@
+/* C-ABI of the MI355X (gfx950) Native Sparse Attention library, libnsa_hip.so.
+ *
+ * Plain pointers and sizes only.  Tensors are dense row-major:
+ *   q, o, dO, dq      [B][Hq][T][D]
+ *   k, v, dk, dv      [B][Hkv][Lk][D]      (Lk = T, or the pooled length)
+ *   lse, dot, scale   [B][Hq][T]  float32
+ *   block_idx         [B][Hkv][T][S] int32, -1 = empty slot
+ *   gate logits       [B][Hq][T][3]
+ * with query head h reading KV head h / (Hq / Hkv).  dtype is NSA_F32 or
+ * NSA_BF16 for every tensor of the call not marked float.  Every launch goes
+ * to `stream` (a hipStream_t); nothing is allocated and nothing synchronises
+ * with the host.  Scratch memory is passed in by the caller.
+ *
+ * Return value: NSA_OK (0) or a negative NSA_ERR_* code.  Host wrappers map
+ * NSA_ERR_SHAPE / NSA_ERR_DTYPE to the reference's assertion failures
+ * (nsa_selection_kernel.py:186-189) and the rest to runtime errors.
+ *
+ * Each entry point names the reference Python function whose work it takes
+ * over (paths relative to the openbox-llm checkout).
+ */
+#ifndef NSA_HIP_H
+#define NSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSA_OK 0
+#define NSA_ERR_SHAPE -1
+#define NSA_ERR_DTYPE -2
+#define NSA_ERR_ARG -3
+#define NSA_ERR_LAUNCH -4
+#define NSA_ERR_WORKSPACE -5
+
+#define NSA_F32 0
+#define NSA_BF16 1
+
+#define NSA_MODE_WINDOW 0
+#define NSA_MODE_COMPRESS 1
+
+/* Library version (major * 100 + minor). */
+int nsa_version(void);
+
+/* Length of a transposed K/V copy row: Lk rounded up with >= 32 keys of zero
+ * padding.  Transposed copies are [B*Hkv][D][nsa_padded_len(Lk)]. */
+int nsa_padded_len(int Lk);
+
+/* ---- layout helpers -------------------------------------------------------
+ * x [BH][L][D] -> xt [BH][D][Lp] (Lp >= L, zero padded).  Used for the V^T /
+ * K^T operands of the attention kernels. */
+int nsa_transpose_kv(const void* x, void* xt, int BH, int L, int D, int Lp, int dtype, void* stream);
+
+/* x [B][Hq][T][D] -> xt [B][Hkv][ceil(G/16)][T][D][16] (heads of a 16-head
+ * chunk contiguous, zero padded).  Used for the Q^T / dO^T operands. */
+int nsa_transpose_rows(const void* x, void* xt, int B, int Hq, int Hkv, int T, int D, int dtype,
+                       void* stream);
+
+/* ---- compression pooling ---------------------------------------------------
+ * Replaces block_mean_pool (nsa_fused_kernel.py:549-554): out[i] = mean of
+ * x[i*d .. i*d+l-1]; n = (T-l)/d + 1 pooled tokens (T//l when l == d). */
+int nsa_pool_fwd(const void* x, void* out, int B, int H, int T, int D, int l, int d, int dtype,
+                 void* stream);
+/* Gradient of nsa_pool_fwd.  dpool [B][H][n][D] in dpool_dtype; dx written. */
+int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int T, int D, int l, int d,
+                 int dtype, void* stream);
+
+/* ---- gate ------------------------------------------------------------------
+ * Replaces the gate blend of nsa_fused_forward (nsa_fused_kernel.py:572-573):
+ * out = sigmoid(g0) o_cmp + sigmoid(g1) o_slc + sigmoid(g2) o_win. rows = B*Hq*T. */
+int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const void* o_win, void* out,
+                 int64_t rows, int D, int dtype, void* stream);
+
+/* Backward prep.  nbr == 1: dot[r] = dO[r] . o0[r] (the delta of
+ * nsa_selection_backward.py:168).  nbr == 3: for each branch c,
+ * dot[c*rows + r] = dO . o_c, rowscale[c*rows + r] = sigmoid(g_c) and
+ * dgate[r][c] = sigmoid'(g_c) dot (autograd of nsa_fused_kernel.py:572-573). */
+int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
+                 void* dgate, float* dot, float* rowscale, int64_t rows, int D, int nbr, int dtype,
+                 void* stream);
+
+/* float32 accumulator -> dtype. */
+int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
+
+/* ---- selection branch ------------------------------------------------------
+ * Forward: replaces _selection_fwd_kernel / selection_forward_triton
+ * (nsa_selection_kernel.py:104-213, FSA variant :232-365).  vt is the
+ * transposed copy of v from nsa_transpose_kv (Lp = nsa_padded_len(T)).
+ * Writes o (dtype) and lse (float, -1e9 on rows with no visible key). */
+int nsa_sel_fwd(const void* q, const void* k, const void* vt, const int32_t* block_idx, void* o,
+                float* lse, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int dtype,
+                void* stream);
+
+/* Backward dQ (query-side half of _selection_bwd_kernel,
+ * nsa_selection_backward.py:63-153).  kt = transposed k.  dot = dO . o per
+ * row; rowscale (nullable) multiplies P per row (gate weight).  dq is float32:
+ * dq = (accumulate ? dq : 0) + dQ. */
+int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, const void* dout,
+               const int32_t* block_idx, const float* lse, const float* dot, const float* rowscale,
+               float* dq, int accumulate, int B, int Hq, int Hkv, int T, int D, int S, int block_size,
+               int dtype, void* stream);
+
+/* Block -> query CSR (replaces build_block_to_query_csr, nsa_fsa.py:14-64):
+ * pairs (t, j) with j >= 0 and j*block_size <= t, grouped by (b, hkv, j), query
+ * ascending.  Outputs: q_of_block [cap], block_offsets [B][Hkv][n_blk+1]
+ * (global offsets), pair_bh [cap], *pair_count (device int).  cap = B*Hkv*T*S.
+ * Scratch from nsa_csr_workspace. */
+size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int block_size);
+int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
+                  int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
+                  int block_size, void* stream);
+
+/* Backward dK/dV (block-outer; replaces _selection_dkdv_kernel /
+ * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
+ * CSR above, split into work items of at most `chunk` queries.  qt/dot_t are
+ * the nsa_transpose_rows copies of q/dO.  dk/dv are float32 accumulators that
+ * the call zero-fills and then accumulates into. */
+size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
+int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* dout, const void* qt,
+                 const void* dout_t, const float* lse, const float* dot, const float* rowscale,
+                 const int32_t* q_of_block, const int32_t* block_offsets, const int32_t* pair_count,
+                 float* dk, float* dv, void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int T,
+                 int D, int S, int block_size, int chunk, int dtype, void* stream);
+
+/* ---- range branches (window / compression) ---------------------------------
+ * Forward: replaces _range_attn_fwd_kernel / _range_attn_fwd_qtiled_kernel
+ * (nsa_fused_kernel.py:61-119, 226-307).  mode NSA_MODE_WINDOW: key p visible
+ * to t iff t-window < p <= t; NSA_MODE_COMPRESS: pooled token i visible iff
+ * i*cmp_stride + cmp_block - 1 <= t.  k [B][Hkv][Lk][D], vt transposed v with
+ * Lp = nsa_padded_len(Lk).  Writes o and lse. */
+int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
+                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                  void* stream);
+
+/* Backward dQ of the range branches (query-side half of
+ * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426). */
+int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
+                 const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
+                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                 void* stream);
+
+/* Backward dK/dV of the range branches (key-outer).  dk/dv float32
+ * [B][Hkv][Lk][D]; the call zero-fills and accumulates into them. */
+int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const void* qt,
+                   const void* dout_t, const float* lse, const float* dot, const float* rowscale, float* dk,
+                   float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block,
+                   int cmp_stride, int dtype, void* stream);
+
+/* ---- block importance + top-n ----------------------------------------------
+ * Replaces the importance / topk block of NSAAttention._forward_fused
+ * (nsa_model.py:343-355): p_cmp = exp(q.k_cmp*scale - lse_cmp) summed over
+ * each GQA group, mapped to selection blocks by span overlap / cmp_stride,
+ * non-causal blocks set to -FLT_MAX, forced blocks (block 0 if force_init,
+ * the n_local most recent blocks) set to +inf, then top-S with ties to the
+ * lower block index.  S = min(n_sel, T / sel_block).  scores (nullable,
+ * float [B][Hkv][T][T/sel_block]) receives the raw importance. */
+int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, int32_t* block_idx,
+                        float* scores, int B, int Hq, int Hkv, int T, int n_cmp, int D, int cmp_block,
+                        int cmp_stride, int sel_block, int n_sel, int force_init, int n_local, int dtype,
+                        void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NSA_HIP_H */

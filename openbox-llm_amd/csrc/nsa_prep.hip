@@ -1,0 +1,302 @@
+// Layout, pooling and gate kernels of the NSA path (all HBM-bound).
+//
+//  * transpose_kv   : x [BH][L][D] -> xt [BH][D][Lp]  (key-contiguous rows, zero pad)
+//  * transpose_rows : q/dO [B][Hq][T][D] -> [B][Hkv][NHC][T][D][16]
+//                     (the 16 heads of a head chunk contiguous, zero padded)
+//  * pool_fwd/bwd   : mean over spans [i*d, i*d+l)        (nsa_fused_kernel.py:549-554)
+//  * gate_fwd       : out = sum_c sigmoid(g_c) o_c         (nsa_fused_kernel.py:572-573)
+//  * bwd_prep       : dot_c = dO . o_c, rowscale_c = sigmoid(g_c),
+//                     dgate_c = sigmoid'(g_c) dot_c        (autograd of nsa_model.py:297-301)
+//  * cast_f32       : fp32 accumulator -> output dtype
+#include "nsa_common.h"
+#include "nsa_launch.h"
+
+namespace nsa {
+
+// ---------------------------------------------------------------------------
+// transpose_kv: 64 x 64 tiles through LDS
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose_kv(const T* __restrict__ x, T* __restrict__ xt,
+                                                      int L, int D, int Lp) {
+  __shared__ float tile[64][65];
+  const int bh = blockIdx.z;
+  const int l0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const T* xb = x + (int64_t)bh * L * D;
+  T* yb = xt + (int64_t)bh * D * Lp;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int r = e / 64, cc = e % 64;          // r: key, cc: d
+    const int l = l0 + r, d = d0 + cc;
+    tile[r][cc] = (l < L && d < D) ? to_f32(xb[(int64_t)l * D + d]) : 0.0f;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int r = e / 64, cc = e % 64;          // r: d, cc: key
+    const int d = d0 + r, l = l0 + cc;
+    if (d < D && l < Lp) yb[(int64_t)d * Lp + l] = from_f32<T>(tile[cc][r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// transpose_rows: one thread per (b, hkv, hc, t, d); writes 16 head values
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose_rows(const T* __restrict__ x, T* __restrict__ xt,
+                                                        int B, int Hq, int Hkv, int T_, int D) {
+  const int G = Hq / Hkv;
+  const int NHC = (G + 15) / 16;
+  const int64_t total = (int64_t)B * Hkv * NHC * T_ * D;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int d = (int)(e % D);
+    int64_t r = e / D;
+    const int t = (int)(r % T_); r /= T_;
+    const int hc = (int)(r % NHC); r /= NHC;
+    const int hkv = (int)(r % Hkv);
+    const int b = (int)(r / Hkv);
+    T vals[16];
+#pragma unroll
+    for (int h = 0; h < 16; ++h) {
+      const int hg = hc * 16 + h;
+      vals[h] = hg < G ? x[(((int64_t)b * Hq + hkv * G + hg) * T_ + t) * D + d] : from_f32<T>(0.0f);
+    }
+    T* dst = xt + e * 16;
+#pragma unroll
+    for (int h = 0; h < 16; ++h) dst[h] = vals[h];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// pooling
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void k_pool_fwd(const T* __restrict__ x, T* __restrict__ out,
+                                                  int BH, int L, int D, int n, int pl, int pd) {
+  const int64_t total = (int64_t)BH * n * D;
+  const float inv = 1.0f / (float)pl;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int d = (int)(e % D);
+    const int64_t r = e / D;
+    const int i = (int)(r % n);
+    const int64_t bh = r / n;
+    const T* src = x + (bh * L + (int64_t)i * pd) * D + d;
+    float s = 0.0f;
+    for (int k = 0; k < pl; ++k) s += to_f32(src[(int64_t)k * D]);
+    out[e] = from_f32<T>(s * inv);
+  }
+}
+
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_pool_bwd(const TI* __restrict__ dp, TO* __restrict__ dx,
+                                                  int BH, int L, int D, int n, int pl, int pd) {
+  const int64_t total = (int64_t)BH * L * D;
+  const float inv = 1.0f / (float)pl;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int d = (int)(e % D);
+    const int64_t r = e / D;
+    const int t = (int)(r % L);
+    const int64_t bh = r / L;
+    // tokens i with i*pd <= t < i*pd + pl
+    int ilo = t - pl + 1 <= 0 ? 0 : (t - pl + 1 + pd - 1) / pd;
+    int ihi = t / pd;
+    if (ihi > n - 1) ihi = n - 1;
+    float s = 0.0f;
+    for (int i = ilo; i <= ihi; ++i) s += to_f32(dp[(bh * n + i) * D + d]);
+    dx[e] = from_f32<TO>(s * inv);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// gate
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_gate_fwd(const T* __restrict__ g, const T* __restrict__ oc,
+                                                  const T* __restrict__ os, const T* __restrict__ ow,
+                                                  T* __restrict__ out, int64_t rows, int D) {
+  const int64_t total = rows * D;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / D;
+    const float g0 = sigmoidf(to_f32(g[r * 3 + 0]));
+    const float g1 = sigmoidf(to_f32(g[r * 3 + 1]));
+    const float g2 = sigmoidf(to_f32(g[r * 3 + 2]));
+    out[e] = from_f32<T>(g0 * to_f32(oc[e]) + g1 * to_f32(os[e]) + g2 * to_f32(ow[e]));
+  }
+}
+
+// One 16-lane group per row (each lane 8 elements of D <= 128); 4 rows per wave.
+// nbr = number of branches (1: plain delta, 3: gated three-branch prep).
+template <typename T>
+__global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, const T* __restrict__ o0,
+                                                  const T* __restrict__ o1, const T* __restrict__ o2,
+                                                  const T* __restrict__ gate, T* __restrict__ dgate,
+                                                  float* __restrict__ dot, float* __restrict__ rowscale,
+                                                  int64_t rows, int D, int nbr) {
+  const int lane16 = threadIdx.x & 15;
+  const int64_t row = blockIdx.x * 16ll + (threadIdx.x >> 4);
+  const bool ok = row < rows;
+  float acc[3] = {0.f, 0.f, 0.f};
+  const T* os[3] = {o0, o1, o2};
+  if (ok) {
+    for (int d = lane16 * 8; d < D; d += 128) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        if (d + k >= D) break;
+        const float go = to_f32(dout[row * D + d + k]);
+        for (int c = 0; c < nbr; ++c) acc[c] += go * to_f32(os[c][row * D + d + k]);
+      }
+    }
+  }
+  for (int c = 0; c < 3; ++c) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
+  }
+  if (!ok || lane16 != 0) return;
+  if (nbr == 1) {
+    dot[row] = acc[0];
+    return;
+  }
+  for (int c = 0; c < nbr; ++c) {
+    const float s = sigmoidf(to_f32(gate[row * 3 + c]));
+    dot[(int64_t)c * rows + row] = acc[c];
+    rowscale[(int64_t)c * rows + row] = s;
+    if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_cast_f32(const float* __restrict__ x, T* __restrict__ y, int64_t n) {
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) y[e] = from_f32<T>(x[e]);
+}
+
+static inline int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace nsa
+
+using namespace nsa;
+
+extern "C" {
+
+int nsa_transpose_kv(const void* x, void* xt, int BH, int L, int D, int Lp, int dtype, void* stream) {
+  NSA_CHECK(BH > 0 && L >= 0 && D > 0 && Lp >= L, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  if (L == 0 && Lp == 0) return NSA_OK;
+  dim3 grid((Lp + 63) / 64, (D + 63) / 64, BH);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_transpose_kv<bf16><<<grid, 256, 0, s>>>((const bf16*)x, (bf16*)xt, L, D, Lp);
+  else
+    k_transpose_kv<float><<<grid, 256, 0, s>>>((const float*)x, (float*)xt, L, D, Lp);
+  return nsa_launch_status();
+}
+
+int nsa_transpose_rows(const void* x, void* xt, int B, int Hq, int Hkv, int T, int D, int dtype,
+                       void* stream) {
+  NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && D > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int NHC = (Hq / Hkv + 15) / 16;
+  const int64_t total = (int64_t)B * Hkv * NHC * T * D;
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_transpose_rows<bf16><<<grid_for(total), 256, 0, s>>>((const bf16*)x, (bf16*)xt, B, Hq, Hkv, T, D);
+  else
+    k_transpose_rows<float><<<grid_for(total), 256, 0, s>>>((const float*)x, (float*)xt, B, Hq, Hkv, T, D);
+  return nsa_launch_status();
+}
+
+int nsa_pool_fwd(const void* x, void* out, int B, int H, int T, int D, int l, int d, int dtype,
+                 void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int n = T >= l ? (T - l) / d + 1 : 0;
+  const int64_t total = (int64_t)B * H * n * D;
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_pool_fwd<bf16><<<grid_for(total), 256, 0, s>>>((const bf16*)x, (bf16*)out, B * H, T, D, n, l, d);
+  else
+    k_pool_fwd<float><<<grid_for(total), 256, 0, s>>>((const float*)x, (float*)out, B * H, T, D, n, l, d);
+  return nsa_launch_status();
+}
+
+// dpool_dtype: dtype of the pooled-gradient input (fp32 accumulators or the model dtype)
+int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int T, int D, int l, int d,
+                 int dtype, void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+  NSA_CHECK((dtype == NSA_F32 || dtype == NSA_BF16) && (dpool_dtype == NSA_F32 || dpool_dtype == NSA_BF16),
+            NSA_ERR_DTYPE);
+  const int n = T >= l ? (T - l) / d + 1 : 0;
+  const int64_t total = (int64_t)B * H * T * D;
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int grid = grid_for(total);
+  if (dpool_dtype == NSA_F32) {
+    if (dtype == NSA_BF16)
+      k_pool_bwd<float, bf16><<<grid, 256, 0, s>>>((const float*)dpool, (bf16*)dx, B * H, T, D, n, l, d);
+    else
+      k_pool_bwd<float, float><<<grid, 256, 0, s>>>((const float*)dpool, (float*)dx, B * H, T, D, n, l, d);
+  } else {
+    if (dtype == NSA_BF16)
+      k_pool_bwd<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)dpool, (bf16*)dx, B * H, T, D, n, l, d);
+    else
+      k_pool_bwd<bf16, float><<<grid, 256, 0, s>>>((const bf16*)dpool, (float*)dx, B * H, T, D, n, l, d);
+  }
+  return nsa_launch_status();
+}
+
+int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const void* o_win, void* out,
+                 int64_t rows, int D, int dtype, void* stream) {
+  NSA_CHECK(rows >= 0 && D > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int64_t total = rows * D;
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_gate_fwd<bf16><<<grid_for(total), 256, 0, s>>>((const bf16*)gate, (const bf16*)o_cmp, (const bf16*)o_slc,
+                                                     (const bf16*)o_win, (bf16*)out, rows, D);
+  else
+    k_gate_fwd<float><<<grid_for(total), 256, 0, s>>>((const float*)gate, (const float*)o_cmp,
+                                                      (const float*)o_slc, (const float*)o_win, (float*)out,
+                                                      rows, D);
+  return nsa_launch_status();
+}
+
+// rows = B*Hq*T.  nbr == 1 and gate == NULL: dot[r] = dO.o0 (plain delta).
+// nbr == 3: dot[c*rows + r], rowscale[c*rows + r] = sigmoid(gate[r,c]), dgate[r,c].
+int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
+                 void* dgate, float* dot, float* rowscale, int64_t rows, int D, int nbr, int dtype,
+                 void* stream) {
+  NSA_CHECK(rows >= 0 && D > 0 && D <= 1024 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(nbr == 1 || (gate && o1 && o2 && rowscale), NSA_ERR_ARG);
+  if (rows == 0) return NSA_OK;
+  const int grid = (int)((rows + 15) / 16);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_bwd_prep<bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1, (const bf16*)o2,
+                                          (const bf16*)gate, (bf16*)dgate, dot, rowscale, rows, D, nbr);
+  else
+    k_bwd_prep<float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
+                                           (const float*)o2, (const float*)gate, (float*)dgate, dot, rowscale,
+                                           rows, D, nbr);
+  return nsa_launch_status();
+}
+
+int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream) {
+  NSA_CHECK(n >= 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  if (n == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    k_cast_f32<bf16><<<grid_for(n), 256, 0, s>>>(x, (bf16*)y, n);
+  else
+    k_cast_f32<float><<<grid_for(n), 256, 0, s>>>(x, (float*)y, n);
+  return nsa_launch_status();
+}
+
+}  // extern "C"

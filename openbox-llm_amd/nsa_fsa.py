@@ -1,0 +1,21 @@
+"""Block -> query CSR on MI355X (drop-in for the reference module nsa_fsa.py).
+
+``build_block_to_query_csr`` keeps the reference contract (nsa_fsa.py:14-64):
+pairs (t, j) with j >= 0 and j*block_size <= t, grouped by (b, hkv, block)
+with queries ascending, global offsets.  It runs as a stable radix sort on the
+GPU (``nsa_csr_build``); the exact pair count is read back once to size the
+returned tensors, as the reference's ``nonzero`` does.
+"""
+
+import torch
+
+import nsa_hip_ops as _ops
+
+
+@torch.no_grad()
+def build_block_to_query_csr(block_idx, block_size):
+    """-> (q_of_block [P], block_offsets [B,Hkv,n_blk+1], pair_bh [P]), int32."""
+    assert block_idx.is_cuda, "block_idx must be a GPU tensor"
+    q_of_block, offsets, pair_bh, count = _ops.csr_device(block_idx, block_size)
+    P = int(count.item())
+    return q_of_block[:P].contiguous(), offsets, pair_bh[:P].contiguous()

@@ -1,0 +1,582 @@
+"""Host side of the MI355X NSA path: tensor plumbing around libnsa_hip.so.
+
+Every function here allocates its outputs with torch on the inputs' device and
+launches HIP kernels on the current stream through the C-ABI (``_nsa_lib``).
+Nothing falls back to another implementation: the library must load.
+
+Branch semantics follow the reference (paths relative to its checkout):
+selection nsa_selection_kernel.py:55-92, window / compression
+nsa_fused_kernel.py:576-597, importance / top-n nsa_model.py:245-258, gate
+nsa_fused_kernel.py:572-573.  The compression geometry is generalised to a
+span ``cmp_block`` with stride ``cmp_stride`` (the reference is the aligned
+case ``cmp_block == cmp_stride == block_size``).
+"""
+
+from __future__ import annotations
+
+import contextlib
+from collections import defaultdict
+from dataclasses import dataclass
+
+import torch
+
+import _nsa_lib as L
+
+MODE_WINDOW = L.MODE_WINDOW
+MODE_COMPRESS = L.MODE_COMPRESS
+SEL_DKDV_CHUNK = 256          # CSR queries per selection dK/dV work item
+
+
+@dataclass(frozen=True)
+class NSAGeometry:
+    """Block geometry of one NSA layer.
+
+    cmp_block / cmp_stride: compression span l and stride d; sel_block: l';
+    n_sel: top-n count (forced blocks included); window: w; force_init and
+    n_local force block 0 and the n_local most recent blocks into the top-n.
+    ``NSAGeometry.aligned(bs, n, w)`` is the reference grid
+    (nsa_model.py:134-140): l = d = l' = bs, no forcing.
+    """
+
+    cmp_block: int
+    cmp_stride: int
+    sel_block: int
+    n_sel: int
+    window: int
+    force_init: bool = False
+    n_local: int = 0
+
+    @staticmethod
+    def aligned(block_size, n_sel, window):
+        return NSAGeometry(block_size, block_size, block_size, n_sel, window)
+
+
+# ---------------------------------------------------------------------------
+# optional per-launch timing (HIP events on the launching stream)
+# ---------------------------------------------------------------------------
+
+class LaunchTimer:
+    """Collects (start, end) HIP events around every library call, by name.
+
+    Installed with ``set_timer``; the events are recorded on the current
+    stream, which is the stream every kernel of the call is launched on.
+    """
+
+    def __init__(self):
+        self.spans = defaultdict(list)
+
+    @contextlib.contextmanager
+    def span(self, name):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        try:
+            yield
+        finally:
+            b.record()
+            self.spans[name].append((a, b))
+
+    def summary_ms(self):
+        """name -> (calls, total ms); call after a device synchronize."""
+        return {k: (len(v), sum(a.elapsed_time(b) for a, b in v)) for k, v in self.spans.items()}
+
+
+_TIMER = None
+
+
+def set_timer(timer):
+    global _TIMER
+    _TIMER = timer
+
+
+def _span(name):
+    return _TIMER.span(name) if _TIMER is not None else contextlib.nullcontext()
+
+
+def _span_name(kind, mode):
+    return f"{kind}[{'win' if mode == MODE_WINDOW else 'cmp'}]"
+
+
+def _call(name, fn, *args):
+    with _span(name):
+        rc = fn(*args)
+    L.check(rc, name)
+
+
+# ---------------------------------------------------------------------------
+# argument checks (the reference's asserts, nsa_selection_kernel.py:186-189)
+# ---------------------------------------------------------------------------
+
+def _contig(x):
+    """Dense row-major with a 16-byte aligned base (the kernels read 16-byte rows)."""
+    if not x.is_contiguous():
+        x = x.contiguous()
+    if x.data_ptr() % 16 != 0:
+        x = x.clone()
+    return x
+
+
+def check_qkv(q, k, v=None):
+    assert q.dim() == 4 and k.dim() == 4, "q/k/v must be [B, H, T, D]"
+    assert q.is_cuda and k.is_cuda, "NSA HIP kernels need GPU tensors"
+    B, Hq, T, D = q.shape
+    assert k.shape[0] == B and k.shape[3] == D, "q/k batch or head dim mismatch"
+    assert Hq % k.shape[1] == 0, "GQA needs n_q_heads divisible by n_kv_heads"
+    assert D in (16, 32, 64, 128), "head dim must be a power of two <= 128"
+    assert q.stride(-1) == 1 and k.stride(-1) == 1, "head dim must be contiguous"
+    assert k.dtype == q.dtype, "q/k dtype mismatch"
+    if v is not None:
+        assert v.shape == k.shape and v.dtype == q.dtype and v.stride(-1) == 1
+    L.dtype_code(q)
+
+
+def _lib():
+    return L.load()
+
+
+def _stream(t):
+    return L.stream_of(t)
+
+
+def padded_len(n):
+    return int(_lib().nsa_padded_len(int(n)))
+
+
+# ---------------------------------------------------------------------------
+# layout helpers
+# ---------------------------------------------------------------------------
+
+def transpose_kv(x):
+    """[B,H,Lk,D] -> [B,H,D,padded_len(Lk)] key-contiguous copy (zero pad)."""
+    x = _contig(x)
+    B, H, Lk, D = x.shape
+    Lp = padded_len(Lk)
+    xt = torch.empty(B, H, D, Lp, device=x.device, dtype=x.dtype)
+    _call("nsa_transpose_kv", _lib().nsa_transpose_kv, L.ptr(x), L.ptr(xt), B * H, Lk, D, Lp, L.dtype_code(x),
+                                    _stream(x))
+    return xt
+
+
+def transpose_rows(x, Hkv):
+    """[B,Hq,T,D] -> [B,Hkv,ceil(G/16),T,D,16] (heads of a 16-chunk contiguous)."""
+    x = _contig(x)
+    B, Hq, T, D = x.shape
+    G = Hq // Hkv
+    nhc = (G + 15) // 16
+    xt = torch.empty(B, Hkv, nhc, T, D, 16, device=x.device, dtype=x.dtype)
+    _call("nsa_transpose_rows", _lib().nsa_transpose_rows, L.ptr(x), L.ptr(xt), B, Hq, Hkv, T, D, L.dtype_code(x),
+                                      _stream(x))
+    return xt
+
+
+def cast_f32(x, dtype):
+    if dtype == torch.float32:
+        return x
+    y = torch.empty(x.shape, device=x.device, dtype=dtype)
+    code = L.NSA_BF16 if dtype == torch.bfloat16 else None
+    assert code is not None, f"dtype {dtype} is not supported"
+    _call("nsa_cast_f32", _lib().nsa_cast_f32, L.ptr(x), L.ptr(y), x.numel(), code, _stream(x))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# pooling
+# ---------------------------------------------------------------------------
+
+def n_cmp_tokens(T, l, d):
+    return (T - l) // d + 1 if T >= l else 0
+
+
+def pool_fwd(x, l, d):
+    x = _contig(x)
+    B, H, T, D = x.shape
+    n = n_cmp_tokens(T, l, d)
+    out = torch.empty(B, H, n, D, device=x.device, dtype=x.dtype)
+    if n > 0:
+        _call("nsa_pool_fwd", _lib().nsa_pool_fwd, L.ptr(x), L.ptr(out), B, H, T, D, l, d, L.dtype_code(x),
+                                    _stream(x))
+    return out
+
+
+def pool_bwd(dpool, T, l, d, dtype):
+    dpool = _contig(dpool)
+    B, H, n, D = dpool.shape
+    dx = torch.empty(B, H, T, D, device=dpool.device, dtype=dtype)
+    if T > 0:
+        _call("nsa_pool_bwd", _lib().nsa_pool_bwd, L.ptr(dpool), L.dtype_code(dpool), L.ptr(dx), B, H, T, D, l, d,
+                                    L.NSA_F32 if dtype == torch.float32 else L.NSA_BF16,
+                                    _stream(dpool))
+    return dx
+
+
+class _PoolMean(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, l, d):
+        ctx.meta = (x.shape[2], l, d, x.dtype)
+        return pool_fwd(x, l, d)
+
+    @staticmethod
+    def backward(ctx, dp):
+        T, l, d, dtype = ctx.meta
+        return pool_bwd(dp, T, l, d, dtype), None, None
+
+
+def pool_mean(x, l, d):
+    """Differentiable mean pool over spans [i*d, i*d+l)."""
+    assert x.is_cuda and x.dim() == 4
+    return _PoolMean.apply(x, l, d)
+
+
+# ---------------------------------------------------------------------------
+# forward kernels
+# ---------------------------------------------------------------------------
+
+def sel_fwd(q, k, v, block_idx, block_size, vt=None):
+    """Selection forward -> (o, lse[f32])."""
+    check_qkv(q, k, v)
+    q, k = _contig(q), _contig(k)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape[2] == T, "selection keys must have the query length"
+    assert block_idx.shape[:3] == (B, Hkv, T), "block_idx must be [B, Hkv, T, S]"
+    assert block_size >= 16 and block_size % 16 == 0, "block_size must be a multiple of 16"
+    idx = block_idx.to(torch.int32).contiguous()
+    S = idx.shape[-1]
+    if vt is None:
+        vt = transpose_kv(v)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
+    _call("fwd[sel]", _lib().nsa_sel_fwd, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(idx), L.ptr(o), L.ptr(lse),
+                               B, Hq, Hkv, T, D, S, block_size, L.dtype_code(q), _stream(q))
+    return o, lse
+
+
+def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None):
+    """Window (mode 0) or compression (mode 1) forward -> (o, lse[f32])."""
+    check_qkv(q, k, v)
+    q, k = _contig(q), _contig(k)
+    B, Hq, T, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if mode == MODE_WINDOW:
+        assert Lk == T and window >= 1, "window keys must have the query length, window >= 1"
+    if vt is None:
+        vt = transpose_kv(v)
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
+    _call(_span_name("fwd", mode), _lib().nsa_range_fwd, mode, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o), L.ptr(lse),
+                                 B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block), int(cmp_stride),
+                                 L.dtype_code(q), _stream(q))
+    return o, lse
+
+
+def gate_fwd(gate, o_c, o_s, o_w):
+    gate, o_c, o_s, o_w = (_contig(t) for t in (gate, o_c, o_s, o_w))
+    assert gate.shape == o_c.shape[:3] + (3,), "gate logits must be [B, Hq, T, 3]"
+    assert gate.dtype == o_c.dtype, "gate logits dtype must match q"
+    out = torch.empty_like(o_c)
+    rows = o_c.shape[0] * o_c.shape[1] * o_c.shape[2]
+    _call("nsa_gate_fwd", _lib().nsa_gate_fwd, L.ptr(gate), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(out), rows,
+                                o_c.shape[3], L.dtype_code(o_c), _stream(o_c))
+    return out
+
+
+def importance_topn(q, k_cmp, lse_cmp, geom: NSAGeometry, T=None, return_scores=False):
+    """Block importance from the compression probabilities + top-n -> block_idx int32."""
+    q, k_cmp = _contig(q), _contig(k_cmp)
+    B, Hq, Tq, D = q.shape
+    Hkv, n_cmp = k_cmp.shape[1], k_cmp.shape[2]
+    T = Tq if T is None else T
+    n_slc = T // geom.sel_block
+    S = min(geom.n_sel, n_slc)
+    idx = torch.empty(B, Hkv, T, S, device=q.device, dtype=torch.int32)
+    scores = (torch.empty(B, Hkv, T, n_slc, device=q.device, dtype=torch.float32)
+              if return_scores else None)
+    if n_slc > 0:
+        _call("nsa_importance_topn", _lib().nsa_importance_topn, 
+            L.ptr(q), L.ptr(k_cmp), L.ptr(lse_cmp), L.ptr(idx), L.ptr(scores), B, Hq, Hkv, T, n_cmp, D,
+            geom.cmp_block, geom.cmp_stride, geom.sel_block, geom.n_sel, int(geom.force_init),
+            geom.n_local, L.dtype_code(q), _stream(q))
+    return (idx, scores) if return_scores else idx
+
+
+# ---------------------------------------------------------------------------
+# backward kernels
+# ---------------------------------------------------------------------------
+
+def delta_of(do, o):
+    """dot[r] = dO[r] . O[r] in float32 (nsa_selection_backward.py:168)."""
+    do, o = _contig(do), _contig(o)
+    rows = o.shape[0] * o.shape[1] * o.shape[2]
+    dot = torch.empty(o.shape[:3], device=o.device, dtype=torch.float32)
+    _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(dot), None, rows,
+                                o.shape[3], 1, L.dtype_code(o), _stream(o))
+    return dot
+
+
+def gate_bwd_prep(do, o_c, o_s, o_w, gate):
+    """-> (dot [3,B,Hq,T], rowscale [3,B,Hq,T], dgate [B,Hq,T,3])."""
+    do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
+    B, Hq, T, D = o_c.shape
+    rows = B * Hq * T
+    dot = torch.empty(3, B, Hq, T, device=o_c.device, dtype=torch.float32)
+    rs = torch.empty(3, B, Hq, T, device=o_c.device, dtype=torch.float32)
+    dgate = torch.empty_like(gate)
+    _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(gate), L.ptr(dgate),
+                                L.ptr(dot), L.ptr(rs), rows, D, 3, L.dtype_code(o_c), _stream(o_c))
+    return dot, rs, dgate
+
+
+def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0, cmp_block=1,
+             cmp_stride=1):
+    B, Hq, T, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    _call(_span_name("dq", mode), _lib().nsa_range_dq, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(lse),
+                                L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
+                                int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q), _stream(q))
+
+
+def range_dkdv(mode, q, k, v, do, qt, dot_t, lse, dot, rowscale, window=0, cmp_block=1, cmp_stride=1):
+    B, Hq, T, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    dk = torch.empty(B, Hkv, Lk, D, device=q.device, dtype=torch.float32)
+    dv = torch.empty_like(dk)
+    _call(_span_name("dkdv", mode), _lib().nsa_range_dkdv, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do), L.ptr(qt), L.ptr(dot_t),
+                                  L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dk), L.ptr(dv), B, Hq, Hkv, T,
+                                  Lk, D, int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q),
+                                  _stream(q))
+    return dk, dv
+
+
+def sel_dq(q, k, v, kt, do, block_idx, block_size, lse, dot, rowscale, dq, accumulate):
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    S = block_idx.shape[-1]
+    _call("dq[sel]", _lib().nsa_sel_dq, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(block_idx),
+                              L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv,
+                              T, D, S, block_size, L.dtype_code(q), _stream(q))
+
+
+def csr_device(block_idx, block_size):
+    """Block -> query CSR on the GPU without a host sync.
+
+    Returns (q_of_block [cap], block_offsets [B,Hkv,n_blk+1], pair_bh [cap],
+    pair_count [1]) int32; entries past pair_count are unused.
+    """
+    idx = block_idx.to(torch.int32).contiguous()
+    B, Hkv, T, S = idx.shape
+    n_blk = T // block_size
+    cap = B * Hkv * T * S
+    dev = idx.device
+    q_of_block = torch.empty(max(cap, 1), device=dev, dtype=torch.int32)
+    pair_bh = torch.empty(max(cap, 1), device=dev, dtype=torch.int32)
+    offsets = torch.empty(B, Hkv, n_blk + 1, device=dev, dtype=torch.int32)
+    count = torch.empty(1, device=dev, dtype=torch.int32)
+    ws_bytes = int(_lib().nsa_csr_workspace(B, Hkv, T, S, block_size))
+    assert ws_bytes > 0 or cap == 0, "CSR workspace size query failed"
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    _call("nsa_csr_build", _lib().nsa_csr_build, L.ptr(idx), L.ptr(q_of_block), L.ptr(offsets), L.ptr(pair_bh), L.ptr(count),
+                                 L.ptr(ws), ws_bytes, B, Hkv, T, S, block_size, _stream(idx))
+    return q_of_block, offsets, pair_bh, count
+
+
+def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, csr=None):
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    idx = block_idx.to(torch.int32).contiguous()
+    S = idx.shape[-1]
+    if csr is None:
+        csr = csr_device(idx, block_size)
+    q_of_block, offsets, _, count = csr
+    dk = torch.empty(B, Hkv, T, D, device=q.device, dtype=torch.float32)
+    dv = torch.empty_like(dk)
+    ws_bytes = int(_lib().nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do), L.ptr(qt), L.ptr(dot_t), L.ptr(lse),
+                                L.ptr(dot), L.ptr(rowscale), L.ptr(q_of_block), L.ptr(offsets), L.ptr(count),
+                                L.ptr(dk), L.ptr(dv), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
+                                SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
+    return dk, dv
+
+
+# ---------------------------------------------------------------------------
+# autograd Functions (the reference's boundaries)
+# ---------------------------------------------------------------------------
+
+class SelectionAttnHIP(torch.autograd.Function):
+    """Selection attention; same boundary as SelectionAttnTriton
+    (nsa_selection_backward.py:337-365): saves q, k, v, block_idx, o, lse and
+    returns None grads for block_idx / block_size."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, block_idx, block_size):
+        q, k, v = _contig(q), _contig(k), _contig(v)
+        idx = block_idx.to(torch.int32).contiguous()
+        o, lse = sel_fwd(q, k, v, idx, block_size)
+        ctx.save_for_backward(q, k, v, idx, o, lse)
+        ctx.block_size = block_size
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, idx, o, lse = ctx.saved_tensors
+        dq, dk, dv = selection_backward(q, k, v, idx, ctx.block_size, do, o, lse)
+        return dq, dk, dv, None, None
+
+
+def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
+    """dq, dk, dv of the selection branch (input dtypes)."""
+    check_qkv(q, k, v)
+    q, k, v, do = (_contig(t) for t in (q, k, v, do))
+    idx = block_idx.to(torch.int32).contiguous()
+    if lse is None:
+        _, lse = sel_fwd(q, k, v, idx, block_size)
+    Hkv = k.shape[1]
+    dot = delta_of(do, o)
+    dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    kt = transpose_kv(k)
+    sel_dq(q, k, v, kt, do, idx, block_size, lse, dot, None, dq, False)
+    qt = transpose_rows(q, Hkv)
+    dot_t = transpose_rows(do, Hkv)
+    dk, dv = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size)
+    return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
+
+
+class RangeAttnHIP(torch.autograd.Function):
+    """Window / compression attention; the boundary of _RangeAttn
+    (nsa_fused_kernel.py:521-534).  ``block_size`` is the compression span;
+    the optional ``cmp_stride`` (default: block_size) generalises the
+    reference's aligned pooling."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mode, window, block_size, cmp_stride=None):
+        q, k, v = _contig(q), _contig(k), _contig(v)
+        cs = block_size if cmp_stride is None else cmp_stride
+        o, lse = range_fwd(mode, q, k, v, window, block_size, cs)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.geo = (mode, window, block_size, cs)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        mode, window, cl, cd = ctx.geo
+        dq, dk, dv = range_backward(mode, q, k, v, o, lse, do, window, cl, cd)
+        return dq, dk, dv, None, None, None, None
+
+
+def range_backward(mode, q, k, v, o, lse, do, window=0, cmp_block=1, cmp_stride=1):
+    do = _contig(do)
+    Hkv = k.shape[1]
+    dot = delta_of(do, o)
+    dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    kt = transpose_kv(k)
+    range_dq(mode, q, k, v, kt, do, lse, dot, None, dq, False, window, cmp_block, cmp_stride)
+    qt = transpose_rows(q, Hkv)
+    dot_t = transpose_rows(do, Hkv)
+    dk, dv = range_dkdv(mode, q, k, v, do, qt, dot_t, lse, dot, None, window, cmp_block, cmp_stride)
+    return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
+
+
+class CompressionWithLse(torch.autograd.Function):
+    """Compression attention that also returns its lse (non-differentiable),
+    which the importance / top-n kernel consumes."""
+
+    @staticmethod
+    def forward(ctx, q, k_cmp, v_cmp, cmp_block, cmp_stride):
+        q, k_cmp, v_cmp = _contig(q), _contig(k_cmp), _contig(v_cmp)
+        o, lse = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, cmp_block, cmp_stride)
+        ctx.save_for_backward(q, k_cmp, v_cmp, o, lse)
+        ctx.geo = (cmp_block, cmp_stride)
+        ctx.mark_non_differentiable(lse)
+        return o, lse
+
+    @staticmethod
+    def backward(ctx, do, _dlse):
+        q, k, v, o, lse = ctx.saved_tensors
+        cl, cd = ctx.geo
+        dq, dk, dv = range_backward(MODE_COMPRESS, q, k, v, o, lse, do, 0, cl, cd)
+        return dq, dk, dv, None, None
+
+
+class NSAFusedHIP(torch.autograd.Function):
+    """All three gated branches in one boundary.
+
+    Forward: pool -> compression -> (importance / top-n when block_idx is None)
+    -> selection -> window -> gate.  Backward: gate prep, dQ of the three
+    branches accumulated into one float32 buffer, key-side dK/dV per branch,
+    pool backward.  Same outputs and gradients as composing the per-branch
+    Functions (nsa_fused_kernel.py:560-573).
+    """
+
+    @staticmethod
+    def forward(ctx, q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom):
+        check_qkv(q, kc, vc)
+        q, kc, vc, ks, vs, kw, vw, gate = (_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate))
+        T = q.shape[2]
+        k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+        v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
+        o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride)
+        if block_idx is None:
+            block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
+        idx = block_idx.to(torch.int32).contiguous()
+        if idx.shape[-1] > 0:
+            o_s, lse_s = sel_fwd(q, ks, vs, idx, geom.sel_block)
+        else:
+            o_s = torch.zeros_like(q)
+            lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
+        o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
+        out = gate_fwd(gate, o_c, o_s, o_w)
+        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w)
+        ctx.geom = geom
+        ctx.T = T
+        ctx.mark_non_differentiable(idx)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, dout, _didx):
+        (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w,
+         lse_c, lse_s, lse_w) = ctx.saved_tensors
+        geom, T = ctx.geom, ctx.T
+        dout = _contig(dout)
+        Hkv = ks.shape[1]
+        dtype = q.dtype
+        dot, rs, dgate = gate_bwd_prep(dout, o_c, o_s, o_w, gate)
+        qt = transpose_rows(q, Hkv)
+        dot_t = transpose_rows(dout, Hkv)
+        dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        # window
+        kt_w = transpose_kv(kw)
+        range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
+        dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, qt, dot_t, lse_w, dot[2], rs[2], geom.window)
+        # compression
+        if k_cmp.shape[2] > 0:
+            kt_c = transpose_kv(k_cmp)
+            range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                     geom.cmp_block, geom.cmp_stride)
+            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, qt, dot_t, lse_c, dot[0], rs[0], 0,
+                                  geom.cmp_block, geom.cmp_stride)
+        else:
+            dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
+            dvp = torch.zeros_like(dkp)
+        dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
+        dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
+        # selection
+        if idx.shape[-1] > 0:
+            kt_s = transpose_kv(ks)
+            sel_dq(q, ks, vs, kt_s, dout, idx, geom.sel_block, lse_s, dot[1], rs[1], dq, True)
+            dks, dvs = sel_dkdv(q, ks, vs, dout, qt, dot_t, lse_s, dot[1], rs[1], idx, geom.sel_block)
+        else:
+            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
+            dvs = torch.zeros_like(dks)
+        return (cast_f32(dq, dtype), dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
+                cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None)
+
+
+def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None):
+    """Full NSA attention (pre out-projection) on the HIP path.
+
+    With ``block_idx=None`` the block choice comes from the compression
+    importance and top-n (nsa_model.py:343-355) computed on the GPU.
+    Returns ``(out, block_idx)``.
+    """
+    return NSAFusedHIP.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom)

@@ -1,0 +1,60 @@
+"""CPU checks of the C-ABI boundary (no compute calls, no GPU needed).
+
+* libnsa_hip.so loads and exports every function declared in include/nsa_hip.h;
+* the ctypes signature table covers exactly those declarations;
+* size queries that touch no device memory return sane values.
+"""
+
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nsa_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(nsa_\w+)\s*\(", text, flags=re.M)))
+
+
+def _lib():
+    import _nsa_lib
+    if not os.path.exists(_nsa_lib.LIB_PATH):
+        pytest.skip("libnsa_hip.so not built")
+    return _nsa_lib, _nsa_lib.load()
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for must in ("nsa_sel_fwd", "nsa_sel_dq", "nsa_sel_dkdv", "nsa_range_fwd", "nsa_range_dq",
+                 "nsa_range_dkdv", "nsa_pool_fwd", "nsa_pool_bwd", "nsa_importance_topn", "nsa_csr_build",
+                 "nsa_gate_fwd", "nsa_bwd_prep"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    mod, lib = _lib()
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} not exported"
+    assert sorted(mod.SIGNATURES) == _declared()
+
+
+def test_size_queries():
+    _, lib = _lib()
+    assert lib.nsa_version() >= 100
+    assert lib.nsa_padded_len(32768) >= 32768 + 32
+    assert lib.nsa_padded_len(1) % 64 == 0
+    assert lib.nsa_sel_dkdv_workspace(1, 4, 32768, 16, 64, 256) > 0
+    assert lib.nsa_csr_workspace(1, 4, 32768, 16, 64) > 4 * 32768 * 16 * 4
+
+
+def test_bad_shapes_are_rejected_without_launching():
+    _, lib = _lib()
+    # D = 48 is not a supported head dim; block 8 is below 16: both fail the checks
+    assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 48, 2, 16, 1, None) == -1
+    assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 64, 2, 8, 1, None) == -1
+    assert lib.nsa_range_fwd(7, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, 1, None) == -3
+    assert lib.nsa_pool_fwd(None, None, 1, 1, 64, 64, 16, 16, 5, None) == -2

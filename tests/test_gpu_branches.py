@@ -1,0 +1,144 @@
+"""GPU parity of the three branch kernels against the float64 CPU oracle.
+
+Selection (nsa_sel_fwd / nsa_sel_dq / nsa_sel_dkdv), window and compression
+(nsa_range_fwd / nsa_range_dq / nsa_range_dkdv) through their autograd
+boundaries, over the reference's kernel-test matrix (test_kernel.py:25-33)
+plus GQA-16 cases, in float32 and bfloat16.  Tolerances: see nsa_testlib.TOL.
+"""
+
+import pytest
+import torch
+
+from oracle import nsa_oracle as O
+from nsa_testlib import (G16_CONFIGS, REF_CONFIGS, assert_close, cfg_id, log, make_block_idx, randn,
+                         require_gpu, to64, window_for)
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.bfloat16]
+CONFIGS = REF_CONFIGS + G16_CONFIGS
+
+
+def _inputs(c, dtype, seed=0):
+    B, Hq, Hkv, D, T = c["B"], c["Hq"], c["Hkv"], c["D"], c["T"]
+    q = randn((B, Hq, T, D), seed + 1, dtype)
+    k = randn((B, Hkv, T, D), seed + 2, dtype)
+    v = randn((B, Hkv, T, D), seed + 3, dtype)
+    do = randn((B, Hq, T, D), seed + 4, dtype)
+    return q, k, v, do
+
+
+def _grads_gpu(fn, q, k, v, do, dev):
+    qg, kg, vg = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = fn(qg, kg, vg)
+    o.backward(do.to(dev))
+    torch.cuda.synchronize()
+    return o, qg.grad, kg.grad, vg.grad
+
+
+def _grads_oracle(fn, q, k, v, do):
+    q64, k64, v64, do64 = to64(q, k, v, do)
+    for t in (q64, k64, v64):
+        t.requires_grad_()
+    o, lse = fn(q64, k64, v64)
+    o.backward(do64)
+    return o.detach(), lse.detach(), q64.grad, k64.grad, v64.grad
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", CONFIGS, ids=cfg_id)
+def test_selection_fwd_bwd(c, dtype):
+    dev = require_gpu()
+    log(f"selection {cfg_id(c)} {dtype}")
+    import nsa_selection_backward as nsb
+    import nsa_selection_kernel as nsk
+    q, k, v, do = _inputs(c, dtype)
+    idx = make_block_idx(c["B"], c["Hkv"], c["T"], c["block_size"], c["S"])
+    bs = c["block_size"]
+    o_ref, lse_ref, dq_r, dk_r, dv_r = _grads_oracle(
+        lambda a, b, v_: O.selection_attention(a, b, v_, idx, bs), q, k, v, do)
+    o, lse = nsk.selection_forward_triton(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), bs, return_lse=True)
+    assert_close(o, o_ref, dtype, "o")
+    has = lse_ref > -1e8
+    assert torch.equal((lse.cpu() > -1e8), has), "empty-row pattern of lse differs"
+    assert_close(lse.cpu()[has], lse_ref[has], torch.float32 if dtype == torch.float32 else dtype, "lse")
+    o2, dq, dk, dv = _grads_gpu(lambda a, b, v_: nsb.selection_attn_triton(a, b, v_, idx.to(dev), bs),
+                                q, k, v, do, dev)
+    assert torch.equal(o2.detach(), o), "autograd forward differs from the plain forward"
+    assert_close(dq, dq_r, dtype, "dq")
+    assert_close(dk, dk_r, dtype, "dk")
+    assert_close(dv, dv_r, dtype, "dv")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", CONFIGS, ids=cfg_id)
+def test_window_fwd_bwd(c, dtype):
+    dev = require_gpu()
+    log(f"window {cfg_id(c)} {dtype}")
+    import nsa_fused_kernel as nfk
+    q, k, v, do = _inputs(c, dtype, seed=10)
+    w = window_for(c)
+    o_ref, _, dq_r, dk_r, dv_r = _grads_oracle(lambda a, b, v_: O.window_attention(a, b, v_, w), q, k, v, do)
+    o, dq, dk, dv = _grads_gpu(lambda a, b, v_: nfk.window_attn_triton(a, b, v_, w), q, k, v, do, dev)
+    assert_close(o, o_ref, dtype, "o")
+    assert_close(dq, dq_r, dtype, "dq")
+    assert_close(dk, dk_r, dtype, "dk")
+    assert_close(dv, dv_r, dtype, "dv")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", CONFIGS, ids=cfg_id)
+def test_compression_fwd_bwd(c, dtype):
+    """Aligned pooling (the reference's compression_attn_triton) and the
+    overlapping l = 2d geometry, pooled keys as the differentiable inputs."""
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    bs = c["block_size"]
+    for cl, cd in ((bs, bs), (bs, bs // 2)):
+        log(f"compression {cfg_id(c)} {dtype} l={cl} d={cd}")
+        q, k, v, do = _inputs(c, dtype, seed=20)
+        n = O.n_cmp_tokens(c["T"], cl, cd)
+        kp = O.pool_mean(k.double(), cl, cd).to(dtype)
+        vp = O.pool_mean(v.double(), cl, cd).to(dtype)
+        o_ref, _, dq_r, dk_r, dv_r = _grads_oracle(
+            lambda a, b, v_: O.compression_attention(a, b, v_, cl, cd), q, kp, vp, do)
+        o, dq, dk, dv = _grads_gpu(lambda a, b, v_: nfk.compression_attn_triton(a, b, v_, cl, cd),
+                                   q, kp, vp, do, dev)
+        assert dk.shape[2] == n
+        assert_close(o, o_ref, dtype, "o")
+        assert_close(dq, dq_r, dtype, "dq")
+        assert_close(dk, dk_r, dtype, "dk")
+        assert_close(dv, dv_r, dtype, "dv")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+def test_pool_fwd_bwd(dtype):
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    x = randn((2, 3, 203, 64), 5, dtype)
+    dy_shape = (2, 3, O.n_cmp_tokens(203, 32, 16), 64)
+    dy = randn(dy_shape, 6, dtype)
+    for cl, cd in ((32, 16), (16, 16), (64, 64)):
+        x64 = x.double().requires_grad_()
+        ref = O.pool_mean(x64, cl, cd)
+        xg = x.to(dev).requires_grad_()
+        out = nfk.block_mean_pool(xg, cl, cd)
+        assert_close(out, ref, dtype, f"pool l={cl} d={cd}")
+        g = randn(ref.shape, 7, dtype)
+        ref.backward(g.double())
+        out.backward(g.to(dev))
+        assert_close(xg.grad, x64.grad, dtype, f"pool grad l={cl} d={cd}")
+    del dy
+
+
+def test_empty_and_tiny_rows():
+    """T smaller than a block, all slots -1, and S = 0."""
+    dev = require_gpu()
+    import nsa_selection_kernel as nsk
+    for T in (1, 15, 17):
+        q, k, v, _ = _inputs(dict(B=1, Hq=2, Hkv=1, D=32, T=T), torch.float32)
+        idx = torch.full((1, 1, T, 4), -1, dtype=torch.int32)
+        o, lse = nsk.selection_forward_triton(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), 16,
+                                              return_lse=True)
+        assert torch.count_nonzero(o) == 0
+        assert (lse == -1e9).all()

@@ -1,0 +1,416 @@
+"""Pins for the CPU oracle (no GPU).
+
+The reference ships no golden vectors for this path, so each oracle function
+is pinned by something independent of its own formula: a library routine it
+must reduce to (SDPA with a causal mask), brute force on tiny inputs written
+as explicit per-row loops, finite differences (gradcheck), closed forms and
+invariants.  The last tests plant plausible mistakes in copies of the oracle
+and check that a pin catches each of them.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import nsa_oracle as O
+
+torch.set_default_dtype(torch.float64)
+
+
+def _rand(*shape, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float64)
+
+
+def _sdpa_causal(q, k, v):
+    G = q.shape[1] // k.shape[1]
+    return F.scaled_dot_product_attention(q, k.repeat_interleave(G, 1),
+                                          v.repeat_interleave(G, 1), is_causal=True)
+
+
+# ---------------------------------------------------------------- brute force
+
+def _brute_attention(q, k, v, visible):
+    """Explicit per-(b, h, t) softmax over the key list visible(b, hkv, t)."""
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(D)
+    o = torch.zeros_like(q)
+    lse = torch.full((B, Hq, T), O.LSE_EMPTY)
+    for b in range(B):
+        for h in range(Hq):
+            kh = h // G
+            for t in range(T):
+                keys = visible(b, kh, t)
+                if not keys:
+                    continue
+                s = [float(q[b, h, t] @ k[b, kh, p]) * scale for p in keys]
+                m = max(s)
+                e = [math.exp(x - m) for x in s]
+                z = sum(e)
+                lse[b, h, t] = m + math.log(z)
+                for p, ei in zip(keys, e):
+                    o[b, h, t] += (ei / z) * v[b, kh, p]
+    return o, lse
+
+
+CASES = [
+    dict(B=1, Hq=4, Hkv=2, T=37, D=16, l=8, d=4, ls=8, n=3, w=7),
+    dict(B=2, Hq=3, Hkv=1, T=24, D=8, l=4, d=4, ls=4, n=5, w=24),
+    dict(B=1, Hq=2, Hkv=2, T=33, D=8, l=16, d=8, ls=16, n=2, w=5),
+]
+
+
+@pytest.mark.parametrize("c", CASES)
+def test_window_matches_brute_force(c):
+    q = _rand(c["B"], c["Hq"], c["T"], c["D"], seed=1)
+    k = _rand(c["B"], c["Hkv"], c["T"], c["D"], seed=2)
+    v = _rand(c["B"], c["Hkv"], c["T"], c["D"], seed=3)
+    w = c["w"]
+    o, lse = O.window_attention(q, k, v, w)
+    ob, lb = _brute_attention(q, k, v, lambda b, h, t: [p for p in range(max(0, t - w + 1), t + 1)])
+    torch.testing.assert_close(o, ob, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse, lb, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("c", CASES)
+def test_compression_matches_brute_force(c):
+    q = _rand(c["B"], c["Hq"], c["T"], c["D"], seed=4)
+    kc = _rand(c["B"], c["Hkv"], c["T"], c["D"], seed=5)
+    vc = _rand(c["B"], c["Hkv"], c["T"], c["D"], seed=6)
+    l, d = c["l"], c["d"]
+    kp, vp = O.pool_mean(kc, l, d), O.pool_mean(vc, l, d)
+    # pooled tokens by explicit means
+    n = (c["T"] - l) // d + 1
+    assert kp.shape[2] == n
+    for i in range(n):
+        torch.testing.assert_close(kp[:, :, i], kc[:, :, i * d:i * d + l].sum(2) / l)
+    o, lse = O.compression_attention(q, kp, vp, l, d)
+    ob, lb = _brute_attention(q, kp, vp, lambda b, h, t: [i for i in range(n) if i * d + l - 1 <= t])
+    torch.testing.assert_close(o, ob, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse, lb, rtol=1e-12, atol=1e-12)
+
+
+def _random_block_idx(B, Hkv, T, ls, S, seed=0):
+    """Causal, duplicate-free block lists with -1 padding (the reference's
+    test generator, test_kernel.py:39-58, restated)."""
+    g = torch.Generator().manual_seed(seed)
+    n_blk = T // ls
+    valid = (torch.arange(n_blk)[None, :] + 1) * ls <= (torch.arange(T)[:, None] + 1)
+    score = torch.rand(B, Hkv, T, n_blk, generator=g).masked_fill(~valid, -1.0)
+    kk = min(S, n_blk)
+    topv, topi = score.topk(kk, dim=-1)
+    sel = torch.where(topv >= 0, topi.int(), torch.full_like(topi, -1, dtype=torch.int32))
+    idx = torch.full((B, Hkv, T, S), -1, dtype=torch.int32)
+    idx[..., :kk] = sel
+    return idx
+
+
+@pytest.mark.parametrize("c", CASES)
+def test_selection_matches_brute_force(c):
+    B, Hkv, T, ls, S = c["B"], c["Hkv"], c["T"], c["ls"], c["n"]
+    q = _rand(B, c["Hq"], T, c["D"], seed=7)
+    k = _rand(B, Hkv, T, c["D"], seed=8)
+    v = _rand(B, Hkv, T, c["D"], seed=9)
+    idx = _random_block_idx(B, Hkv, T, ls, S, seed=3)
+    # also a row whose only block is the partial block containing t
+    idx[0, 0, ls + 1, :] = -1
+    idx[0, 0, ls + 1, 0] = 1
+    o, lse = O.selection_attention(q, k, v, idx, ls)
+
+    def vis(b, h, t):
+        keys = []
+        for j in idx[b, h, t].tolist():
+            if j >= 0:
+                keys += [p for p in range(j * ls, min((j + 1) * ls, T)) if p <= t]
+        return sorted(keys)
+    ob, lb = _brute_attention(q, k, v, vis)
+    torch.testing.assert_close(o, ob, rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse, lb, rtol=1e-12, atol=1e-12)
+    assert (lse == O.LSE_EMPTY).any(), "case must contain an empty row"
+
+
+# ------------------------------------------------------------- library pins
+
+def test_window_wider_than_T_is_causal_sdpa():
+    q, k, v = _rand(2, 4, 50, 16, seed=1), _rand(2, 2, 50, 16, seed=2), _rand(2, 2, 50, 16, seed=3)
+    o, _ = O.window_attention(q, k, v, 50)
+    torch.testing.assert_close(o, _sdpa_causal(q, k, v), rtol=1e-10, atol=1e-10)
+
+
+def test_all_blocks_selected_is_causal_sdpa():
+    T, ls = 64, 16
+    q, k, v = _rand(1, 4, T, 16, seed=4), _rand(1, 1, T, 16, seed=5), _rand(1, 1, T, 16, seed=6)
+    idx = torch.arange(T // ls, dtype=torch.int32).expand(1, 1, T, T // ls).contiguous()
+    o, _ = O.selection_attention(q, k, v, idx, ls)
+    torch.testing.assert_close(o, _sdpa_causal(q, k, v), rtol=1e-10, atol=1e-10)
+
+
+def test_unit_pool_compression_is_causal_sdpa():
+    q, k, v = _rand(1, 2, 40, 8, seed=7), _rand(1, 1, 40, 8, seed=8), _rand(1, 1, 40, 8, seed=9)
+    kp, vp = O.pool_mean(k, 1, 1), O.pool_mean(v, 1, 1)
+    o, _ = O.compression_attention(q, kp, vp, 1, 1)
+    torch.testing.assert_close(o, _sdpa_causal(q, k, v), rtol=1e-10, atol=1e-10)
+
+
+def test_aligned_pool_is_reference_block_mean():
+    x = _rand(2, 3, 70, 8, seed=10)
+    bs = 16
+    n = 70 // bs
+    ref = x[:, :, :n * bs].reshape(2, 3, n, bs, 8).mean(3)      # nsa_fused_kernel.py:549-554
+    torch.testing.assert_close(O.pool_mean(x, bs, bs), ref)
+
+
+# ---------------------------------------------------------------- gradients
+
+def test_gradcheck_masked_attention():
+    q = _rand(1, 2, 9, 4, seed=11).requires_grad_()
+    k = _rand(1, 1, 9, 4, seed=12).requires_grad_()
+    v = _rand(1, 1, 9, 4, seed=13).requires_grad_()
+    keep = O.window_keep(9, 4)[None, None]
+    keep = keep.clone()
+    keep[..., 0, :] = False                                      # one empty row
+    assert torch.autograd.gradcheck(lambda a, b, c: O.masked_attention(a, b, c, keep)[0],
+                                    (q, k, v))
+
+
+@pytest.mark.parametrize("which", ["win", "cmp", "slc"])
+def test_analytic_backward_matches_autograd(which):
+    B, Hq, Hkv, T, D = 1, 4, 2, 40, 8
+    q = _rand(B, Hq, T, D, seed=20).requires_grad_()
+    k = _rand(B, Hkv, T, D, seed=21)
+    v = _rand(B, Hkv, T, D, seed=22)
+    if which == "win":
+        keep = O.window_keep(T, 7)[None, None]
+    elif which == "cmp":
+        k, v = O.pool_mean(k, 8, 4), O.pool_mean(v, 8, 4)
+        keep = O.compress_keep(T, k.shape[2], 8, 4)[None, None]
+    else:
+        keep = O.select_keep(_random_block_idx(B, Hkv, T, 8, 3, seed=1), T, 8)
+    k.requires_grad_()
+    v.requires_grad_()
+    do = _rand(B, Hq, T, D, seed=23)
+    o, _ = O.masked_attention(q, k, v, keep)
+    o.backward(do)
+    dq, dk, dv = O.attention_backward(q.detach(), k.detach(), v.detach(), keep, do)
+    torch.testing.assert_close(dq, q.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dk, k.grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dv, v.grad, rtol=1e-10, atol=1e-10)
+
+
+def test_gradcheck_full_nsa_tiny():
+    cfg = O.NSAConfig(cmp_block=4, cmp_stride=2, sel_block=4, n_sel=2, window=3,
+                      force_init=True, n_local=2)
+    B, Hq, Hkv, T, D = 1, 2, 1, 12, 4
+    ins = [_rand(B, Hq, T, D, seed=30)] + [_rand(B, Hkv, T, D, seed=31 + i) for i in range(6)] \
+        + [_rand(B, Hq, T, 3, seed=40)]
+    ins = [t.requires_grad_() for t in ins]
+    idx = O.select_blocks(ins[0].detach(), O.pool_mean(ins[1].detach(), 4, 2), cfg)[0]
+
+    def f(*a):
+        return O.nsa_fused_reference(*a, idx, cfg)[0]
+    assert torch.autograd.gradcheck(f, tuple(ins))
+
+
+# ------------------------------------------------------------- importance/topn
+
+def test_overlap_weights_identity_when_aligned():
+    W = O.overlap_weights(8, 8, 16, 16, 16)
+    torch.testing.assert_close(W, torch.eye(8))
+
+
+def test_overlap_weights_nsa_paper_pattern():
+    W = O.overlap_weights(n_cmp=31, n_slc=8, l=32, d=16, ls=64)
+    for j in range(1, 7):
+        col = W[:, j]
+        nz = torch.nonzero(col).flatten().tolist()
+        assert nz == [4 * j - 1, 4 * j, 4 * j + 1, 4 * j + 2, 4 * j + 3]
+        assert col[nz].tolist() == [1.0, 2.0, 2.0, 2.0, 1.0]
+    # every token fully inside the grid distributes l/d in total
+    torch.testing.assert_close(W[:29].sum(1), torch.full((29,), 2.0))
+
+
+def test_importance_matches_brute_force():
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=8)
+    B, Hq, Hkv, T, D = 1, 4, 2, 48, 8
+    q = _rand(B, Hq, T, D, seed=50)
+    kc = _rand(B, Hkv, T, D, seed=51)
+    kp = O.pool_mean(kc, 8, 4)
+    n = kp.shape[2]
+    imp = O.importance(q, kp, cfg)
+    G = Hq // Hkv
+    for b in range(B):
+        for hk in range(Hkv):
+            for t in range(T):
+                vis = [i for i in range(n) if i * 4 + 8 - 1 <= t]
+                pc = [0.0] * n
+                for g in range(G):
+                    h = hk * G + g
+                    if not vis:
+                        continue
+                    s = [float(q[b, h, t] @ kp[b, hk, i]) / math.sqrt(D) for i in vis]
+                    m = max(s)
+                    z = sum(math.exp(x - m) for x in s)
+                    for i, x in zip(vis, s):
+                        pc[i] += math.exp(x - m) / z
+                for j in range(T // 16):
+                    ref = 0.0
+                    for i in range(n):
+                        ov = max(0, min(i * 4 + 8, (j + 1) * 16) - max(i * 4, j * 16))
+                        ref += ov / 4 * pc[i]
+                    assert abs(float(imp[b, hk, t, j]) - ref) < 1e-12
+
+
+def _brute_topn(scores_row, S):
+    order = sorted(range(len(scores_row)), key=lambda j: (-scores_row[j], j))
+    return order[:S]
+
+
+def test_topn_ties_go_to_lower_index():
+    sc = torch.tensor([[[[1.0, 3.0, 3.0, 0.5, 3.0, O.F32_MIN, O.F32_MIN, 2.0]]]])
+    assert O.topn_from_scores(sc, 5).flatten().tolist() == [1, 2, 4, 7, 0]
+    assert O.topn_from_scores(sc, 8).flatten().tolist() == [1, 2, 4, 7, 0, 3, 5, 6]
+
+
+def test_topn_matches_brute_force_with_mask_and_forcing():
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=8, n_sel=5, window=8,
+                      force_init=True, n_local=2)
+    g = torch.Generator().manual_seed(3)
+    T, n_slc = 80, 10
+    imp = torch.rand(1, 2, T, n_slc, generator=g).round(decimals=1)  # many exact ties
+    sc = O.selection_scores(imp, cfg)
+    idx = O.topn_from_scores(sc, 5)
+    for h in range(2):
+        for t in range(T):
+            row = []
+            for j in range(n_slc):
+                forced = j == 0 or j in (t // 8, t // 8 - 1)
+                if forced:
+                    row.append(math.inf)
+                elif (j + 1) * 8 - 1 <= t:
+                    row.append(float(imp[0, h, t, j]))
+                else:
+                    row.append(O.F32_MIN)
+            assert idx[0, h, t].tolist() == _brute_topn(row, 5), (h, t)
+
+
+def test_topn_reference_mode_fillers():
+    """Aligned grid, no forcing: rows with fewer valid blocks than S take the
+    lowest non-valid indices, starting with the block that contains t."""
+    cfg = O.NSAConfig.reference(16, 4, 16)
+    imp = torch.rand(1, 1, 64, 4)
+    idx = O.topn_from_scores(O.selection_scores(imp, cfg), 4)
+    assert idx[0, 0, 5].tolist() == [0, 1, 2, 3]                 # nothing complete yet
+    row = idx[0, 0, 20].tolist()                                 # block 0 complete
+    assert row[0] == 0 and row[1:] == [1, 2, 3]
+    row = idx[0, 0, 40].tolist()                                 # blocks 0,1 complete
+    assert sorted(row[:2]) == [0, 1] and row[2:] == [2, 3]
+
+
+# ---------------------------------------------------------------- CSR
+
+def test_csr_invariants_and_counts():
+    B, Hkv, T, ls, S = 2, 2, 64, 8, 4
+    idx = _random_block_idx(B, Hkv, T, ls, S, seed=7)
+    idx[0, 0, 3, 0] = 0          # a non-causal pair (block 0 starts at 0 <= 3: causal)
+    idx[0, 0, 3, 1] = 5          # block 5 starts at 40 > 3: must be dropped
+    idx[1, 1, 40, 3] = idx[1, 1, 40, 0]   # a block listed twice: two pairs
+    qob, off, pbh = O.build_block_to_query_csr(idx, ls)
+    n_blk = T // ls
+    # brute force: walk blocks, then queries, then slots
+    ref_q, ref_off, ref_bh = [], torch.zeros(B, Hkv, n_blk + 1, dtype=torch.int32), []
+    for b in range(B):
+        for h in range(Hkv):
+            for j in range(n_blk):
+                ref_off[b, h, j] = len(ref_q)
+                for t in range(T):
+                    for s in range(S):
+                        if int(idx[b, h, t, s]) == j and j * ls <= t:
+                            ref_q.append(t)
+                            ref_bh.append(b * Hkv + h)
+            ref_off[b, h, n_blk] = len(ref_q)
+    assert qob.tolist() == ref_q
+    assert pbh.tolist() == ref_bh
+    assert torch.equal(off, ref_off)
+    assert (off[..., 1:] >= off[..., :-1]).all()
+    for b in range(B):
+        for h in range(Hkv):
+            for j in range(n_blk):
+                seg = qob[off[b, h, j]:off[b, h, j + 1]].long()
+                assert (seg[1:] >= seg[:-1]).all()                      # ascending
+                assert (seg >= j * ls).all()                            # causal
+
+
+# ------------------------------------------------------------- rows vs dense
+
+def test_rows_path_matches_dense_path():
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10,
+                      force_init=True, n_local=2)
+    B, Hq, Hkv, T, D = 1, 4, 2, 96, 8
+    q = _rand(B, Hq, T, D, seed=60)
+    kv = [_rand(B, Hkv, T, D, seed=61 + i) for i in range(6)]
+    gate = _rand(B, Hq, T, 3, seed=70)
+    out, parts = O.nsa_forward_reference(q, *kv, gate, cfg)
+    rows = torch.tensor([0, 1, 7, 15, 16, 33, 64, 95])
+    out_r, parts_r = O.nsa_rows(q, *kv, gate, parts["block_idx"], cfg, rows)
+    torch.testing.assert_close(out_r, out[:, :, rows], rtol=1e-12, atol=1e-12)
+    for key in ("cmp", "slc", "win"):
+        torch.testing.assert_close(parts_r[key][1], parts[key][1][:, :, rows])
+    imp_r = O.importance_rows(q, parts["k_cmp"], cfg, rows, T)
+    torch.testing.assert_close(imp_r, parts["importance"][:, :, rows])
+
+
+def test_keys_per_row_matches_masks():
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10)
+    T = 96
+    idx = _random_block_idx(1, 2, T, 16, 3, seed=9)
+    kw, kc, ksel = O.keys_per_row(T, cfg, idx)
+    assert kw == int(O.window_keep(T, 10).sum())
+    n = O.n_cmp_tokens(T, 8, 4)
+    assert kc == int(O.compress_keep(T, n, 8, 4).sum())
+    assert ksel == int(O.select_keep(idx, T, 16).sum())
+
+
+# ------------------------------------------------------- planted mistakes
+
+def test_pins_catch_planted_mistakes():
+    """Each mutated oracle variant must fail at least one pin above."""
+    q, k, v = _rand(1, 2, 30, 8, seed=1), _rand(1, 1, 30, 8, seed=2), _rand(1, 1, 30, 8, seed=3)
+    w = 6
+    good = [p for p in range(30)]
+    ob, _ = _brute_attention(q, k, v, lambda b, h, t: [p for p in range(max(0, t - w + 1), t + 1)])
+    # window off by one (t - p <= w)
+    t_ = torch.arange(30)[:, None]
+    p_ = torch.arange(30)[None, :]
+    bad_keep = (p_ <= t_) & (t_ - p_ <= w)
+    o_bad, _ = O.masked_attention(q, k, v, bad_keep[None, None])
+    assert not torch.allclose(o_bad, ob)
+    # wrong GQA mapping (h % Hkv instead of h // G) on Hkv=2
+    k2, v2 = _rand(1, 2, 30, 8, seed=4), _rand(1, 2, 30, 8, seed=5)
+    q4 = _rand(1, 4, 30, 8, seed=6)
+    o_ok, _ = O.window_attention(q4, k2, v2, 30)
+    o_bad = _sdpa_causal(q4, k2[:, [0, 1, 0, 1]], v2[:, [0, 1, 0, 1]])
+    assert torch.allclose(o_ok, _sdpa_causal(q4, k2, v2))
+    assert not torch.allclose(o_ok, o_bad)
+    # compression visibility shifted by one token (i*d + l <= t)
+    kp, vp = O.pool_mean(k, 4, 4), O.pool_mean(v, 4, 4)
+    n = kp.shape[2]
+    bad = (torch.arange(n)[None, :] * 4 + 4 <= torch.arange(30)[:, None])
+    o_bad, _ = O.masked_attention(q, kp, vp, bad[None, None])
+    ob, _ = _brute_attention(q, kp, vp, lambda b, h, t: [i for i in range(n) if i * 4 + 3 <= t])
+    assert not torch.allclose(o_bad, ob)
+    # dropped delta term in dS
+    keep = O.window_keep(30, 30)[None, None]
+    do = _rand(1, 2, 30, 8, seed=7)
+    dq, _, _ = O.attention_backward(q, k, v, keep, do)
+    p = O.attention_probs(q, k, keep)
+    dq_bad = (8 ** -0.5) * (p * (do @ v.repeat_interleave(2, 1).transpose(-1, -2))) @ k.repeat_interleave(2, 1)
+    assert not torch.allclose(dq, dq_bad)
+    # top-n tie broken toward the higher index
+    sc = torch.tensor([[[[2.0, 2.0, 1.0]]]])
+    assert O.topn_from_scores(sc, 1).item() == 0
+    assert torch.sort(sc, descending=True).indices[..., 0].item() in (0, 1)
+    del good
