@@ -103,18 +103,22 @@ int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, cons
                int dtype, void* stream);
 
 /* Block -> query CSR (replaces build_block_to_query_csr, nsa_fsa.py:14-64):
- * pairs (t, j) with j >= 0 and j*block_size <= t, grouped by (b, hkv, j), query
- * ascending.  Outputs: q_of_block [cap], block_offsets [B][Hkv][n_blk+1]
- * (global offsets), pair_bh [cap], *pair_count (device int).  cap = B*Hkv*T*S.
- * Scratch from nsa_csr_workspace. */
-size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int block_size);
+ * pairs (t, j) with 0 <= j < n_blk and j*block_size <= t, grouped by (b, hkv, j),
+ * query ascending.  n_blk is the reference's T / block_size (nsa_fsa.py:36) or
+ * ceil(T / block_size) to include the trailing partial block.  Outputs:
+ * q_of_block [cap], block_offsets [B][Hkv][n_blk+1] (global offsets), pair_bh
+ * [cap], *pair_count (device int).  cap = B*Hkv*T*S.  Scratch from
+ * nsa_csr_workspace. */
+size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int n_blk);
 int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
-                  int block_size, void* stream);
+                  int block_size, int n_blk, void* stream);
 
 /* Backward dK/dV (block-outer; replaces _selection_dkdv_kernel /
  * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
- * CSR above, split into work items of at most `chunk` queries.  qt/dot_t are
+ * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
+ * partial block, which the forward attends to, gets its gradient), split into
+ * work items of at most `chunk` queries.  qt/dot_t are
  * the nsa_transpose_rows copies of q/dO.  dk/dv are float32 accumulators that
  * the call zero-fills and then accumulates into. */
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);

@@ -46,7 +46,7 @@ SIGNATURES = {
     "nsa_sel_dq": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                         _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_csr_workspace": (_Z, [_I, _I, _I, _I, _I]),
-    "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _P]),
+    "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dkdv_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
     "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

@@ -65,10 +65,9 @@ struct CsrLayout {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static CsrLayout csr_layout(int B, int Hkv, int T, int S, int L) {
+static CsrLayout csr_layout(int B, int Hkv, int T, int S, int n_blk) {
   CsrLayout c;
   c.n = (int64_t)B * Hkv * T * S;
-  const int n_blk = T / L;
   const uint64_t sentinel = (uint64_t)B * Hkv * n_blk;
   int bits = 1;
   while (bits < 32 && (1ull << bits) <= sentinel) ++bits;
@@ -97,21 +96,20 @@ using namespace nsa;
 
 extern "C" {
 
-size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int block_size) {
-  if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || block_size <= 0) return 0;
-  if ((int64_t)B * Hkv * T * S >= (1ll << 31)) return 0;
-  return csr_layout(B, Hkv, T, S, block_size).total;
+size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int n_blk) {
+  if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || n_blk < 0) return 0;
+  if ((int64_t)B * Hkv * T * S >= (1ll << 31) || (int64_t)B * Hkv * n_blk >= (1ll << 31)) return 0;
+  return csr_layout(B, Hkv, T, S, n_blk).total;
 }
 
 int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
-                  int block_size, void* stream) {
-  NSA_CHECK(B > 0 && Hkv > 0 && T >= 0 && S >= 0 && block_size > 0, NSA_ERR_SHAPE);
-  NSA_CHECK((int64_t)B * Hkv * T * S < (1ll << 31), NSA_ERR_SHAPE);
-  const CsrLayout c = csr_layout(B, Hkv, T, S, block_size);
+                  int block_size, int n_blk, void* stream) {
+  NSA_CHECK(B > 0 && Hkv > 0 && T >= 0 && S >= 0 && block_size > 0 && n_blk >= 0, NSA_ERR_SHAPE);
+  NSA_CHECK((int64_t)B * Hkv * T * S < (1ll << 31) && (int64_t)B * Hkv * n_blk < (1ll << 31), NSA_ERR_SHAPE);
+  const CsrLayout c = csr_layout(B, Hkv, T, S, n_blk);
   NSA_CHECK(workspace_bytes >= c.total, NSA_ERR_WORKSPACE);
   hipStream_t s = (hipStream_t)stream;
-  const int n_blk = T / block_size;
   const int nbh = B * Hkv;
   char* ws = (char*)workspace;
   uint32_t* kin = (uint32_t*)(ws + c.keys_in);

@@ -315,8 +315,12 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   return nsa_launch_status();
 }
 
+// Selection blocks of the CSR consumed here: every block holding a key, the
+// trailing partial one included (the forward attends to it when selected).
+static inline int sel_csr_blocks(int T, int block_size) { return (T + block_size - 1) / block_size; }
+
 static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size, int chunk) {
-  const size_t nb = (size_t)B * Hkv * (T / block_size);
+  const size_t nb = (size_t)B * Hkv * sel_csr_blocks(T, block_size);
   const size_t pairs = (size_t)B * Hkv * T * S;
   return nb + (pairs + chunk - 1) / chunk + 1;
 }
@@ -339,7 +343,7 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* dout, 
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
   if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;
-  const int n_blk = T / block_size;
+  const int n_blk = sel_csr_blocks(T, block_size);
   if (T == 0 || S == 0 || n_blk == 0) return NSA_OK;
   const size_t cap = sel_items_cap(B, Hkv, T, S, block_size, chunk);
   int4* items = (int4*)workspace;

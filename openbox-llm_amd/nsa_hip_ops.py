@@ -356,26 +356,30 @@ def sel_dq(q, k, v, kt, do, block_idx, block_size, lse, dot, rowscale, dq, accum
                               T, D, S, block_size, L.dtype_code(q), _stream(q))
 
 
-def csr_device(block_idx, block_size):
+def csr_device(block_idx, block_size, n_blk=None):
     """Block -> query CSR on the GPU without a host sync.
 
-    Returns (q_of_block [cap], block_offsets [B,Hkv,n_blk+1], pair_bh [cap],
-    pair_count [1]) int32; entries past pair_count are unused.
+    ``n_blk`` defaults to ``ceil(T / block_size)`` (the trailing partial block
+    included, as the selection forward attends to it); the reference grid is
+    ``T // block_size`` (nsa_fsa.py:36).  Returns (q_of_block [cap],
+    block_offsets [B,Hkv,n_blk+1], pair_bh [cap], pair_count [1]) int32;
+    entries past pair_count are unused.
     """
     idx = block_idx.to(torch.int32).contiguous()
     B, Hkv, T, S = idx.shape
-    n_blk = T // block_size
+    if n_blk is None:
+        n_blk = -(-T // block_size)
     cap = B * Hkv * T * S
     dev = idx.device
     q_of_block = torch.empty(max(cap, 1), device=dev, dtype=torch.int32)
     pair_bh = torch.empty(max(cap, 1), device=dev, dtype=torch.int32)
     offsets = torch.empty(B, Hkv, n_blk + 1, device=dev, dtype=torch.int32)
     count = torch.empty(1, device=dev, dtype=torch.int32)
-    ws_bytes = int(_lib().nsa_csr_workspace(B, Hkv, T, S, block_size))
+    ws_bytes = int(_lib().nsa_csr_workspace(B, Hkv, T, S, n_blk))
     assert ws_bytes > 0 or cap == 0, "CSR workspace size query failed"
     ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
-    _call("nsa_csr_build", _lib().nsa_csr_build, L.ptr(idx), L.ptr(q_of_block), L.ptr(offsets), L.ptr(pair_bh), L.ptr(count),
-                                 L.ptr(ws), ws_bytes, B, Hkv, T, S, block_size, _stream(idx))
+    _call("nsa_csr_build", _lib().nsa_csr_build, L.ptr(idx), L.ptr(q_of_block), L.ptr(offsets), L.ptr(pair_bh),
+          L.ptr(count), L.ptr(ws), ws_bytes, B, Hkv, T, S, block_size, n_blk, _stream(idx))
     return q_of_block, offsets, pair_bh, count
 
 

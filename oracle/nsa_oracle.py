@@ -365,7 +365,7 @@ def attention_backward(q, k, v, keep, do, scale=None):
 # block -> query CSR (restating nsa_fsa.py:14-64)
 # ---------------------------------------------------------------------------
 
-def build_block_to_query_csr(block_idx, block_size):
+def build_block_to_query_csr(block_idx, block_size, n_blk=None):
     """Invert ``block_idx [B,Hkv,T,S]`` into a causal block -> query CSR.
 
     Every slot (t, s) with ``j = block_idx[..., t, s] >= 0`` and
@@ -374,12 +374,20 @@ def build_block_to_query_csr(block_idx, block_size):
     i.e. queries ascending (stable order, nsa_fsa.py:58-62), with global
     offsets.  Returns int32 ``(q_of_block [P], block_offsets [B,Hkv,n_blk+1],
     pair_bh [P])``.
+
+    ``n_blk`` defaults to the reference's ``T // block_size`` (nsa_fsa.py:36);
+    a causal pair on a block at or past it raises IndexError, as the
+    reference's ``scatter_add_`` into ``n_blk`` columns does (nsa_fsa.py:46-48).
+    ``n_blk = ceil(T / block_size)`` covers the trailing partial block.
     """
     B, Hkv, T, S = block_idx.shape
-    n_blk = T // block_size
+    if n_blk is None:
+        n_blk = T // block_size
     idx = block_idx.long()
     tpos = torch.arange(T)[None, None, :, None]
     valid = (idx >= 0) & (idx * block_size <= tpos)
+    if bool((valid & (idx >= n_blk)).any()):
+        raise IndexError(f"block index >= n_blk = {n_blk} on a causal pair")
     bh = (torch.arange(B)[:, None] * Hkv + torch.arange(Hkv)[None, :])[:, :, None, None]
     keys = (bh * n_blk + idx).expand(B, Hkv, T, S)[valid]        # (b, hkv, t, s) order
     vals = tpos.expand(B, Hkv, T, S)[valid]

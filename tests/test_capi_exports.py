@@ -48,7 +48,7 @@ def test_size_queries():
     assert lib.nsa_padded_len(32768) >= 32768 + 32
     assert lib.nsa_padded_len(1) % 64 == 0
     assert lib.nsa_sel_dkdv_workspace(1, 4, 32768, 16, 64, 256) > 0
-    assert lib.nsa_csr_workspace(1, 4, 32768, 16, 64) > 4 * 32768 * 16 * 4
+    assert lib.nsa_csr_workspace(1, 4, 32768, 16, 512) > 4 * 32768 * 16 * 4
 
 
 def test_bad_shapes_are_rejected_without_launching():

@@ -173,12 +173,63 @@ def test_nsa_attention_baseline_geometry(shape, dtype):
 def test_csr_bit_exact():
     dev = require_gpu()
     import nsa_fsa
+    import nsa_hip_ops as ops
     for (B, Hkv, T, bs, S, seed) in ((2, 2, 256, 16, 5, 0), (1, 4, 1024, 64, 16, 1), (1, 1, 100, 32, 4, 2)):
         idx = make_block_idx(B, Hkv, T, bs, S, seed=seed)
-        idx[..., -1] = torch.where(idx[..., -1] < 0, torch.full_like(idx[..., -1], 3), idx[..., -1])
-        idx = torch.where(idx >= 0, idx, idx)  # future block ids and -1 both present
+        # -1 padding becomes block 2: non-causal (future) for early rows, causal later
+        idx[..., -1] = torch.where(idx[..., -1] < 0, torch.full_like(idx[..., -1], 2), idx[..., -1])
         q_ref, off_ref, bh_ref = O.build_block_to_query_csr(idx, bs)
         q_g, off_g, bh_g = nsa_fsa.build_block_to_query_csr(idx.to(dev), bs)
         assert torch.equal(q_g.cpu(), q_ref)
         assert torch.equal(off_g.cpu(), off_ref)
         assert torch.equal(bh_g.cpu(), bh_ref)
+
+
+def test_csr_trailing_partial_block():
+    """T not a multiple of the block: the reference grid rejects a causal pair
+    on the partial block; the extended grid (used by the dK/dV kernel) keeps it."""
+    dev = require_gpu()
+    import nsa_fsa
+    import nsa_hip_ops as ops
+    B, Hkv, T, bs, S = 1, 2, 100, 32, 4
+    idx = make_block_idx(B, Hkv, T, bs, S, seed=2)
+    idx[:, :, 96:, -1] = 3                      # block 3 = tokens 96..99, causal for t >= 96
+    with pytest.raises(IndexError):
+        O.build_block_to_query_csr(idx, bs)
+    with pytest.raises(IndexError):
+        nsa_fsa.build_block_to_query_csr(idx.to(dev), bs)
+    n_ext = -(-T // bs)
+    q_ref, off_ref, bh_ref = O.build_block_to_query_csr(idx, bs, n_ext)
+    q_g, off_g, bh_g, cnt = ops.csr_device(idx.to(dev), bs)
+    P = int(cnt.item())
+    assert P == q_ref.numel()
+    assert torch.equal(q_g[:P].cpu(), q_ref)
+    assert torch.equal(off_g.cpu(), off_ref)
+    assert torch.equal(bh_g[:P].cpu(), bh_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_selection_trailing_partial_block(dtype):
+    """A selected trailing partial block is attended in the forward and gets its
+    dK/dV in the backward (oracle: tokens past the block grid reached through
+    their own block, nsa_selection_kernel.py:141-146)."""
+    dev = require_gpu()
+    import nsa_selection_backward as nsb
+    B, Hq, Hkv, T, D, bs, S = 1, 8, 2, 100, 64, 32, 4
+    q = randn((B, Hq, T, D), 1, dtype)
+    k = randn((B, Hkv, T, D), 2, dtype)
+    v = randn((B, Hkv, T, D), 3, dtype)
+    do = randn((B, Hq, T, D), 4, dtype)
+    idx = make_block_idx(B, Hkv, T, bs, S, seed=5)
+    idx[:, :, 96:, -1] = 3
+    q64, k64, v64, do64 = (t.double().requires_grad_() for t in (q, k, v, do))
+    o_ref, _ = O.selection_attention(q64, k64, v64, idx, bs)
+    o_ref.backward(do64)
+    xs = [t.to(dev).requires_grad_() for t in (q, k, v)]
+    o = nsb.selection_attn_triton(*xs, idx.to(dev), bs)
+    o.backward(do.to(dev))
+    torch.cuda.synchronize()
+    assert_close(o, o_ref, dtype, "o")
+    for nm, x, r in zip("qkv", xs, (q64, k64, v64)):
+        assert_close(x.grad, r.grad, dtype, f"d{nm}")
+    assert float(xs[1].grad[:, :, 96:].abs().max()) > 0

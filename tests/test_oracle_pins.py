@@ -344,6 +344,23 @@ def test_csr_invariants_and_counts():
                 assert (seg >= j * ls).all()                            # causal
 
 
+def test_csr_trailing_partial_block():
+    """Reference grid (T // ls): a causal pair on the partial block raises, like
+    the reference's scatter_add_ into n_blk columns; the ceil grid keeps it as
+    its own last block (brute force)."""
+    B, Hkv, T, ls, S = 1, 1, 50, 16, 3
+    idx = _random_block_idx(B, Hkv, T, ls, S, seed=3)
+    idx[0, 0, 49, 2] = 3                       # tokens 48..49, causal for t = 49
+    with pytest.raises(IndexError):
+        O.build_block_to_query_csr(idx, ls)
+    qob, off, pbh = O.build_block_to_query_csr(idx, ls, 4)
+    assert off.shape == (1, 1, 5)
+    assert qob[off[0, 0, 3]:off[0, 0, 4]].tolist() == [49]
+    idx[0, 0, 20, 2] = 3                       # block 3 starts at 48 > 20: dropped, no error
+    idx[0, 0, 49, 2] = -1
+    O.build_block_to_query_csr(idx, ls)
+
+
 # ------------------------------------------------------------- rows vs dense
 
 def test_rows_path_matches_dense_path():
