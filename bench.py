@@ -200,7 +200,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="c3", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-rows", type=int, default=96, help="query rows of the CPU baseline sample")
+    ap.add_argument("--cpu-rows", type=int, default=1024,
+                    help="query rows of the CPU baseline sample (about 10-20 s of CPU work at c3)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, os.cpu_count())")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--spans", action="store_true", help="print the per-call HIP-event breakdown to stderr")

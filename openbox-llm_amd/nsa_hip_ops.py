@@ -510,15 +510,28 @@ class NSAFusedHIP(torch.autograd.Function):
     branches accumulated into one float32 buffer, key-side dK/dV per branch,
     pool backward.  Same outputs and gradients as composing the per-branch
     Functions (nsa_fused_kernel.py:560-573).
+
+    With ``pooled=True`` the compression inputs ``kc``/``vc`` are already the
+    pooled tokens ``[B,Hkv,n_cmp,D]`` (the learned BlockCompressor of the
+    model path, nsa_model.py:334-337) and receive their gradients directly.
     """
 
     @staticmethod
-    def forward(ctx, q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom):
+    def forward(ctx, q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled=False):
         check_qkv(q, kc, vc)
+        check_qkv(q, ks, vs)
+        check_qkv(q, kw, vw)
         q, kc, vc, ks, vs, kw, vw, gate = (_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate))
         T = q.shape[2]
-        k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
-        v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
+        assert ks.shape[2] == T and kw.shape[2] == T, "selection / window keys must have the query length"
+        if pooled:
+            assert kc.shape[2] == n_cmp_tokens(T, geom.cmp_block, geom.cmp_stride), \
+                "pooled compression keys must have (T - l) // d + 1 tokens"
+            k_cmp, v_cmp = kc, vc
+        else:
+            assert kc.shape[2] == T, "compression keys must have the query length"
+            k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+            v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
         o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride)
         if block_idx is None:
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
@@ -533,6 +546,7 @@ class NSAFusedHIP(torch.autograd.Function):
         ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w)
         ctx.geom = geom
         ctx.T = T
+        ctx.pooled = pooled
         ctx.mark_non_differentiable(idx)
         return out, idx
 
@@ -562,8 +576,11 @@ class NSAFusedHIP(torch.autograd.Function):
         else:
             dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
             dvp = torch.zeros_like(dkp)
-        dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
-        dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
+        if ctx.pooled:
+            dkc, dvc = cast_f32(dkp, dtype), cast_f32(dvp, dtype)
+        else:
+            dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
+            dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
         # selection
         if idx.shape[-1] > 0:
             kt_s = transpose_kv(ks)
@@ -573,14 +590,15 @@ class NSAFusedHIP(torch.autograd.Function):
             dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
             dvs = torch.zeros_like(dks)
         return (cast_f32(dq, dtype), dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
-                cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None)
+                cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None, None)
 
 
-def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None):
+def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None, pooled=False):
     """Full NSA attention (pre out-projection) on the HIP path.
 
     With ``block_idx=None`` the block choice comes from the compression
     importance and top-n (nsa_model.py:343-355) computed on the GPU.
+    ``pooled=True``: ``kc``/``vc`` are pooled compression tokens.
     Returns ``(out, block_idx)``.
     """
-    return NSAFusedHIP.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom)
+    return NSAFusedHIP.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom, pooled)
