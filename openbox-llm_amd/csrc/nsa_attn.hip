@@ -1,10 +1,9 @@
-// Query-side NSA kernels: selection forward / dQ (gathered blocks) and the
-// range branches (sliding window, compression over pooled keys) forward / dQ.
+// Query-side selection kernels: forward and dQ over the gathered blocks.
 //
-// One wave owns one 16-head column block of a query (or QW consecutive
-// queries for the range branches, which share keys) and streams 32-key steps
-// through nsa_tiles.h.  Workgroups are four waves over neighbouring queries of
-// the same KV head, mapped onto one XCD so that shared blocks hit its L2.
+// One wave owns one 16-head column block of a query and streams its selected
+// blocks in 32-key steps through nsa_tiles.h.  Workgroups are four waves over
+// neighbouring queries of the same KV head, mapped onto one XCD so that
+// shared blocks hit its L2.
 #include "nsa_launch.h"
 #include "nsa_tiles.h"
 
@@ -26,23 +25,6 @@ __device__ __forceinline__ QueryMap map_bh_hc(int64_t r, int Hq, int Hkv) {
   m.hkv = m.bh % Hkv;
   m.head0 = m.hkv * m.G + m.hc * 16;
   return m;
-}
-
-// visible key range [lo, hi] of query t in a range branch
-__device__ __forceinline__ void range_bounds(int mode, int t, int Lk, int window, int cl, int cd, int& lo,
-                                             int& hi) {
-  if (mode == NSA_MODE_WINDOW) {
-    lo = t - window + 1 > 0 ? t - window + 1 : 0;
-    hi = t < Lk - 1 ? t : Lk - 1;
-  } else {
-    lo = 0;
-    if (t >= cl - 1) {
-      const int i = (t - cl + 1) / cd;
-      hi = i < Lk - 1 ? i : Lk - 1;
-    } else {
-      hi = -1;
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -88,66 +70,6 @@ __global__ __launch_bounds__(256) void k_sel_fwd(const T* __restrict__ q, const 
     }
   }
   fwd_store<T, D>(acc, col_ok ? o + row * D : nullptr, lse + row, g);
-}
-
-// ---------------------------------------------------------------------------
-// range forward (window / compression), QW queries per wave
-// ---------------------------------------------------------------------------
-template <typename T, int D, int QW>
-__global__ __launch_bounds__(256) void k_range_fwd(int mode, const T* __restrict__ q, const T* __restrict__ k,
-                                                   const T* __restrict__ vt, T* __restrict__ o,
-                                                   float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
-                                                   int Lp, int nqt, int window, int cl, int cd, float sl2) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
-  int qt = (int)(wg % nqt);
-  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first
-  const QueryMap m = map_bh_hc(wg / nqt, Hq, Hkv);
-  const int t0 = (qt * 4 + w) * QW;
-  if (t0 >= T_) return;
-  const bool col_ok = m.hc * 16 + c < m.G;
-  const T* kb_ = k + (int64_t)m.bh * Lk * D;
-  const T* vtb = vt + (int64_t)m.bh * D * Lp;
-  const int64_t row0 = ((int64_t)m.b * Hq + m.head0 + c) * T_;
-  Frag<T> qf[QW][Dims<D>::KC];
-  FwdAcc<D> acc[QW];
-  int lo[QW], hi[QW];
-  int klo = 1 << 30, khi = -1;
-#pragma unroll
-  for (int qi = 0; qi < QW; ++qi) {
-    const int t = t0 + qi;
-    const bool ok = t < T_;
-    load_row_frags<T, D>(qf[qi], (ok && col_ok) ? q + (row0 + t) * D : nullptr, g);
-    acc[qi].init();
-    if (ok) {
-      range_bounds(mode, t, Lk, window, cl, cd, lo[qi], hi[qi]);
-    } else {
-      lo[qi] = 0;
-      hi[qi] = -1;
-    }
-    if (hi[qi] >= lo[qi]) {
-      klo = lo[qi] < klo ? lo[qi] : klo;
-      khi = hi[qi] > khi ? hi[qi] : khi;
-    }
-  }
-  if (khi >= 0) {
-    for (int kb = klo & ~31; kb <= khi; kb += 32) {
-      Frag<T> kf[2][Dims<D>::KC];
-      Frag<T> vf[Dims<D>::DT];
-      load_key_frags<T, D>(kf, kb_, kb, Lk, g, c);
-      load_t_frags<T, D>(vf, vtb, Lp, kb, g, c);
-#pragma unroll
-      for (int qi = 0; qi < QW; ++qi) {
-        const uint32_t vm = col_ok ? range_mask(kb + 8 * g, lo[qi], hi[qi]) : 0u;
-        fwd_step<T, D>(acc[qi], qf[qi], kf, vf, vm, sl2);
-      }
-    }
-  }
-#pragma unroll
-  for (int qi = 0; qi < QW; ++qi) {
-    const int t = t0 + qi;
-    if (t < T_) fwd_store<T, D>(acc[qi], col_ok ? o + (row0 + t) * D : nullptr, lse + row0 + t, g);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -216,77 +138,9 @@ __global__ __launch_bounds__(256) void k_sel_dq(const T* __restrict__ q, const T
   if (col_ok) dq_store<D>(acc, dq + row * D, g, scale, accumulate != 0);
 }
 
-template <typename T, int D, int QW>
-__global__ __launch_bounds__(256) void k_range_dq(int mode, const T* __restrict__ q, const T* __restrict__ k,
-                                                  const T* __restrict__ v, const T* __restrict__ kt,
-                                                  const T* __restrict__ dout, const float* __restrict__ lse,
-                                                  const float* __restrict__ dot,
-                                                  const float* __restrict__ rowscale, float* __restrict__ dq,
-                                                  int accumulate, int Hq, int Hkv, int T_, int Lk, int Lp,
-                                                  int nqt, int window, int cl, int cd, float sl2, float scale) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
-  int qt = (int)(wg % nqt);
-  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;
-  const QueryMap m = map_bh_hc(wg / nqt, Hq, Hkv);
-  const int t0 = (qt * 4 + w) * QW;
-  if (t0 >= T_) return;
-  const bool col_ok = m.hc * 16 + c < m.G;
-  const T* kb_ = k + (int64_t)m.bh * Lk * D;
-  const T* vb_ = v + (int64_t)m.bh * Lk * D;
-  const T* ktb = kt + (int64_t)m.bh * D * Lp;
-  const int64_t row0 = ((int64_t)m.b * Hq + m.head0 + c) * T_;
-  Frag<T> qf[QW][Dims<D>::KC], df[QW][Dims<D>::KC];
-  DqRow rs[QW];
-  f32x4 acc[QW][Dims<D>::DT];
-  int lo[QW], hi[QW];
-  int klo = 1 << 30, khi = -1;
-#pragma unroll
-  for (int qi = 0; qi < QW; ++qi) {
-    const int t = t0 + qi;
-    const bool ok = t < T_ && col_ok;
-    load_row_frags<T, D>(qf[qi], ok ? q + (row0 + t) * D : nullptr, g);
-    load_row_frags<T, D>(df[qi], ok ? dout + (row0 + t) * D : nullptr, g);
-    rs[qi] = load_dq_row(lse, rowscale, dot, row0 + t, ok);
-#pragma unroll
-    for (int dt = 0; dt < Dims<D>::DT; ++dt) acc[qi][dt] = zero4();
-    if (t < T_) {
-      range_bounds(mode, t, Lk, window, cl, cd, lo[qi], hi[qi]);
-    } else {
-      lo[qi] = 0;
-      hi[qi] = -1;
-    }
-    if (hi[qi] >= lo[qi]) {
-      klo = lo[qi] < klo ? lo[qi] : klo;
-      khi = hi[qi] > khi ? hi[qi] : khi;
-    }
-  }
-  if (khi >= 0) {
-    for (int kb = klo & ~31; kb <= khi; kb += 32) {
-      Frag<T> kf[2][Dims<D>::KC], vf[2][Dims<D>::KC];
-      Frag<T> ktf[Dims<D>::DT];
-      load_key_frags<T, D>(kf, kb_, kb, Lk, g, c);
-      load_key_frags<T, D>(vf, vb_, kb, Lk, g, c);
-      load_t_frags<T, D>(ktf, ktb, Lp, kb, g, c);
-#pragma unroll
-      for (int qi = 0; qi < QW; ++qi) {
-        const uint32_t vm = col_ok ? range_mask(kb + 8 * g, lo[qi], hi[qi]) : 0u;
-        dq_step<T, D>(acc[qi], qf[qi], df[qi], kf, vf, ktf, vm, sl2, rs[qi].lse2, rs[qi].rs, rs[qi].dot);
-      }
-    }
-  }
-#pragma unroll
-  for (int qi = 0; qi < QW; ++qi) {
-    const int t = t0 + qi;
-    if (t < T_ && col_ok) dq_store<D>(acc[qi], dq + (row0 + t) * D, g, scale, accumulate != 0);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // dispatch helpers
 // ---------------------------------------------------------------------------
-template <int QW> struct QwFor {};
-
 #define NSA_DISPATCH_D(D_, ...)                  \
   switch (D_) {                                  \
     case 16: { constexpr int DD = 16; __VA_ARGS__; break; } \
@@ -295,8 +149,6 @@ template <int QW> struct QwFor {};
     case 128: { constexpr int DD = 128; __VA_ARGS__; break; } \
     default: return NSA_ERR_SHAPE;               \
   }
-
-template <int D> constexpr int range_qw() { return D >= 128 ? 2 : 4; }
 
 }  // namespace nsa
 
@@ -362,68 +214,6 @@ int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, cons
                                                          (const float*)kt, (const float*)dout, block_idx, lse,
                                                          dot, rowscale, dq, accumulate, Hq, Hkv, T, S,
                                                          block_size, Lp, nqb, sl2, scale);
-  });
-  return nsa_launch_status();
-}
-
-int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
-                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
-                  void* stream) {
-  NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
-  NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && Lk >= 0 && nsa_d_ok(D), NSA_ERR_SHAPE);
-  NSA_CHECK(mode == NSA_MODE_COMPRESS || (window >= 1 && Lk == T), NSA_ERR_SHAPE);
-  NSA_CHECK(mode == NSA_MODE_WINDOW || (cmp_block >= 1 && cmp_stride >= 1), NSA_ERR_SHAPE);
-  NSA_CHECK(nsa_dtype_ok(dtype), NSA_ERR_DTYPE);
-  if (T == 0) return NSA_OK;
-  const int G = Hq / Hkv, NHC = (G + 15) / 16;
-  const int Lp = nsa::padded_len(Lk);
-  const float sl2 = (1.0f / sqrtf((float)D)) * nsa::kLog2e;
-  hipStream_t s = (hipStream_t)stream;
-  NSA_DISPATCH_D(D, {
-    constexpr int QW = range_qw<DD>();
-    const int nqt = (T + 4 * QW - 1) / (4 * QW);
-    const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-    NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-    if (dtype == NSA_BF16)
-      k_range_fwd<bf16, DD, QW><<<(unsigned)grid, 256, 0, s>>>(mode, (const bf16*)q, (const bf16*)k,
-                                                               (const bf16*)vt, (bf16*)o, lse, Hq, Hkv, T, Lk,
-                                                               Lp, nqt, window, cmp_block, cmp_stride, sl2);
-    else
-      k_range_fwd<float, DD, QW><<<(unsigned)grid, 256, 0, s>>>(mode, (const float*)q, (const float*)k,
-                                                                (const float*)vt, (float*)o, lse, Hq, Hkv, T,
-                                                                Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2);
-  });
-  return nsa_launch_status();
-}
-
-int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
-                 const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
-                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
-                 void* stream) {
-  NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
-  NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && Lk >= 0 && nsa_d_ok(D), NSA_ERR_SHAPE);
-  NSA_CHECK(mode == NSA_MODE_COMPRESS || (window >= 1 && Lk == T), NSA_ERR_SHAPE);
-  NSA_CHECK(mode == NSA_MODE_WINDOW || (cmp_block >= 1 && cmp_stride >= 1), NSA_ERR_SHAPE);
-  NSA_CHECK(nsa_dtype_ok(dtype), NSA_ERR_DTYPE);
-  if (T == 0) return NSA_OK;
-  const int G = Hq / Hkv, NHC = (G + 15) / 16;
-  const int Lp = nsa::padded_len(Lk);
-  const float scale = 1.0f / sqrtf((float)D);
-  const float sl2 = scale * nsa::kLog2e;
-  hipStream_t s = (hipStream_t)stream;
-  NSA_DISPATCH_D(D, {
-    constexpr int QW = range_qw<DD>();
-    const int nqt = (T + 4 * QW - 1) / (4 * QW);
-    const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-    NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-    if (dtype == NSA_BF16)
-      k_range_dq<bf16, DD, QW><<<(unsigned)grid, 256, 0, s>>>(
-          mode, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)kt, (const bf16*)dout, lse, dot,
-          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
-    else
-      k_range_dq<float, DD, QW><<<(unsigned)grid, 256, 0, s>>>(
-          mode, (const float*)q, (const float*)k, (const float*)v, (const float*)kt, (const float*)dout, lse,
-          dot, rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
   });
   return nsa_launch_status();
 }

@@ -1,0 +1,560 @@
+// Range branches of NSA (sliding window, compression over pooled keys):
+// forward and dQ, LDS-tiled on 32x32 MFMAs.
+//
+// Rows of the attention are (query, head) pairs: the 16 heads of one GQA head
+// chunk of a query form 16 consecutive rows, so a 32-row MFMA tile holds two
+// queries.  A wave owns NT such tiles (2*NT consecutive queries) and a
+// workgroup of four waves owns 8*NT consecutive queries of one KV head chunk.
+// The workgroup walks the union of its queries' visible key range in 32-key
+// tiles; each tile of K (row-major) and V^T (or K, V and K^T for dQ) is
+// staged once in LDS by direct global -> LDS loads, double-buffered, and read
+// by all four waves.
+//
+//   forward:  S^T = K Q^T (keys on M, rows on N), online softmax per row,
+//             O^T += V^T P^T with P^T taken straight from the S^T accumulator
+//   dQ:       S^T = K Q^T, dP^T = V dO^T, dS^T = P^T (dP^T - delta),
+//             dQ^T += K^T dS^T
+// Key rows of K / V are read through perm32 so that the accumulator registers
+// line up with the next contraction's operand slots (nsa_tile32.h).
+#include "nsa_launch.h"
+#include "nsa_tile32.h"
+
+namespace nsa {
+
+struct RangeMap {
+  int b, hkv, hc, head0, G, NHC;
+};
+
+__device__ __forceinline__ RangeMap range_map(int64_t r, int Hq, int Hkv) {
+  RangeMap m;
+  m.G = Hq / Hkv;
+  m.NHC = (m.G + 15) / 16;
+  m.hc = (int)(r % m.NHC);
+  const int bh = (int)(r / m.NHC);
+  m.b = bh / Hkv;
+  m.hkv = bh % Hkv;
+  m.head0 = m.hkv * m.G + m.hc * 16;
+  return m;
+}
+
+// visible key range [lo, hi] of query t (hi < lo: none)
+__device__ __forceinline__ void visible_range(int mode, int t, int Lk, int window, int cl, int cd, int& lo,
+                                              int& hi) {
+  if (mode == NSA_MODE_WINDOW) {
+    lo = t - window + 1 > 0 ? t - window + 1 : 0;
+    hi = t < Lk - 1 ? t : Lk - 1;
+  } else {
+    lo = 0;
+    hi = t >= cl - 1 ? (t - cl + 1) / cd : -1;
+    hi = hi < Lk - 1 ? hi : Lk - 1;
+  }
+}
+
+// DMA of one 32-key tile into LDS: a row tile of keys kb .. kb+31 from a
+// row-major [Lk][D] tensor (keys past the end read the last key: finite data
+// no row sees) and a column tile from a transposed [D][Lp] copy.
+template <typename T, int D>
+__device__ __forceinline__ void dma_key_rows(T* lds, const T* src, int kb, int Lk, int tid) {
+  using C = Tile32<T, D>;
+  dma_tile<256, C::ROW_CHUNKS>(lds, [&](int P) {
+    int r, c;
+    row_chunk<T, D>(P, r, c);
+    const int key = kb + r < Lk ? kb + r : Lk - 1;
+    return (const void*)(src + (int64_t)key * D + c * C::EPC);
+  }, tid);
+}
+
+template <typename T, int D>
+__device__ __forceinline__ void dma_key_cols(T* lds, const T* src, int kb, int Lp, int tid) {
+  using C = Tile32<T, D>;
+  dma_tile<256, C::COL_CHUNKS>(lds, [&](int P) {
+    int d, c;
+    col_chunk<T, D>(P, d, c);
+    return (const void*)(src + (int64_t)d * Lp + kb + c * C::EPC);
+  }, tid);
+}
+
+// Workgroup / wave query and key ranges of a range launch.
+struct RangeSpan {
+  int klo, khi;     // union of visible keys of the workgroup's queries
+  int wlo, whi;     // union for this wave's queries
+};
+
+__device__ __forceinline__ RangeSpan range_span(int mode, int tb0, int qpb, int tw0, int qpw, int T_, int Lk,
+                                                int window, int cl, int cd) {
+  RangeSpan s;
+  int lo, hi;
+  const int tb1 = tb0 + qpb - 1 < T_ - 1 ? tb0 + qpb - 1 : T_ - 1;
+  visible_range(mode, tb0, Lk, window, cl, cd, s.klo, hi);
+  visible_range(mode, tb1, Lk, window, cl, cd, lo, s.khi);
+  if (tw0 < T_) {
+    const int tw1 = tw0 + qpw - 1 < T_ - 1 ? tw0 + qpw - 1 : T_ - 1;
+    visible_range(mode, tw0, Lk, window, cl, cd, s.wlo, hi);
+    visible_range(mode, tw1, Lk, window, cl, cd, lo, s.whi);
+  } else {
+    s.wlo = 0;
+    s.whi = -1;
+  }
+  return s;
+}
+
+// Keys visible to every valid query of a wave: a tile inside [lo, hi] needs no
+// per-element mask.
+struct FullSpan {
+  int lo, hi;
+};
+
+__device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_, int Lk, int window, int cl,
+                                              int cd) {
+  FullSpan f;
+  if (tw0 >= T_) {
+    f.lo = 0;
+    f.hi = 1 << 30;   // no valid row: nothing to mask
+    return f;
+  }
+  const int tw1 = tw0 + qpw - 1 < T_ - 1 ? tw0 + qpw - 1 : T_ - 1;
+  int lo0, hi0, lo1, hi1;
+  visible_range(mode, tw0, Lk, window, cl, cd, lo0, hi0);
+  visible_range(mode, tw1, Lk, window, cl, cd, lo1, hi1);
+  f.lo = lo1 > lo0 ? lo1 : lo0;   // lo and hi are non-decreasing in t
+  f.hi = hi0 < hi1 ? hi0 : hi1;
+  return f;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kRescale = 8.0f;   // log2 growth of a row maximum that forces a rescale
+
+// One 32-key tile of the forward for NT row tiles.  MASK = false: every key
+// of the tile is visible to every valid row of the wave (no per-element test).
+// The row maximum m is only moved when the tile's maximum exceeds it by more
+// than kRescale (wave-uniform branch); p = exp2(s - m) <= 2^kRescale keeps the
+// sum and the bf16 P operand in range, and the final 1/l normalises exactly.
+template <typename T, int D, int NT, int DT = Tile32<T, D>::DT, int KS = Tile32<T, D>::KS>
+__device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT], float (&l_)[NT],
+                                         const Frag<T> (&qf)[NT][KS], const T* tK, const T* tV, int kb, bool mask,
+                                         const int (&lo)[NT], const int (&hi)[NT], float sl2, int n, int h) {
+  // all K fragments of the tile first, so the LDS reads are in flight together
+  Frag<T> ka[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) lds_row_frag<T, D>(ka[s], tK, n, h, s);
+  f32x16 st[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) st[nt] = zero16();
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) mma32(st[nt], ka[s], qf[nt][s]);
+  // V^T fragments of the tile, issued before the softmax arithmetic
+  Frag<T> va[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) lds_col_frag<T, D>(va[dt][s], tV, dt, n, h, s);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) st[nt][r] *= sl2;
+  if (mask) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + acc_elem(h, r);
+        st[nt][r] = (key >= lo[nt] && key <= hi[nt]) ? st[nt][r] : kNegInf;
+      }
+  }
+  float mx[NT];
+  bool need = false;
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float v = st[nt][0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) v = fmaxf(v, st[nt][r]);
+    mx[nt] = fmaxf(v, __shfl_xor(v, 32, kWave));
+    need |= mx[nt] > m_[nt] + kRescale;
+  }
+  if (__any(need)) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const float mn = mx[nt] > m_[nt] + kRescale ? mx[nt] : m_[nt];
+      const float alpha = fast_exp2(m_[nt] - mn);
+      l_[nt] *= alpha;
+      m_[nt] = mn;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt][nt] *= alpha;
+    }
+  }
+  Frag<T> pf[NT][2];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float p[16];
+    float ps = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = fast_exp2(st[nt][r] - m_[nt]);
+      ps += p[r];
+    }
+    l_[nt] += ps;
+    pf[nt][0].set(p);
+    pf[nt][1].set(p + 8);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], va[dt][s], pf[nt][s]);
+}
+
+template <typename T, int D, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_fwd32(int mode, const T* __restrict__ q, const T* __restrict__ k,
+                                                     const T* __restrict__ vt, T* __restrict__ o,
+                                                     float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
+                                                     int Lp, int nqt, int window, int cl, int cd, float sl2) {
+  using C = Tile32<T, D>;
+  constexpr int QPW = 2 * NT, QPB = 4 * QPW;
+  __shared__ __align__(16) T sK[2][C::ROW_ELEMS];
+  __shared__ __align__(16) T sV[2][C::COL_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
+  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  int qt = (int)(wg % nqt);
+  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first
+  const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
+  const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
+  if (tb0 >= T_) return;
+  const RangeSpan sp = range_span(mode, tb0, QPB, tw0, QPW, T_, Lk, window, cl, cd);
+  const FullSpan fs = full_span(mode, tw0, QPW, T_, Lk, window, cl, cd);
+  const int bh = mp.b * Hkv + mp.hkv;
+  const T* kbase = k + (int64_t)bh * Lk * D;
+  const T* vtbase = vt + (int64_t)bh * D * Lp;
+
+  const int hd = n & 15;
+  const bool hok = mp.hc * 16 + hd < mp.G;
+  const int hsafe = hok ? hd : 0;
+  Frag<T> qf[NT][C::KS];
+  int lo[NT], hi[NT];
+  int64_t row[NT];
+  bool rok[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int t = tw0 + 2 * nt + (n >> 4);
+    rok[nt] = hok && t < T_;
+    row[nt] = ((int64_t)mp.b * Hq + mp.head0 + hd) * T_ + t;
+    const int64_t srow = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + (t < T_ ? t : T_ - 1);
+    visible_range(mode, t < T_ ? t : T_ - 1, Lk, window, cl, cd, lo[nt], hi[nt]);
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) qf[nt][s].load(q + srow * D + 16 * s + 8 * h);
+  }
+  float m_[NT], l_[NT];
+  f32x16 acc[C::DT][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_[nt] = kMaskScore;
+    l_[nt] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) acc[dt][nt] = zero16();
+  }
+
+  const int kt0 = sp.klo & ~31;
+  const int ntile = sp.khi >= sp.klo ? (sp.khi - kt0) / 32 + 1 : 0;
+  if (ntile > 0) {
+    dma_key_rows<T, D>(sK[0], kbase, kt0, Lk, tid);
+    dma_key_cols<T, D>(sV[0], vtbase, kt0, Lp, tid);
+  }
+  lds_dma_wait();
+  __syncthreads();
+  for (int it = 0; it < ntile; ++it) {
+    const int kb = kt0 + 32 * it;
+    const int buf = it & 1;
+    if (it + 1 < ntile) {
+      dma_key_rows<T, D>(sK[buf ^ 1], kbase, kb + 32, Lk, tid);
+      dma_key_cols<T, D>(sV[buf ^ 1], vtbase, kb + 32, Lp, tid);
+    }
+    // every wave takes every tile of the workgroup range (the waves' own ranges
+    // differ by at most a few queries); tiles inside the wave's fully visible
+    // span skip the per-element mask
+    const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
+    fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[buf], sV[buf], kb, mask, lo, hi, sl2, n, h);
+    lds_dma_wait();
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const float lt = l_[nt] + __shfl_xor(l_[nt], 32, kWave);
+    if (!rok[nt]) continue;
+    const bool any_key = lo[nt] <= hi[nt];
+    const float inv = any_key ? 1.0f / lt : 0.0f;
+    T* orow = o + row[nt] * D;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * dt + 8 * g4 + 4 * h;
+        if (D % 32 == 0 || d < D)
+          store4(orow + d, acc[dt][nt][4 * g4] * inv, acc[dt][nt][4 * g4 + 1] * inv, acc[dt][nt][4 * g4 + 2] * inv,
+                 acc[dt][nt][4 * g4 + 3] * inv);
+      }
+    }
+    if (h == 0) lse[row[nt]] = any_key ? (m_[nt] + __log2f(lt)) * kLn2 : kLseEmpty;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+// One 32-key tile of dQ for NT row tiles; c = lse*log2(e) - log2(rowscale) per
+// row, so P = exp2(S*sl2 - c) carries the gate weight.
+template <typename T, int D, int NT, int DT = Tile32<T, D>::DT, int KS = Tile32<T, D>::KS>
+__device__ __forceinline__ void dq_tile(f32x16 (&acc)[DT][NT], const Frag<T> (&qf)[NT][KS],
+                                        const Frag<T> (&df)[NT][KS], const T* tK, const T* tV, const T* tKt, int kb,
+                                        bool mask, const int (&lo)[NT], const int (&hi)[NT], const float (&c)[NT],
+                                        const float (&dlt)[NT], float sl2, int n, int h) {
+  f32x16 st[NT], pt[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    st[nt] = zero16();
+    pt[nt] = zero16();
+  }
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    Frag<T> a, b;
+    lds_row_frag<T, D>(a, tK, n, h, s);
+    lds_row_frag<T, D>(b, tV, n, h, s);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      mma32(st[nt], a, qf[nt][s]);
+      mma32(pt[nt], b, df[nt][s]);
+    }
+  }
+  // K^T fragments of the tile, issued before the dS arithmetic
+  Frag<T> ka[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) lds_col_frag<T, D>(ka[dt][s], tKt, dt, n, h, s);
+  Frag<T> dsf[NT][2];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    float p[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(st[nt][r] * sl2 - c[nt]);
+    if (mask) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = kb + acc_elem(h, r);
+        p[r] = (key >= lo[nt] && key <= hi[nt]) ? p[r] : 0.0f;
+      }
+    }
+    float ds[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ds[r] = p[r] * (pt[nt][r] - dlt[nt]);
+    dsf[nt][0].set(ds);
+    dsf[nt][1].set(ds + 8);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], ka[dt][s], dsf[nt][s]);
+}
+
+template <typename T, int D, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_dq32(int mode, const T* __restrict__ q, const T* __restrict__ k,
+                                                    const T* __restrict__ v, const T* __restrict__ kt,
+                                                    const T* __restrict__ dout, const float* __restrict__ lse,
+                                                    const float* __restrict__ dot,
+                                                    const float* __restrict__ rowscale, float* __restrict__ dq,
+                                                    int accumulate, int Hq, int Hkv, int T_, int Lk, int Lp, int nqt,
+                                                    int window, int cl, int cd, float sl2, float scale) {
+  using C = Tile32<T, D>;
+  constexpr int QPW = 2 * NT, QPB = 4 * QPW;
+  __shared__ __align__(16) T sK[2][C::ROW_ELEMS];
+  __shared__ __align__(16) T sV[2][C::ROW_ELEMS];
+  __shared__ __align__(16) T sKt[2][C::COL_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
+  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  int qt = (int)(wg % nqt);
+  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;
+  const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
+  const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
+  if (tb0 >= T_) return;
+  const RangeSpan sp = range_span(mode, tb0, QPB, tw0, QPW, T_, Lk, window, cl, cd);
+  const FullSpan fs = full_span(mode, tw0, QPW, T_, Lk, window, cl, cd);
+  const int bh = mp.b * Hkv + mp.hkv;
+
+  const int hd = n & 15;
+  const bool hok = mp.hc * 16 + hd < mp.G;
+  const int hsafe = hok ? hd : 0;
+  Frag<T> qf[NT][C::KS], df[NT][C::KS];
+  int lo[NT], hi[NT];
+  int64_t row[NT];
+  bool rok[NT];
+  float c[NT], dlt[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int t = tw0 + 2 * nt + (n >> 4);
+    const int tc = t < T_ ? t : T_ - 1;
+    rok[nt] = hok && t < T_;
+    row[nt] = ((int64_t)mp.b * Hq + mp.head0 + hd) * T_ + t;
+    const int64_t srow = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + tc;
+    visible_range(mode, tc, Lk, window, cl, cd, lo[nt], hi[nt]);
+    const float rs = rowscale != nullptr ? rowscale[srow] : 1.0f;
+    c[nt] = lse[srow] * kLog2e - __log2f(rs);
+    dlt[nt] = dot[srow];
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) {
+      qf[nt][s].load(q + srow * D + 16 * s + 8 * h);
+      df[nt][s].load(dout + srow * D + 16 * s + 8 * h);
+    }
+  }
+  f32x16 acc[C::DT][NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) acc[dt][nt] = zero16();
+
+  const int kt0 = sp.klo & ~31;
+  const int ntile = sp.khi >= sp.klo ? (sp.khi - kt0) / 32 + 1 : 0;
+  const T* kbase = k + (int64_t)bh * Lk * D;
+  const T* vbase = v + (int64_t)bh * Lk * D;
+  const T* ktbase = kt + (int64_t)bh * D * Lp;
+  if (ntile > 0) {
+    dma_key_rows<T, D>(sK[0], kbase, kt0, Lk, tid);
+    dma_key_rows<T, D>(sV[0], vbase, kt0, Lk, tid);
+    dma_key_cols<T, D>(sKt[0], ktbase, kt0, Lp, tid);
+  }
+  lds_dma_wait();
+  __syncthreads();
+  for (int it = 0; it < ntile; ++it) {
+    const int kb = kt0 + 32 * it;
+    const int buf = it & 1;
+    if (it + 1 < ntile) {
+      dma_key_rows<T, D>(sK[buf ^ 1], kbase, kb + 32, Lk, tid);
+      dma_key_rows<T, D>(sV[buf ^ 1], vbase, kb + 32, Lk, tid);
+      dma_key_cols<T, D>(sKt[buf ^ 1], ktbase, kb + 32, Lp, tid);
+    }
+    const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
+    dq_tile<T, D, NT>(acc, qf, df, sK[buf], sV[buf], sKt[buf], kb, mask, lo, hi, c, dlt, sl2, n, h);
+    lds_dma_wait();
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    if (!rok[nt]) continue;
+    float* qrow = dq + row[nt] * D;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * dt + 8 * g4 + 4 * h;
+        if (D % 32 == 0 || d < D) {
+          f32x4 val = (f32x4){acc[dt][nt][4 * g4], acc[dt][nt][4 * g4 + 1], acc[dt][nt][4 * g4 + 2],
+                              acc[dt][nt][4 * g4 + 3]} * scale;
+          if (accumulate) val += *reinterpret_cast<const f32x4*>(qrow + d);
+          *reinterpret_cast<f32x4*>(qrow + d) = val;
+        }
+      }
+    }
+  }
+}
+
+template <typename T> struct RangeNT { static constexpr int fwd = 1; static constexpr int dq = 1; };
+
+}  // namespace nsa
+
+using namespace nsa;
+
+#define NSA_DISPATCH_D(D_, ...)                                 \
+  switch (D_) {                                                 \
+    case 16: { constexpr int DD = 16; __VA_ARGS__; break; }    \
+    case 32: { constexpr int DD = 32; __VA_ARGS__; break; }    \
+    case 64: { constexpr int DD = 64; __VA_ARGS__; break; }    \
+    case 128: { constexpr int DD = 128; __VA_ARGS__; break; }  \
+    default: return NSA_ERR_SHAPE;                              \
+  }
+
+static inline bool range_args_ok(int mode, int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cl,
+                                 int cd) {
+  if (B <= 0 || Hkv <= 0 || Hq % Hkv != 0 || T < 0 || Lk < 0) return false;
+  if (!(D == 16 || D == 32 || D == 64 || D == 128)) return false;
+  if (mode == NSA_MODE_WINDOW) return window >= 1 && Lk == T;
+  return cl >= 1 && cd >= 1;
+}
+
+extern "C" {
+
+int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
+                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                  void* stream) {
+  NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
+  NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  if (T == 0) return NSA_OK;
+  const int NHC = (Hq / Hkv + 15) / 16;
+  const int Lp = padded_len(Lk);
+  const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16) {
+      constexpr int NT = RangeNT<bf16>::fwd;
+      const int nqt = (T + 8 * NT - 1) / (8 * NT);
+      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+      k_range_fwd32<bf16, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const bf16*)q, (const bf16*)k,
+                                                                 (const bf16*)vt, (bf16*)o, lse, Hq, Hkv, T, Lk,
+                                                                 Lp, nqt, window, cmp_block, cmp_stride, sl2);
+    } else {
+      constexpr int NT = RangeNT<float>::fwd;
+      const int nqt = (T + 8 * NT - 1) / (8 * NT);
+      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+      k_range_fwd32<float, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const float*)q, (const float*)k,
+                                                                  (const float*)vt, (float*)o, lse, Hq, Hkv, T,
+                                                                  Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2);
+    }
+  });
+  return nsa_launch_status();
+}
+
+int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
+                 const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
+                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                 void* stream) {
+  NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
+  NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  if (T == 0) return NSA_OK;
+  const int NHC = (Hq / Hkv + 15) / 16;
+  const int Lp = padded_len(Lk);
+  const float scale = 1.0f / sqrtf((float)D);
+  const float sl2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16) {
+      constexpr int NT = RangeNT<bf16>::dq;
+      const int nqt = (T + 8 * NT - 1) / (8 * NT);
+      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+      k_range_dq32<bf16, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
+          mode, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)kt, (const bf16*)dout, lse, dot,
+          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
+    } else {
+      constexpr int NT = RangeNT<float>::dq;
+      const int nqt = (T + 8 * NT - 1) / (8 * NT);
+      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+      k_range_dq32<float, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
+          mode, (const float*)q, (const float*)k, (const float*)v, (const float*)kt, (const float*)dout, lse, dot,
+          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
+    }
+  });
+  return nsa_launch_status();
+}
+
+}  // extern "C"

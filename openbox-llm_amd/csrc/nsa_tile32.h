@@ -1,0 +1,136 @@
+// 32x32 MFMA tiles and LDS staging shared by the LDS-tiled NSA kernels
+// (range forward / dQ, and the key-side dK/dV kernel).
+//
+// One 32x32 MFMA per 16-deep contraction step (bf16: v_mfma_f32_32x32x16_bf16;
+// fp32: eight v_mfma_f32_32x32x2f32 over the same 8 slots per lane):
+//   A (32 x 16): lane (h = lane >> 5, m = lane & 31) holds A[m][slot(h, j)], j = 0..7
+//   B (16 x 32): lane (h, n) holds B[slot(h, j)][n]
+//   C (32 x 32): lane (h, n) register r holds C[8 (r >> 2) + 4 h + (r & 3)][n]
+// slot(h, j) is the same bijection on both operands, so a fragment only has
+// to hold the same 8 contraction indices on the A and B side.
+//
+// Operand rows are permuted inside a 32-row tile by perm32 (bits 2 and 3 of
+// the row swapped).  Accumulator registers 8s .. 8s+7 of lane half h then hold
+// tile elements 16s + 8h .. 16s + 8h + 7, which is exactly the B-operand
+// fragment of contraction step s over that tile: an S^T (or S) accumulator is
+// converted to the next MFMA's operand without moving data between lanes.
+//
+// LDS tiles are unpadded and filled by direct global -> LDS loads
+// (global_load_lds_dwordx4: lane i of a wave writes LDS base + 16 i).  Their
+// 16-byte chunks are XOR-swizzled per row so that the fragment reads of a
+// wave hit distinct banks:
+//   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r)
+//                        (rkey separates the 8 rows perm32 gives 8 adjacent lanes)
+//   column tile [D][32]: logical chunk c of row d sits at c ^ ckey(d)
+#pragma once
+
+#include "nsa_common.h"
+
+namespace nsa {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.0f;
+  return z;
+}
+
+__device__ __forceinline__ void mma32(f32x16& c, const Frag<bf16>& a, const Frag<bf16>& b) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void mma32(f32x16& c, const Frag<float>& a, const Frag<float>& b) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[j], b.lo[j], c, 0, 0, 0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[j], b.hi[j], c, 0, 0, 0);
+}
+
+// operand row m of a 32-row tile reads tile element perm32(m)
+__device__ __forceinline__ int perm32(int m) { return (m & 0x13) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// tile element held by accumulator register r of lane half h (after perm32)
+__device__ __forceinline__ int acc_elem(int h, int r) { return 16 * (r >> 3) + 8 * h + (r & 7); }
+
+template <typename T, int D> struct Tile32 {
+  static constexpr int KS = D / 16;                        // 16-deep contraction steps over D
+  static constexpr int DT = (D + 31) / 32;                 // 32-row tiles over D
+  static constexpr int EPC = 16 / (int)sizeof(T);          // elements per 16-byte chunk
+  static constexpr int RCH = D * (int)sizeof(T) / 16;      // chunks per row of a row tile
+  static constexpr int CCH = 32 * (int)sizeof(T) / 16;     // chunks per row of a column tile
+  static constexpr int ROW_ELEMS = 32 * D;                 // one [32][D] tile
+  static constexpr int COL_ELEMS = D * 32;                 // one [D][32] tile
+  static constexpr int ROW_CHUNKS = 32 * RCH;
+  static constexpr int COL_CHUNKS = D * CCH;
+  static __device__ __forceinline__ int rkey(int r) { return ((r & 3) | ((r >> 1) & 4)) & (RCH - 1); }
+  static __device__ __forceinline__ int ckey(int d) { return (CCH == 4 ? (d >> 1) : d) & (CCH - 1); }
+};
+
+// A fragment of a [32][D] row tile: permuted row, contraction step s
+template <typename T, int D>
+__device__ __forceinline__ void lds_row_frag(Frag<T>& f, const T* tile, int m, int h, int s) {
+  using C = Tile32<T, D>;
+  const int r = perm32(m);
+  const T* row = tile + r * D;
+  const int c0 = (16 * s + 8 * h) / C::EPC;
+  if (sizeof(T) == 2)
+    f.load(row + (c0 ^ C::rkey(r)) * C::EPC);
+  else
+    f.load2(row + (c0 ^ C::rkey(r)) * C::EPC, row + ((c0 + 1) ^ C::rkey(r)) * C::EPC);
+}
+
+// A fragment of a [D][32] column tile: row 32dt + m (zero past D), step s
+template <typename T, int D>
+__device__ __forceinline__ void lds_col_frag(Frag<T>& f, const T* tile, int dt, int m, int h, int s) {
+  using C = Tile32<T, D>;
+  const int d = 32 * dt + m;
+  if (D % 32 == 0 || d < D) {
+    const T* row = tile + d * 32;
+    const int c0 = (16 * s + 8 * h) / C::EPC;
+    if (sizeof(T) == 2)
+      f.load(row + (c0 ^ C::ckey(d)) * C::EPC);
+    else
+      f.load2(row + (c0 ^ C::ckey(d)) * C::EPC, row + ((c0 + 1) ^ C::ckey(d)) * C::EPC);
+  } else {
+    f.zero();
+  }
+}
+
+// Physical chunk P of a row tile -> (row, logical chunk)
+template <typename T, int D>
+__device__ __forceinline__ void row_chunk(int P, int& r, int& c) {
+  using C = Tile32<T, D>;
+  r = P / C::RCH;
+  c = (P % C::RCH) ^ C::rkey(r);
+}
+
+// Physical chunk P of a column tile -> (row d, logical chunk)
+template <typename T, int D>
+__device__ __forceinline__ void col_chunk(int P, int& d, int& c) {
+  using C = Tile32<T, D>;
+  d = P / C::CCH;
+  c = (P % C::CCH) ^ C::ckey(d);
+}
+
+// Fill NCHUNK 16-byte chunks of an LDS tile with direct global -> LDS loads;
+// src(P) is the global address of the data for physical chunk P.  Completion
+// is tracked by vmcnt: wait (lds_dma_wait) before the barrier that publishes
+// the tile.
+template <int NTH, int NCHUNK, typename SrcFn>
+__device__ __forceinline__ void dma_tile(void* lds, SrcFn src, int tid) {
+  const int w = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int j = 0; j < (NCHUNK + NTH - 1) / NTH; ++j) {
+    const int first = j * NTH + 64 * w;   // first physical chunk of this wave's load
+    if (NCHUNK % NTH == 0 || first < NCHUNK)
+      __builtin_amdgcn_global_load_lds(src(first + lane), (char*)lds + 16 * first, 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+}  // namespace nsa

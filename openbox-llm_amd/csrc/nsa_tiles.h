@@ -1,13 +1,10 @@
 // Wave-level attention tiles shared by the forward, dQ and dK/dV kernels.
 //
-// Query-side kernels (forward, dQ) work on one query x 16 heads per N-tile and
-// 32 keys per step:
+// Query-side selection kernels (forward, dQ) and the importance kernel work on
+// one query x 16 heads per N-tile and 32 keys per step:
 //   S^T (32 keys x 16 heads) = K Q^T      two 16x16 accumulators
 //   O^T (D x 16 heads)     += V^T P^T    D/16 accumulators
 //   dQ^T (D x 16 heads)    += K^T dS^T
-// Key-side kernels (dK/dV) work on 16 keys per wave and two queries per step:
-//   S (16 heads x 16 keys) = Q K^T for each query, dV^T += dO^T P, dK^T += Q^T dS
-// with the 32-row contraction made of (query A heads 0..15, query B heads 0..15).
 #pragma once
 
 #include "nsa_common.h"
@@ -173,69 +170,6 @@ __device__ __forceinline__ void dq_store(const f32x4 (&dq)[Dims<D>::DT], float* 
     f32x4 v = dq[dt] * scale;
     if (accumulate) v += *reinterpret_cast<const f32x4*>(p);
     *reinterpret_cast<f32x4*>(p) = v;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// dK/dV step: 16 keys (columns, lane c) x two queries (A, B) x 16 heads
-// ---------------------------------------------------------------------------
-template <int D> struct KvAcc {
-  f32x4 dk[Dims<D>::DT], dv[Dims<D>::DT];   // lane (g, c): rows d = 16dt + 4g + i of key column c
-  __device__ __forceinline__ void init() {
-#pragma unroll
-    for (int dt = 0; dt < Dims<D>::DT; ++dt) {
-      dk[dt] = zero4();
-      dv[dt] = zero4();
-    }
-  }
-};
-
-// Per-query row data for the 4 heads 4g + i of a lane group.
-struct RowStats {
-  float lse2[4], rs[4], dot[4];
-  uint32_t vm;   // bit i: head row valid and key visible
-};
-
-template <typename T, int D>
-__device__ __forceinline__ void kv_step(KvAcc<D>& a, const Frag<T> (&kbf)[Dims<D>::KC],
-                                        const Frag<T> (&vbf)[Dims<D>::KC], const T* qA, const T* qB,
-                                        const T* dA, const T* dB, const T* qtA, const T* qtB, const T* dtA,
-                                        const T* dtB, const RowStats& ra, const RowStats& rb, float sl2, int g,
-                                        int c) {
-  Frag<T> qfA[Dims<D>::KC], qfB[Dims<D>::KC], dfA[Dims<D>::KC], dfB[Dims<D>::KC];
-  load_row_frags<T, D>(qfA, qA, g);
-  load_row_frags<T, D>(qfB, qB, g);
-  load_row_frags<T, D>(dfA, dA, g);
-  load_row_frags<T, D>(dfB, dB, g);
-  f32x4 sA = zero4(), sB = zero4(), pA = zero4(), pB = zero4();
-#pragma unroll
-  for (int kc = 0; kc < Dims<D>::KC; ++kc) {
-    mma(sA, qfA[kc], kbf[kc]);
-    mma(sB, qfB[kc], kbf[kc]);
-    mma(pA, dfA[kc], vbf[kc]);
-    mma(pB, dfB[kc], vbf[kc]);
-  }
-  float P[8], dS[8];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float pa = ((ra.vm >> i) & 1u) ? fast_exp2(sA[i] * sl2 - ra.lse2[i]) * ra.rs[i] : 0.0f;
-    const float pb = ((rb.vm >> i) & 1u) ? fast_exp2(sB[i] * sl2 - rb.lse2[i]) * rb.rs[i] : 0.0f;
-    P[i] = pa;
-    P[4 + i] = pb;
-    dS[i] = pa * (pA[i] - ra.dot[i]);
-    dS[4 + i] = pb * (pB[i] - rb.dot[i]);
-  }
-  Frag<T> Pf, dSf;
-  Pf.set(P);
-  dSf.set(dS);
-#pragma unroll
-  for (int dt = 0; dt < Dims<D>::DT; ++dt) {
-    const int off = (16 * dt + c) * 16 + 4 * g;
-    Frag<T> dOT, QT;
-    dOT.load2(dtA + off, dtB + off);
-    QT.load2(qtA + off, qtB + off);
-    mma(a.dv[dt], dOT, Pf);
-    mma(a.dk[dt], QT, dSf);
   }
 }
 

@@ -123,7 +123,7 @@ def test_fused_vs_ref_loss_parity(dtype):
             opt.zero_grad(set_to_none=True)
             loss.backward()
             opt.step()
-            ls.append(float(loss))
+            ls.append(float(loss.detach()))
         losses[impl] = ls
     d = max(abs(a - b) for a, b in zip(losses["ref"], losses["fused"]))
     log(f"  losses ref {losses['ref'][0]:.4f}->{losses['ref'][-1]:.4f}, max |delta| {d:.2e}")

@@ -16,7 +16,15 @@ import torch.nn.functional as F
 
 from oracle import nsa_oracle as O
 
-torch.set_default_dtype(torch.float64)
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    """Every pin runs in float64; the process default is restored afterwards
+    so other test modules keep torch's float32 default."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def _rand(*shape, seed=0):
