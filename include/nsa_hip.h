@@ -106,27 +106,60 @@ int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, cons
  * pairs (t, j) with 0 <= j < n_blk and j*block_size <= t, grouped by (b, hkv, j),
  * query ascending.  n_blk is the reference's T / block_size (nsa_fsa.py:36) or
  * ceil(T / block_size) to include the trailing partial block.  Outputs:
- * q_of_block [cap], block_offsets [B][Hkv][n_blk+1] (global offsets), pair_bh
- * [cap], *pair_count (device int).  cap = B*Hkv*T*S.  Scratch from
+ * q_of_block [cap] (the query t, or t*S + s -- the pair's slot in block_idx --
+ * when pack_slot != 0), block_offsets [B][Hkv][n_blk+1] (global offsets),
+ * pair_bh [cap], *pair_count (device int).  cap = B*Hkv*T*S.  Scratch from
  * nsa_csr_workspace. */
 size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int n_blk);
 int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
-                  int block_size, int n_blk, void* stream);
+                  int block_size, int n_blk, int pack_slot, void* stream);
 
 /* Backward dK/dV (block-outer; replaces _selection_dkdv_kernel /
  * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
- * work items of at most `chunk` queries.  qt/dot_t are
- * the nsa_transpose_rows copies of q/dO.  dk/dv are float32 accumulators that
- * the call zero-fills and then accumulates into. */
+ * work items of at most `chunk` queries; q_of_block holds t*S + s when
+ * `packed`.  qt/dot_t are the nsa_transpose_rows copies of q/dO, kt the
+ * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
+ * zero-fills and then accumulates into.  dq_part (nullable; needs packed and
+ * kt): the dQ of every (query, slot, pass), scaled, in the input dtype,
+ * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G][D] -- summed by
+ * nsa_sel_dq_reduce. */
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
-int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* dout, const void* qt,
+int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const void* qt,
                  const void* dout_t, const float* lse, const float* dot, const float* rowscale,
-                 const int32_t* q_of_block, const int32_t* block_offsets, const int32_t* pair_count,
-                 float* dk, float* dv, void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int T,
-                 int D, int S, int block_size, int chunk, int dtype, void* stream);
+                 const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
+                 float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq,
+                 int Hkv, int T, int D, int S, int block_size, int chunk, int dtype, void* stream);
+
+/* ---- block-outer selection forward and the partial merges ----------------
+ * The FSA forward (replaces _selection_fwd_blockouter_kernel /
+ * selection_forward_fsa, nsa_selection_kernel.py:232-365): work items as in
+ * nsa_sel_dkdv over a CSR built with pack_slot; for every (query, slot, pass)
+ * it writes the block-local output O_j / l_j (input dtype) to o_part and
+ * (m_j [log2 units], l_j) float pairs to ml_part, both laid out
+ * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G] (x D for o_part).
+ * vt is the nsa_transpose_kv copy of v.  Workspace from
+ * nsa_sel_fwd_bo_workspace. */
+int nsa_sel_partial_slots(int S, int block_size);
+size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
+int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* q_of_block,
+                   const int32_t* block_offsets, void* o_part, float* ml_part, void* workspace,
+                   size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                   int dtype, void* stream);
+
+/* Merge of the forward partials (the log-sum-exp combine of
+ * nsa_selection_kernel.py:336-364): o and lse per row over the valid slots of
+ * block_idx; rows with none get o = 0 and lse = -1e9. */
+int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_part, void* o, float* lse, int B,
+                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream);
+
+/* dq_out = dq_acc (float32, nullable) + sum of the dQ partials of the valid
+ * slots, written in the input dtype (the dQ reduce of
+ * nsa_selection_backward.py:322-334). */
+int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float* dq_acc, void* dq_out, int B,
+                      int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream);
 
 /* ---- range branches (window / compression) ---------------------------------
  * Forward: replaces _range_attn_fwd_kernel / _range_attn_fwd_qtiled_kernel

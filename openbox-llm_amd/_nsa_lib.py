@@ -46,10 +46,15 @@ SIGNATURES = {
     "nsa_sel_dq": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                         _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_csr_workspace": (_Z, [_I, _I, _I, _I, _I]),
-    "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dkdv_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
-    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z,
+    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _Z,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_sel_partial_slots": (_I, [_I, _I]),
+    "nsa_sel_fwd_bo_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
+    "nsa_sel_fwd_bo": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_sel_merge": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_sel_dq_reduce": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

@@ -11,9 +11,10 @@
 
 namespace nsa {
 
+// vals: the query t, or t * S + s (the slot of the pair in block_idx) when pack_slot
 __global__ __launch_bounds__(256) void k_csr_keys(const int32_t* __restrict__ idx, uint32_t* __restrict__ keys,
                                                   int32_t* __restrict__ vals, int64_t n, int T, int S, int n_blk,
-                                                  int L, uint32_t sentinel) {
+                                                  int L, uint32_t sentinel, int pack_slot) {
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int64_t r = e / S;
     const int t = (int)(r % T);
@@ -21,7 +22,7 @@ __global__ __launch_bounds__(256) void k_csr_keys(const int32_t* __restrict__ id
     const int j = idx[e];
     const bool ok = j >= 0 && j < n_blk && (int64_t)j * L <= t;
     keys[e] = ok ? (uint32_t)(bh * n_blk + j) : sentinel;
-    vals[e] = t;
+    vals[e] = pack_slot ? t * S + (int)(e % S) : t;
   }
 }
 
@@ -104,8 +105,9 @@ size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int n_blk) {
 
 int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
-                  int block_size, int n_blk, void* stream) {
+                  int block_size, int n_blk, int pack_slot, void* stream) {
   NSA_CHECK(B > 0 && Hkv > 0 && T >= 0 && S >= 0 && block_size > 0 && n_blk >= 0, NSA_ERR_SHAPE);
+  NSA_CHECK(!pack_slot || (int64_t)T * S < (1ll << 31), NSA_ERR_SHAPE);
   NSA_CHECK((int64_t)B * Hkv * T * S < (1ll << 31) && (int64_t)B * Hkv * n_blk < (1ll << 31), NSA_ERR_SHAPE);
   const CsrLayout c = csr_layout(B, Hkv, T, S, n_blk);
   NSA_CHECK(workspace_bytes >= c.total, NSA_ERR_WORKSPACE);
@@ -118,7 +120,7 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
   void* temp = ws + c.temp;
   if (c.n > 0) {
     k_csr_keys<<<grid_for(c.n), 256, 0, s>>>(block_idx, kin, vin, c.n, T, S, n_blk, block_size,
-                                             (uint32_t)((int64_t)nbh * n_blk));
+                                             (uint32_t)((int64_t)nbh * n_blk), pack_slot);
     if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
     size_t tb = c.temp_bytes;
     if (hipcub::DeviceRadixSort::SortPairs(temp, tb, kin, kout, vin, q_of_block, (int)c.n, 0, c.end_bit, s) !=

@@ -23,6 +23,7 @@
 //   * selection   : work items (block, chunk of its CSR query list) built by
 //                   k_sel_items; a persistent grid drains them; chunks merge with atomics.
 #include "nsa_launch.h"
+#include "nsa_items.h"
 #include "nsa_tile32.h"
 
 namespace nsa {
@@ -124,7 +125,7 @@ template <typename T, int D> struct KeyAcc {
   // One 2-query tile; with `mask`, visA / visB say whether this lane's key is
   // visible to query A / B.
   __device__ __forceinline__ void step(const KvStage<T, D>& s, bool mask, bool visA, bool visB, float sl2, int n,
-                                       int h) {
+                                       int h, float* ds_out = nullptr) {
     // every operand fragment of the tile is read up front so the LDS reads
     // overlap each other and the MFMAs
     Frag<T> qa[C::KS], da[C::KS];
@@ -155,6 +156,10 @@ template <typename T, int D> struct KeyAcc {
       if (mask) p = (r < 8 ? visA : visB) ? p : 0.0f;
       P[r] = p;
       dS[r] = p * (pacc[r] - s.dot[e]);
+    }
+    if (ds_out != nullptr) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ds_out[r] = dS[r];
     }
     Frag<T> pf[2], sf[2];
     pf[0].set(P);
@@ -195,18 +200,22 @@ template <typename T, int D> struct KeyAcc {
   }
 };
 
-// Walk `ntile` 2-query tiles (queries from qsrc(i); tB = -1: none) over every
-// head chunk, double-buffered.  vis(tA, tB, mask, visA, visB) fills the mask
-// flags of a tile for this wave.
-template <typename T, int D, int NTH, typename QSrc, typename Vis>
+// Walk `ntile` 2-query tiles (queries and their block_idx slots from
+// qsrc(i, tA, tB, sA, sB); tB = -1: none) over every head chunk,
+// double-buffered.  vis(tA, tB, mask, visA, visB) fills the mask flags of a
+// tile for this wave.  post(tA, tB, sA, sB, hc, dS) runs on every thread of
+// the workgroup after each tile's step with this lane's 16 dS values (it may
+// synchronise the workgroup); WANT_DS = false skips it.
+template <bool WANT_DS, typename T, int D, int NTH, typename QSrc, typename Vis, typename Post>
 __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[2], const QSide<T>& x, int b,
-                                        int hkv, int ntile, QSrc qsrc, Vis vis, float sl2, int tid, int n, int h) {
+                                        int hkv, int ntile, QSrc qsrc, Vis vis, Post post, float sl2, int tid, int n,
+                                        int h) {
   RowTileLoader<T, D, NTH> ld;
   const int total = ntile * x.NHC;
   if (total == 0) return;
   {
-    int tA, tB;
-    qsrc(0, tA, tB);
+    int tA, tB, sA, sB;
+    qsrc(0, tA, tB, sA, sB);
     ld.issue(stg[0], x, b, hkv, 0, tA, tB, tid);
     ld.finish(stg[0], tid);
   }
@@ -214,21 +223,23 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   __syncthreads();
   int ti = 0, hc = 0;   // tile and head chunk of iteration `it`
   for (int it = 0; it < total; ++it) {
-    int tA, tB;
-    qsrc(ti, tA, tB);
+    int tA, tB, sA, sB;
+    qsrc(ti, tA, tB, sA, sB);
     int ti1 = ti + 1, hc1 = hc;
     if (ti1 == ntile) {
       ti1 = 0;
       ++hc1;
     }
     if (it + 1 < total) {
-      int uA, uB;
-      qsrc(ti1, uA, uB);
+      int uA, uB, vA, vB;
+      qsrc(ti1, uA, uB, vA, vB);
       ld.issue(stg[(it + 1) & 1], x, b, hkv, hc1, uA, uB, tid);
     }
     bool mask, visA, visB;
     vis(tA, tB, mask, visA, visB);
-    acc.step(stg[it & 1], mask, visA, visB, sl2, n, h);
+    float ds[16];
+    acc.step(stg[it & 1], mask, visA, visB, sl2, n, h, WANT_DS ? ds : nullptr);
+    if (WANT_DS) post(tA, tB, sA, sB, hc, ds);
     if (it + 1 < total) ld.finish(stg[(it + 1) & 1], tid);
     lds_dma_wait();
     __syncthreads();
@@ -299,9 +310,10 @@ __global__ __launch_bounds__(64 * NW) void k_range_dkdv32(int mode, const T* __r
   acc.init(k + kvoff, v + kvoff, key_ok ? key : Lk - 1, h);
   const int ntile = (thi - tlo) / 2 + 1;
   const int wlast = kw + 31;   // last key of the wave (may pass Lk: those columns are never stored)
-  auto qsrc = [&](int i, int& tA, int& tB) {
+  auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
     tA = tlo + 2 * i;
     tB = tA + 1 <= thi ? tA + 1 : -1;
+    sA = sB = 0;
   };
   auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
     const int tb = tB >= 0 ? tB : tA;
@@ -315,7 +327,8 @@ __global__ __launch_bounds__(64 * NW) void k_range_dkdv32(int mode, const T* __r
       visB = key * cd + cl - 1 <= tb;
     }
   };
-  kv_walk<T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, sl2, tid, n, h);
+  auto none = [](int, int, int, int, int, const float*) {};
+  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, none, sl2, tid, n, h);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -334,79 +347,84 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// selection dK/dV over CSR work items
+// selection dK/dV over CSR work items (nsa_items.h)
 // ---------------------------------------------------------------------------
-// items[i] = {bh * n_blk + j, begin, end, 0}: pair range [begin, end) of q_of_block
-__global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __restrict__ offsets, int nb, int n_blk,
-                                                    int chunk, int4* __restrict__ items, int32_t* __restrict__ n_items) {
-  __shared__ int part[1024];
-  const int tid = threadIdx.x;
-  const int per = (nb + 1023) / 1024;
-  const int lo = tid * per, hi = lo + per < nb ? lo + per : nb;
-  int cnt = 0;
-  for (int e = lo; e < hi; ++e) {
-    const int bh = e / n_blk, j = e % n_blk;
-    const int n = offsets[bh * (n_blk + 1) + j + 1] - offsets[bh * (n_blk + 1) + j];
-    cnt += (n + chunk - 1) / chunk;
-  }
-  part[tid] = cnt;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over 1024 partial counts
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int add = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += add;
-    __syncthreads();
-  }
-  int pos = part[tid] - cnt;
-  for (int e = lo; e < hi; ++e) {
-    const int bh = e / n_blk, j = e % n_blk;
-    const int beg = offsets[bh * (n_blk + 1) + j];
-    const int end = offsets[bh * (n_blk + 1) + j + 1];
-    for (int s = beg; s < end; s += chunk) {
-      const int se = s + chunk < end ? s + chunk : end;
-      items[pos++] = make_int4(e, s, se, 0);
-    }
-  }
-  if (tid == 1023) *n_items = part[1023];
-}
-
 // Persistent grid over the work items; two waves own 64 keys of the item's
-// block at a time (blocks longer than 64 keys take several passes).
+// block at a time (blocks longer than 64 keys take several passes).  With
+// dq_part, the tile's dS (both waves, 32 rows x 64 keys) is staged in LDS and
+// dQ^T = K^T dS^T is formed for the pass's 64 keys -- each wave covering half
+// of D -- and written, scaled, to the (query, slot, pass) partial that
+// k_sel_dq_reduce sums.
 template <typename T, int D>
 __global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout,
                                                     const T* __restrict__ qt, const T* __restrict__ dt,
                                                     const float* __restrict__ lse, const float* __restrict__ dot,
                                                     const float* __restrict__ rowscale, const T* __restrict__ k,
-                                                    const T* __restrict__ v, const int32_t* __restrict__ q_of_block,
+                                                    const T* __restrict__ v, const T* __restrict__ kt,
+                                                    const int32_t* __restrict__ q_of_block,
                                                     const int4* __restrict__ items,
                                                     const int32_t* __restrict__ n_items, float* __restrict__ dk,
-                                                    float* __restrict__ dv, int Hq, int Hkv, int T_, int n_blk, int L,
-                                                    float sl2, float scale) {
+                                                    float* __restrict__ dv, T* __restrict__ dq_part, int Hq, int Hkv,
+                                                    int T_, int S, int packed, int n_blk, int L, int Lp, float sl2,
+                                                    float scale) {
   constexpr int NW = 2, NTH = 64 * NW;
+  using C = Tile32<T, D>;
+  constexpr int DT = C::DT, DTW = (DT + 1) / 2;          // dQ^T d-tiles per wave
+  constexpr int DSP = 64 + 16 / (int)sizeof(T);          // padded pitch of the dS tile
   __shared__ __align__(16) KvStage<T, D> stg[2];
+  __shared__ __align__(16) T sdS[32 * DSP];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const QSide<T> x = qside(q, dout, qt, dt, lse, dot, rowscale, Hq, Hkv, T_);
+  const int G = x.G;
   const int ni = *n_items;
-  const int npass = (L + 32 * NW - 1) / (32 * NW);
+  const int npass = sel_passes(L);
+  const int NS = S * npass;
   for (int it = blockIdx.x; it < ni * npass; it += gridDim.x) {
     const int4 item = items[it / npass];
     const int pass = it % npass;
     const int bh = item.x / n_blk, j = item.x % n_blk;
     const int b = bh / Hkv, hkv = bh % Hkv;
     const int blk_end = j * L + L < T_ ? j * L + L : T_;
-    const int kw = j * L + 32 * (NW * pass + w);
+    const int kpass = j * L + kSelPass * pass;
+    const int kw = kpass + 32 * w;
     const int key = kw + n;
     const bool key_ok = key < blk_end;
     const int wlast = kw + 31;
     const int64_t kvoff = (int64_t)bh * T_ * D;
     KeyAcc<T, D> acc;
     acc.init(k + kvoff, v + kvoff, key_ok ? key : j * L, h);
+    // K^T fragments of the pass's 64 keys for this wave's dQ^T d-tiles
+    Frag<T> ktf[DTW][4];
+    if (dq_part != nullptr) {
+      const T* ktb = kt + (int64_t)bh * D * Lp;
+#pragma unroll
+      for (int i = 0; i < DTW; ++i)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int d = 32 * (w * DTW + i) + n;
+          int c0 = kpass + 16 * kk + 8 * h;
+          c0 = c0 < Lp - 8 ? c0 : Lp - 8;
+          if (w * DTW + i < DT && (D % 32 == 0 || d < D))
+            ktf[i][kk].load(ktb + (int64_t)d * Lp + c0);
+          else
+            ktf[i][kk].zero();
+        }
+    }
     const int beg = item.y, cnt = item.z - item.y;
     const int ntile = (cnt + 1) / 2;
-    auto qsrc = [&](int i, int& tA, int& tB) {
-      tA = q_of_block[beg + 2 * i];
-      tB = 2 * i + 1 < cnt ? q_of_block[beg + 2 * i + 1] : -1;
+    auto decode = [&](int i, int& t, int& s) {
+      if (i < cnt) {
+        const int val = q_of_block[beg + i];
+        t = packed ? val / S : val;
+        s = packed ? val % S : 0;
+      } else {
+        t = -1;
+        s = 0;
+      }
+    };
+    auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
+      decode(2 * i, tA, sA);
+      decode(2 * i + 1, tB, sB);
     };
     auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
       const int tb = tB >= 0 ? tB : tA;
@@ -414,7 +432,47 @@ __global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, con
       visA = key_ok && key <= tA;
       visB = key_ok && key <= tb;
     };
-    kv_walk<T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, sl2, tid, n, h);
+    auto post = [&](int tA, int tB, int sA, int sB, int hc, const float* ds) {
+      // dS (rows x this wave's 32 keys) -> LDS [row][64 keys]
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sdS[acc_elem(h, r) * DSP + 32 * w + n] = from_f32<T>(ds[r]);
+      __syncthreads();
+      f32x16 dq[DTW];
+#pragma unroll
+      for (int i = 0; i < DTW; ++i) dq[i] = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        Frag<T> bf;
+        const T* src = sdS + n * DSP + 16 * kk + 8 * h;
+        if (sizeof(T) == 2)
+          bf.load(src);
+        else
+          bf.load2(src, src + 4);
+#pragma unroll
+        for (int i = 0; i < DTW; ++i) mma32(dq[i], ktf[i][kk], bf);
+      }
+      const int t = n < 16 ? tA : tB;
+      const int g = hc * 16 + (n & 15);
+      if (t >= 0 && g < G) {
+        const int slot = (n < 16 ? sA : sB) * npass + pass;
+        T* drow = dq_part + ((((int64_t)bh * T_ + t) * NS + slot) * G + g) * D;
+#pragma unroll
+        for (int i = 0; i < DTW; ++i) {
+          if (w * DTW + i >= DT) continue;
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = 32 * (w * DTW + i) + 8 * g4 + 4 * h;
+            if (D % 32 == 0 || d < D)
+              store4(drow + d, dq[i][4 * g4] * scale, dq[i][4 * g4 + 1] * scale, dq[i][4 * g4 + 2] * scale,
+                     dq[i][4 * g4 + 3] * scale);
+          }
+        }
+      }
+    };
+    if (dq_part != nullptr)
+      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid, n, h);
+    else
+      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid, n, h);
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
     __syncthreads();   // the next item's first tile reuses stage 0
   }
@@ -484,32 +542,24 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   return nsa_launch_status();
 }
 
-// Selection blocks of the CSR consumed here: every block holding a key, the
-// trailing partial one included (the forward attends to it when selected).
-static inline int sel_csr_blocks(int T, int block_size) { return (T + block_size - 1) / block_size; }
-
-static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size, int chunk) {
-  const size_t nb = (size_t)B * Hkv * sel_csr_blocks(T, block_size);
-  const size_t pairs = (size_t)B * Hkv * T * S;
-  return nb + (pairs + chunk - 1) / chunk + 1;
-}
-
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk) {
   if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || block_size <= 0 || chunk <= 0) return 0;
   return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sizeof(int4) + 256;
 }
 
-int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* dout, const void* qt, const void* dout_t,
-                 const float* lse, const float* dot, const float* rowscale, const int32_t* q_of_block,
-                 const int32_t* block_offsets, const int32_t* pair_count, float* dk, float* dv, void* workspace,
-                 size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
-                 int dtype, void* stream) {
+int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const void* qt,
+                 const void* dout_t, const float* lse, const float* dot, const float* rowscale,
+                 const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
+                 float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
+                 int T, int D, int S, int block_size, int chunk, int dtype, void* stream) {
   (void)pair_count;
   NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && S >= 0, NSA_ERR_SHAPE);
   NSA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, NSA_ERR_SHAPE);
   NSA_CHECK(block_size >= 16 && block_size % 16 == 0 && chunk >= 2, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(workspace_bytes >= nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
+  NSA_CHECK(dq_part == nullptr || (packed && kt != nullptr), NSA_ERR_ARG);
+  NSA_CHECK(!packed || (int64_t)T * S < (1ll << 31), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
   if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;
@@ -520,20 +570,21 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* dout, 
   int32_t* n_items = (int32_t*)((char*)workspace + cap * sizeof(int4));
   k_sel_items<<<1, 1024, 0, s>>>(block_offsets, B * Hkv * n_blk, n_blk, chunk, items, n_items);
   if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
-  const size_t grid_cap = cap < 4096 ? cap : 4096;
+  const size_t grid_cap = cap * sel_passes(block_size) < 4096 ? cap * sel_passes(block_size) : 4096;
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
+  const int Lp = padded_len(T);
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16)
       k_sel_dkdv32<bf16, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
           (const bf16*)q, (const bf16*)dout, (const bf16*)qt, (const bf16*)dout_t, lse, dot, rowscale,
-          (const bf16*)k, (const bf16*)v, q_of_block, items, n_items, dk, dv, Hq, Hkv, T, n_blk, block_size, sl2,
-          scale);
+          (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block, items, n_items, dk, dv, (bf16*)dq_part, Hq,
+          Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
     else
       k_sel_dkdv32<float, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
           (const float*)q, (const float*)dout, (const float*)qt, (const float*)dout_t, lse, dot, rowscale,
-          (const float*)k, (const float*)v, q_of_block, items, n_items, dk, dv, Hq, Hkv, T, n_blk, block_size, sl2,
-          scale);
+          (const float*)k, (const float*)v, (const float*)kt, q_of_block, items, n_items, dk, dv, (float*)dq_part,
+          Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
   });
   return nsa_launch_status();
 }

@@ -1,0 +1,63 @@
+// Work items of the block-outer selection kernels: (block, chunk of its CSR
+// query list), built on the GPU from the CSR offsets.  Shared by the
+// selection forward (nsa_selbo.hip) and dK/dV (nsa_dkdv.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nsa {
+
+// items[i] = {bh * n_blk + j, begin, end, 0}: pair range [begin, end) of q_of_block
+static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __restrict__ offsets, int nb, int n_blk,
+                                                           int chunk, int4* __restrict__ items,
+                                                           int32_t* __restrict__ n_items) {
+  __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  const int per = (nb + 1023) / 1024;
+  const int lo = tid * per, hi = lo + per < nb ? lo + per : nb;
+  int cnt = 0;
+  for (int e = lo; e < hi; ++e) {
+    const int bh = e / n_blk, j = e % n_blk;
+    const int n = offsets[bh * (n_blk + 1) + j + 1] - offsets[bh * (n_blk + 1) + j];
+    cnt += (n + chunk - 1) / chunk;
+  }
+  part[tid] = cnt;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over 1024 partial counts
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int pos = part[tid] - cnt;
+  for (int e = lo; e < hi; ++e) {
+    const int bh = e / n_blk, j = e % n_blk;
+    const int beg = offsets[bh * (n_blk + 1) + j];
+    const int end = offsets[bh * (n_blk + 1) + j + 1];
+    for (int s = beg; s < end; s += chunk) {
+      const int se = s + chunk < end ? s + chunk : end;
+      items[pos++] = make_int4(e, s, se, 0);
+    }
+  }
+  if (tid == 1023) *n_items = part[1023];
+}
+
+// Selection blocks of the CSR consumed by the block-outer kernels: every
+// block holding a key, the trailing partial one included (the forward attends
+// to it when selected).
+static inline int sel_csr_blocks(int T, int block_size) { return (T + block_size - 1) / block_size; }
+
+static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size, int chunk) {
+  const size_t nb = (size_t)B * Hkv * sel_csr_blocks(T, block_size);
+  const size_t pairs = (size_t)B * Hkv * T * S;
+  return nb + (pairs + chunk - 1) / chunk + 1;
+}
+
+// Keys of a selection block handled per pass of the block-outer kernels; a
+// block longer than this is split into ceil(L / kSelPass) partial slots.
+constexpr int kSelPass = 64;
+__host__ __device__ inline int sel_passes(int block_size) { return (block_size + kSelPass - 1) / kSelPass; }
+
+}  // namespace nsa

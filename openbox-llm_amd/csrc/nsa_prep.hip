@@ -110,48 +110,80 @@ __global__ __launch_bounds__(256) void k_pool_bwd(const TI* __restrict__ dp, TO*
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// 16-byte vectors of T: 8 bf16 or 4 float
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> {
+  static constexpr int N = 8;
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ float operator[](int i) const { return (float)v[i]; }
+  __device__ __forceinline__ void set(int i, float x) { v[i] = (bf16)x; }
+  __device__ __forceinline__ void store(bf16* p) const { *reinterpret_cast<bf16x8*>(p) = v; }
+};
+template <> struct Vec16<float> {
+  static constexpr int N = 4;
+  f32x4 v;
+  __device__ __forceinline__ void load(const float* p) { v = *reinterpret_cast<const f32x4*>(p); }
+  __device__ __forceinline__ float operator[](int i) const { return v[i]; }
+  __device__ __forceinline__ void set(int i, float x) { v[i] = x; }
+  __device__ __forceinline__ void store(float* p) const { *reinterpret_cast<f32x4*>(p) = v; }
+};
+
+// One thread per 16-byte vector of the output (D is a multiple of the vector).
 template <typename T>
 __global__ __launch_bounds__(256) void k_gate_fwd(const T* __restrict__ g, const T* __restrict__ oc,
                                                   const T* __restrict__ os, const T* __restrict__ ow,
                                                   T* __restrict__ out, int64_t rows, int D) {
-  const int64_t total = rows * D;
+  constexpr int N = Vec16<T>::N;
+  const int vpr = D / N;
+  const int64_t total = rows * vpr;
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-    const int64_t r = e / D;
+    const int64_t r = e / vpr;
     const float g0 = sigmoidf(to_f32(g[r * 3 + 0]));
     const float g1 = sigmoidf(to_f32(g[r * 3 + 1]));
     const float g2 = sigmoidf(to_f32(g[r * 3 + 2]));
-    out[e] = from_f32<T>(g0 * to_f32(oc[e]) + g1 * to_f32(os[e]) + g2 * to_f32(ow[e]));
+    Vec16<T> a, b, c, y;
+    a.load(oc + e * N);
+    b.load(os + e * N);
+    c.load(ow + e * N);
+#pragma unroll
+    for (int i = 0; i < N; ++i) y.set(i, g0 * a[i] + g1 * b[i] + g2 * c[i]);
+    y.store(out + e * N);
   }
 }
 
-// One 16-lane group per row (each lane 8 elements of D <= 128); 4 rows per wave.
-// nbr = number of branches (1: plain delta, 3: gated three-branch prep).
+// A group of D / N lanes per row (N = elements per 16-byte vector), each
+// lane one vector; 64 / (D / N) rows per wave.  nbr = number of branches
+// (1: plain delta, 3: gated three-branch prep).
 template <typename T>
 __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, const T* __restrict__ o0,
                                                   const T* __restrict__ o1, const T* __restrict__ o2,
                                                   const T* __restrict__ gate, T* __restrict__ dgate,
                                                   float* __restrict__ dot, float* __restrict__ rowscale,
                                                   int64_t rows, int D, int nbr) {
-  const int lane16 = threadIdx.x & 15;
-  const int64_t row = blockIdx.x * 16ll + (threadIdx.x >> 4);
+  constexpr int N = Vec16<T>::N;
+  const int gs = D / N;                         // lanes per row, a power of two <= 64
+  const int lane = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) / gs;
+  const int sub = lane & (gs - 1);
   const bool ok = row < rows;
   float acc[3] = {0.f, 0.f, 0.f};
-  const T* os[3] = {o0, o1, o2};
   if (ok) {
-    for (int d = lane16 * 8; d < D; d += 128) {
+    Vec16<T> d, x;
+    d.load(dout + row * D + sub * N);
+    const T* os[3] = {o0, o1, o2};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (d + k >= D) break;
-        const float go = to_f32(dout[row * D + d + k]);
-        for (int c = 0; c < nbr; ++c) acc[c] += go * to_f32(os[c][row * D + d + k]);
-      }
+    for (int c = 0; c < 3; ++c) {
+      if (c >= nbr) break;
+      x.load(os[c] + row * D + sub * N);
+#pragma unroll
+      for (int i = 0; i < N; ++i) acc[c] += d[i] * x[i];
     }
   }
-  for (int c = 0; c < 3; ++c) {
 #pragma unroll
-    for (int m = 1; m < 16; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
-  }
-  if (!ok || lane16 != 0) return;
+  for (int c = 0; c < 3; ++c)
+    for (int m = 1; m < gs; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
+  if (!ok || sub != 0) return;
   if (nbr == 1) {
     dot[row] = acc[0];
     return;
@@ -253,7 +285,8 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
                  int64_t rows, int D, int dtype, void* stream) {
   NSA_CHECK(rows >= 0 && D > 0, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  const int64_t total = rows * D;
+  NSA_CHECK(D % 8 == 0, NSA_ERR_SHAPE);
+  const int64_t total = rows * (D / (dtype == NSA_BF16 ? 8 : 4));
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NSA_BF16)
@@ -271,11 +304,16 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, float* dot, float* rowscale, int64_t rows, int D, int nbr, int dtype,
                  void* stream) {
-  NSA_CHECK(rows >= 0 && D > 0 && D <= 1024 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int vec = dtype == NSA_BF16 ? 8 : 4;
+  NSA_CHECK(rows >= 0 && D > 0 && D % vec == 0 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
+  const int gs = D / vec;
+  NSA_CHECK(gs <= 64 && (gs & (gs - 1)) == 0, NSA_ERR_SHAPE);
   NSA_CHECK(nbr == 1 || (gate && o1 && o2 && rowscale), NSA_ERR_ARG);
   if (rows == 0) return NSA_OK;
-  const int grid = (int)((rows + 15) / 16);
+  const int64_t grid64 = (rows * gs + 255) / 256;
+  NSA_CHECK(grid64 < (1ll << 31), NSA_ERR_SHAPE);
+  const int grid = (int)grid64;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NSA_BF16)
     k_bwd_prep<bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1, (const bf16*)o2,

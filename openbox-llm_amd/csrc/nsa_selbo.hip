@@ -1,0 +1,440 @@
+// Block-outer selection forward and the partial merges of the selection
+// branch (the role of the reference's FSA path, nsa_selection_kernel.py:232-365
+// and nsa_selection_backward.py:278-334, with the partial buffers in bf16 /
+// the input dtype and the merges done by dedicated kernels).
+//
+// Work items are (selected block, chunk of the queries that selected it) from
+// the block -> query CSR built with pack_slot (entries t*S + s).  One wave per
+// item holds 64 keys of the block in registers -- K rows as the A operand of
+// S^T = K Q^T, V^T as the A operand of O^T = V^T P^T -- and streams the item's
+// queries two at a time (32 rows = two queries x 16 heads) through LDS.  For
+// every (query, slot, pass) it writes the block-local softmax result: the
+// normalised output O_j / l_j in the input dtype and (m_j, l_j), m in log2
+// units.  k_sel_merge combines the partials of each query into o and lse;
+// k_sel_dq_reduce sums the dQ partials written by the dK/dV kernel.
+#include "nsa_items.h"
+#include "nsa_launch.h"
+#include "nsa_tile32.h"
+
+namespace nsa {
+
+constexpr float kNegInfS = -__builtin_inff();
+
+// Slot of a selected block j in row t is valid (has a CSR pair) iff
+// 0 <= j < n_csr and j * L <= t.
+__device__ __forceinline__ bool sel_slot_valid(int j, int n_csr, int L, int t) {
+  return j >= 0 && j < n_csr && (int64_t)j * L <= t;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, const T* __restrict__ k,
+                                                   const T* __restrict__ vt, const int32_t* __restrict__ q_of_block,
+                                                   const int4* __restrict__ items,
+                                                   const int32_t* __restrict__ n_items, T* __restrict__ opart,
+                                                   float2* __restrict__ mlpart, int Hq, int Hkv, int T_, int S,
+                                                   int n_blk, int L, int Lp, int nsub, float sl2) {
+  using C = Tile32<T, D>;
+  constexpr int KS = C::KS, DT = C::DT;
+  __shared__ __align__(16) T sQ[2][C::ROW_ELEMS];
+  const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
+  const int G = Hq / Hkv, NHC = (G + 15) / 16;
+  const int NS = S * nsub;
+  const int ni = *n_items;
+  for (int it = blockIdx.x; it < ni * nsub; it += gridDim.x) {
+    const int4 item = items[it / nsub];
+    const int pass = it % nsub;
+    const int bh = item.x / n_blk, j = item.x % n_blk;
+    const int b = bh / Hkv, hkv = bh % Hkv;
+    const int kbase = j * L + kSelPass * pass;
+    const int kend = j * L + L < T_ ? j * L + L : T_;
+    // block keys: K rows (perm32 order) and V^T, both in registers
+    Frag<T> kf[2][KS], vf[DT][4];
+    const T* kb_ = k + (int64_t)bh * T_ * D;
+    const T* vtb = vt + (int64_t)bh * D * Lp;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int key = kbase + 32 * mt + perm32(n);
+      const int ks = key < kend ? key : j * L;   // finite stand-in for keys past the block
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kf[mt][s].load(kb_ + (int64_t)ks * D + 16 * s + 8 * h);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const int d = 32 * dt + n;
+        int c0 = kbase + 16 * kk + 8 * h;
+        c0 = c0 < Lp - 8 ? c0 : Lp - 8;
+        if (D % 32 == 0 || d < D)
+          vf[dt][kk].load(vtb + (int64_t)d * Lp + c0);
+        else
+          vf[dt][kk].zero();
+      }
+    const int beg = item.y, cnt = item.z - item.y;
+    const int ntile = (cnt + 1) / 2;
+    const int total = ntile * NHC;
+    auto entry = [&](int i, int& t, int& s) {
+      if (i < cnt) {
+        const int v = q_of_block[beg + i];
+        t = v / S;
+        s = v % S;
+      } else {
+        t = -1;
+        s = 0;
+      }
+    };
+    auto issue = [&](int ix, int buf) {
+      const int hc = ix / ntile, ti = ix % ntile;
+      int tA, sA, tB, sB;
+      entry(2 * ti, tA, sA);
+      entry(2 * ti + 1, tB, sB);
+      const int tq[2] = {tA, tB >= 0 ? tB : tA};
+      const int grem = G - hc * 16;
+      const int64_t hbase = (int64_t)b * Hq + hkv * G + hc * 16;
+      dma_tile<64, C::ROW_CHUNKS>(sQ[buf], [&](int P) {
+        int r, cc;
+        nrow_chunk<T, D>(P, r, cc);
+        const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
+        return (const void*)(q + ((hbase + hd) * T_ + tq[r >> 4]) * D + cc * C::EPC);
+      }, lane);
+    };
+    issue(0, 0);
+    lds_dma_wait();
+    __syncthreads();
+    for (int ix = 0; ix < total; ++ix) {
+      const int buf = ix & 1;
+      if (ix + 1 < total) issue(ix + 1, buf ^ 1);
+      const int hc = ix / ntile, ti = ix % ntile;
+      int tA, sA, tB, sB;
+      entry(2 * ti, tA, sA);
+      entry(2 * ti + 1, tB, sB);
+      const int t = n < 16 ? tA : tB;      // this lane's row: query t, head hc*16 + (n & 15)
+      const int slot = (n < 16 ? sA : sB) * nsub + pass;
+      const int g = hc * 16 + (n & 15);
+      const bool rok = t >= 0 && g < G;
+      Frag<T> qb[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) lds_nrow_frag<T, D>(qb[s], sQ[buf], n, h, s);
+      f32x16 st[2];
+      st[0] = zero16();
+      st[1] = zero16();
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        mma32(st[0], kf[0][s], qb[s]);
+        mma32(st[1], kf[1][s], qb[s]);
+      }
+      float mx = kNegInfS;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kbase + 32 * mt + acc_elem(h, r);
+          const float x = (key < kend && key <= t) ? st[mt][r] * sl2 : kNegInfS;
+          st[mt][r] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float ms = mx == kNegInfS ? 0.0f : mx;
+      float ps = 0.0f;
+      Frag<T> pf[4];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          p[r] = fast_exp2(st[mt][r] - ms);
+          ps += p[r];
+        }
+        pf[2 * mt].set(p);
+        pf[2 * mt + 1].set(p + 8);
+      }
+      const float lt = ps + __shfl_xor(ps, 32, kWave);
+      f32x16 acc[DT];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        acc[dt] = zero16();
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) mma32(acc[dt], vf[dt][kk], pf[kk]);
+      }
+      if (rok) {
+        const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        T* orow = opart + prow * D;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = 32 * dt + 8 * g4 + 4 * h;
+            if (D % 32 == 0 || d < D)
+              store4(orow + d, acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv, acc[dt][4 * g4 + 2] * inv,
+                     acc[dt][4 * g4 + 3] * inv);
+          }
+        if (h == 0) mlpart[prow] = make_float2(mx, lt);
+      }
+      lds_dma_wait();
+      __syncthreads();
+    }
+  }
+}
+
+// 32 consecutive elements of a partial row as float (four 16-byte loads for
+// bf16, eight for float)
+__device__ __forceinline__ void load32(const bf16* p, float (&x)[32]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p + 8 * c);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[8 * c + i] = (float)v[i];
+  }
+}
+__device__ __forceinline__ void load32(const float* p, float (&x)[32]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * c);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[4 * c + i] = v[i];
+  }
+}
+__device__ __forceinline__ void store32(bf16* p, const float (&x)[32]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (bf16)x[8 * c + i];
+    *reinterpret_cast<bf16x8*>(p + 8 * c) = v;
+  }
+}
+__device__ __forceinline__ void store32(float* p, const float (&x)[32]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+    *reinterpret_cast<f32x4*>(p + 4 * c) = (f32x4){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
+}
+
+// o[row] = sum_slots exp2(m - M) l O_slot / sum exp2(m - M) l, lse = (M + log2 L) ln 2.
+// One thread per (b, hkv, t, g, 32-element quarter of D); D = 16 uses one
+// thread per row over the first 16 elements.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const T* __restrict__ opart,
+                                                   const float2* __restrict__ mlpart, T* __restrict__ o,
+                                                   float* __restrict__ lse, int Hq, int Hkv, int T_, int S, int n_csr,
+                                                   int L, int nsub, int64_t total) {
+  constexpr int NQ = D >= 32 ? D / 32 : 1, W = D >= 32 ? 32 : D;
+  const int G = Hq / Hkv, NS = S * nsub;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int dq = (int)(e % NQ);
+    int64_t r = e / NQ;
+    const int g = (int)(r % G);
+    r /= G;
+    const int t = (int)(r % T_);
+    const int64_t bh = r / T_;
+    const int32_t* irow = idx + (bh * T_ + t) * S;
+    const int64_t pbase = (bh * T_ + t) * NS;
+    // pass 1: the largest block maximum over the valid slots
+    float M = kNegInfS;
+    for (int s = 0; s < S; ++s) {
+      if (!sel_slot_valid(irow[s], n_csr, L, t)) continue;
+      for (int p = 0; p < nsub; ++p) {
+        const float2 ml = mlpart[(pbase + s * nsub + p) * G + g];
+        if (ml.y > 0.0f) M = fmaxf(M, ml.x);
+      }
+    }
+    // pass 2: weights exp2(m - M) l and the weighted sum of the partial outputs
+    float acc[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] = 0.0f;
+    float Ls = 0.0f;
+    if (M != kNegInfS) {
+      for (int sl = 0; sl < NS; ++sl) {
+        if (!sel_slot_valid(irow[sl / nsub], n_csr, L, t)) continue;
+        const int64_t pr = (pbase + sl) * G + g;
+        const float2 ml = mlpart[pr];
+        if (!(ml.y > 0.0f)) continue;
+        const float w = fast_exp2(ml.x - M) * ml.y;
+        Ls += w;
+        float x[32];
+        if (W == 32) {
+          load32(opart + pr * D + dq * 32, x);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) x[i] = i < W ? to_f32(opart[pr * D + i]) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] += w * x[i];
+      }
+    }
+    const int64_t orow = (((bh / Hkv) * Hq + (bh % Hkv) * G + g) * T_ + t);
+    const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) acc[i] *= inv;
+    if (W == 32) {
+      store32(o + orow * D + dq * 32, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) o[orow * D + i] = from_f32<T>(acc[i]);
+    }
+    if (dq == 0) lse[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
+  }
+}
+
+// dq_out[row] = (dq_acc[row] or 0) + sum over valid slots of dqpart (already scaled).
+// One thread per (b, hq, t, 32-element quarter of D).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void k_sel_dq_reduce(const int32_t* __restrict__ idx, const T* __restrict__ dqpart,
+                                                       const float* __restrict__ dq_acc, T* __restrict__ dq_out,
+                                                       int Hq, int Hkv, int T_, int S, int n_csr, int L, int nsub,
+                                                       int64_t total) {
+  constexpr int NQ = D >= 32 ? D / 32 : 1, W = D >= 32 ? 32 : D;
+  const int G = Hq / Hkv, NS = S * nsub;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int dq = (int)(e % NQ);
+    int64_t r = e / NQ;
+    const int t = (int)(r % T_);
+    r /= T_;
+    const int hq = (int)(r % Hq);
+    const int b = (int)(r / Hq);
+    const int hkv = hq / G, g = hq % G;
+    const int64_t bh = (int64_t)b * Hkv + hkv;
+    const int32_t* irow = idx + (bh * T_ + t) * S;
+    const int64_t pbase = (bh * T_ + t) * NS;
+    const int64_t orow = ((int64_t)b * Hq + hq) * T_ + t;
+    float acc[32];
+    if (dq_acc != nullptr && W == 32) {
+      load32(dq_acc + orow * D + dq * 32, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc[i] = (dq_acc != nullptr && i < W) ? dq_acc[orow * D + i] : 0.0f;
+    }
+    for (int s = 0; s < S; ++s) {
+      if (!sel_slot_valid(irow[s], n_csr, L, t)) continue;
+      for (int p = 0; p < nsub; ++p) {
+        const T* src = dqpart + ((pbase + s * nsub + p) * G + g) * D;
+        float x[32];
+        if (W == 32) {
+          load32(src + dq * 32, x);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32; ++i) x[i] = i < W ? to_f32(src[i]) : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) acc[i] += x[i];
+      }
+    }
+    if (W == 32) {
+      store32(dq_out + orow * D + dq * 32, acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < W; ++i) dq_out[orow * D + i] = from_f32<T>(acc[i]);
+    }
+  }
+}
+
+static inline int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace nsa
+
+using namespace nsa;
+
+#define NSA_DISPATCH_D(D_, ...)                                 \
+  switch (D_) {                                                 \
+    case 16: { constexpr int DD = 16; __VA_ARGS__; break; }    \
+    case 32: { constexpr int DD = 32; __VA_ARGS__; break; }    \
+    case 64: { constexpr int DD = 64; __VA_ARGS__; break; }    \
+    case 128: { constexpr int DD = 128; __VA_ARGS__; break; }  \
+    default: return NSA_ERR_SHAPE;                              \
+  }
+
+static inline bool sel_args_ok(int B, int Hq, int Hkv, int T, int D, int S, int block_size) {
+  return B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && S >= 0 && (D == 16 || D == 32 || D == 64 || D == 128) &&
+         block_size >= 16 && block_size % 16 == 0;
+}
+
+extern "C" {
+
+int nsa_sel_partial_slots(int S, int block_size) { return S * sel_passes(block_size); }
+
+size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk) {
+  if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || block_size <= 0 || chunk <= 0) return 0;
+  return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sizeof(int4) + 256;
+}
+
+int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* q_of_block,
+                   const int32_t* block_offsets, void* o_part, float* ml_part, void* workspace,
+                   size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                   int dtype, void* stream) {
+  NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size) && chunk >= 2, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(workspace_bytes >= nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
+  const int n_blk = sel_csr_blocks(T, block_size);
+  if (T == 0 || S == 0 || n_blk == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const size_t cap = sel_items_cap(B, Hkv, T, S, block_size, chunk);
+  int4* items = (int4*)workspace;
+  int32_t* n_items = (int32_t*)((char*)workspace + cap * sizeof(int4));
+  k_sel_items<<<1, 1024, 0, s>>>(block_offsets, B * Hkv * n_blk, n_blk, chunk, items, n_items);
+  if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
+  const int nsub = sel_passes(block_size);
+  const size_t grid = cap * nsub < 8192 ? cap * nsub : 8192;
+  const int Lp = padded_len(T);
+  const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16)
+      k_sel_fwd_bo<bf16, DD><<<(unsigned)grid, 64, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)vt,
+                                                           q_of_block, items, n_items, (bf16*)o_part,
+                                                           (float2*)ml_part, Hq, Hkv, T, S, n_blk, block_size, Lp,
+                                                           nsub, sl2);
+    else
+      k_sel_fwd_bo<float, DD><<<(unsigned)grid, 64, 0, s>>>((const float*)q, (const float*)k, (const float*)vt,
+                                                            q_of_block, items, n_items, (float*)o_part,
+                                                            (float2*)ml_part, Hq, Hkv, T, S, n_blk, block_size, Lp,
+                                                            nsub, sl2);
+  });
+  return nsa_launch_status();
+}
+
+int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_part, void* o, float* lse, int B,
+                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream) {
+  NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int64_t total = (int64_t)B * Hq * T * (D >= 32 ? D / 32 : 1);
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int n_csr = sel_csr_blocks(T, block_size), nsub = sel_passes(block_size);
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16)
+      k_sel_merge<bf16, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const bf16*)o_part, (const float2*)ml_part,
+                                                            (bf16*)o, lse, Hq, Hkv, T, S, n_csr, block_size, nsub,
+                                                            total);
+    else
+      k_sel_merge<float, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const float*)o_part,
+                                                             (const float2*)ml_part, (float*)o, lse, Hq, Hkv, T, S,
+                                                             n_csr, block_size, nsub, total);
+  });
+  return nsa_launch_status();
+}
+
+int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float* dq_acc, void* dq_out, int B,
+                      int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream) {
+  NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int64_t total = (int64_t)B * Hq * T * (D >= 32 ? D / 32 : 1);
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int n_csr = sel_csr_blocks(T, block_size), nsub = sel_passes(block_size);
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16)
+      k_sel_dq_reduce<bf16, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const bf16*)dq_part, dq_acc,
+                                                                (bf16*)dq_out, Hq, Hkv, T, S, n_csr, block_size,
+                                                                nsub, total);
+    else
+      k_sel_dq_reduce<float, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const float*)dq_part, dq_acc,
+                                                                 (float*)dq_out, Hq, Hkv, T, S, n_csr, block_size,
+                                                                 nsub, total);
+  });
+  return nsa_launch_status();
+}
+
+}  // extern "C"

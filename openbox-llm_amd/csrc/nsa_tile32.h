@@ -65,6 +65,8 @@ template <typename T, int D> struct Tile32 {
   static constexpr int ROW_CHUNKS = 32 * RCH;
   static constexpr int COL_CHUNKS = D * CCH;
   static __device__ __forceinline__ int rkey(int r) { return ((r & 3) | ((r >> 1) & 4)) & (RCH - 1); }
+  // row tiles read in natural row order (lanes 0..7 read rows 0..7)
+  static __device__ __forceinline__ int nkey(int r) { return r & 7 & (RCH - 1); }
   static __device__ __forceinline__ int ckey(int d) { return (CCH == 4 ? (d >> 1) : d) & (CCH - 1); }
 };
 
@@ -79,6 +81,19 @@ __device__ __forceinline__ void lds_row_frag(Frag<T>& f, const T* tile, int m, i
     f.load(row + (c0 ^ C::rkey(r)) * C::EPC);
   else
     f.load2(row + (c0 ^ C::rkey(r)) * C::EPC, row + ((c0 + 1) ^ C::rkey(r)) * C::EPC);
+}
+
+// B fragment of a [32][D] row tile read in natural row order (swizzled by
+// nkey): lane (h, n) holds row n, elements 16s + 8h .. 16s + 8h + 7
+template <typename T, int D>
+__device__ __forceinline__ void lds_nrow_frag(Frag<T>& f, const T* tile, int n, int h, int s) {
+  using C = Tile32<T, D>;
+  const T* row = tile + n * D;
+  const int c0 = (16 * s + 8 * h) / C::EPC;
+  if (sizeof(T) == 2)
+    f.load(row + (c0 ^ C::nkey(n)) * C::EPC);
+  else
+    f.load2(row + (c0 ^ C::nkey(n)) * C::EPC, row + ((c0 + 1) ^ C::nkey(n)) * C::EPC);
 }
 
 // A fragment of a [D][32] column tile: row 32dt + m (zero past D), step s
@@ -104,6 +119,14 @@ __device__ __forceinline__ void row_chunk(int P, int& r, int& c) {
   using C = Tile32<T, D>;
   r = P / C::RCH;
   c = (P % C::RCH) ^ C::rkey(r);
+}
+
+// Physical chunk P of a natural-order row tile -> (row, logical chunk)
+template <typename T, int D>
+__device__ __forceinline__ void nrow_chunk(int P, int& r, int& c) {
+  using C = Tile32<T, D>;
+  r = P / C::RCH;
+  c = (P % C::RCH) ^ C::nkey(r);
 }
 
 // Physical chunk P of a column tile -> (row d, logical chunk)

@@ -356,12 +356,13 @@ def sel_dq(q, k, v, kt, do, block_idx, block_size, lse, dot, rowscale, dq, accum
                               T, D, S, block_size, L.dtype_code(q), _stream(q))
 
 
-def csr_device(block_idx, block_size, n_blk=None):
+def csr_device(block_idx, block_size, n_blk=None, pack_slot=False):
     """Block -> query CSR on the GPU without a host sync.
 
     ``n_blk`` defaults to ``ceil(T / block_size)`` (the trailing partial block
     included, as the selection forward attends to it); the reference grid is
-    ``T // block_size`` (nsa_fsa.py:36).  Returns (q_of_block [cap],
+    ``T // block_size`` (nsa_fsa.py:36).  ``pack_slot``: q_of_block holds
+    ``t * S + s`` (query and slot of the pair).  Returns (q_of_block [cap],
     block_offsets [B,Hkv,n_blk+1], pair_bh [cap], pair_count [1]) int32;
     entries past pair_count are unused.
     """
@@ -379,27 +380,83 @@ def csr_device(block_idx, block_size, n_blk=None):
     assert ws_bytes > 0 or cap == 0, "CSR workspace size query failed"
     ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     _call("nsa_csr_build", _lib().nsa_csr_build, L.ptr(idx), L.ptr(q_of_block), L.ptr(offsets), L.ptr(pair_bh),
-          L.ptr(count), L.ptr(ws), ws_bytes, B, Hkv, T, S, block_size, n_blk, _stream(idx))
+          L.ptr(count), L.ptr(ws), ws_bytes, B, Hkv, T, S, block_size, n_blk, int(pack_slot), _stream(idx))
     return q_of_block, offsets, pair_bh, count
 
 
-def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, csr=None):
+def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, csr=None, kt=None,
+             want_dq=False):
+    """dK, dV (float32) of the selection branch over the block -> query CSR;
+    with ``want_dq`` also the dQ partials of every (query, slot, pass) for
+    ``sel_dq_reduce`` (the CSR must then be built with ``pack_slot``)."""
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     idx = block_idx.to(torch.int32).contiguous()
     S = idx.shape[-1]
     if csr is None:
-        csr = csr_device(idx, block_size)
+        csr = csr_device(idx, block_size, pack_slot=want_dq)
     q_of_block, offsets, _, count = csr
     dk = torch.empty(B, Hkv, T, D, device=q.device, dtype=torch.float32)
     dv = torch.empty_like(dk)
+    dq_part = None
+    if want_dq:
+        if kt is None:
+            kt = transpose_kv(k)
+        ns = int(_lib().nsa_sel_partial_slots(S, block_size))
+        dq_part = torch.empty(B, Hkv, T, ns, Hq // Hkv, D, device=q.device, dtype=q.dtype)
     ws_bytes = int(_lib().nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do), L.ptr(qt), L.ptr(dot_t), L.ptr(lse),
-                                L.ptr(dot), L.ptr(rowscale), L.ptr(q_of_block), L.ptr(offsets), L.ptr(count),
-                                L.ptr(dk), L.ptr(dv), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
-                                SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
-    return dk, dv
+    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(qt),
+          L.ptr(dot_t), L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(q_of_block), int(want_dq), L.ptr(offsets),
+          L.ptr(count), L.ptr(dk), L.ptr(dv), L.ptr(dq_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
+          SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
+    return dk, dv, dq_part
+
+
+def sel_dq_reduce(block_idx, dq_part, dq_acc, block_size, dtype):
+    """dQ of the selection branch (+ the float32 ``dq_acc`` of the other
+    branches, if given) in ``dtype``."""
+    idx = block_idx.to(torch.int32).contiguous()
+    B, Hkv, T, S = idx.shape
+    G, D = dq_part.shape[-2], dq_part.shape[-1]
+    Hq = Hkv * G
+    out = torch.empty(B, Hq, T, D, device=dq_part.device, dtype=dtype)
+    _call("dq[sel]", _lib().nsa_sel_dq_reduce, L.ptr(idx), L.ptr(dq_part), L.ptr(dq_acc), L.ptr(out), B, Hq, Hkv,
+          T, D, S, block_size, L.dtype_code(out), _stream(dq_part))
+    return out
+
+
+def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None):
+    """Block-outer selection forward -> (o, lse[f32], csr); ``csr`` is the
+    packed block -> query CSR (built here when not given)."""
+    check_qkv(q, k, v)
+    q, k = _contig(q), _contig(k)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    assert k.shape[2] == T, "selection keys must have the query length"
+    assert block_idx.shape[:3] == (B, Hkv, T), "block_idx must be [B, Hkv, T, S]"
+    assert block_size >= 16 and block_size % 16 == 0, "block_size must be a multiple of 16"
+    idx = block_idx.to(torch.int32).contiguous()
+    S = idx.shape[-1]
+    if csr is None:
+        csr = csr_device(idx, block_size, pack_slot=True)
+    if vt is None:
+        vt = transpose_kv(v)
+    q_of_block, offsets, _, _ = csr
+    ns = int(_lib().nsa_sel_partial_slots(S, block_size))
+    G = Hq // Hkv
+    o_part = torch.empty(B, Hkv, T, ns, G, D, device=q.device, dtype=q.dtype)
+    ml_part = torch.empty(B, Hkv, T, ns, G, 2, device=q.device, dtype=torch.float32)
+    ws_bytes = int(_lib().nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    _call("fwd[sel]", _lib().nsa_sel_fwd_bo, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(q_of_block), L.ptr(offsets),
+          L.ptr(o_part), L.ptr(ml_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size, SEL_DKDV_CHUNK,
+          L.dtype_code(q), _stream(q))
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
+    _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
+          Hq, Hkv, T, D, S, block_size, L.dtype_code(q), _stream(q))
+    return o, lse, csr
 
 
 # ---------------------------------------------------------------------------
@@ -409,26 +466,29 @@ def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, 
 class SelectionAttnHIP(torch.autograd.Function):
     """Selection attention; same boundary as SelectionAttnTriton
     (nsa_selection_backward.py:337-365): saves q, k, v, block_idx, o, lse and
-    returns None grads for block_idx / block_size."""
+    returns None grads for block_idx / block_size.  Forward and backward run
+    block-outer over one packed block -> query CSR built in the forward."""
 
     @staticmethod
     def forward(ctx, q, k, v, block_idx, block_size):
         q, k, v = _contig(q), _contig(k), _contig(v)
         idx = block_idx.to(torch.int32).contiguous()
-        o, lse = sel_fwd(q, k, v, idx, block_size)
-        ctx.save_for_backward(q, k, v, idx, o, lse)
+        o, lse, csr = sel_fwd_fsa(q, k, v, idx, block_size)
+        ctx.save_for_backward(q, k, v, idx, o, lse, *csr)
         ctx.block_size = block_size
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, idx, o, lse = ctx.saved_tensors
-        dq, dk, dv = selection_backward(q, k, v, idx, ctx.block_size, do, o, lse)
+        q, k, v, idx, o, lse, *csr = ctx.saved_tensors
+        dq, dk, dv = selection_backward_fsa(q, k, v, idx, ctx.block_size, do, o, lse, csr=tuple(csr))
         return dq, dk, dv, None, None
 
 
 def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
-    """dq, dk, dv of the selection branch (input dtypes)."""
+    """dq, dk, dv of the selection branch (input dtypes): dQ query-outer
+    (nsa_sel_dq), dK/dV block-outer (the roles of the reference's atomic
+    kernel, nsa_selection_backward.py:63-189)."""
     check_qkv(q, k, v)
     q, k, v, do = (_contig(t) for t in (q, k, v, do))
     idx = block_idx.to(torch.int32).contiguous()
@@ -441,8 +501,24 @@ def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
     sel_dq(q, k, v, kt, do, idx, block_size, lse, dot, None, dq, False)
     qt = transpose_rows(q, Hkv)
     dot_t = transpose_rows(do, Hkv)
-    dk, dv = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size)
+    dk, dv, _ = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size)
     return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
+
+
+def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None):
+    """dq, dk, dv of the selection branch (input dtypes), all block-outer
+    (the roles of selection_backward_fsa, nsa_selection_backward.py:278-334):
+    one kernel writes dK/dV and the dQ partials, a reduce sums the partials."""
+    check_qkv(q, k, v)
+    q, k, v, do = (_contig(t) for t in (q, k, v, do))
+    idx = block_idx.to(torch.int32).contiguous()
+    Hkv = k.shape[1]
+    dot = delta_of(do, o)
+    qt = transpose_rows(q, Hkv)
+    dot_t = transpose_rows(do, Hkv)
+    dk, dv, dq_part = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size, csr=csr, want_dq=True)
+    dq = sel_dq_reduce(idx, dq_part, None, block_size, q.dtype)
+    return dq, cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
 class RangeAttnHIP(torch.autograd.Function):
@@ -537,13 +613,14 @@ class NSAFusedHIP(torch.autograd.Function):
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
         idx = block_idx.to(torch.int32).contiguous()
         if idx.shape[-1] > 0:
-            o_s, lse_s = sel_fwd(q, ks, vs, idx, geom.sel_block)
+            o_s, lse_s, csr = sel_fwd_fsa(q, ks, vs, idx, geom.sel_block)
         else:
             o_s = torch.zeros_like(q)
             lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
+            csr = ()
         o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
         out = gate_fwd(gate, o_c, o_s, o_w)
-        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w)
+        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, *csr)
         ctx.geom = geom
         ctx.T = T
         ctx.pooled = pooled
@@ -553,7 +630,7 @@ class NSAFusedHIP(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, _didx):
         (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w,
-         lse_c, lse_s, lse_w) = ctx.saved_tensors
+         lse_c, lse_s, lse_w, *csr) = ctx.saved_tensors
         geom, T = ctx.geom, ctx.T
         dout = _contig(dout)
         Hkv = ks.shape[1]
@@ -581,15 +658,17 @@ class NSAFusedHIP(torch.autograd.Function):
         else:
             dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
             dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
-        # selection
+        # selection: dK/dV and dQ partials block-outer; the reduce adds the
+        # window / compression dQ and writes the input dtype
         if idx.shape[-1] > 0:
-            kt_s = transpose_kv(ks)
-            sel_dq(q, ks, vs, kt_s, dout, idx, geom.sel_block, lse_s, dot[1], rs[1], dq, True)
-            dks, dvs = sel_dkdv(q, ks, vs, dout, qt, dot_t, lse_s, dot[1], rs[1], idx, geom.sel_block)
+            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, qt, dot_t, lse_s, dot[1], rs[1], idx, geom.sel_block,
+                                         csr=tuple(csr), want_dq=True)
+            dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
         else:
             dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
             dvs = torch.zeros_like(dks)
-        return (cast_f32(dq, dtype), dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
+            dq_out = cast_f32(dq, dtype)
+        return (dq_out, dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
                 cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None, None)
 
 

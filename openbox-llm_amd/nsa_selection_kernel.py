@@ -2,11 +2,14 @@
 nsa_selection_kernel.py).
 
 ``selection_forward_triton`` / ``selection_forward_fsa`` keep their names and
-return conventions (nsa_selection_kernel.py:175-213, :294-365) but run the HIP
-kernel ``nsa_sel_fwd``: one wave per query and 16-head column block, the
-selected blocks gathered 32 keys per bf16 MFMA step (fp32 inputs use fp32
-MFMA), lse written alongside the output.  One kernel serves every shape, so
-the module switch ``USE_FSA_FWD`` is accepted and ignored.
+return conventions (nsa_selection_kernel.py:175-213, :294-365) on HIP
+kernels.  ``selection_forward_triton`` is query-outer (``nsa_sel_fwd``: one
+wave per query and 16-head column block, the selected blocks gathered 32 keys
+per MFMA step).  ``selection_forward_fsa`` is block-outer (``nsa_sel_fwd_bo``:
+one wave holds a selected block's keys and streams the queries that chose
+it, writing per-(query, block) partials that ``nsa_sel_merge`` combines).  The
+module switch ``USE_FSA_FWD`` is accepted and ignored: the autograd boundary
+always runs block-outer.
 
 ``selection_forward_reference`` is the reference's dense torch definition of
 the branch (nsa_selection_kernel.py:55-92), kept for API parity; the HIP path
@@ -49,8 +52,10 @@ def selection_forward_hip(q, k, v, block_idx, block_size, return_lse=False):
 
 
 def selection_forward_fsa(q, k, v, block_idx, block_size):
-    """Same outputs as the reference's block-outer forward: (o, lse)."""
-    return _ops.sel_fwd(q, k, v, block_idx, block_size)
+    """Block-outer forward over the block -> query CSR: (o, lse), as the
+    reference's FSA path (nsa_selection_kernel.py:294-365)."""
+    o, lse, _ = _ops.sel_fwd_fsa(q, k, v, block_idx, block_size)
+    return o, lse
 
 
 selection_forward_triton = selection_forward_hip

@@ -64,7 +64,9 @@ def test_selection_fwd_bwd(c, dtype):
     assert_close(lse.cpu()[has], lse_ref[has], torch.float32 if dtype == torch.float32 else dtype, "lse")
     o2, dq, dk, dv = _grads_gpu(lambda a, b, v_: nsb.selection_attn_triton(a, b, v_, idx.to(dev), bs),
                                 q, k, v, do, dev)
-    assert torch.equal(o2.detach(), o), "autograd forward differs from the plain forward"
+    o_fsa, _ = nsk.selection_forward_fsa(q.to(dev), k.to(dev), v.to(dev), idx.to(dev), bs)
+    assert torch.equal(o2.detach(), o_fsa), "autograd forward differs from the block-outer forward it runs"
+    assert_close(o2, o_ref, dtype, "o (autograd)")
     assert_close(dq, dq_r, dtype, "dq")
     assert_close(dk, dk_r, dtype, "dk")
     assert_close(dv, dv_r, dtype, "dv")
@@ -142,3 +144,40 @@ def test_empty_and_tiny_rows():
                                               return_lse=True)
         assert torch.count_nonzero(o) == 0
         assert (lse == -1e9).all()
+
+
+FSA_CONFIGS = CONFIGS + [dict(B=1, Hq=8, Hkv=2, D=64, T=640, block_size=128, S=3),
+                         dict(B=1, Hq=16, Hkv=1, D=128, T=300, block_size=48, S=4)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+@pytest.mark.parametrize("c", FSA_CONFIGS, ids=cfg_id)
+def test_selection_fsa_and_query_outer_paths(c, dtype):
+    """Both forward paths (block-outer partials + merge, query-outer) and both
+    backward paths (dQ partials + reduce, query-outer dQ) against the oracle;
+    blocks of 128 keys take two 64-key passes, 48-key blocks leave a ragged pass."""
+    dev = require_gpu()
+    log(f"selection fsa/query-outer {cfg_id(c)} {dtype}")
+    import nsa_selection_backward as nsb
+    import nsa_selection_kernel as nsk
+    q, k, v, do = _inputs(c, dtype, seed=40)
+    idx = make_block_idx(c["B"], c["Hkv"], c["T"], c["block_size"], c["S"], seed=3)
+    bs = c["block_size"]
+    o_ref, lse_ref, dq_r, dk_r, dv_r = _grads_oracle(
+        lambda a, b, v_: O.selection_attention(a, b, v_, idx, bs), q, k, v, do)
+    qd, kd, vd, dod, idd = (t.to(dev) for t in (q, k, v, do, idx))
+    has = lse_ref > -1e8
+    for name, fn in (("fsa", nsk.selection_forward_fsa),
+                     ("query-outer", lambda *a: nsk.selection_forward_triton(*a, return_lse=True))):
+        o, lse = fn(qd, kd, vd, idd, bs)
+        assert_close(o, o_ref, dtype, f"o ({name})")
+        assert torch.equal(lse.cpu() > -1e8, has), f"empty-row pattern of lse differs ({name})"
+        assert_close(lse.cpu()[has], lse_ref[has], torch.float32 if dtype == torch.float32 else dtype, f"lse ({name})")
+    o, lse = nsk.selection_forward_fsa(qd, kd, vd, idd, bs)
+    for name, fn in (("fsa", lambda: nsb.selection_backward_fsa(qd, kd, vd, idd, bs, dod, o, lse)),
+                     ("query-outer", lambda: nsb.selection_backward_triton(qd, kd, vd, idd, bs, dod, o))):
+        dq, dk, dv = fn()
+        torch.cuda.synchronize()
+        assert_close(dq, dq_r, dtype, f"dq ({name})")
+        assert_close(dk, dk_r, dtype, f"dk ({name})")
+        assert_close(dv, dv_r, dtype, f"dv ({name})")
