@@ -53,11 +53,6 @@ int nsa_padded_len(int Lk);
  * K^T operands of the attention kernels. */
 int nsa_transpose_kv(const void* x, void* xt, int BH, int L, int D, int Lp, int dtype, void* stream);
 
-/* x [B][Hq][T][D] -> xt [B][Hkv][ceil(G/16)][T][D][16] (heads of a 16-head
- * chunk contiguous, zero padded).  Used for the Q^T / dO^T operands. */
-int nsa_transpose_rows(const void* x, void* xt, int B, int Hq, int Hkv, int T, int D, int dtype,
-                       void* stream);
-
 /* ---- compression pooling ---------------------------------------------------
  * Replaces block_mean_pool (nsa_fused_kernel.py:549-554): out[i] = mean of
  * x[i*d .. i*d+l-1]; n = (T-l)/d + 1 pooled tokens (T//l when l == d). */
@@ -76,10 +71,13 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 /* Backward prep.  nbr == 1: dot[r] = dO[r] . o0[r] (the delta of
  * nsa_selection_backward.py:168).  nbr == 3: for each branch c,
  * dot[c*rows + r] = dO . o_c, rowscale[c*rows + r] = sigmoid(g_c) and
- * dgate[r][c] = sigmoid'(g_c) dot (autograd of nsa_fused_kernel.py:572-573). */
+ * dgate[r][c] = sigmoid'(g_c) dot (autograd of nsa_fused_kernel.py:572-573).
+ * coff (nullable, laid out like dot) receives the per-row exponent offset
+ * lse_c[r] * log2(e) - log2(rowscale) (rowscale 1 when nbr == 1) that the
+ * dK/dV kernels take; it needs lse_c for every branch c < nbr. */
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
-                 void* dgate, float* dot, float* rowscale, int64_t rows, int D, int nbr, int dtype,
-                 void* stream);
+                 void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
+                 float* rowscale, float* coff, int64_t rows, int D, int nbr, int dtype, void* stream);
 
 /* float32 accumulator -> dtype. */
 int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
@@ -120,16 +118,15 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
  * work items of at most `chunk` queries; q_of_block holds t*S + s when
- * `packed`.  qt/dot_t are the nsa_transpose_rows copies of q/dO, kt the
+ * `packed`.  coff / dot are the row offsets and deltas of nsa_bwd_prep, kt the
  * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
  * zero-fills and then accumulates into.  dq_part (nullable; needs packed and
  * kt): the dQ of every (query, slot, pass), scaled, in the input dtype,
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G][D] -- summed by
  * nsa_sel_dq_reduce. */
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
-int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const void* qt,
-                 const void* dout_t, const float* lse, const float* dot, const float* rowscale,
-                 const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
+int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const float* coff,
+                 const float* dot, const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
                  float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq,
                  int Hkv, int T, int D, int S, int block_size, int chunk, int dtype, void* stream);
 
@@ -178,12 +175,13 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
                  int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
                  void* stream);
 
-/* Backward dK/dV of the range branches (key-outer).  dk/dv float32
- * [B][Hkv][Lk][D]; the call zero-fills and accumulates into them. */
-int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const void* qt,
-                   const void* dout_t, const float* lse, const float* dot, const float* rowscale, float* dk,
-                   float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block,
-                   int cmp_stride, int dtype, void* stream);
+/* Backward dK/dV of the range branches (key-outer; the key-side half of
+ * _range_attn_bwd_qtiled_kernel).  coff / dot: row offsets and deltas from
+ * nsa_bwd_prep.  dk/dv float32 [B][Hkv][Lk][D]; the call zero-fills and
+ * accumulates into them. */
+int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const float* coff,
+                   const float* dot, float* dk, float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window,
+                   int cmp_block, int cmp_stride, int dtype, void* stream);
 
 /* ---- block importance + top-n ----------------------------------------------
  * Replaces the importance / topk block of NSAAttention._forward_fused

@@ -36,11 +36,10 @@ SIGNATURES = {
     "nsa_version": (_I, []),
     "nsa_padded_len": (_I, [_I]),
     "nsa_transpose_kv": (_I, [_P, _P, _I, _I, _I, _I, _I, _P]),
-    "nsa_transpose_rows": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_pool_fwd": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_pool_bwd": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_gate_fwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _P]),
-    "nsa_bwd_prep": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _P]),
+    "nsa_bwd_prep": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _I, _I, _I, _P]),
     "nsa_cast_f32": (_I, [_P, _P, _L, _I, _P]),
     "nsa_sel_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dq": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
@@ -48,7 +47,7 @@ SIGNATURES = {
     "nsa_csr_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dkdv_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
-    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _Z,
+    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _Z,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_partial_slots": (_I, [_I, _I]),
     "nsa_sel_fwd_bo_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
@@ -58,7 +57,7 @@ SIGNATURES = {
     "nsa_range_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+    "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_importance_topn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _P]),

@@ -58,6 +58,7 @@ template <> struct Frag<bf16> {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (bf16)x[j];
   }
+  __device__ __forceinline__ bf16 elem(int j) const { return v[j]; }
 };
 
 template <> struct Frag<float> {
@@ -78,6 +79,7 @@ template <> struct Frag<float> {
     lo = (f32x4){x[0], x[1], x[2], x[3]};
     hi = (f32x4){x[4], x[5], x[6], x[7]};
   }
+  __device__ __forceinline__ float elem(int j) const { return j < 4 ? lo[j] : hi[j - 4]; }
 };
 
 __device__ __forceinline__ void mma(f32x4& c, const Frag<bf16>& a, const Frag<bf16>& b) {

@@ -5,21 +5,20 @@
 // A wave owns 32 keys: their K and V fragments stay in registers and their
 // dK^T / dV^T accumulate in registers for the whole walk.  The queries that
 // see those keys stream through LDS two at a time (32 rows = two queries x 16
-// heads of a head chunk): row tiles of Q and dO, their transposed copies
-// (direct global -> LDS loads, double-buffered) and per-row statistics
-// c = lse*log2(e) - log2(rowscale) (+inf for rows that do not exist) and
-// delta, shared by the workgroup's waves.
+// heads of a head chunk): row tiles of Q and dO (direct global -> LDS loads,
+// kKvStages deep) and per-row statistics c = lse*log2(e) - log2(rowscale)
+// and delta, shared by the workgroup's waves.
 //   S = Q K^T, dP = dO V^T                     (rows on M, keys on N)
 //   P = exp2(S*scale*log2(e) - c), dS = P (dP - delta)
 //   dV^T += dO^T P,  dK^T += Q^T dS             (P / dS straight from the accumulators)
-// Query rows of Q / dO are read through perm32 so the S / dP accumulators
-// line up with the operand slots of the second pair of contractions.  Tiles
-// whose two queries see all 32 keys of a wave skip the per-element mask.
+// Q / dO are read through perm32 for the first pair of products and
+// transposed (ds_read_b64_tr_b16) for the second, so one copy of each tile
+// serves both and the S / dP accumulators line up with the operand slots.
+// Tiles whose two queries see all 32 keys of a wave skip the per-element mask.
 //
-//   * window      : a workgroup owns 32*NW keys and walks queries [k0, k0 + 32 NW + w - 2];
-//                   one writer per key, plain stores.
-//   * compression : same, over query chunks of kCmpChunk (grid.y); chunks merge with
-//                   float atomics.
+//   * window      : a workgroup owns 32*NW keys and walks queries [k0, k0 + 32 NW + w - 2].
+//   * compression : same, over query chunks of kCmpChunk; chunks merge with
+//                   float atomics; the key blocks of one chunk share an XCD.
 //   * selection   : work items (block, chunk of its CSR query list) built by
 //                   k_sel_items; a persistent grid drains them; chunks merge with atomics.
 #include "nsa_launch.h"
@@ -28,79 +27,71 @@
 
 namespace nsa {
 
+constexpr int kKvStages = 4;   // query tiles in flight per workgroup (3 loads ahead)
+
+// Row offset of rows that do not exist (a missing second query, heads past
+// the group): exp2(s - inf) = 0 removes them from every product.
+__device__ const float kAbsentRow = __builtin_inff();
+
 template <typename T, int D> struct KvStage {
   using C = Tile32<T, D>;
-  T qr[C::ROW_ELEMS];    // Q rows   [32][D]
+  T qr[C::ROW_ELEMS];    // Q rows   [32][D]; row r = query (r >> 4), head (r & 15)
   T dr[C::ROW_ELEMS];    // dO rows  [32][D]
-  T qt[C::COL_ELEMS];    // Q^T      [D][32]
-  T dt[C::COL_ELEMS];    // dO^T     [D][32]
-  float c[32], dot[32];
+  float c[32], dot[32];  // filled by one 64-lane load: c then dot
+  int meta[4];           // tA, tB, sA, sB of the tile (tB = -1: none)
 };
 
 // Read-only inputs of the query side.
 template <typename T> struct QSide {
   const T* q;
   const T* dout;
-  const T* qt;     // [B][Hkv][NHC][T][D][16]
-  const T* dt;
-  const float* lse;
+  const float* c;     // per-row exponent offset lse*log2(e) - log2(rowscale)
   const float* dot;
-  const float* rowscale;
   int Hq, Hkv, G, NHC, T_;
 };
 
-// Loads of one 2-query row tile: the four operand tiles go straight to LDS;
-// the row statistics are loaded into registers by threads 0..31 and written
-// (combined) after the tile in flight has been consumed.
-template <typename T, int D, int NTH> struct RowTileLoader {
+// vector-memory loads one wave issues per query tile
+template <typename T, int D, int NTH>
+constexpr int kv_tile_loads() {
+  return 2 * dma_uniform_loads<NTH, Tile32<T, D>::ROW_CHUNKS>() + 1;
+}
+
+// Issue the loads of one 2-query row tile into stage `s`: both operand tiles
+// and the row statistics go straight to LDS; the tile's query / slot ids are
+// written for the consumer.  Rows that do not exist (heads past the group, a
+// missing second query) read finite operand rows of a real row and the row
+// offset +inf, so their P and dS are exactly 0.
+template <typename T, int D, int NTH>
+__device__ __forceinline__ void kv_issue(KvStage<T, D>& s, const QSide<T>& x, int b, int hkv, int hc, int tA,
+                                         int tB, int sA, int sB, int tid) {
   using C = Tile32<T, D>;
-  float lse_, rs_, dot_;
-  bool ok_;
-
-  __device__ __forceinline__ void issue(KvStage<T, D>& s, const QSide<T>& x, int b, int hkv, int hc, int tA, int tB,
-                                        int tid) {
-    const int tq[2] = {tA, tB >= 0 ? tB : tA};      // a missing second query re-reads the first
-    const int grem = x.G - hc * 16;                   // heads of this chunk
-    const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
-    const int64_t cbase = (((int64_t)b * x.Hkv + hkv) * x.NHC + hc) * x.T_;
-    auto rows = [&](const T* src) {
-      return [&, src](int P) {
-        int r, cc;
-        row_chunk<T, D>(P, r, cc);
-        const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
-        return (const void*)(src + ((hbase + hd) * x.T_ + tq[r >> 4]) * D + cc * C::EPC);
-      };
+  const int tq[2] = {tA, tB >= 0 ? tB : tA};
+  const int grem = x.G - hc * 16;                   // heads of this chunk
+  const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
+  auto rows = [&](const T* src) {
+    return [&, src](int P) {
+      int r, cc;
+      row_chunk<T, D>(P, r, cc);
+      const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
+      return (const void*)(src + ((hbase + hd) * x.T_ + tq[r >> 4]) * D + cc * C::EPC);
     };
-    auto cols = [&](const T* src) {
-      return [&, src](int P) {
-        int d, cc;
-        col_chunk<T, D>(P, d, cc);
-        const int r0 = cc * C::EPC;
-        return (const void*)(src + ((cbase + tq[r0 >> 4]) * D + d) * 16 + (r0 & 15));
-      };
-    };
-    dma_tile<NTH, C::ROW_CHUNKS>(s.qr, rows(x.q), tid);
-    dma_tile<NTH, C::ROW_CHUNKS>(s.dr, rows(x.dout), tid);
-    dma_tile<NTH, C::COL_CHUNKS>(s.qt, cols(x.qt), tid);
-    dma_tile<NTH, C::COL_CHUNKS>(s.dt, cols(x.dt), tid);
-    if (tid < 32) {
-      const int t = tid < 16 ? tA : tB;
-      const int hd = tid & 15;
-      ok_ = t >= 0 && hd < grem;
-      const int64_t ri = (hbase + (hd < grem ? hd : grem - 1)) * x.T_ + (t >= 0 ? t : tA);
-      lse_ = x.lse[ri];
-      rs_ = x.rowscale != nullptr ? x.rowscale[ri] : 1.0f;
-      dot_ = x.dot[ri];
-    }
+  };
+  dma_tile_uniform<NTH, C::ROW_CHUNKS>(s.qr, rows(x.q), tid);
+  dma_tile_uniform<NTH, C::ROW_CHUNKS>(s.dr, rows(x.dout), tid);
+  {
+    const int lane = tid & 63, r = lane & 31;
+    const bool real = (r & 15) < grem && (r < 16 || tB >= 0);
+    const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
+    const int64_t ri = (hbase + hd) * x.T_ + tq[r >> 4];
+    lds_dma4(lane < 32 ? (real ? x.c + ri : &kAbsentRow) : x.dot + ri, s.c);
   }
-
-  __device__ __forceinline__ void finish(KvStage<T, D>& s, int tid) const {
-    if (tid < 32) {
-      s.c[tid] = ok_ ? lse_ * kLog2e - __log2f(rs_) : __builtin_inff();
-      s.dot[tid] = dot_;
-    }
+  if (tid == 0) {
+    s.meta[0] = tA;
+    s.meta[1] = tB;
+    s.meta[2] = sA;
+    s.meta[3] = sB;
   }
-};
+}
 
 // Per-wave key state: 32 keys, their K / V fragments and dK^T / dV^T.
 template <typename T, int D> struct KeyAcc {
@@ -120,52 +111,76 @@ template <typename T, int D> struct KeyAcc {
       dk[dt] = zero16();
       dv[dt] = zero16();
     }
+    // complete the loads here: the walk's loads are invisible to the
+    // compiler, which would otherwise wait on these inside the loop -- with
+    // counts that also drain the walk's tiles in flight
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(kf[s]), settle(vf[s]);
   }
 
-  // One 2-query tile; with `mask`, visA / visB say whether this lane's key is
-  // visible to query A / B.
-  __device__ __forceinline__ void step(const KvStage<T, D>& s, bool mask, bool visA, bool visB, float sl2, int n,
-                                       int h, float* ds_out = nullptr) {
-    // every operand fragment of the tile is read up front so the LDS reads
-    // overlap each other and the MFMAs
+  // Q / dO fragments of one tile (row operands of S and dP, read through perm32)
+  struct Rows {
     Frag<T> qa[C::KS], da[C::KS];
+  };
+  __device__ __forceinline__ static void read_rows(Rows& q, const KvStage<T, D>& s, int lane) {
+    const int h = lane >> 5, n = lane & 31;
 #pragma unroll
     for (int k = 0; k < C::KS; ++k) {
-      lds_row_frag<T, D>(qa[k], s.qr, n, h, k);
-      lds_row_frag<T, D>(da[k], s.dr, n, h, k);
+      lds_row_frag<T, D>(q.qa[k], s.qr, n, h, k);
+      lds_row_frag<T, D>(q.da[k], s.dr, n, h, k);
     }
-    f32x16 sacc = zero16(), pacc = zero16();
-#pragma unroll
-    for (int k = 0; k < C::KS; ++k) {
-      mma32(sacc, qa[k], kf[k]);
-      mma32(pacc, da[k], vf[k]);
-    }
-    Frag<T> ta[C::DT][2], tb[C::DT][2];
+  }
+
+  // First half of a tile: S and dP from the row fragments read earlier, the
+  // transposed fragments dO^T (ta) and Q^T (tb) read while those MFMAs run,
+  // then P and dS packed as the operands of the second half.  visA / visB
+  // say whether this lane's key is visible to query A / B.
+  __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, bool visA, bool visB, float sl2,
+                                        int lane, Frag<T> (&ta)[C::DT][2], Frag<T> (&tb)[C::DT][2],
+                                        Frag<T> (&pf)[2], Frag<T> (&sf)[2]) {
+    const int h = lane >> 5;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        lds_col_frag<T, D>(ta[dt][k], s.dt, dt, n, h, k);
-        lds_col_frag<T, D>(tb[dt][k], s.qt, dt, n, h, k);
+        lds_tr_frag<T, D>(ta[dt][k], s.dr, dt, lane, k);
+        lds_tr_frag<T, D>(tb[dt][k], s.qr, dt, lane, k);
       }
+    f32x16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+    for (int k = 0; k < C::KS; ++k) {
+      mma32(sacc, q.qa[k], kf[k]);
+      mma32(pacc, q.da[k], vf[k]);
+    }
+    if constexpr (sizeof(T) == 2) {
+      // one MFMA, then its share of the transposed reads (left alone, the
+      // scheduler issues each read right before its first use)
+      constexpr int NTR = 2 * 2 * C::DT * 2;
+      constexpr int PER = (NTR + 2 * C::KS - 1) / (2 * C::KS);
+#pragma unroll
+      for (int i = 0; i < 2 * C::KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+      }
+    }
     float P[16], dS[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int e = acc_elem(h, r);
       float p = fast_exp2(sacc[r] * sl2 - s.c[e]);
-      if (mask) p = (r < 8 ? visA : visB) ? p : 0.0f;
+      p = (r < 8 ? visA : visB) ? p : 0.0f;
       P[r] = p;
       dS[r] = p * (pacc[r] - s.dot[e]);
     }
-    if (ds_out != nullptr) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ds_out[r] = dS[r];
-    }
-    Frag<T> pf[2], sf[2];
     pf[0].set(P);
     pf[1].set(P + 8);
     sf[0].set(dS);
     sf[1].set(dS + 8);
+  }
+
+  // Second half: dV^T += dO^T P, dK^T += Q^T dS (registers only)
+  __device__ __forceinline__ void back(const Frag<T> (&ta)[C::DT][2], const Frag<T> (&tb)[C::DT][2],
+                                       const Frag<T> (&pf)[2], const Frag<T> (&sf)[2]) {
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
@@ -201,64 +216,86 @@ template <typename T, int D> struct KeyAcc {
 };
 
 // Walk `ntile` 2-query tiles (queries and their block_idx slots from
-// qsrc(i, tA, tB, sA, sB); tB = -1: none) over every head chunk,
-// double-buffered.  vis(tA, tB, mask, visA, visB) fills the mask flags of a
-// tile for this wave.  post(tA, tB, sA, sB, hc, dS) runs on every thread of
-// the workgroup after each tile's step with this lane's 16 dS values (it may
-// synchronise the workgroup); WANT_DS = false skips it.
+// qsrc(i, tA, tB, sA, sB); tB = -1: none) over every head chunk, kKvStages
+// tiles deep, one workgroup barrier per tile, in the middle of it:
+//   front(i)                     S / dP MFMAs, transposed reads, P / dS
+//   wait for tile i+1, barrier   tile i+1 visible; stage i retired by every wave
+//   read rows of tile i+1        LDS reads overlapping ...
+//   back(i), post(i)             ... the dK / dV MFMAs
+//   request tile i + kKvStages   into stage i
+// Every vector-memory operation a wave issues in the loop is counted: LT
+// loads per request (kv_tile_loads), and posts (whose stores only ever add
+// younger operations), so waiting for at most (kKvStages - 2) LT outstanding
+// operations completes tile i + 1 while the two younger tiles stay in flight.
+// vis(tA, tB, mask, visA, visB) fills the mask flags of a tile for this wave
+// (tB = -1: query B's rows are absent, whatever visB says).
+// post(tA, tB, sA, sB, hc, dS) runs on every thread of the workgroup after
+// each tile's back half with this lane's dS as two operand-dtype fragments
+// (element j of fragment k: accumulator register 8 k + j; it may synchronise
+// the workgroup); WANT_DS = false skips it.
 template <bool WANT_DS, typename T, int D, int NTH, typename QSrc, typename Vis, typename Post>
-__device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[2], const QSide<T>& x, int b,
-                                        int hkv, int ntile, QSrc qsrc, Vis vis, Post post, float sl2, int tid, int n,
-                                        int h) {
-  RowTileLoader<T, D, NTH> ld;
+__device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], const QSide<T>& x,
+                                        int b, int hkv, int ntile, QSrc qsrc, Vis vis, Post post, float sl2,
+                                        int tid) {
+  using C = Tile32<T, D>;
+  constexpr int NST = kKvStages;
+  constexpr int LT = kv_tile_loads<T, D, NTH>();
+  static_assert(NST >= 3 && (NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
   const int total = ntile * x.NHC;
   if (total == 0) return;
-  {
+  const int lane = tid & 63;
+  int iti = 0, ihc = 0;   // next tile to request: tile and head chunk
+  auto request = [&](KvStage<T, D>& s) {
     int tA, tB, sA, sB;
-    qsrc(0, tA, tB, sA, sB);
-    ld.issue(stg[0], x, b, hkv, 0, tA, tB, tid);
-    ld.finish(stg[0], tid);
-  }
-  lds_dma_wait();
+    qsrc(iti, tA, tB, sA, sB);
+    kv_issue<T, D, NTH>(s, x, b, hkv, ihc, tA, tB, sA, sB, tid);
+    if (++iti == ntile) {
+      iti = 0;
+      ++ihc;
+    }
+  };
+#pragma unroll
+  for (int p = 0; p < NST; ++p)
+    if (p < total) request(stg[p]);
+  if (total >= NST)
+    vm_wait<(NST - 1) * LT>();
+  else
+    vm_wait<0>();
   __syncthreads();
-  int ti = 0, hc = 0;   // tile and head chunk of iteration `it`
+  typename KeyAcc<T, D>::Rows rows;
+  KeyAcc<T, D>::read_rows(rows, stg[0], lane);
+  int hc = 0, ti = 0;   // head chunk and tile of iteration `it`
   for (int it = 0; it < total; ++it) {
-    int tA, tB, sA, sB;
-    qsrc(ti, tA, tB, sA, sB);
-    int ti1 = ti + 1, hc1 = hc;
-    if (ti1 == ntile) {
-      ti1 = 0;
-      ++hc1;
-    }
-    if (it + 1 < total) {
-      int uA, uB, vA, vB;
-      qsrc(ti1, uA, uB, vA, vB);
-      ld.issue(stg[(it + 1) & 1], x, b, hkv, hc1, uA, uB, tid);
-    }
+    const KvStage<T, D>& s = stg[it % NST];
+    const int tA = s.meta[0], tB = s.meta[1], sA = s.meta[2], sB = s.meta[3];
     bool mask, visA, visB;
     vis(tA, tB, mask, visA, visB);
-    float ds[16];
-    acc.step(stg[it & 1], mask, visA, visB, sl2, n, h, WANT_DS ? ds : nullptr);
-    if (WANT_DS) post(tA, tB, sA, sB, hc, ds);
-    if (it + 1 < total) ld.finish(stg[(it + 1) & 1], tid);
-    lds_dma_wait();
+    Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2];
+    acc.front(s, rows, visA || !mask, visB || !mask, sl2, lane, ta, tb, pf, sf);
+    if (it + NST - 1 < total)
+      vm_wait<(NST - 2) * LT>();
+    else
+      vm_wait<0>();
     __syncthreads();
-    ti = ti1;
-    hc = hc1;
+    if (it + 1 < total) KeyAcc<T, D>::read_rows(rows, stg[(it + 1) % NST], lane);
+    acc.back(ta, tb, pf, sf);
+    if (WANT_DS) post(tA, tB, sA, sB, hc, sf);
+    if (it + NST < total) request(stg[it % NST]);
+    if (++ti == ntile) {
+      ti = 0;
+      ++hc;
+    }
   }
 }
 
 template <typename T>
-__device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const T* qt, const T* dt, const float* lse,
-                                          const float* dot, const float* rowscale, int Hq, int Hkv, int T_) {
+__device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const float* c, const float* dot, int Hq,
+                                          int Hkv, int T_) {
   QSide<T> x;
   x.q = q;
   x.dout = dout;
-  x.qt = qt;
-  x.dt = dt;
-  x.lse = lse;
+  x.c = c;
   x.dot = dot;
-  x.rowscale = rowscale;
   x.Hq = Hq;
   x.Hkv = Hkv;
   x.G = Hq / Hkv;
@@ -267,29 +304,66 @@ __device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const T* qt
   return x;
 }
 
+// Compression dK/dV work: key block kb (keys 32 NW kb ..) is seen by queries
+// t >= 32 NW kb cd + cl - 1, so query chunk ch has work for key blocks
+// 0 .. cmp_active_blocks(ch) - 1; ch = -1 gives the total over all chunks.
+__host__ __device__ inline int cmp_active_blocks(int T, int Lk, int chunk, int NW, int cl, int cd, int ch) {
+  const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
+  const int nch = (T + chunk - 1) / chunk;
+  if (ch < 0) {
+    int tot = 0;
+    for (int c = 0; c < nch; ++c) tot += cmp_active_blocks(T, Lk, chunk, NW, cl, cd, c);
+    return tot;
+  }
+  const int last = (ch * chunk + chunk - 1 < T - 1 ? ch * chunk + chunk - 1 : T - 1) - (cl - 1);
+  if (last < 0) return 0;
+  const int n = last / (32 * NW * cd) + 1;
+  return n < nkb ? n : nkb;
+}
+
 // ---------------------------------------------------------------------------
-// range dK/dV: grid (ceil(Lk / (32 NW)), n_chunks, B*Hkv)
+// range dK/dV: window: ceil(Lk / (32 NW)) * B*Hkv workgroups; compression:
+// cmp_active_blocks(-1) * B*Hkv
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NW>
-__global__ __launch_bounds__(64 * NW) void k_range_dkdv32(int mode, const T* __restrict__ q,
-                                                          const T* __restrict__ dout, const T* __restrict__ qt,
-                                                          const T* __restrict__ dt, const float* __restrict__ lse,
-                                                          const float* __restrict__ dot,
-                                                          const float* __restrict__ rowscale,
-                                                          const T* __restrict__ k, const T* __restrict__ v,
-                                                          float* __restrict__ dk, float* __restrict__ dv, int Hq,
-                                                          int Hkv, int T_, int Lk, int chunk, int window, int cl,
-                                                          int cd, float sl2, float scale) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
+                    const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
+                    float* __restrict__ dk, float* __restrict__ dv, int Hq, int Hkv, int T_, int Lk, int chunk,
+                    int window, int cl, int cd, float sl2, float scale) {
   constexpr int NTH = 64 * NW;
-  __shared__ __align__(16) KvStage<T, D> stg[2];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
-  const int bh = blockIdx.z;
+  __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: its masks branch
+  // 1-D grid over the (key block, query chunk) pairs that have work, per bh,
+  // chunk-major: the workgroups of one chunk (which stream the same queries)
+  // are consecutive, and XCD x takes a contiguous, equal share of them.  The
+  // window has one chunk and uniform work per key block.
+  const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
+  int kblk, ch, bh;
+  if (mode == NSA_MODE_COMPRESS) {
+    const int per_bh = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, -1);
+    const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+    bh = (int)(wg / per_bh);
+    int r = (int)(wg % per_bh);
+    const int nch = (T_ + chunk - 1) / chunk;
+    for (ch = 0; ch < nch - 1; ++ch) {   // chunk ch holds the first cmp_active_blocks(.., ch) key blocks
+      const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+      if (r < nb) break;
+      r -= nb;
+    }
+    kblk = r;
+  } else {
+    kblk = (int)(blockIdx.x % nkb);
+    ch = 0;
+    bh = (int)(blockIdx.x / nkb);
+  }
   const int b = bh / Hkv, hkv = bh % Hkv;
-  const int k0 = blockIdx.x * 32 * NW;
+  const int k0 = kblk * 32 * NW;
   const int kw = k0 + 32 * w;
   const int key = kw + n;
   const bool key_ok = key < Lk;
-  const QSide<T> x = qside(q, dout, qt, dt, lse, dot, rowscale, Hq, Hkv, T_);
+  const QSide<T> x = qside(q, dout, coff, dot, Hq, Hkv, T_);
   // query range of the workgroup
   int tlo, thi;
   const int klast = k0 + 32 * NW - 1 < Lk - 1 ? k0 + 32 * NW - 1 : Lk - 1;
@@ -299,7 +373,7 @@ __global__ __launch_bounds__(64 * NW) void k_range_dkdv32(int mode, const T* __r
   } else {
     tlo = k0 * cd + cl - 1;
     thi = T_ - 1;
-    const int c0 = blockIdx.y * chunk, c1 = c0 + chunk - 1;
+    const int c0 = ch * chunk, c1 = c0 + chunk - 1;
     tlo = tlo > c0 ? tlo : c0;
     thi = thi < c1 ? thi : c1;
   }
@@ -327,8 +401,8 @@ __global__ __launch_bounds__(64 * NW) void k_range_dkdv32(int mode, const T* __r
       visB = key * cd + cl - 1 <= tb;
     }
   };
-  auto none = [](int, int, int, int, int, const float*) {};
-  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, none, sl2, tid, n, h);
+  auto none = [](int, int, int, int, int, const Frag<T>*) {};
+  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, none, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -356,25 +430,22 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // of D -- and written, scaled, to the (query, slot, pass) partial that
 // k_sel_dq_reduce sums.
 template <typename T, int D>
-__global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout,
-                                                    const T* __restrict__ qt, const T* __restrict__ dt,
-                                                    const float* __restrict__ lse, const float* __restrict__ dot,
-                                                    const float* __restrict__ rowscale, const T* __restrict__ k,
-                                                    const T* __restrict__ v, const T* __restrict__ kt,
-                                                    const int32_t* __restrict__ q_of_block,
-                                                    const int4* __restrict__ items,
-                                                    const int32_t* __restrict__ n_items, float* __restrict__ dk,
-                                                    float* __restrict__ dv, T* __restrict__ dq_part, int Hq, int Hkv,
-                                                    int T_, int S, int packed, int n_blk, int L, int Lp, float sl2,
-                                                    float scale) {
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
+                  const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
+                  const T* __restrict__ kt, const int32_t* __restrict__ q_of_block, const int4* __restrict__ items,
+                  const int32_t* __restrict__ n_items, float* __restrict__ dk, float* __restrict__ dv,
+                  T* __restrict__ dq_part, int Hq, int Hkv, int T_, int S, int packed, int n_blk, int L, int Lp,
+                  float sl2, float scale) {
   constexpr int NW = 2, NTH = 64 * NW;
   using C = Tile32<T, D>;
   constexpr int DT = C::DT, DTW = (DT + 1) / 2;          // dQ^T d-tiles per wave
   constexpr int DSP = 64 + 16 / (int)sizeof(T);          // padded pitch of the dS tile
-  __shared__ __align__(16) KvStage<T, D> stg[2];
+  __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
   __shared__ __align__(16) T sdS[32 * DSP];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
-  const QSide<T> x = qside(q, dout, qt, dt, lse, dot, rowscale, Hq, Hkv, T_);
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const QSide<T> x = qside(q, dout, coff, dot, Hq, Hkv, T_);
   const int G = x.G;
   const int ni = *n_items;
   const int npass = sel_passes(L);
@@ -410,6 +481,12 @@ __global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, con
             ktf[i][kk].zero();
         }
     }
+    if (dq_part != nullptr) {
+#pragma unroll
+      for (int i = 0; i < DTW; ++i)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) settle(ktf[i][kk]);
+    }
     const int beg = item.y, cnt = item.z - item.y;
     const int ntile = (cnt + 1) / 2;
     auto decode = [&](int i, int& t, int& s) {
@@ -432,10 +509,10 @@ __global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, con
       visA = key_ok && key <= tA;
       visB = key_ok && key <= tb;
     };
-    auto post = [&](int tA, int tB, int sA, int sB, int hc, const float* ds) {
+    auto post = [&](int tA, int tB, int sA, int sB, int hc, const Frag<T>* ds) {
       // dS (rows x this wave's 32 keys) -> LDS [row][64 keys]
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sdS[acc_elem(h, r) * DSP + 32 * w + n] = from_f32<T>(ds[r]);
+      for (int r = 0; r < 16; ++r) sdS[acc_elem(h, r) * DSP + 32 * w + n] = ds[r >> 3].elem(r & 7);
       __syncthreads();
       f32x16 dq[DTW];
 #pragma unroll
@@ -470,11 +547,11 @@ __global__ __launch_bounds__(128) void k_sel_dkdv32(const T* __restrict__ q, con
       }
     };
     if (dq_part != nullptr)
-      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid, n, h);
+      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid);
     else
-      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid, n, h);
+      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid);
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
-    __syncthreads();   // the next item's first tile reuses stage 0
+    __syncthreads();   // the next item's first tiles reuse stages 0 ..
   }
 }
 
@@ -496,10 +573,9 @@ static constexpr int kCmpChunk = 1024;   // queries per compression dK/dV work i
 
 extern "C" {
 
-int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const void* qt,
-                   const void* dout_t, const float* lse, const float* dot, const float* rowscale, float* dk,
-                   float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block,
-                   int cmp_stride, int dtype, void* stream) {
+int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const float* coff,
+                   const float* dot, float* dk, float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window,
+                   int cmp_block, int cmp_stride, int dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && Lk >= 0, NSA_ERR_SHAPE);
   NSA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, NSA_ERR_SHAPE);
@@ -512,26 +588,26 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
     if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;
   }
   if (T == 0 || Lk == 0) return NSA_OK;
-  const int nch = mode == NSA_MODE_COMPRESS ? (T + kCmpChunk - 1) / kCmpChunk : 1;
-  NSA_CHECK((int64_t)B * Hkv < 65536, NSA_ERR_SHAPE);
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
   // window: 2 waves (64 keys) per workgroup keep the query range tight;
   // compression: 4 waves share each streamed query tile
 #define NSA_RANGE_DKDV_LAUNCH(NW_)                                                                               \
   {                                                                                                            \
-    dim3 grid((Lk + 32 * NW_ - 1) / (32 * NW_), nch, B * Hkv);                                                  \
+    const int64_t grid = (int64_t)(mode == NSA_MODE_COMPRESS                                                   \
+                                       ? cmp_active_blocks(T, Lk, kCmpChunk, NW_, cmp_block, cmp_stride, -1)  \
+                                       : (Lk + 32 * NW_ - 1) / (32 * NW_)) * B * Hkv;                          \
+    if (grid == 0) return NSA_OK;                                                                              \
+    NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);                                                              \
     NSA_DISPATCH_D(D, {                                                                                        \
       if (dtype == NSA_BF16)                                                                                   \
-        k_range_dkdv32<bf16, DD, NW_><<<grid, 64 * NW_, 0, s>>>(                                               \
-            mode, (const bf16*)q, (const bf16*)dout, (const bf16*)qt, (const bf16*)dout_t, lse, dot, rowscale, \
-            (const bf16*)k, (const bf16*)v, dk, dv, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride,  \
-            sl2, scale);                                                                                       \
+        k_range_dkdv32<bf16, DD, NW_><<<(unsigned)grid, 64 * NW_, 0, s>>>(                                     \
+            mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, dk, dv, Hq,     \
+            Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, sl2, scale);                                 \
       else                                                                                                     \
-        k_range_dkdv32<float, DD, NW_><<<grid, 64 * NW_, 0, s>>>(                                              \
-            mode, (const float*)q, (const float*)dout, (const float*)qt, (const float*)dout_t, lse, dot,        \
-            rowscale, (const float*)k, (const float*)v, dk, dv, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block,  \
-            cmp_stride, sl2, scale);                                                                           \
+        k_range_dkdv32<float, DD, NW_><<<(unsigned)grid, 64 * NW_, 0, s>>>(                                    \
+            mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, Hq, \
+            Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, sl2, scale);                                 \
     });                                                                                                        \
   }
   if (mode == NSA_MODE_WINDOW)
@@ -547,9 +623,8 @@ size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int 
   return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sizeof(int4) + 256;
 }
 
-int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const void* qt,
-                 const void* dout_t, const float* lse, const float* dot, const float* rowscale,
-                 const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
+int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const float* coff,
+                 const float* dot, const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
                  float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
                  int T, int D, int S, int block_size, int chunk, int dtype, void* stream) {
   (void)pair_count;
@@ -577,13 +652,11 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16)
       k_sel_dkdv32<bf16, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
-          (const bf16*)q, (const bf16*)dout, (const bf16*)qt, (const bf16*)dout_t, lse, dot, rowscale,
-          (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block, items, n_items, dk, dv, (bf16*)dq_part, Hq,
+          (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block, items, n_items, dk, dv, (bf16*)dq_part, Hq,
           Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
     else
       k_sel_dkdv32<float, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
-          (const float*)q, (const float*)dout, (const float*)qt, (const float*)dout_t, lse, dot, rowscale,
-          (const float*)k, (const float*)v, (const float*)kt, q_of_block, items, n_items, dk, dv, (float*)dq_part,
+          (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, (const float*)kt, q_of_block, items, n_items, dk, dv, (float*)dq_part,
           Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
   });
   return nsa_launch_status();

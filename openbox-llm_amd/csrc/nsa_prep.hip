@@ -1,12 +1,11 @@
 // Layout, pooling and gate kernels of the NSA path (all HBM-bound).
 //
 //  * transpose_kv   : x [BH][L][D] -> xt [BH][D][Lp]  (key-contiguous rows, zero pad)
-//  * transpose_rows : q/dO [B][Hq][T][D] -> [B][Hkv][NHC][T][D][16]
-//                     (the 16 heads of a head chunk contiguous, zero padded)
 //  * pool_fwd/bwd   : mean over spans [i*d, i*d+l)        (nsa_fused_kernel.py:549-554)
 //  * gate_fwd       : out = sum_c sigmoid(g_c) o_c         (nsa_fused_kernel.py:572-573)
 //  * bwd_prep       : dot_c = dO . o_c, rowscale_c = sigmoid(g_c),
-//                     dgate_c = sigmoid'(g_c) dot_c        (autograd of nsa_model.py:297-301)
+//                     dgate_c = sigmoid'(g_c) dot_c        (autograd of nsa_model.py:297-301),
+//                     coff_c = lse_c log2(e) - log2(rowscale_c) for the dK/dV kernels
 //  * cast_f32       : fp32 accumulator -> output dtype
 #include "nsa_common.h"
 #include "nsa_launch.h"
@@ -34,34 +33,6 @@ __global__ __launch_bounds__(256) void k_transpose_kv(const T* __restrict__ x, T
     const int r = e / 64, cc = e % 64;          // r: d, cc: key
     const int d = d0 + r, l = l0 + cc;
     if (d < D && l < Lp) yb[(int64_t)d * Lp + l] = from_f32<T>(tile[cc][r]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// transpose_rows: one thread per (b, hkv, hc, t, d); writes 16 head values
-// ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(256) void k_transpose_rows(const T* __restrict__ x, T* __restrict__ xt,
-                                                        int B, int Hq, int Hkv, int T_, int D) {
-  const int G = Hq / Hkv;
-  const int NHC = (G + 15) / 16;
-  const int64_t total = (int64_t)B * Hkv * NHC * T_ * D;
-  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-    const int d = (int)(e % D);
-    int64_t r = e / D;
-    const int t = (int)(r % T_); r /= T_;
-    const int hc = (int)(r % NHC); r /= NHC;
-    const int hkv = (int)(r % Hkv);
-    const int b = (int)(r / Hkv);
-    T vals[16];
-#pragma unroll
-    for (int h = 0; h < 16; ++h) {
-      const int hg = hc * 16 + h;
-      vals[h] = hg < G ? x[(((int64_t)b * Hq + hkv * G + hg) * T_ + t) * D + d] : from_f32<T>(0.0f);
-    }
-    T* dst = xt + e * 16;
-#pragma unroll
-    for (int h = 0; h < 16; ++h) dst[h] = vals[h];
   }
 }
 
@@ -159,7 +130,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, const T* __restrict__ o0,
                                                   const T* __restrict__ o1, const T* __restrict__ o2,
                                                   const T* __restrict__ gate, T* __restrict__ dgate,
-                                                  float* __restrict__ dot, float* __restrict__ rowscale,
+                                                  const float* __restrict__ lse0, const float* __restrict__ lse1,
+                                                  const float* __restrict__ lse2, float* __restrict__ dot,
+                                                  float* __restrict__ rowscale, float* __restrict__ coff,
                                                   int64_t rows, int D, int nbr) {
   constexpr int N = Vec16<T>::N;
   const int gs = D / N;                         // lanes per row, a power of two <= 64
@@ -186,12 +159,15 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   if (!ok || sub != 0) return;
   if (nbr == 1) {
     dot[row] = acc[0];
+    if (coff) coff[row] = lse0[row] * kLog2e;
     return;
   }
+  const float* lse[3] = {lse0, lse1, lse2};
   for (int c = 0; c < nbr; ++c) {
     const float s = sigmoidf(to_f32(gate[row * 3 + c]));
     dot[(int64_t)c * rows + row] = acc[c];
     rowscale[(int64_t)c * rows + row] = s;
+    if (coff) coff[(int64_t)c * rows + row] = lse[c][row] * kLog2e - __log2f(s);
     if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
   }
 }
@@ -223,21 +199,6 @@ int nsa_transpose_kv(const void* x, void* xt, int BH, int L, int D, int Lp, int 
     k_transpose_kv<bf16><<<grid, 256, 0, s>>>((const bf16*)x, (bf16*)xt, L, D, Lp);
   else
     k_transpose_kv<float><<<grid, 256, 0, s>>>((const float*)x, (float*)xt, L, D, Lp);
-  return nsa_launch_status();
-}
-
-int nsa_transpose_rows(const void* x, void* xt, int B, int Hq, int Hkv, int T, int D, int dtype,
-                       void* stream) {
-  NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && D > 0, NSA_ERR_SHAPE);
-  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  const int NHC = (Hq / Hkv + 15) / 16;
-  const int64_t total = (int64_t)B * Hkv * NHC * T * D;
-  if (total == 0) return NSA_OK;
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    k_transpose_rows<bf16><<<grid_for(total), 256, 0, s>>>((const bf16*)x, (bf16*)xt, B, Hq, Hkv, T, D);
-  else
-    k_transpose_rows<float><<<grid_for(total), 256, 0, s>>>((const float*)x, (float*)xt, B, Hq, Hkv, T, D);
   return nsa_launch_status();
 }
 
@@ -301,15 +262,17 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 
 // rows = B*Hq*T.  nbr == 1 and gate == NULL: dot[r] = dO.o0 (plain delta).
 // nbr == 3: dot[c*rows + r], rowscale[c*rows + r] = sigmoid(gate[r,c]), dgate[r,c].
+// coff (nullable): lse_c * log2(e) - log2(rowscale_c), laid out like dot.
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
-                 void* dgate, float* dot, float* rowscale, int64_t rows, int D, int nbr, int dtype,
-                 void* stream) {
+                 void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
+                 float* rowscale, float* coff, int64_t rows, int D, int nbr, int dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   const int vec = dtype == NSA_BF16 ? 8 : 4;
   NSA_CHECK(rows >= 0 && D > 0 && D % vec == 0 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
   const int gs = D / vec;
   NSA_CHECK(gs <= 64 && (gs & (gs - 1)) == 0, NSA_ERR_SHAPE);
   NSA_CHECK(nbr == 1 || (gate && o1 && o2 && rowscale), NSA_ERR_ARG);
+  NSA_CHECK(!coff || (lse0 && (nbr == 1 || (lse1 && lse2))), NSA_ERR_ARG);
   if (rows == 0) return NSA_OK;
   const int64_t grid64 = (rows * gs + 255) / 256;
   NSA_CHECK(grid64 < (1ll << 31), NSA_ERR_SHAPE);
@@ -317,11 +280,12 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   hipStream_t s = (hipStream_t)stream;
   if (dtype == NSA_BF16)
     k_bwd_prep<bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1, (const bf16*)o2,
-                                          (const bf16*)gate, (bf16*)dgate, dot, rowscale, rows, D, nbr);
+                                          (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2, dot, rowscale,
+                                          coff, rows, D, nbr);
   else
     k_bwd_prep<float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
-                                           (const float*)o2, (const float*)gate, (float*)dgate, dot, rowscale,
-                                           rows, D, nbr);
+                                           (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1, lse2,
+                                           dot, rowscale, coff, rows, D, nbr);
   return nsa_launch_status();
 }
 

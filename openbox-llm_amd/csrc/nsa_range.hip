@@ -219,7 +219,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __align__(16) T sK[2][C::ROW_ELEMS];
   __shared__ __align__(16) T sV[2][C::COL_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
-  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  // window: neighbouring query tiles (which share keys) on one XCD;
+  // compression: every tile reads the same small key set and the work grows
+  // with t, so tiles go out round-robin, longest first, to balance the XCDs
+  const int64_t wg = mode == NSA_MODE_COMPRESS ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, gridDim.x);
   int qt = (int)(wg % nqt);
   if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first
   const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
@@ -377,9 +380,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   __shared__ __align__(16) T sV[2][C::ROW_ELEMS];
   __shared__ __align__(16) T sKt[2][C::COL_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
-  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t wg = mode == NSA_MODE_COMPRESS ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, gridDim.x);
   int qt = (int)(wg % nqt);
-  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;
+  if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first, round-robin (as the forward)
   const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
   const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
   if (tb0 >= T_) return;

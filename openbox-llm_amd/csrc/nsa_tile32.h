@@ -19,9 +19,18 @@
 // (global_load_lds_dwordx4: lane i of a wave writes LDS base + 16 i).  Their
 // 16-byte chunks are XOR-swizzled per row so that the fragment reads of a
 // wave hit distinct banks:
-//   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r)
-//                        (rkey separates the 8 rows perm32 gives 8 adjacent lanes)
+//   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r),
+//                        rkey(r) = 2 (r & 3) + bit 3 of r: the 8 rows perm32
+//                        gives 8 adjacent lanes get 8 distinct keys, and 4
+//                        consecutive rows get keys 2 apart, so the 32-byte
+//                        pieces a transposed read takes from them (lds_tr_frag)
+//                        land on disjoint banks
 //   column tile [D][32]: logical chunk c of row d sits at c ^ ckey(d)
+//
+// Transposed operands (a contraction over the tile's rows) come straight from
+// a row tile through ds_read_b64_tr_b16: within each group of 16 lanes, lane
+// l receives element (l & 3) of the 8-byte pieces addressed by lanes
+// 4j + (l >> 2), j = 0..3 (measured on gfx950).
 #pragma once
 
 #include "nsa_common.h"
@@ -64,7 +73,7 @@ template <typename T, int D> struct Tile32 {
   static constexpr int COL_ELEMS = D * 32;                 // one [D][32] tile
   static constexpr int ROW_CHUNKS = 32 * RCH;
   static constexpr int COL_CHUNKS = D * CCH;
-  static __device__ __forceinline__ int rkey(int r) { return ((r & 3) | ((r >> 1) & 4)) & (RCH - 1); }
+  static __device__ __forceinline__ int rkey(int r) { return (((r & 3) << 1) | ((r >> 3) & 1)) & (RCH - 1); }
   // row tiles read in natural row order (lanes 0..7 read rows 0..7)
   static __device__ __forceinline__ int nkey(int r) { return r & 7 & (RCH - 1); }
   static __device__ __forceinline__ int ckey(int d) { return (CCH == 4 ? (d >> 1) : d) & (CCH - 1); }
@@ -113,6 +122,65 @@ __device__ __forceinline__ void lds_col_frag(Frag<T>& f, const T* tile, int dt, 
   }
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16.  Kernels that fill LDS with the builtin DMA
+// (__builtin_amdgcn_global_load_lds) get a full vmcnt wait in front of this
+// read from the compiler; the asm DMA of lds_dma16 / lds_dma4 does not.
+__device__ __forceinline__ s16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+}
+
+// A use of the fragment's registers: the compiler completes the loads that
+// produce them here rather than at a later first use.
+template <typename T>
+__device__ __forceinline__ void settle(Frag<T>& f) {
+  if constexpr (sizeof(T) == 2)
+    asm volatile("" : "+v"(f.v));
+  else
+    asm volatile("" : "+v"(f.lo), "+v"(f.hi));
+}
+
+// Transposed operand from a [32][D] row tile (natural row order, rkey
+// swizzle): lane (h, m) holds tile[16 s + 8 h + j][32 dt + m], j = 0..7 --
+// the A operand of a product contracting over the tile's rows, slot-matched
+// to the accumulator-as-B fragments of the same rows.  Columns past D (D < 32)
+// repeat earlier columns and only feed accumulator rows that are never stored.
+template <typename T, int D>
+__device__ __forceinline__ void lds_tr_frag(Frag<T>& f, const T* tile, int dt, int lane, int s) {
+  using C = Tile32<T, D>;
+  if constexpr (sizeof(T) == 2) {
+    // two 4-row transposed reads; source lane (g, jj, q) addresses row
+    // 16 s + 8 (g >> 1) + 4 rd + jj, columns 32 dt + 16 (g & 1) + 4 q .. + 3
+    const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+    int col = 32 * dt + 16 * (g & 1) + 4 * q;
+    if (D % 32 != 0) col = col < D - 4 ? col : D - 4;
+    const int ch = col / C::EPC, off = col % C::EPC;
+    s16x4 r[2];
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int row = 16 * s + 8 * (g >> 1) + 4 * rd + jj;
+      r[rd] = lds_read_tr16(tile + row * D + (ch ^ C::rkey(row)) * C::EPC + off);
+    }
+    const s16x4 a = r[0], b = r[1];
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 v = (s16x8){a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    f.v = __builtin_bit_cast(bf16x8, v);
+  } else {
+    // float: eight single-element reads (lanes of a row read consecutive columns)
+    const int h = lane >> 5;
+    int col = 32 * dt + (lane & 31);
+    if (D % 32 != 0) col = col < D ? col : D - 1;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 16 * s + 8 * h + j;
+      x[j] = tile[row * D + ((col / C::EPC) ^ C::rkey(row)) * C::EPC + col % C::EPC];
+    }
+    f.set(x);
+  }
+}
+
 // Physical chunk P of a row tile -> (row, logical chunk)
 template <typename T, int D>
 __device__ __forceinline__ void row_chunk(int P, int& r, int& c) {
@@ -152,7 +220,52 @@ __device__ __forceinline__ void dma_tile(void* lds, SrcFn src, int tid) {
   }
 }
 
+// Direct global -> LDS loads as volatile asm (lane i writes lds + SIZE i):
+// the compiler neither tracks them nor adds waits for them, so LDS reads of
+// other stages are not held behind loads still in flight.  The caller owns
+// the ordering: vm_wait() before the barrier that publishes the data, and no
+// reuse of a stage before the barrier that retires it.  `lds` must be
+// wave-uniform; M0 is written here and is used by nothing else in the
+// kernels that call these.
+__device__ __forceinline__ uint32_t lds_addr_uniform(const void* lds) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
+}
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :: "s"(lds_addr_uniform(lds)), "v"(gsrc) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
+               :: "s"(lds_addr_uniform(lds)), "v"(gsrc) : "memory", "m0");
+}
+
+// As dma_tile, but through lds_dma16 and with every wave issuing the same
+// number of loads (ceil(NCHUNK / NTH); surplus loads repeat a chunk of the
+// tile with the same data), so a wave's outstanding-load count per tile is a
+// constant that partial vmcnt waits can rely on.  NCHUNK must be a multiple
+// of 64.
+template <int NTH, int NCHUNK, typename SrcFn>
+__device__ __forceinline__ void dma_tile_uniform(void* lds, SrcFn src, int tid) {
+  static_assert(NCHUNK % 64 == 0, "tile chunks come in whole waves");
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+#pragma unroll
+  for (int j = 0; j < (NCHUNK + NTH - 1) / NTH; ++j) {
+    const int first = (j * NTH + 64 * w) % NCHUNK;
+    lds_dma16(src(first + lane), (char*)lds + 16 * first);
+  }
+}
+template <int NTH, int NCHUNK>
+constexpr int dma_uniform_loads() { return (NCHUNK + NTH - 1) / NTH; }
+
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (they complete in issue order); LDS and export counters are not waited on.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

@@ -157,18 +157,6 @@ def transpose_kv(x):
     return xt
 
 
-def transpose_rows(x, Hkv):
-    """[B,Hq,T,D] -> [B,Hkv,ceil(G/16),T,D,16] (heads of a 16-chunk contiguous)."""
-    x = _contig(x)
-    B, Hq, T, D = x.shape
-    G = Hq // Hkv
-    nhc = (G + 15) // 16
-    xt = torch.empty(B, Hkv, nhc, T, D, 16, device=x.device, dtype=x.dtype)
-    _call("nsa_transpose_rows", _lib().nsa_transpose_rows, L.ptr(x), L.ptr(xt), B, Hq, Hkv, T, D, L.dtype_code(x),
-                                      _stream(x))
-    return xt
-
-
 def cast_f32(x, dtype):
     if dtype == torch.float32:
         return x
@@ -303,27 +291,34 @@ def importance_topn(q, k_cmp, lse_cmp, geom: NSAGeometry, T=None, return_scores=
 # backward kernels
 # ---------------------------------------------------------------------------
 
-def delta_of(do, o):
-    """dot[r] = dO[r] . O[r] in float32 (nsa_selection_backward.py:168)."""
-    do, o = _contig(do), _contig(o)
+def delta_of(do, o, lse):
+    """-> (dot, coff): dot[r] = dO[r] . O[r] in float32
+    (nsa_selection_backward.py:168) and the row offset lse[r] * log2(e) that
+    the dK/dV kernels take."""
+    do, o, lse = _contig(do), _contig(o), _contig(lse)
     rows = o.shape[0] * o.shape[1] * o.shape[2]
     dot = torch.empty(o.shape[:3], device=o.device, dtype=torch.float32)
-    _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(dot), None, rows,
-                                o.shape[3], 1, L.dtype_code(o), _stream(o))
-    return dot
+    coff = torch.empty_like(dot)
+    _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(lse), None, None,
+          L.ptr(dot), None, L.ptr(coff), rows, o.shape[3], 1, L.dtype_code(o), _stream(o))
+    return dot, coff
 
 
-def gate_bwd_prep(do, o_c, o_s, o_w, gate):
-    """-> (dot [3,B,Hq,T], rowscale [3,B,Hq,T], dgate [B,Hq,T,3])."""
+def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w):
+    """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3]); branch order
+    compression, selection, window; coff = lse * log2(e) - log2(rowscale)."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
+    lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
     B, Hq, T, D = o_c.shape
     rows = B * Hq * T
     dot = torch.empty(3, B, Hq, T, device=o_c.device, dtype=torch.float32)
-    rs = torch.empty(3, B, Hq, T, device=o_c.device, dtype=torch.float32)
+    rs = torch.empty_like(dot)
+    coff = torch.empty_like(dot)
     dgate = torch.empty_like(gate)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(gate), L.ptr(dgate),
-                                L.ptr(dot), L.ptr(rs), rows, D, 3, L.dtype_code(o_c), _stream(o_c))
-    return dot, rs, dgate
+          L.ptr(lse_c), L.ptr(lse_s), L.ptr(lse_w), L.ptr(dot), L.ptr(rs), L.ptr(coff), rows, D, 3,
+          L.dtype_code(o_c), _stream(o_c))
+    return dot, rs, coff, dgate
 
 
 def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0, cmp_block=1,
@@ -335,15 +330,14 @@ def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0
                                 int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q), _stream(q))
 
 
-def range_dkdv(mode, q, k, v, do, qt, dot_t, lse, dot, rowscale, window=0, cmp_block=1, cmp_stride=1):
+def range_dkdv(mode, q, k, v, do, coff, dot, window=0, cmp_block=1, cmp_stride=1):
     B, Hq, T, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     dk = torch.empty(B, Hkv, Lk, D, device=q.device, dtype=torch.float32)
     dv = torch.empty_like(dk)
-    _call(_span_name("dkdv", mode), _lib().nsa_range_dkdv, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do), L.ptr(qt), L.ptr(dot_t),
-                                  L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dk), L.ptr(dv), B, Hq, Hkv, T,
-                                  Lk, D, int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q),
-                                  _stream(q))
+    _call(_span_name("dkdv", mode), _lib().nsa_range_dkdv, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do),
+          L.ptr(coff), L.ptr(dot), L.ptr(dk), L.ptr(dv), B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block),
+          int(cmp_stride), L.dtype_code(q), _stream(q))
     return dk, dv
 
 
@@ -384,8 +378,7 @@ def csr_device(block_idx, block_size, n_blk=None, pack_slot=False):
     return q_of_block, offsets, pair_bh, count
 
 
-def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, csr=None, kt=None,
-             want_dq=False):
+def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, want_dq=False):
     """dK, dV (float32) of the selection branch over the block -> query CSR;
     with ``want_dq`` also the dQ partials of every (query, slot, pass) for
     ``sel_dq_reduce`` (the CSR must then be built with ``pack_slot``)."""
@@ -406,8 +399,8 @@ def sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, rowscale, block_idx, block_size, 
         dq_part = torch.empty(B, Hkv, T, ns, Hq // Hkv, D, device=q.device, dtype=q.dtype)
     ws_bytes = int(_lib().nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(qt),
-          L.ptr(dot_t), L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(q_of_block), int(want_dq), L.ptr(offsets),
+    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(coff),
+          L.ptr(dot), L.ptr(q_of_block), int(want_dq), L.ptr(offsets),
           L.ptr(count), L.ptr(dk), L.ptr(dv), L.ptr(dq_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
           SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
     return dk, dv, dq_part
@@ -494,14 +487,11 @@ def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
     idx = block_idx.to(torch.int32).contiguous()
     if lse is None:
         _, lse = sel_fwd(q, k, v, idx, block_size)
-    Hkv = k.shape[1]
-    dot = delta_of(do, o)
+    dot, coff = delta_of(do, o, lse)
     dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
     kt = transpose_kv(k)
     sel_dq(q, k, v, kt, do, idx, block_size, lse, dot, None, dq, False)
-    qt = transpose_rows(q, Hkv)
-    dot_t = transpose_rows(do, Hkv)
-    dk, dv, _ = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size)
+    dk, dv, _ = sel_dkdv(q, k, v, do, coff, dot, idx, block_size)
     return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
@@ -512,11 +502,8 @@ def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None)
     check_qkv(q, k, v)
     q, k, v, do = (_contig(t) for t in (q, k, v, do))
     idx = block_idx.to(torch.int32).contiguous()
-    Hkv = k.shape[1]
-    dot = delta_of(do, o)
-    qt = transpose_rows(q, Hkv)
-    dot_t = transpose_rows(do, Hkv)
-    dk, dv, dq_part = sel_dkdv(q, k, v, do, qt, dot_t, lse, dot, None, idx, block_size, csr=csr, want_dq=True)
+    dot, coff = delta_of(do, o, lse)
+    dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True)
     dq = sel_dq_reduce(idx, dq_part, None, block_size, q.dtype)
     return dq, cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
@@ -546,14 +533,11 @@ class RangeAttnHIP(torch.autograd.Function):
 
 def range_backward(mode, q, k, v, o, lse, do, window=0, cmp_block=1, cmp_stride=1):
     do = _contig(do)
-    Hkv = k.shape[1]
-    dot = delta_of(do, o)
+    dot, coff = delta_of(do, o, lse)
     dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
     kt = transpose_kv(k)
     range_dq(mode, q, k, v, kt, do, lse, dot, None, dq, False, window, cmp_block, cmp_stride)
-    qt = transpose_rows(q, Hkv)
-    dot_t = transpose_rows(do, Hkv)
-    dk, dv = range_dkdv(mode, q, k, v, do, qt, dot_t, lse, dot, None, window, cmp_block, cmp_stride)
+    dk, dv = range_dkdv(mode, q, k, v, do, coff, dot, window, cmp_block, cmp_stride)
     return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
@@ -633,22 +617,19 @@ class NSAFusedHIP(torch.autograd.Function):
          lse_c, lse_s, lse_w, *csr) = ctx.saved_tensors
         geom, T = ctx.geom, ctx.T
         dout = _contig(dout)
-        Hkv = ks.shape[1]
         dtype = q.dtype
-        dot, rs, dgate = gate_bwd_prep(dout, o_c, o_s, o_w, gate)
-        qt = transpose_rows(q, Hkv)
-        dot_t = transpose_rows(dout, Hkv)
+        dot, rs, coff, dgate = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w)
         dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
         # window
         kt_w = transpose_kv(kw)
         range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
-        dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, qt, dot_t, lse_w, dot[2], rs[2], geom.window)
+        dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
         # compression
         if k_cmp.shape[2] > 0:
             kt_c = transpose_kv(k_cmp)
             range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
                      geom.cmp_block, geom.cmp_stride)
-            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, qt, dot_t, lse_c, dot[0], rs[0], 0,
+            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
                                   geom.cmp_block, geom.cmp_stride)
         else:
             dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
@@ -661,7 +642,7 @@ class NSAFusedHIP(torch.autograd.Function):
         # selection: dK/dV and dQ partials block-outer; the reduce adds the
         # window / compression dQ and writes the input dtype
         if idx.shape[-1] > 0:
-            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, qt, dot_t, lse_s, dot[1], rs[1], idx, geom.sel_block,
+            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
                                          csr=tuple(csr), want_dq=True)
             dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
         else:
