@@ -177,161 +177,143 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
   }
 }
 
-// 32 consecutive elements of a partial row as float (four 16-byte loads for
-// bf16, eight for float)
-__device__ __forceinline__ void load32(const bf16* p, float (&x)[32]) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(p + 8 * c);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[8 * c + i] = (float)v[i];
-  }
-}
-__device__ __forceinline__ void load32(const float* p, float (&x)[32]) {
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * c);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[4 * c + i] = v[i];
-  }
-}
-__device__ __forceinline__ void store32(bf16* p, const float (&x)[32]) {
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    bf16x8 v;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (bf16)x[8 * c + i];
-    *reinterpret_cast<bf16x8*>(p + 8 * c) = v;
-  }
-}
-__device__ __forceinline__ void store32(float* p, const float (&x)[32]) {
-#pragma unroll
-  for (int c = 0; c < 8; ++c)
-    *reinterpret_cast<f32x4*>(p + 4 * c) = (f32x4){x[4 * c], x[4 * c + 1], x[4 * c + 2], x[4 * c + 3]};
+static inline int grid_for(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
 }
 
-// o[row] = sum_slots exp2(m - M) l O_slot / sum exp2(m - M) l, lse = (M + log2 L) ln 2.
-// One thread per (b, hkv, t, g, 32-element quarter of D); D = 16 uses one
-// thread per row over the first 16 elements.
+// 8 consecutive elements of a row (one 16-byte load for bf16, two for float)
+__device__ __forceinline__ void load8(const bf16* p, float (&x)[8]) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+}
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
+}
+__device__ __forceinline__ void store8(bf16* p, const float (&x)[8]) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+__device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
+  *reinterpret_cast<f32x4*>(p) = (f32x4){x[0], x[1], x[2], x[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = (f32x4){x[4], x[5], x[6], x[7]};
+}
+
+// Both reductions below take one thread per 8 elements of a row, rows ordered
+// (b, hkv, t, g) so that a wave reads contiguous partial rows, and go through
+// the slots kSlotBatch at a time with every load of a batch issued before any
+// is used (slots that do not count get weight 0 and read slot 0).
+constexpr int kSlotBatch = 8;
+
+// o[row] = sum_slots exp2(m - M) l O_slot / sum exp2(m - M) l over the valid
+// slots, lse = (M + log2 L) ln 2, with a running maximum M across batches.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const T* __restrict__ opart,
                                                    const float2* __restrict__ mlpart, T* __restrict__ o,
                                                    float* __restrict__ lse, int Hq, int Hkv, int T_, int S, int n_csr,
                                                    int L, int nsub, int64_t total) {
-  constexpr int NQ = D >= 32 ? D / 32 : 1, W = D >= 32 ? 32 : D;
+  constexpr int NC = D / 8;
   const int G = Hq / Hkv, NS = S * nsub;
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-    const int dq = (int)(e % NQ);
-    int64_t r = e / NQ;
+    const int c = (int)(e % NC);
+    int64_t r = e / NC;
     const int g = (int)(r % G);
     r /= G;
     const int t = (int)(r % T_);
     const int64_t bh = r / T_;
     const int32_t* irow = idx + (bh * T_ + t) * S;
     const int64_t pbase = (bh * T_ + t) * NS;
-    // pass 1: the largest block maximum over the valid slots
-    float M = kNegInfS;
-    for (int s = 0; s < S; ++s) {
-      if (!sel_slot_valid(irow[s], n_csr, L, t)) continue;
-      for (int p = 0; p < nsub; ++p) {
-        const float2 ml = mlpart[(pbase + s * nsub + p) * G + g];
-        if (ml.y > 0.0f) M = fmaxf(M, ml.x);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float M = kNegInfS, Ls = 0.0f;
+    for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
+      float2 ml[kSlotBatch];
+      float x[kSlotBatch][8];
+      bool ok[kSlotBatch];
+#pragma unroll
+      for (int k = 0; k < kSlotBatch; ++k) {
+        const int sl = s0 + k;
+        ok[k] = sl < NS && sel_slot_valid(irow[sl < NS ? sl / nsub : 0], n_csr, L, t);
+        const int64_t pr = (pbase + (ok[k] ? sl : 0)) * G + g;
+        ml[k] = mlpart[pr];
+        load8(opart + pr * D + 8 * c, x[k]);
       }
-    }
-    // pass 2: weights exp2(m - M) l and the weighted sum of the partial outputs
-    float acc[32];
+      float bm = M;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc[i] = 0.0f;
-    float Ls = 0.0f;
-    if (M != kNegInfS) {
-      for (int sl = 0; sl < NS; ++sl) {
-        if (!sel_slot_valid(irow[sl / nsub], n_csr, L, t)) continue;
-        const int64_t pr = (pbase + sl) * G + g;
-        const float2 ml = mlpart[pr];
-        if (!(ml.y > 0.0f)) continue;
-        const float w = fast_exp2(ml.x - M) * ml.y;
-        Ls += w;
-        float x[32];
-        if (W == 32) {
-          load32(opart + pr * D + dq * 32, x);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 32; ++i) x[i] = i < W ? to_f32(opart[pr * D + i]) : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) acc[i] += w * x[i];
+      for (int k = 0; k < kSlotBatch; ++k) {
+        ok[k] = ok[k] && ml[k].y > 0.0f;
+        bm = ok[k] ? fmaxf(bm, ml[k].x) : bm;
       }
+      if (bm == kNegInfS) continue;   // nothing valid yet
+      const float rs = M == kNegInfS ? 0.0f : fast_exp2(M - bm);
+      Ls *= rs;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= rs;
+#pragma unroll
+      for (int k = 0; k < kSlotBatch; ++k) {
+        const float wk = ok[k] ? fast_exp2(ml[k].x - bm) * ml[k].y : 0.0f;
+        Ls += wk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += wk * x[k][i];
+      }
+      M = bm;
     }
     const int64_t orow = (((bh / Hkv) * Hq + (bh % Hkv) * G + g) * T_ + t);
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) acc[i] *= inv;
-    if (W == 32) {
-      store32(o + orow * D + dq * 32, acc);
-    } else {
-#pragma unroll
-      for (int i = 0; i < W; ++i) o[orow * D + i] = from_f32<T>(acc[i]);
-    }
-    if (dq == 0) lse[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
+    for (int i = 0; i < 8; ++i) acc[i] *= inv;
+    store8(o + orow * D + 8 * c, acc);
+    if (c == 0) lse[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
   }
 }
 
-// dq_out[row] = (dq_acc[row] or 0) + sum over valid slots of dqpart (already scaled).
-// One thread per (b, hq, t, 32-element quarter of D).
+// dq_out[row] = (dq_acc[row] or 0) + sum over the valid slots of dqpart
+// (already scaled), written in the input dtype.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_sel_dq_reduce(const int32_t* __restrict__ idx, const T* __restrict__ dqpart,
                                                        const float* __restrict__ dq_acc, T* __restrict__ dq_out,
                                                        int Hq, int Hkv, int T_, int S, int n_csr, int L, int nsub,
                                                        int64_t total) {
-  constexpr int NQ = D >= 32 ? D / 32 : 1, W = D >= 32 ? 32 : D;
+  constexpr int NC = D / 8;
   const int G = Hq / Hkv, NS = S * nsub;
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-    const int dq = (int)(e % NQ);
-    int64_t r = e / NQ;
+    const int c = (int)(e % NC);
+    int64_t r = e / NC;
+    const int g = (int)(r % G);
+    r /= G;
     const int t = (int)(r % T_);
-    r /= T_;
-    const int hq = (int)(r % Hq);
-    const int b = (int)(r / Hq);
-    const int hkv = hq / G, g = hq % G;
-    const int64_t bh = (int64_t)b * Hkv + hkv;
+    const int64_t bh = r / T_;
     const int32_t* irow = idx + (bh * T_ + t) * S;
     const int64_t pbase = (bh * T_ + t) * NS;
-    const int64_t orow = ((int64_t)b * Hq + hq) * T_ + t;
-    float acc[32];
-    if (dq_acc != nullptr && W == 32) {
-      load32(dq_acc + orow * D + dq * 32, acc);
+    const int64_t orow = (((bh / Hkv) * Hq + (bh % Hkv) * G + g) * T_ + t);
+    float acc[8];
+    if (dq_acc != nullptr) {
+      load8(dq_acc + orow * D + 8 * c, acc);
     } else {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) acc[i] = (dq_acc != nullptr && i < W) ? dq_acc[orow * D + i] : 0.0f;
+      for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     }
-    for (int s = 0; s < S; ++s) {
-      if (!sel_slot_valid(irow[s], n_csr, L, t)) continue;
-      for (int p = 0; p < nsub; ++p) {
-        const T* src = dqpart + ((pbase + s * nsub + p) * G + g) * D;
-        float x[32];
-        if (W == 32) {
-          load32(src + dq * 32, x);
-        } else {
+    for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
+      float x[kSlotBatch][8];
+      bool ok[kSlotBatch];
 #pragma unroll
-          for (int i = 0; i < 32; ++i) x[i] = i < W ? to_f32(src[i]) : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < 32; ++i) acc[i] += x[i];
+      for (int k = 0; k < kSlotBatch; ++k) {
+        const int sl = s0 + k;
+        ok[k] = sl < NS && sel_slot_valid(irow[sl < NS ? sl / nsub : 0], n_csr, L, t);
+        load8(dqpart + ((pbase + (ok[k] ? sl : 0)) * G + g) * D + 8 * c, x[k]);
       }
-    }
-    if (W == 32) {
-      store32(dq_out + orow * D + dq * 32, acc);
-    } else {
 #pragma unroll
-      for (int i = 0; i < W; ++i) dq_out[orow * D + i] = from_f32<T>(acc[i]);
+      for (int k = 0; k < kSlotBatch; ++k)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += ok[k] ? x[k][i] : 0.0f;
     }
+    store8(dq_out + orow * D + 8 * c, acc);
   }
-}
-
-static inline int grid_for(int64_t n) {
-  int64_t g = (n + 255) / 256;
-  if (g > 65536) g = 65536;
-  return (int)(g < 1 ? 1 : g);
 }
 
 }  // namespace nsa
@@ -399,7 +381,7 @@ int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_
                   int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream) {
   NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  const int64_t total = (int64_t)B * Hq * T * (D >= 32 ? D / 32 : 1);
+  const int64_t total = (int64_t)B * Hq * T * (D / 8);
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
   const int n_csr = sel_csr_blocks(T, block_size), nsub = sel_passes(block_size);
@@ -420,7 +402,7 @@ int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float
                       int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream) {
   NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  const int64_t total = (int64_t)B * Hq * T * (D >= 32 ? D / 32 : 1);
+  const int64_t total = (int64_t)B * Hq * T * (D / 8);
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
   const int n_csr = sel_csr_blocks(T, block_size), nsub = sel_passes(block_size);

@@ -1,17 +1,26 @@
 // Block importance + top-n selection (the block choice of NSAAttention,
-// nsa_model.py:245-258 and :343-355), one wave per (b, hkv, t).
+// nsa_model.py:245-258 and :343-355).
 //
-//  1. p_cmp = exp2(q.k_cmp * scale*log2e - lse_cmp*log2e) over the visible
-//     pooled tokens (lse_cmp from the compression forward), 32 tokens per MFMA
-//     step, summed over the 16 heads of each head chunk with a butterfly
-//     inside the 16-lane groups, accumulated per token in LDS (head chunks in
-//     order, so the sum order is fixed).
-//  2. imp_slc[j] = sum_i imp_cmp[i] * |span_i & block_j| / d (tokens ascending).
-//  3. score = +inf for forced blocks, -FLT_MAX for blocks not yet complete,
-//     else imp_slc; keys (orderable score << 32 | ~j) make a wave-wide u64 max
-//     pick the highest score and, among equal scores, the lowest block index.
+// A workgroup of 4 waves takes 8 consecutive queries of one (b, hkv); a wave
+// holds the Q fragments of its 2 queries x 16 heads (a 32-row MFMA operand)
+// and walks the pooled tokens the group's last query sees, 32 per tile, the
+// tiles shared through LDS (direct global -> LDS loads, double-buffered):
+//
+//  1. S = Q K_cmp^T on 32x32 MFMAs (rows on M, tokens on N); p_cmp =
+//     exp2(S * scale*log2e - lse_cmp*log2e) with lse_cmp from the compression
+//     forward, tokens the query cannot see set to 0.
+//  2. imp_cmp[q][i] = sum over the group's heads of p_cmp: each lane holds 8
+//     heads of each of its token's 2 rows, summed in order, then the two
+//     lane halves are added (head chunks of groups wider than 16 follow in
+//     chunk order), so every sum has a fixed order.
+//  3. after each tile the tile's tokens fold into the selection blocks:
+//     imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d, tokens ascending.
+//  4. per query: score = +inf for forced blocks, -FLT_MAX for blocks not yet
+//     complete, else imp_slc; keys (orderable score << 32 | ~j) make a
+//     wave-wide u64 max pick the highest score and, among equal scores, the
+//     lowest block index, S times.
 #include "nsa_launch.h"
-#include "nsa_tiles.h"
+#include "nsa_tile32.h"
 
 namespace nsa {
 
@@ -32,113 +41,189 @@ __device__ __forceinline__ void wave_fence() {
   __builtin_amdgcn_wave_barrier();
 }
 
+constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
+constexpr int kImpQPB = 4 * kImpQPW;      // queries per workgroup
+
+// last pooled token visible to t (-1: none)
+__device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) {
+  if (t < cl - 1 || n_cmp <= 0) return -1;
+  const int hi = (t - cl + 1) / cd;
+  return hi < n_cmp - 1 ? hi : n_cmp - 1;
+}
+
+// LDS: K tiles [2][32][D], per-wave token scratch [4][2][32], block sums [8][nsp]
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_topn(const T* __restrict__ q, const T* __restrict__ kc,
-                                              const float* __restrict__ lse, int32_t* __restrict__ out_idx,
-                                              float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
-                                              int ncp, int n_slc, int S, int cl, int cd, int ls, int force_init,
-                                              int n_local, int wpb, int64_t nrows, float sl2) {
-  extern __shared__ float smem[];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, c = lane & 15;
-  const int64_t r = (int64_t)blockIdx.x * wpb + w;
-  if (r >= nrows) return;
-  float* imp = smem + (int64_t)w * (ncp + n_slc);
-  float* sc = imp + ncp;
-  const int t = (int)(r % T_);
-  const int bh = (int)(r / T_);
+__global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
+                                                  const float* __restrict__ lse, int32_t* __restrict__ out_idx,
+                                                  float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
+                                                  int n_slc, int nsp, int S, int cl, int cd, int ls, int force_init,
+                                                  int n_local, int nqb, float sl2) {
+  using C = Tile32<T, D>;
+  extern __shared__ __align__(16) char smem[];
+  T* sK = reinterpret_cast<T*>(smem);                                   // [2][ROW_ELEMS]
+  float* stok = reinterpret_cast<float*>(sK + 2 * C::ROW_ELEMS);        // [4][2][32]
+  float* sblk = stok + 4 * kImpQPW * 32;                                 // [8][nsp]
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // long rows first: workgroups go out round-robin, the latest queries first
+  const int qb = nqb - 1 - (int)(blockIdx.x % nqb);
+  const int bh = (int)(blockIdx.x / nqb);
   const int b = bh / Hkv, hkv = bh % Hkv;
   const int G = Hq / Hkv, NHC = (G + 15) / 16;
-  for (int i = lane; i < ncp; i += kWave) imp[i] = 0.0f;
-  wave_fence();
+  const int t0 = qb * kImpQPB;
+  const int tq0 = t0 + kImpQPW * w;   // this wave's queries tq0, tq0 + 1
+  const int tlast = t0 + kImpQPB - 1 < T_ - 1 ? t0 + kImpQPB - 1 : T_ - 1;
+  const int hi_wg = imp_last_token(tlast, n_cmp, cl, cd);
+  const int ntile = hi_wg < 0 ? 0 : hi_wg / 32 + 1;
+  int hi_q[kImpQPW];
+#pragma unroll
+  for (int i = 0; i < kImpQPW; ++i) hi_q[i] = tq0 + i < T_ ? imp_last_token(tq0 + i, n_cmp, cl, cd) : -1;
 
-  int hi = -1;
-  if (t >= cl - 1 && n_cmp > 0) {
-    hi = (t - cl + 1) / cd;
-    hi = hi < n_cmp - 1 ? hi : n_cmp - 1;
-  }
+  for (int i = tid; i < kImpQPB * nsp; i += 256) sblk[i] = 0.0f;
   const T* kbase = kc + (int64_t)bh * n_cmp * D;
-  for (int hc = 0; hc < NHC; ++hc) {
-    const int hg = hc * 16 + c;
-    const bool col_ok = hg < G;
-    const int64_t row = ((int64_t)b * Hq + hkv * G + hg) * T_ + t;
-    Frag<T> qf[Dims<D>::KC];
-    load_row_frags<T, D>(qf, col_ok ? q + row * D : nullptr, g);
-    const float lse2 = col_ok ? lse[row] * kLog2e : 0.0f;
-    for (int kb = 0; kb <= hi; kb += 32) {
-      Frag<T> kf[2][Dims<D>::KC];
-      load_key_frags<T, D>(kf, kbase, kb, n_cmp, g, c);
-      f32x4 s0 = zero4(), s1 = zero4();
+  auto load_tile = [&](int buf, int kt) {
+    dma_tile<256, C::ROW_CHUNKS>(sK + buf * C::ROW_ELEMS, [&](int P) {
+      int r, cc;
+      nrow_chunk<T, D>(P, r, cc);
+      int tok = kt * 32 + r;
+      tok = tok < n_cmp ? tok : n_cmp - 1;
+      return (const void*)(kbase + (int64_t)tok * D + cc * C::EPC);
+    }, tid);
+  };
+  if (ntile > 0) load_tile(0, 0);
+
+  // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
+  float* my_tok = stok + w * kImpQPW * 32;
+  float* my_blk = sblk + w * kImpQPW * nsp;
+  Frag<T> qf[C::KS];
+  float lse2[16];
+  auto load_rows = [&](int hc) {
+    const int row = perm32(n);            // A operand row this lane supplies
+    const int hd = hc * 16 + (row & 15);
+    const int hs = hd < G ? hd : G - 1;
+    int tq = tq0 + (row >> 4);
+    tq = tq < T_ ? tq : T_ - 1;
+    const T* qrow = q + (((int64_t)b * Hq + hkv * G + hs) * T_ + tq) * D;
 #pragma unroll
-      for (int kc2 = 0; kc2 < Dims<D>::KC; ++kc2) {
-        mma(s0, kf[0][kc2], qf[kc2]);
-        mma(s1, kf[1][kc2], qf[kc2]);
+    for (int s = 0; s < C::KS; ++s) qf[s].load(qrow + 16 * s + 8 * h);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int e = acc_elem(h, r);
+      const int he = hc * 16 + (e & 15);
+      int te = tq0 + (e >> 4);
+      const bool ok = he < G && te < T_;
+      te = te < T_ ? te : T_ - 1;
+      // absent rows (heads past the group, queries past T) get p = 0
+      lse2[r] = ok ? lse[((int64_t)b * Hq + hkv * G + he) * T_ + te] * kLog2e : __builtin_inff();
+    }
+  };
+  if (NHC == 1) load_rows(0);
+  for (int kt = 0; kt < ntile; ++kt) {
+    const int buf = kt & 1;
+    lds_dma_wait();
+    __syncthreads();
+    if (kt + 1 < ntile) load_tile(buf ^ 1, kt + 1);
+    const T* tile = sK + buf * C::ROW_ELEMS;
+    const int tok = kt * 32 + n;
+    for (int hc = 0; hc < NHC; ++hc) {
+      if (NHC > 1) load_rows(hc);   // groups wider than 16 heads: one chunk at a time
+      f32x16 sacc = zero16();
+#pragma unroll
+      for (int s = 0; s < C::KS; ++s) {
+        Frag<T> kf;
+        lds_nrow_frag<T, D>(kf, tile, n, h, s);
+        mma32(sacc, qf[s], kf);
       }
-      const uint32_t vm = col_ok ? range_mask(kb + 8 * g, 0, hi) : 0u;
-      float p[8];
+      float part[kImpQPW];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float s = j < 4 ? s0[j & 3] : s1[j & 3];
-        p[j] = ((vm >> j) & 1u) ? fast_exp2(s * sl2 - lse2) : 0.0f;
+      for (int i = 0; i < kImpQPW; ++i) {
+        const bool vis = tok <= hi_q[i];
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float p = fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
+          acc += vis ? p : 0.0f;
+        }
+        part[i] = acc;
       }
+      // heads 8h .. 8h+7 of each row are in lane half h: add the other half
 #pragma unroll
-      for (int m = 1; m < 16; m <<= 1) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p[j] += __shfl_xor(p[j], m, kWave);
+      for (int i = 0; i < kImpQPW; ++i) part[i] += __shfl_xor(part[i], 32, kWave);
+      // lane half h keeps query h's value for token `tok`
+      const float mine = h == 0 ? part[0] : part[1];
+      if (hc == 0)
+        my_tok[h * 32 + n] = mine;
+      else
+        my_tok[h * 32 + n] += mine;
+    }
+    wave_fence();
+    // fold the tile's tokens into the blocks they overlap, tokens ascending;
+    // lane = (query, block of the tile's span)
+    const int i0 = kt * 32;
+    const int i1 = i0 + 31 < n_cmp - 1 ? i0 + 31 : n_cmp - 1;
+    const int jlo = (i0 * cd) / ls;
+    int jhi = (i1 * cd + cl - 1) / ls;
+    jhi = jhi < n_slc - 1 ? jhi : n_slc - 1;
+    const int nj = jhi - jlo + 1;
+    for (int u = lane; u < kImpQPW * nj; u += kWave) {
+      const int qi = u / nj, j = jlo + u % nj;
+      int a_i = j * ls - cl + 1 <= 0 ? 0 : (j * ls - cl + 1 + cd - 1) / cd;
+      int b_i = ((j + 1) * ls - 1) / cd;
+      a_i = a_i > i0 ? a_i : i0;
+      b_i = b_i < i1 ? b_i : i1;
+      float sj = my_blk[qi * nsp + j];
+      for (int i = a_i; i <= b_i; ++i) {
+        const int a = i * cd > j * ls ? i * cd : j * ls;
+        const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
+        if (e > a) sj += my_tok[qi * 32 + (i - i0)] * ((float)(e - a) / (float)cd);
       }
-      float mine = p[0];
-#pragma unroll
-      for (int j = 1; j < 8; ++j) mine = (c == j) ? p[j] : mine;
-      const int tok = kb + 8 * g + c;
-      if (c < 8 && tok < ncp) imp[tok] += mine;
+      my_blk[qi * nsp + j] = sj;
     }
     wave_fence();
   }
+  __syncthreads();
 
-  // selection-block importance, masking and forcing
-  const int tb = t / ls;
-  for (int j = lane; j < n_slc; j += kWave) {
-    const int lo_i = j * ls - cl + 1 <= 0 ? 0 : (j * ls - cl + 1 + cd - 1) / cd;
-    int hi_i = ((j + 1) * ls - 1) / cd;
-    hi_i = hi_i < n_cmp - 1 ? hi_i : n_cmp - 1;
-    float s = 0.0f;
-    for (int i = lo_i; i <= hi_i; ++i) {
-      const int a = i * cd > j * ls ? i * cd : j * ls;
-      const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
-      if (e > a) s += imp[i] * ((float)(e - a) / (float)cd);
+  // per query of this wave: scores, masking and forcing, then top-S
+  for (int qi = 0; qi < kImpQPW; ++qi) {
+    const int t = tq0 + qi;
+    if (t >= T_) break;
+    const int64_t r = (int64_t)bh * T_ + t;
+    float* sc = my_blk + qi * nsp;
+    const int tb = t / ls;
+    for (int j = lane; j < n_slc; j += kWave) {
+      const float s = sc[j];
+      if (scores != nullptr) scores[r * n_slc + j] = s;
+      const bool valid = (j + 1) * ls - 1 <= t;
+      const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
+      sc[j] = forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f);
     }
-    if (scores != nullptr) scores[r * n_slc + j] = s;
-    const bool valid = (j + 1) * ls - 1 <= t;
-    const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
-    sc[j] = forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f);
-  }
-  wave_fence();
-
-  // top-S: wave-wide argmax of (score, lower index), S times
-  uint64_t removed = 0;
-  auto lane_best = [&]() {
-    uint64_t best = 0;
-    int k = 0;
-    for (int j = lane; j < n_slc; j += kWave, ++k) {
-      if ((removed >> k) & 1ull) continue;
-      const uint64_t key = topn_key(sc[j], j);
-      best = key > best ? key : best;
-    }
-    return best;
-  };
-  uint64_t mine = lane_best();
-  int32_t* orow = out_idx + r * S;
-  for (int s = 0; s < S; ++s) {
-    uint64_t bk = mine;
+    wave_fence();
+    uint64_t removed = 0;
+    auto lane_best = [&]() {
+      uint64_t best = 0;
+      int k = 0;
+      for (int j = lane; j < n_slc; j += kWave, ++k) {
+        if ((removed >> k) & 1ull) continue;
+        const uint64_t key = topn_key(sc[j], j);
+        best = key > best ? key : best;
+      }
+      return best;
+    };
+    uint64_t mine = lane_best();
+    int32_t* orow = out_idx + r * S;
+    for (int s = 0; s < S; ++s) {
+      uint64_t bk = mine;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-      const uint64_t o = shfl_xor_u64(bk, m);
-      bk = o > bk ? o : bk;
-    }
-    const int jw = (int)(0xFFFFFFFFu - (uint32_t)(bk & 0xFFFFFFFFu));
-    if (lane == 0) orow[s] = jw;
-    if ((jw & (kWave - 1)) == lane) {
-      removed |= 1ull << (jw / kWave);
-      mine = lane_best();
+      for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = shfl_xor_u64(bk, m);
+        bk = o > bk ? o : bk;
+      }
+      const int jw = (int)(0xFFFFFFFFu - (uint32_t)(bk & 0xFFFFFFFFu));
+      if (lane == 0) orow[s] = jw;
+      if ((jw & (kWave - 1)) == lane) {
+        removed |= 1ull << (jw / kWave);
+        mine = lane_best();
+      }
     }
   }
 }
@@ -160,36 +245,38 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const int S = n_sel < n_slc ? n_sel : n_slc;
   NSA_CHECK(n_slc <= 64 * 64, NSA_ERR_SHAPE);
   if (T == 0 || n_slc == 0) return NSA_OK;
-  const int ncp = ((n_cmp + 31) / 32) * 32 + 32;
-  const size_t per_wave = (size_t)(ncp + n_slc) * sizeof(float);
-  NSA_CHECK(per_wave <= 65536, NSA_ERR_SHAPE);
-  int wpb = (int)(65536 / per_wave);
-  wpb = wpb > 4 ? 4 : wpb;
-  const int64_t nrows = (int64_t)B * Hkv * T;
-  const int64_t grid = (nrows + wpb - 1) / wpb;
+  const int nsp = n_slc + 1;   // per-query block-sum pitch (odd: spreads the 8 queries over banks)
+  const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)2 * 32 * D;
+  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 + (size_t)kImpQPB * nsp);
+  NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
+  const int nqb = (T + kImpQPB - 1) / kImpQPB;
+  const int64_t grid = (int64_t)B * Hkv * nqb;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  const size_t lds = per_wave * wpb;
+  // more than 64 KB of dynamic LDS must be allowed per kernel
+#define NSA_TOPN_LDS(K) (lds <= 65536 || hipFuncSetAttribute((const void*)(K), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
   switch (D) {
-#define NSA_TOPN_CASE(DD)                                                                                        \
-  case DD:                                                                                                       \
-    if (dtype == NSA_BF16)                                                                                       \
-      k_topn<bf16, DD><<<(unsigned)grid, 64 * wpb, lds, s>>>((const bf16*)q, (const bf16*)k_cmp, lse_cmp,      \
-                                                             block_idx, scores, Hq, Hkv, T, n_cmp, ncp, n_slc, S, \
-                                                             cmp_block, cmp_stride, sel_block, force_init,       \
-                                                             n_local, wpb, nrows, sl2);                          \
-    else                                                                                                         \
-      k_topn<float, DD><<<(unsigned)grid, 64 * wpb, lds, s>>>((const float*)q, (const float*)k_cmp, lse_cmp,   \
-                                                              block_idx, scores, Hq, Hkv, T, n_cmp, ncp, n_slc,  \
-                                                              S, cmp_block, cmp_stride, sel_block, force_init,   \
-                                                              n_local, wpb, nrows, sl2);                         \
+#define NSA_TOPN_CASE(DD)                                                                                       \
+  case DD:                                                                                                      \
+    NSA_CHECK(NSA_TOPN_LDS((k_imp_topn<bf16, DD>)) && NSA_TOPN_LDS((k_imp_topn<float, DD>)), NSA_ERR_LAUNCH);  \
+    if (dtype == NSA_BF16)                                                                                      \
+      k_imp_topn<bf16, DD><<<(unsigned)grid, 256, lds, s>>>((const bf16*)q, (const bf16*)k_cmp, lse_cmp,      \
+                                                            block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp, S, \
+                                                            cmp_block, cmp_stride, sel_block, force_init,       \
+                                                            n_local, nqb, sl2);                                 \
+    else                                                                                                        \
+      k_imp_topn<float, DD><<<(unsigned)grid, 256, lds, s>>>((const float*)q, (const float*)k_cmp, lse_cmp,   \
+                                                             block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp,  \
+                                                             S, cmp_block, cmp_stride, sel_block, force_init,   \
+                                                             n_local, nqb, sl2);                                \
     break;
     NSA_TOPN_CASE(16)
     NSA_TOPN_CASE(32)
     NSA_TOPN_CASE(64)
     NSA_TOPN_CASE(128)
 #undef NSA_TOPN_CASE
+#undef NSA_TOPN_LDS
     default:
       return NSA_ERR_SHAPE;
   }
