@@ -85,10 +85,12 @@ def keys_visible(w, idx):
 def kernel_flops(w, kv):
     """Algorithmic FLOPs of one launch of each timed kernel (span name -> flops).
 
-    Per (query head, visible key): forward 4*D (QK^T and PV); dK/dV kernel
-    8*D (S, dP, dV, dK); dQ kernel 2*D (dQ only: its S and dP are recomputed
-    work, counted once in the dK/dV kernel).  Sum = 14*D per key, the
-    fwd+bwd convention of the metric.
+    Per (query head, visible key): forward 4*D (QK^T and PV); range dK/dV
+    kernels 8*D (S, dP, dV, dK); range dQ kernels 2*D (dQ only: their S and
+    dP are recomputed work, counted once in the dK/dV kernel).  The selection
+    dK/dV kernel also forms the dQ partials (10*D); dq[sel] only sums them
+    and has no FLOP model.  Sum = 14*D per key, the fwd+bwd convention of
+    the metric.
     """
     G = w["Hq"] // w["Hkv"]
     D = w["D"]
@@ -97,9 +99,20 @@ def kernel_flops(w, kv):
     for br, k in (("win", k_win), ("cmp", k_cmp), ("sel", k_sel)):
         rows_keys = k * G
         out[f"fwd[{br}]"] = 4 * D * rows_keys
-        out[f"dq[{br}]"] = 2 * D * rows_keys
-        out[f"dkdv[{br}]"] = 8 * D * rows_keys
+        if br == "sel":
+            out["dkdv[sel]"] = 10 * D * rows_keys
+        else:
+            out[f"dq[{br}]"] = 2 * D * rows_keys
+            out[f"dkdv[{br}]"] = 8 * D * rows_keys
     return out
+
+
+# HBM bytes per launch of the dominant kernel, measured with two rocprofv3
+# PMC passes of this bench (FETCH_SIZE, then WRITE_SIZE) and scaled by what
+# the same counters read for a plain 1 GiB device copy (x2.0 and x1.0); the
+# commands and counter values are kept under profiles/.  Reported only for
+# the workload and kernel they were measured on.
+MEASURED_TRAFFIC = {("c3", "dkdv[sel]"): 2.011e10 + 1.084e10}
 
 
 def run_gpu(args, w):
@@ -229,7 +242,7 @@ def main():
     ms, spans, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
     tokens = w["B"] * w["T"]
     value = tokens / (ms / 1e3)
-    total_flops = sum(flops_of[f"{p}[{b}]"] for p in ("fwd", "dq", "dkdv") for b in ("win", "cmp", "sel"))
+    total_flops = sum(flops_of.values())
 
     # dominant kernel: the timed call with the largest total time that has a FLOP model
     named = {}
@@ -247,7 +260,8 @@ def main():
         achieved = flops_of[name] / per_launch_s / 1e12
         roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved, 2),
                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                    "traffic": None, "launch_ms": round(per_launch_s * 1e3, 4)}
+                    "traffic": MEASURED_TRAFFIC.get((args.workload, name)),
+                    "launch_ms": round(per_launch_s * 1e3, 4)}
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
