@@ -104,7 +104,7 @@ int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, cons
  * pairs (t, j) with 0 <= j < n_blk and j*block_size <= t, grouped by (b, hkv, j),
  * query ascending.  n_blk is the reference's T / block_size (nsa_fsa.py:36) or
  * ceil(T / block_size) to include the trailing partial block.  Outputs:
- * q_of_block [cap] (the query t, or t*S + s -- the pair's slot in block_idx --
+ * q_of_block [cap] (the query t, or (t << b) | s with b = ceil(log2 S) -- s the pair's slot in block_idx --
  * when pack_slot != 0), block_offsets [B][Hkv][n_blk+1] (global offsets),
  * pair_bh [cap], *pair_count (device int).  cap = B*Hkv*T*S.  Scratch from
  * nsa_csr_workspace. */
@@ -117,7 +117,7 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
- * work items of at most `chunk` queries; q_of_block holds t*S + s when
+ * work items of at most `chunk` queries; q_of_block holds (t << b) | s when
  * `packed`.  coff / dot are the row offsets and deltas of nsa_bwd_prep, kt the
  * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
  * zero-fills and then accumulates into.  dq_part (nullable; needs packed and

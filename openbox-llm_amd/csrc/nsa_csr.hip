@@ -8,13 +8,16 @@
 #include <hipcub/hipcub.hpp>
 
 #include "nsa_launch.h"
+#include "nsa_items.h"
 
 namespace nsa {
 
-// vals: the query t, or t * S + s (the slot of the pair in block_idx) when pack_slot
+// vals: the query t, or (t << sel_slot_bits(S)) | s (s: the slot of the pair in
+// block_idx) when pack_slot
 __global__ __launch_bounds__(256) void k_csr_keys(const int32_t* __restrict__ idx, uint32_t* __restrict__ keys,
                                                   int32_t* __restrict__ vals, int64_t n, int T, int S, int n_blk,
                                                   int L, uint32_t sentinel, int pack_slot) {
+  const int sbits = sel_slot_bits(S);
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) {
     const int64_t r = e / S;
     const int t = (int)(r % T);
@@ -22,7 +25,7 @@ __global__ __launch_bounds__(256) void k_csr_keys(const int32_t* __restrict__ id
     const int j = idx[e];
     const bool ok = j >= 0 && j < n_blk && (int64_t)j * L <= t;
     keys[e] = ok ? (uint32_t)(bh * n_blk + j) : sentinel;
-    vals[e] = pack_slot ? t * S + (int)(e % S) : t;
+    vals[e] = pack_slot ? (t << sbits) | (int)(e % S) : t;
   }
 }
 
@@ -107,7 +110,7 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
                   int block_size, int n_blk, int pack_slot, void* stream) {
   NSA_CHECK(B > 0 && Hkv > 0 && T >= 0 && S >= 0 && block_size > 0 && n_blk >= 0, NSA_ERR_SHAPE);
-  NSA_CHECK(!pack_slot || (int64_t)T * S < (1ll << 31), NSA_ERR_SHAPE);
+  NSA_CHECK(!pack_slot || ((int64_t)T << sel_slot_bits(S)) < (1ll << 31), NSA_ERR_SHAPE);
   NSA_CHECK((int64_t)B * Hkv * T * S < (1ll << 31) && (int64_t)B * Hkv * n_blk < (1ll << 31), NSA_ERR_SHAPE);
   const CsrLayout c = csr_layout(B, Hkv, T, S, n_blk);
   NSA_CHECK(workspace_bytes >= c.total, NSA_ERR_WORKSPACE);

@@ -56,42 +56,73 @@ constexpr int kv_tile_loads() {
   return 2 * dma_uniform_loads<NTH, Tile32<T, D>::ROW_CHUNKS>() + 1;
 }
 
-// Issue the loads of one 2-query row tile into stage `s`: both operand tiles
-// and the row statistics go straight to LDS; the tile's query / slot ids are
-// written for the consumer.  Rows that do not exist (heads past the group, a
-// missing second query) read finite operand rows of a real row and the row
-// offset +inf, so their P and dS are exactly 0.
-template <typename T, int D, int NTH>
-__device__ __forceinline__ void kv_issue(KvStage<T, D>& s, const QSide<T>& x, int b, int hkv, int hc, int tA,
-                                         int tB, int sA, int sB, int tid) {
+// Issues the loads of one 2-query row tile into a stage: both operand tiles
+// and the row statistics go straight to LDS, and the tile's query / slot ids
+// are written for the consumer.  Rows that do not exist (heads past the
+// group, a missing second query) read finite operand rows of a real row and
+// the row offset +inf, so their P and dS are exactly 0.
+//
+// Everything that depends only on the lane and the head chunk is prepared
+// once (prepare()): each load's 32-bit byte offset below the tile's first
+// row and whether its row is query B's.  Per tile, the base of query A's rows
+// is wave-uniform and every load adds one select to its lane's offset.
+template <typename T, int D, int NTH> struct KvIssuer {
   using C = Tile32<T, D>;
-  const int tq[2] = {tA, tB >= 0 ? tB : tA};
-  const int grem = x.G - hc * 16;                   // heads of this chunk
-  const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
-  auto rows = [&](const T* src) {
-    return [&, src](int P) {
+  static constexpr int LPT = dma_uniform_loads<NTH, C::ROW_CHUNKS>();   // loads per operand tile
+  uint32_t off[LPT];   // (head * T * D + column) * sizeof(T) of this lane's chunk of load j
+  uint32_t qsel;       // bit j: load j's row belongs to query B
+  uint32_t sbit;       // stats: this lane's row belongs to query B
+  int shead, sreal;    // stats: head of this lane's row (clamped); the head exists
+  int grem;            // heads in the prepared chunk
+
+  __device__ __forceinline__ void prepare(const QSide<T>& x, int hc, int tid) {
+    grem = x.G - hc * 16;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    qsel = 0;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
       int r, cc;
-      row_chunk<T, D>(P, r, cc);
+      row_chunk<T, D>((j * NTH + 64 * w) % C::ROW_CHUNKS + lane, r, cc);
       const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
-      return (const void*)(src + ((hbase + hd) * x.T_ + tq[r >> 4]) * D + cc * C::EPC);
-    };
-  };
-  dma_tile_uniform<NTH, C::ROW_CHUNKS>(s.qr, rows(x.q), tid);
-  dma_tile_uniform<NTH, C::ROW_CHUNKS>(s.dr, rows(x.dout), tid);
-  {
-    const int lane = tid & 63, r = lane & 31;
-    const bool real = (r & 15) < grem && (r < 16 || tB >= 0);
-    const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
-    const int64_t ri = (hbase + hd) * x.T_ + tq[r >> 4];
-    lds_dma4(lane < 32 ? (real ? x.c + ri : &kAbsentRow) : x.dot + ri, s.c);
+      off[j] = (uint32_t)(((uint64_t)hd * x.T_ * D + cc * C::EPC) * sizeof(T));
+      qsel |= (uint32_t)(r >> 4) << j;
+    }
+    const int r = lane & 31;
+    sbit = r >> 4;
+    shead = (r & 15) < grem ? (r & 15) : grem - 1;
+    sreal = (r & 15) < grem;
   }
-  if (tid == 0) {
-    s.meta[0] = tA;
-    s.meta[1] = tB;
-    s.meta[2] = sA;
-    s.meta[3] = sB;
+
+  __device__ __forceinline__ void issue(KvStage<T, D>& s, const QSide<T>& x, int b, int hkv, int hc, int tA,
+                                        int tB, int sA, int sB, int tid) const {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int tBq = tB >= 0 ? tB : tA;   // a missing second query re-reads the first
+    const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
+    const int64_t rowA = hbase * x.T_ + tA;
+    const uint32_t dB = (uint32_t)(tBq - tA) * (uint32_t)(D * sizeof(T));
+    const T* qa = x.q + rowA * D;
+    const T* da = x.dout + rowA * D;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const uint32_t v = off[j] + (((qsel >> j) & 1u) ? dB : 0u);
+      const int first = (j * NTH + 64 * w) % C::ROW_CHUNKS;
+      lds_dma16_sbase(qa, v, (char*)s.qr + 16 * first);
+      lds_dma16_sbase(da, v, (char*)s.dr + 16 * first);
+    }
+    {
+      // lanes 0-31: c of row lane, lanes 32-63: delta of row lane - 32
+      const int64_t ri = rowA + (int64_t)shead * x.T_ + (sbit ? tBq - tA : 0);
+      const bool real = sreal && (!sbit || tB >= 0);
+      lds_dma4(lane < 32 ? (real ? x.c + ri : &kAbsentRow) : x.dot + ri, s.c);
+    }
+    if (tid == 0) {
+      s.meta[0] = tA;
+      s.meta[1] = tB;
+      s.meta[2] = sA;
+      s.meta[3] = sB;
+    }
   }
-}
+};
 
 // Per-wave key state: 32 keys, their K / V fragments and dK^T / dV^T.
 template <typename T, int D> struct KeyAcc {
@@ -228,15 +259,15 @@ template <typename T, int D> struct KeyAcc {
 // younger operations), so waiting for at most (kKvStages - 2) LT outstanding
 // operations completes tile i + 1 while the two younger tiles stay in flight.
 // vis(tA, tB, mask, visA, visB) fills the mask flags of a tile for this wave
-// (tB = -1: query B's rows are absent, whatever visB says).
-// post(tA, tB, sA, sB, hc, dS) runs on every thread of the workgroup after
-// each tile's back half with this lane's dS as two operand-dtype fragments
-// (element j of fragment k: accumulator register 8 k + j; it may synchronise
-// the workgroup); WANT_DS = false skips it.
-template <bool WANT_DS, typename T, int D, int NTH, typename QSrc, typename Vis, typename Post>
+// (tB = -1: query B's rows are absent, whatever visB says).  With WANT_DS,
+// pre(dS, i) runs before the barrier with this lane's dS as two operand-dtype
+// fragments (element j of fragment k: accumulator register 8 k + j), and
+// post(tA, tB, sA, sB, hc, i) after the back half, so what pre stages in LDS
+// is visible to post without a second barrier.
+template <bool WANT_DS, typename T, int D, int NTH, typename QSrc, typename Vis, typename Pre, typename Post>
 __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], const QSide<T>& x,
-                                        int b, int hkv, int ntile, QSrc qsrc, Vis vis, Post post, float sl2,
-                                        int tid) {
+                                        int b, int hkv, int ntile, QSrc qsrc, Vis vis, Pre pre, Post post,
+                                        float sl2, int tid) {
   using C = Tile32<T, D>;
   constexpr int NST = kKvStages;
   constexpr int LT = kv_tile_loads<T, D, NTH>();
@@ -245,13 +276,15 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   if (total == 0) return;
   const int lane = tid & 63;
   int iti = 0, ihc = 0;   // next tile to request: tile and head chunk
+  KvIssuer<T, D, NTH> iss;
+  iss.prepare(x, 0, tid);
   auto request = [&](KvStage<T, D>& s) {
     int tA, tB, sA, sB;
     qsrc(iti, tA, tB, sA, sB);
-    kv_issue<T, D, NTH>(s, x, b, hkv, ihc, tA, tB, sA, sB, tid);
+    iss.issue(s, x, b, hkv, ihc, tA, tB, sA, sB, tid);
     if (++iti == ntile) {
       iti = 0;
-      ++ihc;
+      if (++ihc < x.NHC) iss.prepare(x, ihc, tid);
     }
   };
 #pragma unroll
@@ -272,6 +305,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
     vis(tA, tB, mask, visA, visB);
     Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2];
     acc.front(s, rows, visA || !mask, visB || !mask, sl2, lane, ta, tb, pf, sf);
+    if (WANT_DS) pre(sf, it);
     if (it + NST - 1 < total)
       vm_wait<(NST - 2) * LT>();
     else
@@ -279,7 +313,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
     __syncthreads();
     if (it + 1 < total) KeyAcc<T, D>::read_rows(rows, stg[(it + 1) % NST], lane);
     acc.back(ta, tb, pf, sf);
-    if (WANT_DS) post(tA, tB, sA, sB, hc, sf);
+    if (WANT_DS) post(tA, tB, sA, sB, hc, it);
     if (it + NST < total) request(stg[it % NST]);
     if (++ti == ntile) {
       ti = 0;
@@ -401,8 +435,9 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
       visB = key * cd + cl - 1 <= tb;
     }
   };
-  auto none = [](int, int, int, int, int, const Frag<T>*) {};
-  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, none, sl2, tid);
+  auto no_pre = [](const Frag<T>*, int) {};
+  auto no_post = [](int, int, int, int, int, int) {};
+  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -425,9 +460,10 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // Persistent grid over the work items; two waves own 64 keys of the item's
 // block at a time (blocks longer than 64 keys take several passes).  With
-// dq_part, the tile's dS (both waves, 32 rows x 64 keys) is staged in LDS and
-// dQ^T = K^T dS^T is formed for the pass's 64 keys -- each wave covering half
-// of D -- and written, scaled, to the (query, slot, pass) partial that
+// dq_part, the tile's dS^T (both waves, 64 keys x 32 rows) is staged in LDS
+// before the tile's barrier (double-buffered by tile parity) and dQ^T =
+// K^T dS^T is formed after it for the pass's 64 keys -- each wave covering
+// half of D -- and written, scaled, to the (query, slot, pass) partial that
 // k_sel_dq_reduce sums.
 template <typename T, int D>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
@@ -440,9 +476,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   constexpr int NW = 2, NTH = 64 * NW;
   using C = Tile32<T, D>;
   constexpr int DT = C::DT, DTW = (DT + 1) / 2;          // dQ^T d-tiles per wave
-  constexpr int DSP = 64 + 16 / (int)sizeof(T);          // padded pitch of the dS tile
+  using CS = Tile32<T, 32>;                              // dS^T tiles: [keys][32 rows]
   __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
-  __shared__ __align__(16) T sdS[32 * DSP];
+  __shared__ __align__(16) T sdT[2][64 * 32];            // double-buffered by tile parity
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const QSide<T> x = qside(q, dout, coff, dot, Hq, Hkv, T_);
@@ -450,6 +486,7 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   const int ni = *n_items;
   const int npass = sel_passes(L);
   const int NS = S * npass;
+  const int sbits = sel_slot_bits(S);
   for (int it = blockIdx.x; it < ni * npass; it += gridDim.x) {
     const int4 item = items[it / npass];
     const int pass = it % npass;
@@ -492,8 +529,8 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
     auto decode = [&](int i, int& t, int& s) {
       if (i < cnt) {
         const int val = q_of_block[beg + i];
-        t = packed ? val / S : val;
-        s = packed ? val % S : 0;
+        t = packed ? val >> sbits : val;
+        s = packed ? val & ((1 << sbits) - 1) : 0;
       } else {
         t = -1;
         s = 0;
@@ -509,24 +546,35 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       visA = key_ok && key <= tA;
       visB = key_ok && key <= tb;
     };
-    auto post = [&](int tA, int tB, int sA, int sB, int hc, const Frag<T>* ds) {
-      // dS (rows x this wave's 32 keys) -> LDS [row][64 keys]
+    // dS^T (this wave's 32 keys x the tile's 32 rows) -> LDS, two 16-byte
+    // pieces per lane: row 32 w + n of sdT, elements 8 h .. and 16 + 8 h ..
+    auto pre = [&](const Frag<T>* ds, int i) {
+      T* tile = sdT[i & 1] + (32 * w) * 32;
+      const int r = n;   // row of this wave's 32-key sub-tile
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sdS[acc_elem(h, r) * DSP + 32 * w + n] = ds[r >> 3].elem(r & 7);
-      __syncthreads();
+      for (int kf = 0; kf < 2; ++kf) {
+        if constexpr (sizeof(T) == 2) {
+          const int c = (16 * kf + 8 * h) / CS::EPC;
+          *reinterpret_cast<bf16x8*>(tile + r * 32 + (c ^ CS::rkey(r)) * CS::EPC) = ds[kf].v;
+        } else {
+          const int c = (16 * kf + 8 * h) / CS::EPC;
+          *reinterpret_cast<f32x4*>(tile + r * 32 + (c ^ CS::rkey(r)) * CS::EPC) = ds[kf].lo;
+          *reinterpret_cast<f32x4*>(tile + r * 32 + ((c + 1) ^ CS::rkey(r)) * CS::EPC) = ds[kf].hi;
+        }
+      }
+    };
+    // dQ^T = K^T dS^T over the pass's 64 keys, this wave's d-tiles; written
+    // scaled to the (query, slot, pass) partial
+    auto post = [&](int tA, int tB, int sA, int sB, int hc, int i) {
       f32x16 dq[DTW];
 #pragma unroll
-      for (int i = 0; i < DTW; ++i) dq[i] = zero16();
+      for (int d = 0; d < DTW; ++d) dq[d] = zero16();
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         Frag<T> bf;
-        const T* src = sdS + n * DSP + 16 * kk + 8 * h;
-        if (sizeof(T) == 2)
-          bf.load(src);
-        else
-          bf.load2(src, src + 4);
+        lds_tr_frag<T, 32>(bf, sdT[i & 1] + (kk >> 1) * 32 * 32, 0, lane, kk & 1);
 #pragma unroll
-        for (int i = 0; i < DTW; ++i) mma32(dq[i], ktf[i][kk], bf);
+        for (int d = 0; d < DTW; ++d) mma32(dq[d], ktf[d][kk], bf);
       }
       const int t = n < 16 ? tA : tB;
       const int g = hc * 16 + (n & 15);
@@ -534,22 +582,22 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
         const int slot = (n < 16 ? sA : sB) * npass + pass;
         T* drow = dq_part + ((((int64_t)bh * T_ + t) * NS + slot) * G + g) * D;
 #pragma unroll
-        for (int i = 0; i < DTW; ++i) {
-          if (w * DTW + i >= DT) continue;
+        for (int d = 0; d < DTW; ++d) {
+          if (w * DTW + d >= DT) continue;
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
-            const int d = 32 * (w * DTW + i) + 8 * g4 + 4 * h;
-            if (D % 32 == 0 || d < D)
-              store4(drow + d, dq[i][4 * g4] * scale, dq[i][4 * g4 + 1] * scale, dq[i][4 * g4 + 2] * scale,
-                     dq[i][4 * g4 + 3] * scale);
+            const int dd = 32 * (w * DTW + d) + 8 * g4 + 4 * h;
+            if (D % 32 == 0 || dd < D)
+              store4(drow + dd, dq[d][4 * g4] * scale, dq[d][4 * g4 + 1] * scale, dq[d][4 * g4 + 2] * scale,
+                     dq[d][4 * g4 + 3] * scale);
           }
         }
       }
     };
     if (dq_part != nullptr)
-      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid);
+      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     else
-      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, post, sl2, tid);
+      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
     __syncthreads();   // the next item's first tiles reuse stages 0 ..
   }
@@ -634,7 +682,7 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(workspace_bytes >= nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
   NSA_CHECK(dq_part == nullptr || (packed && kt != nullptr), NSA_ERR_ARG);
-  NSA_CHECK(!packed || (int64_t)T * S < (1ll << 31), NSA_ERR_SHAPE);
+  NSA_CHECK(!packed || ((int64_t)T << sel_slot_bits(S)) < (1ll << 31), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
   if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;

@@ -60,4 +60,13 @@ static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size,
 constexpr int kSelPass = 64;
 __host__ __device__ inline int sel_passes(int block_size) { return (block_size + kSelPass - 1) / kSelPass; }
 
+// Packed (query, slot) entries of the CSR built with pack_slot:
+// (t << sel_slot_bits(S)) | s, so that the kernels split them with a shift
+// and a mask; they sort like (t, s).
+__host__ __device__ inline int sel_slot_bits(int S) {
+  int b = 0;
+  while ((1 << b) < S) ++b;
+  return b;
+}
+
 }  // namespace nsa

@@ -4,7 +4,7 @@
 // the input dtype and the merges done by dedicated kernels).
 //
 // Work items are (selected block, chunk of the queries that selected it) from
-// the block -> query CSR built with pack_slot (entries t*S + s).  One wave per
+// the block -> query CSR built with pack_slot (entries (t << sel_slot_bits(S)) | s).  One wave per
 // item holds 64 keys of the block in registers -- K rows as the A operand of
 // S^T = K Q^T, V^T as the A operand of O^T = V^T P^T -- and streams the item's
 // queries two at a time (32 rows = two queries x 16 heads) through LDS.  For
@@ -39,6 +39,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
   const int G = Hq / Hkv, NHC = (G + 15) / 16;
   const int NS = S * nsub;
+  const int sbits = sel_slot_bits(S);
   const int ni = *n_items;
   for (int it = blockIdx.x; it < ni * nsub; it += gridDim.x) {
     const int4 item = items[it / nsub];
@@ -76,8 +77,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
     auto entry = [&](int i, int& t, int& s) {
       if (i < cnt) {
         const int v = q_of_block[beg + i];
-        t = v / S;
-        s = v % S;
+        t = v >> sbits;
+        s = v & ((1 << sbits) - 1);
       } else {
         t = -1;
         s = 0;
@@ -235,10 +236,15 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
       float2 ml[kSlotBatch];
       float x[kSlotBatch][8];
       bool ok[kSlotBatch];
+      int jv[kSlotBatch];
+      // every load of the batch is unconditional (clamped) so that none waits
+      // on a branch: block indices first, then the partials
+#pragma unroll
+      for (int k = 0; k < kSlotBatch; ++k) jv[k] = irow[(s0 + k < NS ? s0 + k : NS - 1) / nsub];
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
         const int sl = s0 + k;
-        ok[k] = sl < NS && sel_slot_valid(irow[sl < NS ? sl / nsub : 0], n_csr, L, t);
+        ok[k] = (sl < NS) & sel_slot_valid(jv[k], n_csr, L, t);
         const int64_t pr = (pbase + (ok[k] ? sl : 0)) * G + g;
         ml[k] = mlpart[pr];
         load8(opart + pr * D + 8 * c, x[k]);
@@ -301,10 +307,13 @@ __global__ __launch_bounds__(256) void k_sel_dq_reduce(const int32_t* __restrict
     for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
       float x[kSlotBatch][8];
       bool ok[kSlotBatch];
+      int jv[kSlotBatch];
+#pragma unroll
+      for (int k = 0; k < kSlotBatch; ++k) jv[k] = irow[(s0 + k < NS ? s0 + k : NS - 1) / nsub];
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
         const int sl = s0 + k;
-        ok[k] = sl < NS && sel_slot_valid(irow[sl < NS ? sl / nsub : 0], n_csr, L, t);
+        ok[k] = (sl < NS) & sel_slot_valid(jv[k], n_csr, L, t);
         load8(dqpart + ((pbase + (ok[k] ? sl : 0)) * G + g) * D + 8 * c, x[k]);
       }
 #pragma unroll

@@ -234,6 +234,18 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :: "s"(lds_addr_uniform(lds)), "v"(gsrc) : "memory", "m0");
 }
+// As lds_dma16 with a wave-uniform 64-bit base and a per-lane 32-bit byte
+// offset (the SGPR-base form: no per-lane 64-bit address arithmetic).
+__device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, void* lds) {
+  const uint64_t b = (uint64_t)(uintptr_t)sbase;
+  // readfirstlane returns int: each half goes through uint32_t so that the
+  // low half is zero-extended (a sign-extended low half corrupts the base)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :: "s"(lds_addr_uniform(lds)), "v"(voff), "s"(bu) : "memory", "m0");
+}
 __device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off"
                :: "s"(lds_addr_uniform(lds)), "v"(gsrc) : "memory", "m0");

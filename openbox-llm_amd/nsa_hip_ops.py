@@ -356,7 +356,7 @@ def csr_device(block_idx, block_size, n_blk=None, pack_slot=False):
     ``n_blk`` defaults to ``ceil(T / block_size)`` (the trailing partial block
     included, as the selection forward attends to it); the reference grid is
     ``T // block_size`` (nsa_fsa.py:36).  ``pack_slot``: q_of_block holds
-    ``t * S + s`` (query and slot of the pair).  Returns (q_of_block [cap],
+    ``(t << ceil(log2 S)) | s`` (query and slot of the pair).  Returns (q_of_block [cap],
     block_offsets [B,Hkv,n_blk+1], pair_bh [cap], pair_count [1]) int32;
     entries past pair_count are unused.
     """
