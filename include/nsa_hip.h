@@ -82,6 +82,13 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
 /* float32 accumulator -> dtype. */
 int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
 
+/* [B][Hkv*G][T][D] -> [B][Hkv][T][G][D]: the query-side layout the selection
+ * kernels read (the G heads of one query and KV head contiguous).  No
+ * reference counterpart: the reference reads [B][H][T][D] directly
+ * (nsa_selection_kernel.py:186-189).  D * sizeof(dtype) must be a multiple
+ * of 16; src and dst must not overlap. */
+int nsa_pack_heads(const void* src, void* dst, int B, int Hkv, int G, int T, int D, int dtype, void* stream);
+
 /* ---- selection branch ------------------------------------------------------
  * Forward: replaces _selection_fwd_kernel / selection_forward_triton
  * (nsa_selection_kernel.py:104-213, FSA variant :232-365).  vt is the
@@ -117,8 +124,10 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
- * work items of at most `chunk` queries; q_of_block holds (t << b) | s when
- * `packed`.  coff / dot are the row offsets and deltas of nsa_bwd_prep, kt the
+ * work items of at most `chunk` (<= 256) queries; q_of_block holds (t << b) | s
+ * when `packed`.  q and dout are in the nsa_pack_heads layout
+ * [B][Hkv][T][G][D].  coff / dot are the row offsets and deltas of
+ * nsa_bwd_prep ([B][Hq][T]), kt the
  * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
  * zero-fills and then accumulates into.  dq_part (nullable; needs packed and
  * kt): the dQ of every (query, slot, pass), scaled, in the input dtype,
@@ -137,7 +146,8 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
  * it writes the block-local output O_j / l_j (input dtype) to o_part and
  * (m_j [log2 units], l_j) float pairs to ml_part, both laid out
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G] (x D for o_part).
- * vt is the nsa_transpose_kv copy of v.  Workspace from
+ * q is in the nsa_pack_heads layout [B][Hkv][T][G][D], vt is the
+ * nsa_transpose_kv copy of v; chunk <= 256.  Workspace from
  * nsa_sel_fwd_bo_workspace. */
 int nsa_sel_partial_slots(int S, int block_size);
 size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);

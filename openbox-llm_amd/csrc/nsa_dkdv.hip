@@ -41,13 +41,17 @@ template <typename T, int D> struct KvStage {
   int meta[4];           // tA, tB, sA, sB of the tile (tB = -1: none)
 };
 
-// Read-only inputs of the query side.
+// Read-only inputs of the query side.  Q and dO are either [B, Hq, T, D]
+// (hs = T D, ts = D) or packed per query [B, Hkv, T, G, D] (hs = D, ts = G D):
+// element (b, hkv, head g of the group, query t) is at
+// (b Hkv + hkv) G T D + g hs + t ts either way.  c and dot are [B, Hq, T].
 template <typename T> struct QSide {
   const T* q;
   const T* dout;
   const float* c;     // per-row exponent offset lse*log2(e) - log2(rowscale)
   const float* dot;
   int Hq, Hkv, G, NHC, T_;
+  int64_t hs, ts;     // element strides between heads of a group / queries
 };
 
 // vector-memory loads one wave issues per query tile
@@ -84,7 +88,7 @@ template <typename T, int D, int NTH> struct KvIssuer {
       int r, cc;
       row_chunk<T, D>((j * NTH + 64 * w) % C::ROW_CHUNKS + lane, r, cc);
       const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
-      off[j] = (uint32_t)(((uint64_t)hd * x.T_ * D + cc * C::EPC) * sizeof(T));
+      off[j] = (uint32_t)(((uint64_t)hd * x.hs + cc * C::EPC) * sizeof(T));
       qsel |= (uint32_t)(r >> 4) << j;
     }
     const int r = lane & 31;
@@ -98,10 +102,11 @@ template <typename T, int D, int NTH> struct KvIssuer {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int tBq = tB >= 0 ? tB : tA;   // a missing second query re-reads the first
     const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
-    const int64_t rowA = hbase * x.T_ + tA;
-    const uint32_t dB = (uint32_t)(tBq - tA) * (uint32_t)(D * sizeof(T));
-    const T* qa = x.q + rowA * D;
-    const T* da = x.dout + rowA * D;
+    const int64_t rowA = hbase * x.T_ + tA;   // statistics row of query A, head hc * 16
+    const int64_t qoff = ((int64_t)b * x.Hkv + hkv) * x.G * x.T_ * D + hc * 16 * x.hs + tA * x.ts;
+    const uint32_t dB = (uint32_t)(tBq - tA) * (uint32_t)(x.ts * sizeof(T));
+    const T* qa = x.q + qoff;
+    const T* da = x.dout + qoff;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const uint32_t v = off[j] + (((qsel >> j) & 1u) ? dB : 0u);
@@ -255,23 +260,28 @@ template <typename T, int D> struct KeyAcc {
 //   back(i), post(i)             ... the dK / dV MFMAs
 //   request tile i + kKvStages   into stage i
 // Every vector-memory operation a wave issues in the loop is counted: LT
-// loads per request (kv_tile_loads), and posts (whose stores only ever add
-// younger operations), so waiting for at most (kKvStages - 2) LT outstanding
-// operations completes tile i + 1 while the two younger tiles stay in flight.
+// loads per request (kv_tile_loads) and at least NSW stores per post.  The
+// operations younger than tile i+1's loads are the kKvStages - 2 requests
+// after it and the min(i, kKvStages - 2) posts issued since, so waiting for
+// at most that many outstanding operations completes tile i + 1 while the two
+// younger tiles stay in flight (operations complete in issue order; a post
+// that stores more than NSW only makes the wait longer).
 // vis(tA, tB, mask, visA, visB) fills the mask flags of a tile for this wave
 // (tB = -1: query B's rows are absent, whatever visB says).  With WANT_DS,
 // pre(dS, i) runs before the barrier with this lane's dS as two operand-dtype
 // fragments (element j of fragment k: accumulator register 8 k + j), and
 // post(tA, tB, sA, sB, hc, i) after the back half, so what pre stages in LDS
 // is visible to post without a second barrier.
-template <bool WANT_DS, typename T, int D, int NTH, typename QSrc, typename Vis, typename Pre, typename Post>
+template <bool WANT_DS, int NSW, typename T, int D, int NTH, typename QSrc, typename Vis, typename Pre,
+          typename Post>
 __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], const QSide<T>& x,
                                         int b, int hkv, int ntile, QSrc qsrc, Vis vis, Pre pre, Post post,
                                         float sl2, int tid) {
   using C = Tile32<T, D>;
   constexpr int NST = kKvStages;
   constexpr int LT = kv_tile_loads<T, D, NTH>();
-  static_assert(NST >= 3 && (NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
+  static_assert(NST >= 3 && (NST - 1) * LT < 64 && (NST - 2) * (LT + NSW) < 64,
+                "in-flight operations exceed the vmcnt range");
   const int total = ntile * x.NHC;
   if (total == 0) return;
   const int lane = tid & 63;
@@ -307,7 +317,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
     acc.front(s, rows, visA || !mask, visB || !mask, sl2, lane, ta, tb, pf, sf);
     if (WANT_DS) pre(sf, it);
     if (it + NST - 1 < total)
-      vm_wait<(NST - 2) * LT>();
+      vm_wait_steps<(NST - 2) * LT, WANT_DS ? NSW : 0, NST - 2>(it);
     else
       vm_wait<0>();
     __syncthreads();
@@ -322,9 +332,9 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   }
 }
 
-template <typename T>
+template <typename T, int D>
 __device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const float* c, const float* dot, int Hq,
-                                          int Hkv, int T_) {
+                                          int Hkv, int T_, bool packed) {
   QSide<T> x;
   x.q = q;
   x.dout = dout;
@@ -335,6 +345,8 @@ __device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const float
   x.G = Hq / Hkv;
   x.NHC = (x.G + 15) / 16;
   x.T_ = T_;
+  x.hs = packed ? (int64_t)D : (int64_t)T_ * D;
+  x.ts = packed ? (int64_t)x.G * D : (int64_t)D;
   return x;
 }
 
@@ -397,7 +409,7 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   const int kw = k0 + 32 * w;
   const int key = kw + n;
   const bool key_ok = key < Lk;
-  const QSide<T> x = qside(q, dout, coff, dot, Hq, Hkv, T_);
+  const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, false);
   // query range of the workgroup
   int tlo, thi;
   const int klast = k0 + 32 * NW - 1 < Lk - 1 ? k0 + 32 * NW - 1 : Lk - 1;
@@ -437,7 +449,7 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   };
   auto no_pre = [](const Frag<T>*, int) {};
   auto no_post = [](int, int, int, int, int, int) {};
-  kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
+  kv_walk<false, 0, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -479,9 +491,12 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   using CS = Tile32<T, 32>;                              // dS^T tiles: [keys][32 rows]
   __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
   __shared__ __align__(16) T sdT[2][64 * 32];            // double-buffered by tile parity
+  __shared__ int32_t sent[kSelItemMax];                  // the item's CSR entries
+  // dQ^T partial stores per post and wave (a lower bound over the waves)
+  constexpr int NSW = D >= 64 ? DTW * 4 : 0;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const QSide<T> x = qside(q, dout, coff, dot, Hq, Hkv, T_);
+  const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, true);   // packed Q / dO
   const int G = x.G;
   const int ni = *n_items;
   const int npass = sel_passes(L);
@@ -499,6 +514,10 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
     const bool key_ok = key < blk_end;
     const int wlast = kw + 31;
     const int64_t kvoff = (int64_t)bh * T_ * D;
+    const int beg = item.y, cnt = item.z - item.y;
+    // the item's entries go to LDS once: a global load per tile would be
+    // waited for with every tile load in flight
+    for (int i = tid; i < cnt; i += NTH) sent[i] = q_of_block[beg + i];
     KeyAcc<T, D> acc;
     acc.init(k + kvoff, v + kvoff, key_ok ? key : j * L, h);
     // K^T fragments of the pass's 64 keys for this wave's dQ^T d-tiles
@@ -524,11 +543,11 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) settle(ktf[i][kk]);
     }
-    const int beg = item.y, cnt = item.z - item.y;
     const int ntile = (cnt + 1) / 2;
+    __syncthreads();   // sent visible to every wave
     auto decode = [&](int i, int& t, int& s) {
       if (i < cnt) {
-        const int val = q_of_block[beg + i];
+        const int val = sent[i];
         t = packed ? val >> sbits : val;
         s = packed ? val & ((1 << sbits) - 1) : 0;
       } else {
@@ -595,11 +614,11 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       }
     };
     if (dq_part != nullptr)
-      kv_walk<true, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
+      kv_walk<true, NSW, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     else
-      kv_walk<false, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
+      kv_walk<false, 0, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
-    __syncthreads();   // the next item's first tiles reuse stages 0 ..
+    __syncthreads();   // the next item's first tiles reuse stages 0 .. and sent
   }
 }
 
@@ -630,6 +649,8 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   NSA_CHECK(mode == NSA_MODE_COMPRESS || (window >= 1 && Lk == T), NSA_ERR_SHAPE);
   NSA_CHECK(mode == NSA_MODE_WINDOW || (cmp_block >= 1 && cmp_stride >= 1), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  // the tile loads address a group's Q / dO rows with 32-bit byte offsets
+  NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * Lk * D;
   if (mode == NSA_MODE_COMPRESS || T == 0) {
@@ -678,11 +699,13 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   (void)pair_count;
   NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && S >= 0, NSA_ERR_SHAPE);
   NSA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, NSA_ERR_SHAPE);
-  NSA_CHECK(block_size >= 16 && block_size % 16 == 0 && chunk >= 2, NSA_ERR_SHAPE);
+  NSA_CHECK(block_size >= 16 && block_size % 16 == 0 && chunk >= 2 && chunk <= kSelItemMax, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(workspace_bytes >= nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
   NSA_CHECK(dq_part == nullptr || (packed && kt != nullptr), NSA_ERR_ARG);
   NSA_CHECK(!packed || ((int64_t)T << sel_slot_bits(S)) < (1ll << 31), NSA_ERR_SHAPE);
+  // the tile loads address a group's Q / dO rows with 32-bit byte offsets
+  NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
   if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;

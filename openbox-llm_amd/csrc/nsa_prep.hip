@@ -172,6 +172,21 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   }
 }
 
+// [B, Hkv*G, T, D] -> [B, Hkv, T, G, D] in 16-byte chunks (CH per row):
+// thread e writes chunk e of the destination.
+__global__ __launch_bounds__(256) void k_pack_heads(const uint4* __restrict__ src, uint4* __restrict__ dst, int G,
+                                                    int T, int CH, int64_t total) {
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % CH);
+    int64_t r = e / CH;                    // destination row (bh, t, g)
+    const int g = (int)(r % G);
+    r /= G;
+    const int t = (int)(r % T);
+    const int64_t bh = r / T;
+    dst[e] = src[((bh * G + g) * T + t) * CH + c];
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_cast_f32(const float* __restrict__ x, T* __restrict__ y, int64_t n) {
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) y[e] = from_f32<T>(x[e]);
@@ -286,6 +301,19 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
     k_bwd_prep<float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
                                            (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1, lse2,
                                            dot, rowscale, coff, rows, D, nbr);
+  return nsa_launch_status();
+}
+
+int nsa_pack_heads(const void* src, void* dst, int B, int Hkv, int G, int T, int D, int dtype, void* stream) {
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(B >= 0 && Hkv >= 0 && G > 0 && T >= 0, NSA_ERR_SHAPE);
+  const int bytes = D * (dtype == NSA_BF16 ? 2 : 4);
+  NSA_CHECK(D > 0 && bytes % 16 == 0, NSA_ERR_SHAPE);
+  NSA_CHECK(src != dst, NSA_ERR_ARG);
+  const int64_t total = (int64_t)B * Hkv * G * T * (bytes / 16);
+  if (total == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  k_pack_heads<<<grid_for(total), 256, 0, s>>>((const uint4*)src, (uint4*)dst, G, T, bytes / 16, total);
   return nsa_launch_status();
 }
 

@@ -26,6 +26,46 @@ __device__ __forceinline__ bool sel_slot_valid(int j, int n_csr, int L, int t) {
   return j >= 0 && j < n_csr && (int64_t)j * L <= t;
 }
 
+constexpr int kFwdStages = 2;   // query tiles in flight per wave of k_sel_fwd_bo
+
+// Loads of one 2-query Q tile into a natural-order row stage, issued by the
+// one wave of the workgroup.  Q is packed per query, [B, Hkv, T, G, D]: the
+// group's heads of one query are contiguous.  Per load a 32-bit byte offset
+// below query A's rows (prepared once per head chunk) plus, for query B's
+// rows, a wave-uniform distance.  Heads past the group read the group's last
+// head (finite rows whose output is never stored).
+template <typename T, int D> struct FwdIssuer {
+  using C = Tile32<T, D>;
+  static constexpr int LPT = C::ROW_CHUNKS / 64;   // loads per tile
+  uint32_t off[LPT];
+  uint32_t qsel;   // bit j: load j's row belongs to query B
+
+  __device__ __forceinline__ void prepare(int grem, int lane) {
+    qsel = 0;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int r, cc;
+      nrow_chunk<T, D>(j * 64 + lane, r, cc);
+      const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
+      off[j] = (uint32_t)((hd * D + cc * C::EPC) * sizeof(T));
+      qsel |= (uint32_t)(r >> 4) << j;
+    }
+  }
+  __device__ __forceinline__ void issue(T* stage, const T* qa, int tA, int tB, int G) const {
+    const uint32_t dB = (uint32_t)((tB >= 0 ? tB : tA) - tA) * (uint32_t)(G * D * sizeof(T));
+#pragma unroll
+    for (int j = 0; j < LPT; ++j)
+      lds_dma16_sbase(qa, off[j] + (((qsel >> j) & 1u) ? dB : 0u), (char*)stage + 1024 * j);
+  }
+};
+
+// vector-memory stores of one tile's partials per lane-group (a lower bound:
+// float tiles and D < 32 count none, which only lengthens the waits)
+template <typename T, int D>
+constexpr int fwd_bo_stores() {
+  return (sizeof(T) == 2 && D >= 32) ? Tile32<T, D>::DT * 4 + 1 : 0;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ vt, const int32_t* __restrict__ q_of_block,
@@ -35,7 +75,12 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
                                                    int n_blk, int L, int Lp, int nsub, float sl2) {
   using C = Tile32<T, D>;
   constexpr int KS = C::KS, DT = C::DT;
-  __shared__ __align__(16) T sQ[2][C::ROW_ELEMS];
+  constexpr int NST = kFwdStages;
+  constexpr int LT = FwdIssuer<T, D>::LPT;
+  constexpr int NSW = fwd_bo_stores<T, D>();
+  static_assert((NST - 1) * (LT + NSW) < 64, "in-flight operations exceed the vmcnt range");
+  __shared__ __align__(16) T sQ[NST][C::ROW_ELEMS];
+  __shared__ int32_t sent[kSelItemMax];   // the item's CSR entries
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
   const int G = Hq / Hkv, NHC = (G + 15) / 16;
   const int NS = S * nsub;
@@ -48,6 +93,10 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
     const int b = bh / Hkv, hkv = bh % Hkv;
     const int kbase = j * L + kSelPass * pass;
     const int kend = j * L + L < T_ ? j * L + L : T_;
+    const int beg = item.y, cnt = item.z - item.y;
+    // the item's entries go to LDS once: a global load per tile would be
+    // waited for with every tile load in flight
+    for (int i = lane; i < cnt; i += 64) sent[i] = q_of_block[beg + i];
     // block keys: K rows (perm32 order) and V^T, both in registers
     Frag<T> kf[2][KS], vf[DT][4];
     const T* kb_ = k + (int64_t)bh * T_ * D;
@@ -71,12 +120,22 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         else
           vf[dt][kk].zero();
       }
-    const int beg = item.y, cnt = item.z - item.y;
+    // complete these loads before the walk, whose loads the compiler does not
+    // see (a wait it placed inside the loop would also drain the tiles)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int s = 0; s < KS; ++s) settle(kf[mt][s]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) settle(vf[dt][kk]);
+    __syncthreads();   // sent written
     const int ntile = (cnt + 1) / 2;
     const int total = ntile * NHC;
     auto entry = [&](int i, int& t, int& s) {
       if (i < cnt) {
-        const int v = q_of_block[beg + i];
+        const int v = sent[i];
         t = v >> sbits;
         s = v & ((1 << sbits) - 1);
       } else {
@@ -84,27 +143,33 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         s = 0;
       }
     };
-    auto issue = [&](int ix, int buf) {
-      const int hc = ix / ntile, ti = ix % ntile;
+    FwdIssuer<T, D> iss;
+    int pix = 0, phc = 0, pti = 0;   // next tile to request
+    iss.prepare(G, lane);
+    auto request = [&](T* stage) {
       int tA, sA, tB, sB;
-      entry(2 * ti, tA, sA);
-      entry(2 * ti + 1, tB, sB);
-      const int tq[2] = {tA, tB >= 0 ? tB : tA};
-      const int grem = G - hc * 16;
-      const int64_t hbase = (int64_t)b * Hq + hkv * G + hc * 16;
-      dma_tile<64, C::ROW_CHUNKS>(sQ[buf], [&](int P) {
-        int r, cc;
-        nrow_chunk<T, D>(P, r, cc);
-        const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
-        return (const void*)(q + ((hbase + hd) * T_ + tq[r >> 4]) * D + cc * C::EPC);
-      }, lane);
+      entry(2 * pti, tA, sA);
+      entry(2 * pti + 1, tB, sB);
+      const int64_t qrow = (((int64_t)b * Hkv + hkv) * T_ + tA) * G + phc * 16;   // packed row
+      iss.issue(stage, q + qrow * D, tA, tB, G);
+      ++pix;
+      if (++pti == ntile) {
+        pti = 0;
+        if (++phc < NHC) iss.prepare(G - phc * 16, lane);
+      }
     };
-    issue(0, 0);
-    lds_dma_wait();
-    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < NST; ++p)
+      if (p < total) request(sQ[p]);
     for (int ix = 0; ix < total; ++ix) {
-      const int buf = ix & 1;
-      if (ix + 1 < total) issue(ix + 1, buf ^ 1);
+      // tile ix is complete once at most the younger tiles' loads and the
+      // stores of the tiles since its request are outstanding
+      if (ix + NST - 1 < total)
+        vm_wait_steps<(NST - 1) * LT, NSW, NST - 1>(ix);
+      else
+        vm_wait<0>();
+      __syncthreads();
+      const T* tile = sQ[ix % NST];
       const int hc = ix / ntile, ti = ix % ntile;
       int tA, sA, tB, sB;
       entry(2 * ti, tA, sA);
@@ -115,7 +180,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       const bool rok = t >= 0 && g < G;
       Frag<T> qb[KS];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) lds_nrow_frag<T, D>(qb[s], sQ[buf], n, h, s);
+      for (int s = 0; s < KS; ++s) lds_nrow_frag<T, D>(qb[s], tile, n, h, s);
       f32x16 st[2];
       st[0] = zero16();
       st[1] = zero16();
@@ -157,6 +222,9 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) mma32(acc[dt], vf[dt][kk], pf[kk]);
       }
+      // refill the stage once its reads are complete
+      lds_reads_done();
+      if (pix < total) request(sQ[ix % NST]);
       if (rok) {
         const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
@@ -172,9 +240,9 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
           }
         if (h == 0) mlpart[prow] = make_float2(mx, lt);
       }
-      lds_dma_wait();
-      __syncthreads();
     }
+    vm_wait<0>();      // the walk's stores and loads are done before sent and sQ are reused
+    __syncthreads();
   }
 }
 
@@ -356,8 +424,10 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
                    const int32_t* block_offsets, void* o_part, float* ml_part, void* workspace,
                    size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
                    int dtype, void* stream) {
-  NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size) && chunk >= 2, NSA_ERR_SHAPE);
+  NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size) && chunk >= 2 && chunk <= kSelItemMax, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  // the tile loads address a group's Q rows with 32-bit byte offsets
+  NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   NSA_CHECK(workspace_bytes >= nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
   const int n_blk = sel_csr_blocks(T, block_size);
   if (T == 0 || S == 0 || n_blk == 0) return NSA_OK;

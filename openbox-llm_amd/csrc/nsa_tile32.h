@@ -228,7 +228,9 @@ __device__ __forceinline__ void dma_tile(void* lds, SrcFn src, int tid) {
 // wave-uniform; M0 is written here and is used by nothing else in the
 // kernels that call these.
 __device__ __forceinline__ uint32_t lds_addr_uniform(const void* lds) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)lds);
+  // a generic pointer into LDS carries the LDS byte address in its low 32
+  // bits (the aperture is the high half), so truncation is the conversion
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
 }
 __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
@@ -271,12 +273,30 @@ constexpr int dma_uniform_loads() { return (NCHUNK + NTH - 1) / NTH; }
 
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Wait for this wave's LDS operations only (lgkmcnt 0; vmcnt and expcnt at
+// their maxima): a stage's reads are complete before a DMA refills it.
+__device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
 // Wait until at most N vector-memory operations of this wave are outstanding
 // (they complete in issue order); LDS and export counters are not waited on.
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Wait until at most BASE + min(n, K) * STEP vector-memory operations are
+// outstanding; n is wave-uniform and picks one of K + 1 immediates.
+template <int BASE, int STEP, int K>
+__device__ __forceinline__ void vm_wait_steps(int n) {
+  if constexpr (K == 0) {
+    vm_wait<BASE>();
+  } else {
+    if (n >= K)
+      vm_wait<BASE + K * STEP>();
+    else
+      vm_wait_steps<BASE, STEP, K - 1>(n);
+  }
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

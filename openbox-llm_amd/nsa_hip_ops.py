@@ -157,6 +157,19 @@ def transpose_kv(x):
     return xt
 
 
+def pack_heads(x, Hkv):
+    """[B,Hkv*G,T,D] -> [B,Hkv,T,G,D]: the G heads of one query and KV head
+    contiguous, the query-side layout of the selection kernels."""
+    x = _contig(x)
+    B, Hq, T, D = x.shape
+    assert Hq % Hkv == 0, "query heads must be a multiple of the KV heads"
+    G = Hq // Hkv
+    xp = torch.empty(B, Hkv, T, G, D, device=x.device, dtype=x.dtype)
+    _call("nsa_pack_heads", _lib().nsa_pack_heads, L.ptr(x), L.ptr(xp), B, Hkv, G, T, D, L.dtype_code(x),
+          _stream(x))
+    return xp
+
+
 def cast_f32(x, dtype):
     if dtype == torch.float32:
         return x
@@ -378,12 +391,19 @@ def csr_device(block_idx, block_size, n_blk=None, pack_slot=False):
     return q_of_block, offsets, pair_bh, count
 
 
-def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, want_dq=False):
+def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, want_dq=False, qp=None,
+             dop=None):
     """dK, dV (float32) of the selection branch over the block -> query CSR;
     with ``want_dq`` also the dQ partials of every (query, slot, pass) for
-    ``sel_dq_reduce`` (the CSR must then be built with ``pack_slot``)."""
+    ``sel_dq_reduce`` (the CSR must then be built with ``pack_slot``).
+    ``qp`` / ``dop``: ``pack_heads`` copies of q / do (made here when not
+    given)."""
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
+    if qp is None:
+        qp = pack_heads(q, Hkv)
+    if dop is None:
+        dop = pack_heads(do, Hkv)
     idx = block_idx.to(torch.int32).contiguous()
     S = idx.shape[-1]
     if csr is None:
@@ -399,7 +419,7 @@ def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, w
         dq_part = torch.empty(B, Hkv, T, ns, Hq // Hkv, D, device=q.device, dtype=q.dtype)
     ws_bytes = int(_lib().nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(coff),
+    _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(qp), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(dop), L.ptr(coff),
           L.ptr(dot), L.ptr(q_of_block), int(want_dq), L.ptr(offsets),
           L.ptr(count), L.ptr(dk), L.ptr(dv), L.ptr(dq_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
           SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
@@ -419,9 +439,10 @@ def sel_dq_reduce(block_idx, dq_part, dq_acc, block_size, dtype):
     return out
 
 
-def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None):
+def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
     """Block-outer selection forward -> (o, lse[f32], csr); ``csr`` is the
-    packed block -> query CSR (built here when not given)."""
+    packed block -> query CSR (built here when not given), ``qp`` the
+    ``pack_heads`` copy of q (made here when not given)."""
     check_qkv(q, k, v)
     q, k = _contig(q), _contig(k)
     B, Hq, T, D = q.shape
@@ -435,6 +456,8 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None):
         csr = csr_device(idx, block_size, pack_slot=True)
     if vt is None:
         vt = transpose_kv(v)
+    if qp is None:
+        qp = pack_heads(q, Hkv)
     q_of_block, offsets, _, _ = csr
     ns = int(_lib().nsa_sel_partial_slots(S, block_size))
     G = Hq // Hkv
@@ -442,7 +465,7 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None):
     ml_part = torch.empty(B, Hkv, T, ns, G, 2, device=q.device, dtype=torch.float32)
     ws_bytes = int(_lib().nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-    _call("fwd[sel]", _lib().nsa_sel_fwd_bo, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(q_of_block), L.ptr(offsets),
+    _call("fwd[sel]", _lib().nsa_sel_fwd_bo, L.ptr(qp), L.ptr(k), L.ptr(vt), L.ptr(q_of_block), L.ptr(offsets),
           L.ptr(o_part), L.ptr(ml_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size, SEL_DKDV_CHUNK,
           L.dtype_code(q), _stream(q))
     o = torch.empty_like(q)
@@ -597,14 +620,17 @@ class NSAFusedHIP(torch.autograd.Function):
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
         idx = block_idx.to(torch.int32).contiguous()
         if idx.shape[-1] > 0:
-            o_s, lse_s, csr = sel_fwd_fsa(q, ks, vs, idx, geom.sel_block)
+            qp = pack_heads(q, ks.shape[1])
+            o_s, lse_s, csr = sel_fwd_fsa(q, ks, vs, idx, geom.sel_block, qp=qp)
         else:
+            qp = torch.empty(0, device=q.device, dtype=q.dtype)
             o_s = torch.zeros_like(q)
             lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
             csr = ()
         o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
         out = gate_fwd(gate, o_c, o_s, o_w)
-        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, *csr)
+        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, qp,
+                              *csr)
         ctx.geom = geom
         ctx.T = T
         ctx.pooled = pooled
@@ -614,7 +640,7 @@ class NSAFusedHIP(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, _didx):
         (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w,
-         lse_c, lse_s, lse_w, *csr) = ctx.saved_tensors
+         lse_c, lse_s, lse_w, qp, *csr) = ctx.saved_tensors
         geom, T = ctx.geom, ctx.T
         dout = _contig(dout)
         dtype = q.dtype
@@ -643,7 +669,7 @@ class NSAFusedHIP(torch.autograd.Function):
         # window / compression dQ and writes the input dtype
         if idx.shape[-1] > 0:
             dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                         csr=tuple(csr), want_dq=True)
+                                         csr=tuple(csr), want_dq=True, qp=qp)
             dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
         else:
             dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)

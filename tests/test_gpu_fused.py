@@ -10,6 +10,7 @@ choice and the block -> query CSR against the CPU oracle.
   equal to the oracle's on every row whose S-th / (S+1)-th oracle scores are
   not a near tie.
 * CSR: bit-exact equal to the oracle's restatement of nsa_fsa.py:14-64.
+* nsa_pack_heads: the packed query-side layout of the selection kernels.
 """
 
 import pytest
@@ -183,6 +184,20 @@ def test_csr_bit_exact():
         assert torch.equal(q_g.cpu(), q_ref)
         assert torch.equal(off_g.cpu(), off_ref)
         assert torch.equal(bh_g.cpu(), bh_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_pack_heads_layout(dtype):
+    """nsa_pack_heads: [B, Hkv*G, T, D] -> [B, Hkv, T, G, D], bit-exact (a pure
+    permutation), including a group wider than one 16-head chunk."""
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    for (B, Hkv, G, T, D) in ((2, 2, 4, 37, 32), (1, 1, 20, 64, 128), (1, 4, 16, 5, 16)):
+        x = randn((B, Hkv * G, T, D), 7, torch.float32).to(dtype).to(dev)
+        xp = ops.pack_heads(x, Hkv)
+        ref = x.view(B, Hkv, G, T, D).permute(0, 1, 3, 2, 4).contiguous()
+        assert xp.shape == (B, Hkv, T, G, D)
+        assert torch.equal(xp, ref)
 
 
 def test_csr_trailing_partial_block():
