@@ -85,8 +85,8 @@ int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
 /* [B][Hkv*G][T][D] -> [B][Hkv][T][G][D]: the query-side layout the selection
  * kernels read (the G heads of one query and KV head contiguous).  No
  * reference counterpart: the reference reads [B][H][T][D] directly
- * (nsa_selection_kernel.py:186-189).  D * sizeof(dtype) must be a multiple
- * of 16; src and dst must not overlap. */
+ * (nsa_selection_kernel.py:186-189).  D * sizeof(dtype) must be 16 bytes
+ * times a power of two; src and dst must not overlap. */
 int nsa_pack_heads(const void* src, void* dst, int B, int Hkv, int G, int T, int D, int dtype, void* stream);
 
 /* ---- selection branch ------------------------------------------------------

@@ -172,18 +172,20 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   }
 }
 
-// [B, Hkv*G, T, D] -> [B, Hkv, T, G, D] in 16-byte chunks (CH per row):
-// thread e writes chunk e of the destination.
+// [B, Hkv*G, T, D] -> [B, Hkv, T, G, D] in 16-byte chunks, 2^cs per row:
+// workgroup r = (b, hkv, t) writes the G contiguous rows of query t.
 __global__ __launch_bounds__(256) void k_pack_heads(const uint4* __restrict__ src, uint4* __restrict__ dst, int G,
-                                                    int T, int CH, int64_t total) {
-  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
-    const int c = (int)(e % CH);
-    int64_t r = e / CH;                    // destination row (bh, t, g)
-    const int g = (int)(r % G);
-    r /= G;
-    const int t = (int)(r % T);
+                                                    int T, int cs, int64_t rows) {
+  const int n = G << cs;
+  for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
     const int64_t bh = r / T;
-    dst[e] = src[((bh * G + g) * T + t) * CH + c];
+    const int t = (int)(r - bh * T);
+    const uint4* sp = src + ((bh * G * T + t) << cs);   // head 0 of the group
+    uint4* dp = dst + r * n;
+    for (int i = threadIdx.x; i < n; i += 256) {
+      const int g = i >> cs, c = i & ((1 << cs) - 1);
+      dp[i] = sp[(((int64_t)g * T) << cs) + c];
+    }
   }
 }
 
@@ -310,10 +312,13 @@ int nsa_pack_heads(const void* src, void* dst, int B, int Hkv, int G, int T, int
   const int bytes = D * (dtype == NSA_BF16 ? 2 : 4);
   NSA_CHECK(D > 0 && bytes % 16 == 0, NSA_ERR_SHAPE);
   NSA_CHECK(src != dst, NSA_ERR_ARG);
-  const int64_t total = (int64_t)B * Hkv * G * T * (bytes / 16);
-  if (total == 0) return NSA_OK;
+  const int ch = bytes / 16;
+  NSA_CHECK((ch & (ch - 1)) == 0 && (int64_t)G * ch < (1ll << 31), NSA_ERR_SHAPE);
+  const int64_t rows = (int64_t)B * Hkv * T;
+  if (rows == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  k_pack_heads<<<grid_for(total), 256, 0, s>>>((const uint4*)src, (uint4*)dst, G, T, bytes / 16, total);
+  const int grid = rows < 65536 ? (int)rows : 65536;
+  k_pack_heads<<<grid, 256, 0, s>>>((const uint4*)src, (uint4*)dst, G, T, __builtin_ctz(ch), rows);
   return nsa_launch_status();
 }
 

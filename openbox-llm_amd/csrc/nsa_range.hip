@@ -74,6 +74,28 @@ __device__ __forceinline__ void dma_key_cols(T* lds, const T* src, int kb, int L
   }, tid);
 }
 
+// The same tiles through the asm DMA with a uniform per-wave load count
+// (dma_tile_uniform), for partial vmcnt waits over several stages.
+template <typename T, int D>
+__device__ __forceinline__ void dma_key_rows_u(T* lds, const T* src, int kb, int Lk, int tid) {
+  using C = Tile32<T, D>;
+  dma_tile_uniform<256, C::ROW_CHUNKS>(lds, [&](int P) {
+    int r, c;
+    row_chunk<T, D>(P, r, c);
+    const int key = kb + r < Lk ? kb + r : Lk - 1;
+    return (const void*)(src + (int64_t)key * D + c * C::EPC);
+  }, tid);
+}
+template <typename T, int D>
+__device__ __forceinline__ void dma_key_cols_u(T* lds, const T* src, int kb, int Lp, int tid) {
+  using C = Tile32<T, D>;
+  dma_tile_uniform<256, C::COL_CHUNKS>(lds, [&](int P) {
+    int d, c;
+    col_chunk<T, D>(P, d, c);
+    return (const void*)(src + (int64_t)d * Lp + kb + c * C::EPC);
+  }, tid);
+}
+
 // Workgroup / wave query and key ranges of a range launch.
 struct RangeSpan {
   int klo, khi;     // union of visible keys of the workgroup's queries
@@ -216,8 +238,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                      int Lp, int nqt, int window, int cl, int cd, float sl2) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
-  __shared__ __align__(16) T sK[2][C::ROW_ELEMS];
-  __shared__ __align__(16) T sV[2][C::COL_ELEMS];
+  constexpr int NST = 4;   // key tiles in flight + 1
+  __shared__ __align__(16) T sK[NST][C::ROW_ELEMS];
+  __shared__ __align__(16) T sV[NST][C::COL_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   // window: neighbouring query tiles (which share keys) on one XCD;
   // compression: every tile reads the same small key set and the work grows
@@ -263,27 +286,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const int kt0 = sp.klo & ~31;
   const int ntile = sp.khi >= sp.klo ? (sp.khi - kt0) / 32 + 1 : 0;
-  if (ntile > 0) {
-    dma_key_rows<T, D>(sK[0], kbase, kt0, Lk, tid);
-    dma_key_cols<T, D>(sV[0], vtbase, kt0, Lp, tid);
-  }
-  lds_dma_wait();
-  __syncthreads();
-  for (int it = 0; it < ntile; ++it) {
+  // the Q fragments complete before the walk (whose loads the compiler does
+  // not see: a wait it placed in the loop would drain the tiles in flight)
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(qf[nt][s]);
+  constexpr int LT = dma_uniform_loads<256, C::ROW_CHUNKS>() + dma_uniform_loads<256, C::COL_CHUNKS>();
+  key_pipeline<NST, LT>(ntile, [&](int i) {
+    dma_key_rows_u<T, D>(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
+    dma_key_cols_u<T, D>(sV[i % NST], vtbase, kt0 + 32 * i, Lp, tid);
+  }, [&](int it) {
     const int kb = kt0 + 32 * it;
-    const int buf = it & 1;
-    if (it + 1 < ntile) {
-      dma_key_rows<T, D>(sK[buf ^ 1], kbase, kb + 32, Lk, tid);
-      dma_key_cols<T, D>(sV[buf ^ 1], vtbase, kb + 32, Lp, tid);
-    }
     // every wave takes every tile of the workgroup range (the waves' own ranges
     // differ by at most a few queries); tiles inside the wave's fully visible
     // span skip the per-element mask
     const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
-    fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[buf], sV[buf], kb, mask, lo, hi, sl2, n, h);
-    lds_dma_wait();
-    __syncthreads();
-  }
+    fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[it % NST], sV[it % NST], kb, mask, lo, hi, sl2, n, h);
+  });
 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
@@ -376,9 +396,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                     int window, int cl, int cd, float sl2, float scale) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
-  __shared__ __align__(16) T sK[2][C::ROW_ELEMS];
-  __shared__ __align__(16) T sV[2][C::ROW_ELEMS];
-  __shared__ __align__(16) T sKt[2][C::COL_ELEMS];
+  constexpr int NST = 3;   // key tiles in flight + 1
+  __shared__ __align__(16) T sK[NST][C::ROW_ELEMS];
+  __shared__ __align__(16) T sV[NST][C::ROW_ELEMS];
+  __shared__ __align__(16) T sKt[NST][C::COL_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int64_t wg = mode == NSA_MODE_COMPRESS ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, gridDim.x);
   int qt = (int)(wg % nqt);
@@ -426,26 +447,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const T* kbase = k + (int64_t)bh * Lk * D;
   const T* vbase = v + (int64_t)bh * Lk * D;
   const T* ktbase = kt + (int64_t)bh * D * Lp;
-  if (ntile > 0) {
-    dma_key_rows<T, D>(sK[0], kbase, kt0, Lk, tid);
-    dma_key_rows<T, D>(sV[0], vbase, kt0, Lk, tid);
-    dma_key_cols<T, D>(sKt[0], ktbase, kt0, Lp, tid);
-  }
-  lds_dma_wait();
-  __syncthreads();
-  for (int it = 0; it < ntile; ++it) {
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(qf[nt][s]), settle(df[nt][s]);
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(c[nt]), "+v"(dlt[nt]));
+  constexpr int LT = 2 * dma_uniform_loads<256, C::ROW_CHUNKS>() + dma_uniform_loads<256, C::COL_CHUNKS>();
+  key_pipeline<NST, LT>(ntile, [&](int i) {
+    dma_key_rows_u<T, D>(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
+    dma_key_rows_u<T, D>(sV[i % NST], vbase, kt0 + 32 * i, Lk, tid);
+    dma_key_cols_u<T, D>(sKt[i % NST], ktbase, kt0 + 32 * i, Lp, tid);
+  }, [&](int it) {
     const int kb = kt0 + 32 * it;
-    const int buf = it & 1;
-    if (it + 1 < ntile) {
-      dma_key_rows<T, D>(sK[buf ^ 1], kbase, kb + 32, Lk, tid);
-      dma_key_rows<T, D>(sV[buf ^ 1], vbase, kb + 32, Lk, tid);
-      dma_key_cols<T, D>(sKt[buf ^ 1], ktbase, kb + 32, Lp, tid);
-    }
     const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
-    dq_tile<T, D, NT>(acc, qf, df, sK[buf], sV[buf], sKt[buf], kb, mask, lo, hi, c, dlt, sl2, n, h);
-    lds_dma_wait();
-    __syncthreads();
-  }
+    dq_tile<T, D, NT>(acc, qf, df, sK[it % NST], sV[it % NST], sKt[it % NST], kb, mask, lo, hi, c, dlt, sl2, n,
+                      h);
+  });
 
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {

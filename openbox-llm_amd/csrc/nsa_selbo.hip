@@ -274,11 +274,44 @@ __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
   *reinterpret_cast<f32x4*>(p + 4) = (f32x4){x[4], x[5], x[6], x[7]};
 }
 
+// 8 consecutive elements of a row as loaded (one 16-byte load for bf16, two
+// for float), converted at use.
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
+  __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
+    u32x4 u = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = ok ? u[i] : 0u;
+    v = __builtin_bit_cast(bf16x8, u);
+  }
+};
+template <> struct Raw8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+  __device__ __forceinline__ void keep_if(bool ok) {
+    u32x4 ua = __builtin_bit_cast(u32x4, a), ub = __builtin_bit_cast(u32x4, b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ua[i] = ok ? ua[i] : 0u, ub[i] = ok ? ub[i] : 0u;
+    a = __builtin_bit_cast(f32x4, ua);
+    b = __builtin_bit_cast(f32x4, ub);
+  }
+};
+
 // Both reductions below take one thread per 8 elements of a row, rows ordered
-// (b, hkv, t, g) so that a wave reads contiguous partial rows, and go through
-// the slots kSlotBatch at a time with every load of a batch issued before any
-// is used (slots that do not count get weight 0 and read slot 0).
-constexpr int kSlotBatch = 8;
+// (b, hkv, t, g) so that a wave reads contiguous partial rows.  Every slot's
+// partial is loaded -- the buffers hold all NS slots of a row, and a slot
+// without a pair was never written -- kSlotBatch at a time, with all loads of
+// a batch issued together and none of their addresses depending on the block
+// indices; a slot that does not count is then replaced by zeros (bit for bit)
+// and weight 0, so whatever an unwritten slot holds never reaches a result.
+constexpr int kSlotBatch = 16;
 
 // o[row] = sum_slots exp2(m - M) l O_slot / sum exp2(m - M) l over the valid
 // slots, lse = (M + log2 L) ln 2, with a running maximum M across batches.
@@ -302,25 +335,21 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
     float M = kNegInfS, Ls = 0.0f;
     for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
       float2 ml[kSlotBatch];
-      float x[kSlotBatch][8];
+      Raw8<T> x[kSlotBatch];
       bool ok[kSlotBatch];
       int jv[kSlotBatch];
-      // every load of the batch is unconditional (clamped) so that none waits
-      // on a branch: block indices first, then the partials
-#pragma unroll
-      for (int k = 0; k < kSlotBatch; ++k) jv[k] = irow[(s0 + k < NS ? s0 + k : NS - 1) / nsub];
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
-        const int sl = s0 + k;
-        ok[k] = (sl < NS) & sel_slot_valid(jv[k], n_csr, L, t);
-        const int64_t pr = (pbase + (ok[k] ? sl : 0)) * G + g;
+        const int sl = s0 + k < NS ? s0 + k : NS - 1;
+        const int64_t pr = (pbase + sl) * G + g;
+        jv[k] = irow[sl / nsub];
         ml[k] = mlpart[pr];
-        load8(opart + pr * D + 8 * c, x[k]);
+        x[k].load(opart + pr * D + 8 * c);
       }
       float bm = M;
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
-        ok[k] = ok[k] && ml[k].y > 0.0f;
+        ok[k] = (s0 + k < NS) && sel_slot_valid(jv[k], n_csr, L, t) && ml[k].y > 0.0f;
         bm = ok[k] ? fmaxf(bm, ml[k].x) : bm;
       }
       if (bm == kNegInfS) continue;   // nothing valid yet
@@ -331,9 +360,10 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
         const float wk = ok[k] ? fast_exp2(ml[k].x - bm) * ml[k].y : 0.0f;
+        x[k].keep_if(ok[k]);
         Ls += wk;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += wk * x[k][i];
+        for (int i = 0; i < 8; ++i) acc[i] += wk * x[k].get(i);
       }
       M = bm;
     }
@@ -373,21 +403,20 @@ __global__ __launch_bounds__(256) void k_sel_dq_reduce(const int32_t* __restrict
       for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
     }
     for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
-      float x[kSlotBatch][8];
-      bool ok[kSlotBatch];
+      Raw8<T> x[kSlotBatch];
       int jv[kSlotBatch];
 #pragma unroll
-      for (int k = 0; k < kSlotBatch; ++k) jv[k] = irow[(s0 + k < NS ? s0 + k : NS - 1) / nsub];
-#pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
-        const int sl = s0 + k;
-        ok[k] = (sl < NS) & sel_slot_valid(jv[k], n_csr, L, t);
-        load8(dqpart + ((pbase + (ok[k] ? sl : 0)) * G + g) * D + 8 * c, x[k]);
+        const int sl = s0 + k < NS ? s0 + k : NS - 1;
+        jv[k] = irow[sl / nsub];
+        x[k].load(dqpart + ((pbase + sl) * G + g) * D + 8 * c);
       }
 #pragma unroll
-      for (int k = 0; k < kSlotBatch; ++k)
+      for (int k = 0; k < kSlotBatch; ++k) {
+        x[k].keep_if((s0 + k < NS) && sel_slot_valid(jv[k], n_csr, L, t));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += ok[k] ? x[k][i] : 0.0f;
+        for (int i = 0; i < 8; ++i) acc[i] += x[k].get(i);
+      }
     }
     store8(dq_out + orow * D + 8 * c, acc);
   }

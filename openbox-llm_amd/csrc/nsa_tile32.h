@@ -299,6 +299,29 @@ __device__ __forceinline__ void vm_wait_steps(int n) {
   }
 }
 
+// Key-tile pipeline of the query-outer kernels: NST stages, tiles 0 ..
+// NST-2 requested up front; iteration i waits for tile i (the NST-2 younger
+// tiles stay in flight), passes the workgroup barrier -- after which no wave
+// reads tile i-1 -- refills that stage with tile i + NST - 1 and computes
+// tile i.  LT: vector-memory loads one wave issues per tile (the loop issues
+// no other vector-memory operation).
+template <int NST, int LT, typename Req, typename Body>
+__device__ __forceinline__ void key_pipeline(int ntile, Req request, Body body) {
+  static_assert(NST >= 2 && (NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
+#pragma unroll
+  for (int p = 0; p < NST - 1; ++p)
+    if (p < ntile) request(p);
+  for (int it = 0; it < ntile; ++it) {
+    if (it + NST - 2 < ntile)
+      vm_wait<(NST - 2) * LT>();
+    else
+      vm_wait<0>();
+    __syncthreads();
+    if (it + NST - 1 < ntile) request(it + NST - 1);
+    body(it);
+  }
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 }  // namespace nsa

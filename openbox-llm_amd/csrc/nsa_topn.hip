@@ -4,7 +4,7 @@
 // A workgroup of 4 waves takes 8 consecutive queries of one (b, hkv); a wave
 // holds the Q fragments of its 2 queries x 16 heads (a 32-row MFMA operand)
 // and walks the pooled tokens the group's last query sees, 32 per tile, the
-// tiles shared through LDS (direct global -> LDS loads, double-buffered):
+// tiles shared through LDS (direct global -> LDS loads, kImpStages deep):
 //
 //  1. S = Q K_cmp^T on 32x32 MFMAs (rows on M, tokens on N); p_cmp =
 //     exp2(S * scale*log2e - lse_cmp*log2e) with lse_cmp from the compression
@@ -30,10 +30,38 @@ __device__ __forceinline__ uint64_t topn_key(float x, int j) {
   return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)j);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((unsigned)(v & 0xFFFFFFFFu), m, kWave);
-  const uint32_t hi = __shfl_xor((unsigned)(v >> 32), m, kWave);
-  return ((uint64_t)hi << 32) | lo;
+// Maximum of a u64 over the wave, in every lane: within rows of 16 lanes by
+// DPP (quad swaps, half-row and row mirrors), across rows by the gfx950 row
+// swaps (permlane16: row pairs, permlane32: wave halves) -- register moves
+// only, no LDS round trips.
+template <int CTRL>
+__device__ __forceinline__ uint64_t max_dpp(uint64_t k) {
+  const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+  const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xF, 0xF, false);
+  const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xF, 0xF, false);
+  const uint64_t o = ((uint64_t)ohi << 32) | olo;
+  return o > k ? o : k;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
+  k = max_dpp<0xB1>(k);    // quad_perm [1,0,3,2]
+  k = max_dpp<0x4E>(k);    // quad_perm [2,3,0,1]
+  k = max_dpp<0x141>(k);   // row_half_mirror
+  k = max_dpp<0x140>(k);   // row_mirror: every lane holds its row's maximum
+  {
+    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    const uint64_t a = ((uint64_t)ph[0] << 32) | pl[0], b = ((uint64_t)ph[1] << 32) | pl[1];
+    k = a > b ? a : b;     // rows 2r and 2r+1 hold their pair's maximum
+  }
+  {
+    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
+    const auto pl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto ph = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    const uint64_t a = ((uint64_t)ph[0] << 32) | pl[0], b = ((uint64_t)ph[1] << 32) | pl[1];
+    k = a > b ? a : b;     // both halves: the wave's maximum
+  }
+  return k;
 }
 
 __device__ __forceinline__ void wave_fence() {
@@ -42,6 +70,7 @@ __device__ __forceinline__ void wave_fence() {
 }
 
 constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
+constexpr int kImpStages = 4;             // K tiles in flight + 1
 constexpr int kImpQPB = 4 * kImpQPW;      // queries per workgroup
 
 // last pooled token visible to t (-1: none)
@@ -51,17 +80,23 @@ __device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) 
   return hi < n_cmp - 1 ? hi : n_cmp - 1;
 }
 
-// LDS: K tiles [2][32][D], per-wave token scratch [4][2][32], block sums [8][nsp]
+// x / 2^sh when sh >= 0 (x >= 0), else x / d
+__device__ __forceinline__ int div_sh(int x, int d, int sh) { return sh >= 0 ? x >> sh : x / d; }
+
+// LDS: K tiles [kImpStages][32][D], per-wave token scratch [4][2][32], block
+// sums [8][nsp].  cd_sh / ls_sh: log2 of cd / ls when they are powers of two,
+// else -1 (the block fold then divides).
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
                                                   const float* __restrict__ lse, int32_t* __restrict__ out_idx,
                                                   float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
                                                   int n_slc, int nsp, int S, int cl, int cd, int ls, int force_init,
-                                                  int n_local, int nqb, float sl2) {
+                                                  int n_local, int nqb, int cd_sh, int ls_sh, float sl2) {
   using C = Tile32<T, D>;
+  constexpr int NST = kImpStages;
   extern __shared__ __align__(16) char smem[];
-  T* sK = reinterpret_cast<T*>(smem);                                   // [2][ROW_ELEMS]
-  float* stok = reinterpret_cast<float*>(sK + 2 * C::ROW_ELEMS);        // [4][2][32]
+  T* sK = reinterpret_cast<T*>(smem);                                   // [NST][ROW_ELEMS]
+  float* stok = reinterpret_cast<float*>(sK + NST * C::ROW_ELEMS);      // [4][2][32]
   float* sblk = stok + 4 * kImpQPW * 32;                                 // [8][nsp]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -81,8 +116,8 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
 
   for (int i = tid; i < kImpQPB * nsp; i += 256) sblk[i] = 0.0f;
   const T* kbase = kc + (int64_t)bh * n_cmp * D;
-  auto load_tile = [&](int buf, int kt) {
-    dma_tile<256, C::ROW_CHUNKS>(sK + buf * C::ROW_ELEMS, [&](int P) {
+  auto load_tile = [&](int kt) {
+    dma_tile_uniform<256, C::ROW_CHUNKS>(sK + (kt % NST) * C::ROW_ELEMS, [&](int P) {
       int r, cc;
       nrow_chunk<T, D>(P, r, cc);
       int tok = kt * 32 + r;
@@ -90,7 +125,6 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       return (const void*)(kbase + (int64_t)tok * D + cc * C::EPC);
     }, tid);
   };
-  if (ntile > 0) load_tile(0, 0);
 
   // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
   float* my_tok = stok + w * kImpQPW * 32;
@@ -117,13 +151,20 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       lse2[r] = ok ? lse[((int64_t)b * Hq + hkv * G + he) * T_ + te] * kLog2e : __builtin_inff();
     }
   };
-  if (NHC == 1) load_rows(0);
-  for (int kt = 0; kt < ntile; ++kt) {
-    const int buf = kt & 1;
-    lds_dma_wait();
-    __syncthreads();
-    if (kt + 1 < ntile) load_tile(buf ^ 1, kt + 1);
-    const T* tile = sK + buf * C::ROW_ELEMS;
+  if (NHC == 1) {
+    load_rows(0);
+    // complete these loads before the walk, whose loads the compiler does
+    // not see (a wait it placed in the loop would drain the tiles in flight);
+    // wider groups load their rows inside the loop, and the compiler's waits
+    // for those only lengthen the walk's
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(qf[s]);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(lse2[r]));
+  }
+  __syncthreads();   // sblk cleared
+  key_pipeline<NST, dma_uniform_loads<256, C::ROW_CHUNKS>()>(ntile, load_tile, [&](int kt) {
+    const T* tile = sK + (kt % NST) * C::ROW_ELEMS;
     const int tok = kt * 32 + n;
     for (int hc = 0; hc < NHC; ++hc) {
       if (NHC > 1) load_rows(hc);   // groups wider than 16 heads: one chunk at a time
@@ -161,14 +202,15 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     // lane = (query, block of the tile's span)
     const int i0 = kt * 32;
     const int i1 = i0 + 31 < n_cmp - 1 ? i0 + 31 : n_cmp - 1;
-    const int jlo = (i0 * cd) / ls;
-    int jhi = (i1 * cd + cl - 1) / ls;
+    const int jlo = div_sh(i0 * cd, ls, ls_sh);
+    int jhi = div_sh(i1 * cd + cl - 1, ls, ls_sh);
     jhi = jhi < n_slc - 1 ? jhi : n_slc - 1;
     const int nj = jhi - jlo + 1;
+    static_assert(kImpQPW == 2, "lane -> (query, block) split below assumes two queries");
     for (int u = lane; u < kImpQPW * nj; u += kWave) {
-      const int qi = u / nj, j = jlo + u % nj;
-      int a_i = j * ls - cl + 1 <= 0 ? 0 : (j * ls - cl + 1 + cd - 1) / cd;
-      int b_i = ((j + 1) * ls - 1) / cd;
+      const int qi = u >= nj ? 1 : 0, j = jlo + u - qi * nj;
+      int a_i = j * ls - cl + 1 <= 0 ? 0 : div_sh(j * ls - cl + 1 + cd - 1, cd, cd_sh);
+      int b_i = div_sh((j + 1) * ls - 1, cd, cd_sh);
       a_i = a_i > i0 ? a_i : i0;
       b_i = b_i < i1 ? b_i : i1;
       float sj = my_blk[qi * nsp + j];
@@ -180,7 +222,7 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       my_blk[qi * nsp + j] = sj;
     }
     wave_fence();
-  }
+  });
   __syncthreads();
 
   // per query of this wave: scores, masking and forcing, then top-S
@@ -212,12 +254,7 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     uint64_t mine = lane_best();
     int32_t* orow = out_idx + r * S;
     for (int s = 0; s < S; ++s) {
-      uint64_t bk = mine;
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = shfl_xor_u64(bk, m);
-        bk = o > bk ? o : bk;
-      }
+      const uint64_t bk = wave_max_u64(mine);
       const int jw = (int)(0xFFFFFFFFu - (uint32_t)(bk & 0xFFFFFFFFu));
       if (lane == 0) orow[s] = jw;
       if ((jw & (kWave - 1)) == lane) {
@@ -246,13 +283,15 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   NSA_CHECK(n_slc <= 64 * 64, NSA_ERR_SHAPE);
   if (T == 0 || n_slc == 0) return NSA_OK;
   const int nsp = n_slc + 1;   // per-query block-sum pitch (odd: spreads the 8 queries over banks)
-  const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)2 * 32 * D;
+  const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)kImpStages * 32 * D;
   const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 + (size_t)kImpQPB * nsp);
   NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
   const int nqb = (T + kImpQPB - 1) / kImpQPB;
   const int64_t grid = (int64_t)B * Hkv * nqb;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
+  const int cd_sh = (cmp_stride & (cmp_stride - 1)) == 0 ? __builtin_ctz(cmp_stride) : -1;
+  const int ls_sh = (sel_block & (sel_block - 1)) == 0 ? __builtin_ctz(sel_block) : -1;
   hipStream_t s = (hipStream_t)stream;
   // more than 64 KB of dynamic LDS must be allowed per kernel
 #define NSA_TOPN_LDS(K) (lds <= 65536 || hipFuncSetAttribute((const void*)(K), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
@@ -264,12 +303,12 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
       k_imp_topn<bf16, DD><<<(unsigned)grid, 256, lds, s>>>((const bf16*)q, (const bf16*)k_cmp, lse_cmp,      \
                                                             block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp, S, \
                                                             cmp_block, cmp_stride, sel_block, force_init,       \
-                                                            n_local, nqb, sl2);                                 \
+                                                            n_local, nqb, cd_sh, ls_sh, sl2);                                 \
     else                                                                                                        \
       k_imp_topn<float, DD><<<(unsigned)grid, 256, lds, s>>>((const float*)q, (const float*)k_cmp, lse_cmp,   \
                                                              block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp,  \
                                                              S, cmp_block, cmp_stride, sel_block, force_init,   \
-                                                             n_local, nqb, sl2);                                \
+                                                             n_local, nqb, cd_sh, ls_sh, sl2);                                \
     break;
     NSA_TOPN_CASE(16)
     NSA_TOPN_CASE(32)
