@@ -179,10 +179,17 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
                   void* stream);
 
 /* Backward dQ of the range branches (query-side half of
- * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426). */
+ * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426): dq (float32)
+ * receives this branch's dQ, added to its contents when `accumulate`.
+ * With sel_part (nullable) the call instead finishes the rows and writes
+ * dq_out in the input dtype: dq_out = (dq if accumulate) + this branch's dQ +
+ * the selection dQ partials of nsa_sel_dkdv for the valid slots of sel_idx
+ * ([B][Hkv][T][S] block indices of block size sel_block) -- the role of
+ * nsa_sel_dq_reduce folded into this kernel; dq is then only read. */
 int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
                  const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
-                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                 const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
                  void* stream);
 
 /* Backward dK/dV of the range branches (key-outer; the key-side half of

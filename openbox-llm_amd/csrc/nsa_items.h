@@ -47,7 +47,7 @@ static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __rest
 // Selection blocks of the CSR consumed by the block-outer kernels: every
 // block holding a key, the trailing partial one included (the forward attends
 // to it when selected).
-static inline int sel_csr_blocks(int T, int block_size) { return (T + block_size - 1) / block_size; }
+__host__ __device__ inline int sel_csr_blocks(int T, int block_size) { return (T + block_size - 1) / block_size; }
 
 static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size, int chunk) {
   const size_t nb = (size_t)B * Hkv * sel_csr_blocks(T, block_size);
@@ -71,6 +71,12 @@ __host__ __device__ inline int sel_slot_bits(int S) {
   int b = 0;
   while ((1 << b) < S) ++b;
   return b;
+}
+
+// Slot of a selected block j in row t is valid (has a CSR pair) iff
+// 0 <= j < n_csr and j * L <= t.
+__device__ __forceinline__ bool sel_slot_valid(int j, int n_csr, int L, int t) {
+  return j >= 0 && j < n_csr && (int64_t)j * L <= t;
 }
 
 }  // namespace nsa

@@ -16,6 +16,7 @@
 //             dQ^T += K^T dS^T
 // Key rows of K / V are read through perm32 so that the accumulator registers
 // line up with the next contraction's operand slots (nsa_tile32.h).
+#include "nsa_items.h"
 #include "nsa_launch.h"
 #include "nsa_tile32.h"
 
@@ -393,13 +394,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                     const float* __restrict__ dot,
                                                     const float* __restrict__ rowscale, float* __restrict__ dq,
                                                     int accumulate, int Hq, int Hkv, int T_, int Lk, int Lp, int nqt,
-                                                    int window, int cl, int cd, float sl2, float scale) {
+                                                    int window, int cl, int cd, float sl2, float scale,
+                                                    const T* __restrict__ sel_part, const int32_t* __restrict__ sel_idx,
+                                                    T* __restrict__ dq_out, int S, int sel_L) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 3;   // key tiles in flight + 1
-  __shared__ __align__(16) T sK[NST][C::ROW_ELEMS];
-  __shared__ __align__(16) T sV[NST][C::ROW_ELEMS];
-  __shared__ __align__(16) T sKt[NST][C::COL_ELEMS];
+  // one LDS buffer: the key stages during the walk, then (finishing rows)
+  // each wave's float dQ tile [32][D + 4]
+  constexpr int FIN_PITCH = D + 4;
+  constexpr int STAGE_BYTES = NST * (2 * C::ROW_ELEMS + C::COL_ELEMS) * (int)sizeof(T);
+  constexpr int FIN_BYTES = 4 * 32 * FIN_PITCH * (int)sizeof(float);
+  __shared__ __align__(16) char smem[STAGE_BYTES > FIN_BYTES ? STAGE_BYTES : FIN_BYTES];
+  T (*sK)[C::ROW_ELEMS] = reinterpret_cast<T (*)[C::ROW_ELEMS]>(smem);
+  T (*sV)[C::ROW_ELEMS] = reinterpret_cast<T (*)[C::ROW_ELEMS]>(smem + NST * C::ROW_ELEMS * sizeof(T));
+  T (*sKt)[C::COL_ELEMS] = reinterpret_cast<T (*)[C::COL_ELEMS]>(smem + 2 * NST * C::ROW_ELEMS * sizeof(T));
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   const int64_t wg = mode == NSA_MODE_COMPRESS ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, gridDim.x);
   int qt = (int)(wg % nqt);
@@ -465,6 +474,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                       h);
   });
 
+  if (sel_part != nullptr) {
+    // finish the rows: dq_out = (dq if accumulate) + this branch's dQ + the
+    // selection dQ partials of the row's valid slots (nsa_sel_dkdv's layout
+    // [B][Hkv][T][NS][G][D]); the wave's tile goes through LDS so that every
+    // partial is read as whole 16-byte row chunks
+    static_assert(NT == 1, "one 32-row tile per wave is staged");
+    __syncthreads();   // the key stages are free
+    float* fin = reinterpret_cast<float*>(smem) + w * 32 * FIN_PITCH;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * dt + 8 * g4 + 4 * h;
+        if (D % 32 == 0 || d < D)
+          *reinterpret_cast<f32x4*>(fin + n * FIN_PITCH + d) =
+              (f32x4){acc[dt][0][4 * g4], acc[dt][0][4 * g4 + 1], acc[dt][0][4 * g4 + 2], acc[dt][0][4 * g4 + 3]} *
+              scale;
+      }
+    __syncthreads();
+    constexpr int CPR = D / 8, RPI = 64 / CPR;   // 8-element chunks per row, rows per pass
+    const int c8 = lane % CPR, rsub = lane / CPR;
+    const int nsub = sel_passes(sel_L), NS = S * nsub, n_csr = sel_csr_blocks(T_, sel_L);
+    const int G = mp.G;
+    for (int r0 = 0; r0 < 32; r0 += RPI) {
+      const int r = r0 + rsub;
+      const int t = tw0 + (r >> 4);
+      const int gl = mp.hc * 16 + (r & 15);   // head within the group
+      if (t >= T_ || gl >= G) continue;
+      const int64_t orow = ((int64_t)mp.b * Hq + mp.hkv * G + gl) * T_ + t;
+      float v[8];
+      {
+        const f32x4 a = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8);
+        const f32x4 b2 = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8 + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = a[i], v[4 + i] = b2[i];
+      }
+      if (accumulate) {
+        float u[8];
+        load8(dq + orow * D + 8 * c8, u);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] += u[i];
+      }
+      const int64_t qrow_sel = (int64_t)bh * T_ + t;
+      const int32_t* irow = sel_idx + qrow_sel * S;
+      for (int s0 = 0; s0 < NS; s0 += 16) {
+        Raw8<T> x[16];
+        int jv[16];
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) {
+          const int sl = s0 + k2 < NS ? s0 + k2 : NS - 1;
+          jv[k2] = irow[sl / nsub];
+          x[k2].load(sel_part + ((qrow_sel * NS + sl) * G + gl) * D + 8 * c8);
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) {
+          x[k2].keep_if(s0 + k2 < NS && sel_slot_valid(jv[k2], n_csr, sel_L, t));
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] += x[k2].get(i);
+        }
+      }
+      store8(dq_out + orow * D + 8 * c8, v);
+    }
+    return;
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     if (!rok[nt]) continue;
@@ -545,11 +618,15 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
 
 int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
                  const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
-                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                 int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                 const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
                  void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(sel_part == nullptr || (sel_idx != nullptr && dq_out != nullptr && S >= 1 && sel_block >= 16 &&
+                                    sel_block % 16 == 0 && (!accumulate || dq != nullptr)),
+            NSA_ERR_ARG);
   if (T == 0) return NSA_OK;
   const int NHC = (Hq / Hkv + 15) / 16;
   const int Lp = padded_len(Lk);
@@ -564,7 +641,8 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
       NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
       k_range_dq32<bf16, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
           mode, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)kt, (const bf16*)dout, lse, dot,
-          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
+          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale,
+          (const bf16*)sel_part, sel_idx, (bf16*)dq_out, S, sel_block);
     } else {
       constexpr int NT = RangeNT<float>::dq;
       const int nqt = (T + 8 * NT - 1) / (8 * NT);
@@ -572,7 +650,8 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
       NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
       k_range_dq32<float, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
           mode, (const float*)q, (const float*)k, (const float*)v, (const float*)kt, (const float*)dout, lse, dot,
-          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale);
+          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale,
+          (const float*)sel_part, sel_idx, (float*)dq_out, S, sel_block);
     }
   });
   return nsa_launch_status();

@@ -20,12 +20,6 @@ namespace nsa {
 
 constexpr float kNegInfS = -__builtin_inff();
 
-// Slot of a selected block j in row t is valid (has a CSR pair) iff
-// 0 <= j < n_csr and j * L <= t.
-__device__ __forceinline__ bool sel_slot_valid(int j, int n_csr, int L, int t) {
-  return j >= 0 && j < n_csr && (int64_t)j * L <= t;
-}
-
 constexpr int kFwdStages = 2;   // query tiles in flight per wave of k_sel_fwd_bo
 
 // Loads of one 2-query Q tile into a natural-order row stage, issued by the
@@ -251,58 +245,6 @@ static inline int grid_for(int64_t n) {
   if (g > 65536) g = 65536;
   return (int)(g < 1 ? 1 : g);
 }
-
-// 8 consecutive elements of a row (one 16-byte load for bf16, two for float)
-__device__ __forceinline__ void load8(const bf16* p, float (&x)[8]) {
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
-}
-__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
-}
-__device__ __forceinline__ void store8(bf16* p, const float (&x)[8]) {
-  bf16x8 v;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
-  *reinterpret_cast<bf16x8*>(p) = v;
-}
-__device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
-  *reinterpret_cast<f32x4*>(p) = (f32x4){x[0], x[1], x[2], x[3]};
-  *reinterpret_cast<f32x4*>(p + 4) = (f32x4){x[4], x[5], x[6], x[7]};
-}
-
-// 8 consecutive elements of a row as loaded (one 16-byte load for bf16, two
-// for float), converted at use.
-template <typename T> struct Raw8;
-template <> struct Raw8<bf16> {
-  bf16x8 v;
-  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
-  __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
-  __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
-    u32x4 u = __builtin_bit_cast(u32x4, v);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) u[i] = ok ? u[i] : 0u;
-    v = __builtin_bit_cast(bf16x8, u);
-  }
-};
-template <> struct Raw8<float> {
-  f32x4 a, b;
-  __device__ __forceinline__ void load(const float* p) {
-    a = *reinterpret_cast<const f32x4*>(p);
-    b = *reinterpret_cast<const f32x4*>(p + 4);
-  }
-  __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
-  __device__ __forceinline__ void keep_if(bool ok) {
-    u32x4 ua = __builtin_bit_cast(u32x4, a), ub = __builtin_bit_cast(u32x4, b);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) ua[i] = ok ? ua[i] : 0u, ub[i] = ok ? ub[i] : 0u;
-    a = __builtin_bit_cast(f32x4, ua);
-    b = __builtin_bit_cast(f32x4, ub);
-  }
-};
 
 // Both reductions below take one thread per 8 elements of a row, rows ordered
 // (b, hkv, t, g) so that a wave reads contiguous partial rows.  Every slot's

@@ -324,4 +324,56 @@ __device__ __forceinline__ void key_pipeline(int ntile, Req request, Body body) 
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// 8 consecutive elements of a row (one 16-byte load for bf16, two for float)
+__device__ __forceinline__ void load8(const bf16* p, float (&x)[8]) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+}
+__device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = a[i], x[4 + i] = b[i];
+}
+__device__ __forceinline__ void store8(bf16* p, const float (&x)[8]) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+__device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
+  *reinterpret_cast<f32x4*>(p) = (f32x4){x[0], x[1], x[2], x[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = (f32x4){x[4], x[5], x[6], x[7]};
+}
+
+// 8 consecutive elements of a row as loaded (one 16-byte load for bf16, two
+// for float), converted at use.
+template <typename T> struct Raw8;
+template <> struct Raw8<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
+  __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
+    u32x4 u = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = ok ? u[i] : 0u;
+    v = __builtin_bit_cast(bf16x8, u);
+  }
+};
+template <> struct Raw8<float> {
+  f32x4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const f32x4*>(p);
+    b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
+  __device__ __forceinline__ void keep_if(bool ok) {
+    u32x4 ua = __builtin_bit_cast(u32x4, a), ub = __builtin_bit_cast(u32x4, b);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ua[i] = ok ? ua[i] : 0u, ub[i] = ok ? ub[i] : 0u;
+    a = __builtin_bit_cast(f32x4, ua);
+    b = __builtin_bit_cast(f32x4, ub);
+  }
+};
+
 }  // namespace nsa

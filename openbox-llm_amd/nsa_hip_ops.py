@@ -335,12 +335,24 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w):
 
 
 def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0, cmp_block=1,
-             cmp_stride=1):
+             cmp_stride=1, sel_part=None, sel_idx=None, sel_block=0):
+    """dQ of a range branch into the float32 ``dq`` (added when
+    ``accumulate``).  With ``sel_part`` (the selection dQ partials of
+    ``sel_dkdv``) and ``sel_idx`` the rows are finished instead: returns
+    dq_out in q's dtype = (dq if accumulate) + this branch + the selection
+    partials of the valid slots."""
     B, Hq, T, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
-    _call(_span_name("dq", mode), _lib().nsa_range_dq, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do), L.ptr(lse),
-                                L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
-                                int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q), _stream(q))
+    out = None
+    S = 0
+    if sel_part is not None:
+        out = torch.empty(B, Hq, T, D, device=q.device, dtype=q.dtype)
+        S = sel_idx.shape[-1]
+    _call(_span_name("dq", mode), _lib().nsa_range_dq, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do),
+          L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
+          int(window), int(cmp_block), int(cmp_stride), L.ptr(sel_part), L.ptr(sel_idx), S, int(sel_block),
+          L.ptr(out), L.dtype_code(q), _stream(q))
+    return out
 
 
 def range_dkdv(mode, q, k, v, do, coff, dot, window=0, cmp_block=1, cmp_stride=1):
@@ -650,31 +662,38 @@ class NSAFusedHIP(torch.autograd.Function):
         kt_w = transpose_kv(kw)
         range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
         dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
-        # compression
+        # selection: dK/dV and the dQ partials block-outer
+        dq_part = None
+        if idx.shape[-1] > 0:
+            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
+                                         csr=tuple(csr), want_dq=True, qp=qp)
+        else:
+            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
+            dvs = torch.zeros_like(dks)
+        # compression; its dQ kernel finishes the rows: window dQ + its own +
+        # the selection partials, written in the input dtype
         if k_cmp.shape[2] > 0:
             kt_c = transpose_kv(k_cmp)
-            range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
-                     geom.cmp_block, geom.cmp_stride)
+            if dq_part is not None:
+                dq_out = range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                                  geom.cmp_block, geom.cmp_stride, sel_part=dq_part, sel_idx=idx,
+                                  sel_block=geom.sel_block)
+            else:
+                range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                         geom.cmp_block, geom.cmp_stride)
+                dq_out = cast_f32(dq, dtype)
             dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
                                   geom.cmp_block, geom.cmp_stride)
         else:
             dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
             dvp = torch.zeros_like(dkp)
+            dq_out = (sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype) if dq_part is not None
+                      else cast_f32(dq, dtype))
         if ctx.pooled:
             dkc, dvc = cast_f32(dkp, dtype), cast_f32(dvp, dtype)
         else:
             dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
             dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
-        # selection: dK/dV and dQ partials block-outer; the reduce adds the
-        # window / compression dQ and writes the input dtype
-        if idx.shape[-1] > 0:
-            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                         csr=tuple(csr), want_dq=True, qp=qp)
-            dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
-        else:
-            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
-            dvs = torch.zeros_like(dks)
-            dq_out = cast_f32(dq, dtype)
         return (dq_out, dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
                 cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None, None)
 
