@@ -178,6 +178,19 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
                   void* stream);
 
+/* nsa_range_fwd that also finishes the rows of the gated three-branch layer
+ * (no reference counterpart as one call: nsa_sel_merge and nsa_gate_fwd
+ * folded into the last branch's forward).  Besides this branch's o / lse it
+ * merges the selection partials of nsa_sel_fwd_bo (o_part, ml_part, with the
+ * [B][Hkv][T][S] block_idx of block size sel_block) into o_sel / lse_sel
+ * and writes out = sigmoid(g0) o_cmp + sigmoid(g1) o_sel + sigmoid(g2) o from
+ * the gate logits [B][Hq][T][3], each branch rounded to the dtype first. */
+int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
+                         int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                         const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
+                         void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
+                         void* stream);
+
 /* Backward dQ of the range branches (query-side half of
  * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426): dq (float32)
  * receives this branch's dQ, added to its contents when `accumulate`.

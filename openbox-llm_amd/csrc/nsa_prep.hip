@@ -79,7 +79,6 @@ __global__ __launch_bounds__(256) void k_pool_bwd(const TI* __restrict__ dp, TO*
 // ---------------------------------------------------------------------------
 // gate
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // 16-byte vectors of T: 8 bf16 or 4 float
 template <typename T> struct Vec16;

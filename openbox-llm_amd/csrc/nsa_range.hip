@@ -147,6 +147,129 @@ __device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
+// Optional finishing of the rows by the last branch's forward (the window):
+// with opart set, the launch also merges the selection partials of
+// nsa_sel_fwd_bo for its rows into o_sel / lse_sel (the role of
+// nsa_sel_merge) and blends the three branches through the gate into out
+// (the role of nsa_gate_fwd), each from the same rounded branch outputs the
+// separate kernels would read.
+template <typename T> struct FwdFinish {
+  const T* opart;          // [B][Hkv][T][NS][G][D] block-local outputs O_j / l_j
+  const float2* ml;        // [B][Hkv][T][NS][G] (m_j [log2 units], l_j)
+  const int32_t* idx;      // [B][Hkv][T][S] selected blocks
+  T* o_sel;                // [B][Hq][T][D]
+  float* lse_sel;          // [B][Hq][T]
+  const T* o_cmp;          // [B][Hq][T][D] compression output
+  const T* gate;           // [B][Hq][T][3] gate logits
+  T* out;                  // [B][Hq][T][D]
+  int S, sel_L;
+};
+
+// The wave's own output rows (this branch, unnormalised acc with the row
+// statistics l_, m_) go through LDS so that every row is handled in 8-element
+// chunks: lane (row sub-index, chunk) per pass.
+template <typename T, int D>
+__device__ __forceinline__ void finish_rows(const FwdFinish<T>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
+                                            float l_row, float m_row, bool any_key, bool rok, int64_t row, T* o,
+                                            float* lse, char* smem, int w, int lane, int tw0, const RangeMap& mp,
+                                            int Hq, int Hkv, int T_) {
+  using C = Tile32<T, D>;
+  constexpr int FIN_PITCH = D + 4;
+  const int h = lane >> 5, n = lane & 31;
+  const float lt = l_row + __shfl_xor(l_row, 32, kWave);
+  const float inv = any_key ? 1.0f / lt : 0.0f;
+  if (rok && h == 0) lse[row] = any_key ? (m_row + __log2f(lt)) * kLn2 : kLseEmpty;
+  __syncthreads();   // the key stages are free
+  float* fin = reinterpret_cast<float*>(smem) + w * 32 * FIN_PITCH;
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * dt + 8 * g4 + 4 * h;
+      if (D % 32 == 0 || d < D)
+        *reinterpret_cast<f32x4*>(fin + n * FIN_PITCH + d) =
+            (f32x4){acc[dt][0][4 * g4], acc[dt][0][4 * g4 + 1], acc[dt][0][4 * g4 + 2], acc[dt][0][4 * g4 + 3]} *
+            inv;
+    }
+  __syncthreads();
+  constexpr int CPR = D / 8, RPI = 64 / CPR;   // 8-element chunks per row, rows per pass
+  const int c8 = lane % CPR, rsub = lane / CPR;
+  const int nsub = sel_passes(f.sel_L), NS = f.S * nsub, n_csr = sel_csr_blocks(T_, f.sel_L);
+  const int G = mp.G;
+  const int64_t bh = (int64_t)mp.b * Hkv + mp.hkv;
+  for (int r0 = 0; r0 < 32; r0 += RPI) {
+    const int r = r0 + rsub;
+    const int t = tw0 + (r >> 4);
+    const int gl = mp.hc * 16 + (r & 15);   // head within the group
+    if (t >= T_ || gl >= G) continue;
+    const int64_t orow = ((int64_t)mp.b * Hq + mp.hkv * G + gl) * T_ + t;
+    // this branch's row chunk, rounded as stored
+    float ow[8];
+    {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8);
+      const f32x4 b2 = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8 + 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ow[i] = a[i], ow[4 + i] = b2[i];
+      store8(o + orow * D + 8 * c8, ow);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ow[i] = to_f32(from_f32<T>(ow[i]));
+    }
+    // selection: merge the slot partials (running maximum over batches of 16)
+    const int64_t qs = bh * T_ + t;
+    const int32_t* irow = f.idx + qs * f.S;
+    float acc_s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float M = -__builtin_inff(), Ls = 0.0f;
+    for (int s0 = 0; s0 < NS; s0 += 16) {
+      Raw8<T> x[16];
+      float2 ml[16];
+      int jv[16];
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        const int sl = s0 + k2 < NS ? s0 + k2 : NS - 1;
+        const int64_t pr = (qs * NS + sl) * G + gl;
+        jv[k2] = irow[sl / nsub];
+        ml[k2] = f.ml[pr];
+        x[k2].load(f.opart + pr * D + 8 * c8);
+      }
+      bool ok[16];
+      float bm = M;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        ok[k2] = s0 + k2 < NS && sel_slot_valid(jv[k2], n_csr, f.sel_L, t) && ml[k2].y > 0.0f;
+        bm = ok[k2] ? fmaxf(bm, ml[k2].x) : bm;
+      }
+      if (bm == -__builtin_inff()) continue;   // nothing valid yet
+      const float rs = M == -__builtin_inff() ? 0.0f : fast_exp2(M - bm);
+      Ls *= rs;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc_s[i] *= rs;
+#pragma unroll
+      for (int k2 = 0; k2 < 16; ++k2) {
+        const float wk = ok[k2] ? fast_exp2(ml[k2].x - bm) * ml[k2].y : 0.0f;
+        x[k2].keep_if(ok[k2]);
+        Ls += wk;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc_s[i] += wk * x[k2].get(i);
+      }
+      M = bm;
+    }
+    const float inv_s = Ls > 0.0f ? 1.0f / Ls : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc_s[i] *= inv_s;
+    store8(f.o_sel + orow * D + 8 * c8, acc_s);
+    if (c8 == 0) f.lse_sel[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
+    // gate: sigmoid-weighted sum of the three rounded branch outputs
+    float oc[8];
+    load8(f.o_cmp + orow * D + 8 * c8, oc);
+    const float g0 = sigmoidf(to_f32(f.gate[orow * 3 + 0]));
+    const float g1 = sigmoidf(to_f32(f.gate[orow * 3 + 1]));
+    const float g2 = sigmoidf(to_f32(f.gate[orow * 3 + 2]));
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * to_f32(from_f32<T>(acc_s[i])) + g2 * ow[i];
+    store8(f.out + orow * D + 8 * c8, y);
+  }
+}
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kRescale = 8.0f;   // log2 growth of a row maximum that forces a rescale
 
@@ -236,12 +359,19 @@ template <typename T, int D, int NT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_fwd32(int mode, const T* __restrict__ q, const T* __restrict__ k,
                                                      const T* __restrict__ vt, T* __restrict__ o,
                                                      float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
-                                                     int Lp, int nqt, int window, int cl, int cd, float sl2) {
+                                                     int Lp, int nqt, int window, int cl, int cd, float sl2,
+                                                     const FwdFinish<T> fin_args) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 4;   // key tiles in flight + 1
-  __shared__ __align__(16) T sK[NST][C::ROW_ELEMS];
-  __shared__ __align__(16) T sV[NST][C::COL_ELEMS];
+  // one LDS buffer: the key stages during the walk, then (finishing rows)
+  // each wave's float output tile [32][D + 4]
+  constexpr int FIN_PITCH = D + 4;
+  constexpr int STAGE_BYTES = NST * (C::ROW_ELEMS + C::COL_ELEMS) * (int)sizeof(T);
+  constexpr int FIN_BYTES = 4 * 32 * FIN_PITCH * (int)sizeof(float);
+  __shared__ __align__(16) char smem[STAGE_BYTES > FIN_BYTES ? STAGE_BYTES : FIN_BYTES];
+  T (*sK)[C::ROW_ELEMS] = reinterpret_cast<T (*)[C::ROW_ELEMS]>(smem);
+  T (*sV)[C::COL_ELEMS] = reinterpret_cast<T (*)[C::COL_ELEMS]>(smem + NST * C::ROW_ELEMS * sizeof(T));
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, h = lane >> 5, n = lane & 31;
   // window: neighbouring query tiles (which share keys) on one XCD;
   // compression: every tile reads the same small key set and the work grows
@@ -306,6 +436,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[it % NST], sV[it % NST], kb, mask, lo, hi, sl2, n, h);
   });
 
+  if (fin_args.opart != nullptr) {
+    static_assert(NT == 1, "one 32-row tile per wave is staged");
+    finish_rows<T, D>(fin_args, acc, l_[0], m_[0], lo[0] <= hi[0], rok[0], row[0], o, lse, smem, w, lane,
+                      tw0, mp, Hq, Hkv, T_);
+    return;
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const float lt = l_[nt] + __shfl_xor(l_[nt], 32, kWave);
@@ -583,6 +719,29 @@ static inline bool range_args_ok(int mode, int B, int Hq, int Hkv, int T, int Lk
 
 extern "C" {
 
+}  // extern "C"
+
+template <typename E>
+static int range_fwd_launch(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
+                            int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                            const FwdFinish<E>& fin, hipStream_t s) {
+  const int NHC = (Hq / Hkv + 15) / 16;
+  const int Lp = padded_len(Lk);
+  const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
+  constexpr int NT = RangeNT<E>::fwd;
+  const int nqt = (T + 8 * NT - 1) / (8 * NT);
+  const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+  NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  NSA_DISPATCH_D(D, {
+    k_range_fwd32<E, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)vt, (E*)o,
+                                                            lse, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block,
+                                                            cmp_stride, sl2, fin);
+  });
+  return nsa_launch_status();
+}
+
+extern "C" {
+
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
                   void* stream) {
@@ -590,30 +749,37 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   if (T == 0) return NSA_OK;
-  const int NHC = (Hq / Hkv + 15) / 16;
-  const int Lp = padded_len(Lk);
-  const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  NSA_DISPATCH_D(D, {
-    if (dtype == NSA_BF16) {
-      constexpr int NT = RangeNT<bf16>::fwd;
-      const int nqt = (T + 8 * NT - 1) / (8 * NT);
-      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-      k_range_fwd32<bf16, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const bf16*)q, (const bf16*)k,
-                                                                 (const bf16*)vt, (bf16*)o, lse, Hq, Hkv, T, Lk,
-                                                                 Lp, nqt, window, cmp_block, cmp_stride, sl2);
-    } else {
-      constexpr int NT = RangeNT<float>::fwd;
-      const int nqt = (T + 8 * NT - 1) / (8 * NT);
-      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-      k_range_fwd32<float, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const float*)q, (const float*)k,
-                                                                  (const float*)vt, (float*)o, lse, Hq, Hkv, T,
-                                                                  Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2);
-    }
-  });
-  return nsa_launch_status();
+  if (dtype == NSA_BF16)
+    return range_fwd_launch<bf16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+                                  FwdFinish<bf16>{}, s);
+  return range_fwd_launch<float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+                                 FwdFinish<float>{}, s);
+}
+
+int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
+                         int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                         const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
+                         void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
+                         void* stream) {
+  NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
+  NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(o_part && ml_part && block_idx && o_sel && lse_sel && o_cmp && gate && out, NSA_ERR_ARG);
+  NSA_CHECK(S >= 1 && sel_block >= 16 && sel_block % 16 == 0, NSA_ERR_SHAPE);
+  if (T == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == NSA_BF16)
+    return range_fwd_launch<bf16>(
+        mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+        FwdFinish<bf16>{(const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel, lse_sel,
+                        (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
+        s);
+  return range_fwd_launch<float>(
+      mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+      FwdFinish<float>{(const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel, lse_sel,
+                       (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block},
+      s);
 }
 
 int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,

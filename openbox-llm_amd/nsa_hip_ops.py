@@ -270,6 +270,31 @@ def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None):
     return o, lse
 
 
+def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=None):
+    """Window forward that also finishes the gated layer's rows: returns
+    (o_w, lse_w, o_s, lse_s, out), with the selection partials ``sel_parts``
+    = (o_part, ml_part) of ``sel_fwd_partials`` merged into o_s / lse_s and
+    out = sum_c sigmoid(gate_c) o_c over the three branches."""
+    check_qkv(q, k, v)
+    q, k, gate, o_c = _contig(q), _contig(k), _contig(gate), _contig(o_c)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    assert gate.shape == (B, Hq, T, 3) and gate.dtype == q.dtype, "gate logits must be [B, Hq, T, 3] in q's dtype"
+    if vt is None:
+        vt = transpose_kv(v)
+    o_part, ml_part = sel_parts
+    o_w = torch.empty_like(q)
+    lse_w = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
+    o_s = torch.empty_like(q)
+    lse_s = torch.empty_like(lse_w)
+    out = torch.empty_like(q)
+    _call("fwd[win]", _lib().nsa_range_fwd_finish, MODE_WINDOW, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o_w),
+          L.ptr(lse_w), B, Hq, Hkv, T, T, D, int(window), 1, 1, L.ptr(o_part), L.ptr(ml_part), L.ptr(idx),
+          idx.shape[-1], int(sel_block), L.ptr(o_s), L.ptr(lse_s), L.ptr(o_c), L.ptr(gate), L.ptr(out),
+          L.dtype_code(q), _stream(q))
+    return o_w, lse_w, o_s, lse_s, out
+
+
 def gate_fwd(gate, o_c, o_s, o_w):
     gate, o_c, o_s, o_w = (_contig(t) for t in (gate, o_c, o_s, o_w))
     assert gate.shape == o_c.shape[:3] + (3,), "gate logits must be [B, Hq, T, 3]"
@@ -455,6 +480,20 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
     """Block-outer selection forward -> (o, lse[f32], csr); ``csr`` is the
     packed block -> query CSR (built here when not given), ``qp`` the
     ``pack_heads`` copy of q (made here when not given)."""
+    (o_part, ml_part), csr = sel_fwd_partials(q, k, v, block_idx, block_size, csr, vt, qp)
+    B, Hq, T, D = q.shape
+    idx = block_idx.to(torch.int32).contiguous()
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
+    _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
+          Hq, k.shape[1], T, D, idx.shape[-1], block_size, L.dtype_code(q), _stream(q))
+    return o, lse, csr
+
+
+def sel_fwd_partials(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
+    """The block-local selection outputs of every (query, slot, pass):
+    -> ((o_part, ml_part), csr), merged by ``sel_fwd_fsa`` or
+    ``range_fwd_finish``."""
     check_qkv(q, k, v)
     q, k = _contig(q), _contig(k)
     B, Hq, T, D = q.shape
@@ -480,11 +519,7 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
     _call("fwd[sel]", _lib().nsa_sel_fwd_bo, L.ptr(qp), L.ptr(k), L.ptr(vt), L.ptr(q_of_block), L.ptr(offsets),
           L.ptr(o_part), L.ptr(ml_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size, SEL_DKDV_CHUNK,
           L.dtype_code(q), _stream(q))
-    o = torch.empty_like(q)
-    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
-    _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
-          Hq, Hkv, T, D, S, block_size, L.dtype_code(q), _stream(q))
-    return o, lse, csr
+    return (o_part, ml_part), csr
 
 
 # ---------------------------------------------------------------------------
@@ -632,15 +667,18 @@ class NSAFusedHIP(torch.autograd.Function):
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
         idx = block_idx.to(torch.int32).contiguous()
         if idx.shape[-1] > 0:
+            # selection partials; the window forward merges them and applies the gate
             qp = pack_heads(q, ks.shape[1])
-            o_s, lse_s, csr = sel_fwd_fsa(q, ks, vs, idx, geom.sel_block, qp=qp)
+            parts, csr = sel_fwd_partials(q, ks, vs, idx, geom.sel_block, qp=qp)
+            o_w, lse_w, o_s, lse_s, out = range_fwd_finish(q, kw, vw, geom.window, parts, idx, geom.sel_block,
+                                                           o_c, gate)
         else:
             qp = torch.empty(0, device=q.device, dtype=q.dtype)
             o_s = torch.zeros_like(q)
             lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
             csr = ()
-        o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
-        out = gate_fwd(gate, o_c, o_s, o_w)
+            o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
+            out = gate_fwd(gate, o_c, o_s, o_w)
         ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, qp,
                               *csr)
         ctx.geom = geom
