@@ -74,10 +74,13 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
  * dgate[r][c] = sigmoid'(g_c) dot (autograd of nsa_fused_kernel.py:572-573).
  * coff (nullable, laid out like dot) receives the per-row exponent offset
  * lse_c[r] * log2(e) - log2(rowscale) (rowscale 1 when nbr == 1) that the
- * dK/dV kernels take; it needs lse_c for every branch c < nbr. */
+ * dK/dV kernels take; it needs lse_c for every branch c < nbr.  dout_packed
+ * (nullable) receives dO in the nsa_pack_heads layout, G heads per KV head
+ * and T queries per row block (rows = B Hq T). */
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
-                 float* rowscale, float* coff, int64_t rows, int D, int nbr, int dtype, void* stream);
+                 float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
+                 int dtype, void* stream);
 
 /* float32 accumulator -> dtype. */
 int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);

@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
                                                   const float* __restrict__ lse0, const float* __restrict__ lse1,
                                                   const float* __restrict__ lse2, float* __restrict__ dot,
                                                   float* __restrict__ rowscale, float* __restrict__ coff,
-                                                  int64_t rows, int D, int nbr) {
+                                                  T* __restrict__ dout_packed, int G, int T_, int64_t rows, int D,
+                                                  int nbr) {
   constexpr int N = Vec16<T>::N;
   const int gs = D / N;                         // lanes per row, a power of two <= 64
   const int lane = threadIdx.x & 63;
@@ -143,6 +144,12 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   if (ok) {
     Vec16<T> d, x;
     d.load(dout + row * D + sub * N);
+    if (dout_packed != nullptr) {
+      // row (b, hkv G + g, t) -> packed row ((b Hkv + hkv) T + t) G + g
+      const int64_t bhq = row / T_;
+      const int64_t prow = ((bhq / G) * T_ + (row - bhq * T_)) * G + bhq % G;
+      d.store(dout_packed + prow * D + sub * N);
+    }
     const T* os[3] = {o0, o1, o2};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
@@ -281,7 +288,8 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 // coff (nullable): lse_c * log2(e) - log2(rowscale_c), laid out like dot.
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
-                 float* rowscale, float* coff, int64_t rows, int D, int nbr, int dtype, void* stream) {
+                 float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
+                 int dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   const int vec = dtype == NSA_BF16 ? 8 : 4;
   NSA_CHECK(rows >= 0 && D > 0 && D % vec == 0 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
@@ -289,6 +297,8 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   NSA_CHECK(gs <= 64 && (gs & (gs - 1)) == 0, NSA_ERR_SHAPE);
   NSA_CHECK(nbr == 1 || (gate && o1 && o2 && rowscale), NSA_ERR_ARG);
   NSA_CHECK(!coff || (lse0 && (nbr == 1 || (lse1 && lse2))), NSA_ERR_ARG);
+  NSA_CHECK(!dout_packed || (G >= 1 && T >= 1 && rows % ((int64_t)G * T) == 0 && dout_packed != dout),
+            NSA_ERR_ARG);
   if (rows == 0) return NSA_OK;
   const int64_t grid64 = (rows * gs + 255) / 256;
   NSA_CHECK(grid64 < (1ll << 31), NSA_ERR_SHAPE);
@@ -297,11 +307,11 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   if (dtype == NSA_BF16)
     k_bwd_prep<bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1, (const bf16*)o2,
                                           (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2, dot, rowscale,
-                                          coff, rows, D, nbr);
+                                          coff, (bf16*)dout_packed, G, T, rows, D, nbr);
   else
     k_bwd_prep<float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
                                            (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1, lse2,
-                                           dot, rowscale, coff, rows, D, nbr);
+                                           dot, rowscale, coff, (float*)dout_packed, G, T, rows, D, nbr);
   return nsa_launch_status();
 }
 

@@ -338,13 +338,15 @@ def delta_of(do, o, lse):
     dot = torch.empty(o.shape[:3], device=o.device, dtype=torch.float32)
     coff = torch.empty_like(dot)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(lse), None, None,
-          L.ptr(dot), None, L.ptr(coff), rows, o.shape[3], 1, L.dtype_code(o), _stream(o))
+          L.ptr(dot), None, L.ptr(coff), None, 1, 1, rows, o.shape[3], 1, L.dtype_code(o), _stream(o))
     return dot, coff
 
 
-def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w):
-    """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3]); branch order
-    compression, selection, window; coff = lse * log2(e) - log2(rowscale)."""
+def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
+    """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3], dop); branch
+    order compression, selection, window; coff = lse * log2(e) -
+    log2(rowscale).  With ``pack_hkv`` > 0, dop is dO packed for that many KV
+    heads (the ``pack_heads`` layout), else None."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
     lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
     B, Hq, T, D = o_c.shape
@@ -353,10 +355,15 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w):
     rs = torch.empty_like(dot)
     coff = torch.empty_like(dot)
     dgate = torch.empty_like(gate)
+    dop = None
+    G = 1
+    if pack_hkv > 0:
+        G = Hq // pack_hkv
+        dop = torch.empty(B, pack_hkv, T, G, D, device=do.device, dtype=do.dtype)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(gate), L.ptr(dgate),
-          L.ptr(lse_c), L.ptr(lse_s), L.ptr(lse_w), L.ptr(dot), L.ptr(rs), L.ptr(coff), rows, D, 3,
+          L.ptr(lse_c), L.ptr(lse_s), L.ptr(lse_w), L.ptr(dot), L.ptr(rs), L.ptr(coff), L.ptr(dop), G, T, rows, D, 3,
           L.dtype_code(o_c), _stream(o_c))
-    return dot, rs, coff, dgate
+    return dot, rs, coff, dgate, dop
 
 
 def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0, cmp_block=1,
@@ -694,7 +701,8 @@ class NSAFusedHIP(torch.autograd.Function):
         geom, T = ctx.geom, ctx.T
         dout = _contig(dout)
         dtype = q.dtype
-        dot, rs, coff, dgate = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w)
+        dot, rs, coff, dgate, dop = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w,
+                                                  pack_hkv=ks.shape[1] if idx.shape[-1] > 0 else 0)
         dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
         # window
         kt_w = transpose_kv(kw)
@@ -704,7 +712,7 @@ class NSAFusedHIP(torch.autograd.Function):
         dq_part = None
         if idx.shape[-1] > 0:
             dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                         csr=tuple(csr), want_dq=True, qp=qp)
+                                         csr=tuple(csr), want_dq=True, qp=qp, dop=dop)
         else:
             dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
             dvs = torch.zeros_like(dks)
