@@ -176,9 +176,10 @@ int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float
  * (nsa_fused_kernel.py:61-119, 226-307).  mode NSA_MODE_WINDOW: key p visible
  * to t iff t-window < p <= t; NSA_MODE_COMPRESS: pooled token i visible iff
  * i*cmp_stride + cmp_block - 1 <= t.  k [B][Hkv][Lk][D], vt transposed v with
- * Lp = nsa_padded_len(Lk).  Writes o and lse. */
+ * Lp = nsa_padded_len(Lk).  Writes o and lse; q_packed (nullable) also
+ * receives q in the nsa_pack_heads layout (the rows are loaded anyway). */
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
-                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, void* q_packed, int dtype,
                   void* stream);
 
 /* nsa_range_fwd that also finishes the rows of the gated three-branch layer

@@ -55,7 +55,7 @@ SIGNATURES = {
     "nsa_sel_fwd_bo": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_merge": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dq_reduce": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "nsa_range_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_range_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P]),
     "nsa_range_fwd_finish": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                                   _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "nsa_range_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,

@@ -59,6 +59,7 @@ template <> struct Frag<bf16> {
     for (int j = 0; j < 8; ++j) v[j] = (bf16)x[j];
   }
   __device__ __forceinline__ bf16 elem(int j) const { return v[j]; }
+  __device__ __forceinline__ void store(bf16* p) const { *reinterpret_cast<bf16x8*>(p) = v; }
 };
 
 template <> struct Frag<float> {
@@ -80,6 +81,10 @@ template <> struct Frag<float> {
     hi = (f32x4){x[4], x[5], x[6], x[7]};
   }
   __device__ __forceinline__ float elem(int j) const { return j < 4 ? lo[j] : hi[j - 4]; }
+  __device__ __forceinline__ void store(float* p) const {
+    *reinterpret_cast<f32x4*>(p) = lo;
+    *reinterpret_cast<f32x4*>(p + 4) = hi;
+  }
 };
 
 __device__ __forceinline__ void mma(f32x4& c, const Frag<bf16>& a, const Frag<bf16>& b) {

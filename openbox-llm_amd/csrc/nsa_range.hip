@@ -147,13 +147,15 @@ __device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-// Optional finishing of the rows by the last branch's forward (the window):
-// with opart set, the launch also merges the selection partials of
-// nsa_sel_fwd_bo for its rows into o_sel / lse_sel (the role of
-// nsa_sel_merge) and blends the three branches through the gate into out
-// (the role of nsa_gate_fwd), each from the same rounded branch outputs the
-// separate kernels would read.
-template <typename T> struct FwdFinish {
+// Optional extra outputs of a forward launch.  q_packed: the Q rows the
+// launch loads, also stored in the nsa_pack_heads layout.  opart: the launch
+// finishes the rows of the gated layer (as the last branch, the window): it
+// merges the selection partials of nsa_sel_fwd_bo for its rows into o_sel /
+// lse_sel (the role of nsa_sel_merge) and blends the three branches through
+// the gate into out (the role of nsa_gate_fwd), each from the same rounded
+// branch outputs the separate kernels would read.
+template <typename T> struct FwdExtras {
+  T* q_packed;             // [B][Hkv][T][G][D] (nullable)
   const T* opart;          // [B][Hkv][T][NS][G][D] block-local outputs O_j / l_j
   const float2* ml;        // [B][Hkv][T][NS][G] (m_j [log2 units], l_j)
   const int32_t* idx;      // [B][Hkv][T][S] selected blocks
@@ -169,7 +171,7 @@ template <typename T> struct FwdFinish {
 // statistics l_, m_) go through LDS so that every row is handled in 8-element
 // chunks: lane (row sub-index, chunk) per pass.
 template <typename T, int D>
-__device__ __forceinline__ void finish_rows(const FwdFinish<T>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
+__device__ __forceinline__ void finish_rows(const FwdExtras<T>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
                                             float l_row, float m_row, bool any_key, bool rok, int64_t row, T* o,
                                             float* lse, char* smem, int w, int lane, int tw0, const RangeMap& mp,
                                             int Hq, int Hkv, int T_) {
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                      const T* __restrict__ vt, T* __restrict__ o,
                                                      float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
                                                      int Lp, int nqt, int window, int cl, int cd, float sl2,
-                                                     const FwdFinish<T> fin_args) {
+                                                     const FwdExtras<T> fin_args) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 4;   // key tiles in flight + 1
@@ -404,6 +406,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     visible_range(mode, t < T_ ? t : T_ - 1, Lk, window, cl, cd, lo[nt], hi[nt]);
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) qf[nt][s].load(q + srow * D + 16 * s + 8 * h);
+    if (fin_args.q_packed != nullptr && rok[nt]) {
+      T* dst = fin_args.q_packed + (((int64_t)bh * T_ + t) * mp.G + mp.hc * 16 + hd) * D;
+#pragma unroll
+      for (int s = 0; s < C::KS; ++s) qf[nt][s].store(dst + 16 * s + 8 * h);
+    }
   }
   float m_[NT], l_[NT];
   f32x16 acc[C::DT][NT];
@@ -724,7 +731,7 @@ extern "C" {
 template <typename E>
 static int range_fwd_launch(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                             int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
-                            const FwdFinish<E>& fin, hipStream_t s) {
+                            const FwdExtras<E>& fin, hipStream_t s) {
   const int NHC = (Hq / Hkv + 15) / 16;
   const int Lp = padded_len(Lk);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
@@ -743,18 +750,24 @@ static int range_fwd_launch(int mode, const void* q, const void* k, const void* 
 extern "C" {
 
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
-                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype,
+                  int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, void* q_packed, int dtype,
                   void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   if (T == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    return range_fwd_launch<bf16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-                                  FwdFinish<bf16>{}, s);
-  return range_fwd_launch<float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-                                 FwdFinish<float>{}, s);
+  NSA_CHECK(q_packed != q, NSA_ERR_ARG);
+  if (dtype == NSA_BF16) {
+    FwdExtras<bf16> ex{};
+    ex.q_packed = (bf16*)q_packed;
+    return range_fwd_launch<bf16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, ex,
+                                  s);
+  }
+  FwdExtras<float> ex{};
+  ex.q_packed = (float*)q_packed;
+  return range_fwd_launch<float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, ex,
+                                 s);
 }
 
 int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
@@ -772,12 +785,12 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
   if (dtype == NSA_BF16)
     return range_fwd_launch<bf16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-        FwdFinish<bf16>{(const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel, lse_sel,
+        FwdExtras<bf16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel, lse_sel,
                         (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
         s);
   return range_fwd_launch<float>(
       mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-      FwdFinish<float>{(const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel, lse_sel,
+      FwdExtras<float>{nullptr, (const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel, lse_sel,
                        (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block},
       s);
 }

@@ -252,8 +252,10 @@ def sel_fwd(q, k, v, block_idx, block_size, vt=None):
     return o, lse
 
 
-def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None):
-    """Window (mode 0) or compression (mode 1) forward -> (o, lse[f32])."""
+def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_packed=None):
+    """Window (mode 0) or compression (mode 1) forward -> (o, lse[f32]);
+    ``q_packed`` (optional, [B, Hkv, T, G, D]) also receives the
+    ``pack_heads`` copy of q."""
     check_qkv(q, k, v)
     q, k = _contig(q), _contig(k)
     B, Hq, T, D = q.shape
@@ -266,7 +268,7 @@ def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None):
     lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
     _call(_span_name("fwd", mode), _lib().nsa_range_fwd, mode, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o), L.ptr(lse),
                                  B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block), int(cmp_stride),
-                                 L.dtype_code(q), _stream(q))
+                                 L.ptr(q_packed), L.dtype_code(q), _stream(q))
     return o, lse
 
 
@@ -669,18 +671,20 @@ class NSAFusedHIP(torch.autograd.Function):
             assert kc.shape[2] == T, "compression keys must have the query length"
             k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
             v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
-        o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride)
+        want_sel = block_idx is None or block_idx.shape[-1] > 0
+        qp = (torch.empty(q.shape[0], ks.shape[1], T, q.shape[1] // ks.shape[1], q.shape[3], device=q.device,
+                          dtype=q.dtype) if want_sel else torch.empty(0, device=q.device, dtype=q.dtype))
+        o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride,
+                               q_packed=qp if want_sel else None)
         if block_idx is None:
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
         idx = block_idx.to(torch.int32).contiguous()
         if idx.shape[-1] > 0:
             # selection partials; the window forward merges them and applies the gate
-            qp = pack_heads(q, ks.shape[1])
             parts, csr = sel_fwd_partials(q, ks, vs, idx, geom.sel_block, qp=qp)
             o_w, lse_w, o_s, lse_s, out = range_fwd_finish(q, kw, vw, geom.window, parts, idx, geom.sel_block,
                                                            o_c, gate)
         else:
-            qp = torch.empty(0, device=q.device, dtype=q.dtype)
             o_s = torch.zeros_like(q)
             lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
             csr = ()
