@@ -24,7 +24,7 @@ import _nsa_lib as L
 
 MODE_WINDOW = L.MODE_WINDOW
 MODE_COMPRESS = L.MODE_COMPRESS
-SEL_DKDV_CHUNK = 256          # CSR queries per selection dK/dV work item
+SEL_DKDV_CHUNK = 512          # CSR queries per selection dK/dV work item
 
 
 @dataclass(frozen=True)
