@@ -13,55 +13,46 @@
 //     heads of each of its token's 2 rows, summed in order, then the two
 //     lane halves are added (head chunks of groups wider than 16 follow in
 //     chunk order), so every sum has a fixed order.
-//  3. after each tile the tile's tokens fold into the selection blocks:
-//     imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d, tokens ascending.
+//  3. every F tiles (and after the last) the tiles' tokens fold into the
+//     selection blocks: imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d,
+//     tokens ascending; F is the most tiles whose blocks (for both queries)
+//     fit one lane each.
 //  4. per query: score = +inf for forced blocks, -FLT_MAX for blocks not yet
-//     complete, else imp_slc; keys (orderable score << 32 | ~j) make a
-//     wave-wide u64 max pick the highest score and, among equal scores, the
-//     lowest block index, S times.
+//     complete, else imp_slc; the order keys of the scores, KPL per lane in
+//     registers (block lane + 64 k), give S picks, each the highest score by
+//     a wave max and, among equal scores, the lowest block index by a wave
+//     min; a picked key is zeroed.
 #include "nsa_launch.h"
 #include "nsa_tile32.h"
 
 namespace nsa {
 
-__device__ __forceinline__ uint64_t topn_key(float x, int j) {
-  uint32_t u = __float_as_uint(x);
-  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)u << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)j);
+// float -> u32 with the same order (+inf highest); every float maps above 0
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Maximum of a u64 over the wave, in every lane: within rows of 16 lanes by
-// DPP (quad swaps, half-row and row mirrors), across rows by the gfx950 row
-// swaps (permlane16: row pairs, permlane32: wave halves) -- register moves
-// only, no LDS round trips.
-template <int CTRL>
-__device__ __forceinline__ uint64_t max_dpp(uint64_t k) {
-  const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
-  const uint32_t olo = __builtin_amdgcn_update_dpp(lo, lo, CTRL, 0xF, 0xF, false);
-  const uint32_t ohi = __builtin_amdgcn_update_dpp(hi, hi, CTRL, 0xF, 0xF, false);
-  const uint64_t o = ((uint64_t)ohi << 32) | olo;
-  return o > k ? o : k;
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t k) {
-  k = max_dpp<0xB1>(k);    // quad_perm [1,0,3,2]
-  k = max_dpp<0x4E>(k);    // quad_perm [2,3,0,1]
-  k = max_dpp<0x141>(k);   // row_half_mirror
-  k = max_dpp<0x140>(k);   // row_mirror: every lane holds its row's maximum
+// Maximum (MAX) or minimum of a u32 over the wave, in every lane: within rows
+// of 16 lanes by DPP (quad swaps, half-row and row mirrors), across rows by
+// the gfx950 row swaps (permlane16: row pairs, permlane32: wave halves) --
+// register moves only, no LDS round trips.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x) {
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xF, 0xF, false));   // row_half_mirror
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xF, 0xF, false));   // row_mirror
   {
-    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
-    const auto pl = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
-    const auto ph = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
-    const uint64_t a = ((uint64_t)ph[0] << 32) | pl[0], b = ((uint64_t)ph[1] << 32) | pl[1];
-    k = a > b ? a : b;     // rows 2r and 2r+1 hold their pair's maximum
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = op(p[0], p[1]);   // rows 2r and 2r+1 hold their pair's result
   }
   {
-    const uint32_t lo = (uint32_t)k, hi = (uint32_t)(k >> 32);
-    const auto pl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
-    const auto ph = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
-    const uint64_t a = ((uint64_t)ph[0] << 32) | pl[0], b = ((uint64_t)ph[1] << 32) | pl[1];
-    k = a > b ? a : b;     // both halves: the wave's maximum
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = op(p[0], p[1]);   // both halves: the wave's result
   }
-  return k;
+  return x;
 }
 
 __device__ __forceinline__ void wave_fence() {
@@ -70,6 +61,8 @@ __device__ __forceinline__ void wave_fence() {
 }
 
 constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
+constexpr int kImpFold = 8;               // tokens read per step of a block's fold
+constexpr int kImpFoldTiles = 4;          // most tiles per fold
 constexpr int kImpStages = 4;             // K tiles in flight + 1
 constexpr int kImpQPB = 4 * kImpQPW;      // queries per workgroup
 
@@ -85,19 +78,21 @@ __device__ __forceinline__ int div_sh(int x, int d, int sh) { return sh >= 0 ? x
 
 // LDS: K tiles [kImpStages][32][D], per-wave token scratch [4][2][32], block
 // sums [8][nsp].  cd_sh / ls_sh: log2 of cd / ls when they are powers of two,
-// else -1 (the block fold then divides).
-template <typename T, int D>
+// else -1 (the block fold then divides); rcd = 1 / cd scales the overlap
+// weights; fold_tiles: F above (1 .. kImpFoldTiles).  KPL:
+// block keys per lane in the top-S phase (n_slc <= 64 * KPL).
+template <typename T, int D, int KPL>
 __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
                                                   const float* __restrict__ lse, int32_t* __restrict__ out_idx,
                                                   float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
                                                   int n_slc, int nsp, int S, int cl, int cd, int ls, int force_init,
-                                                  int n_local, int nqb, int cd_sh, int ls_sh, float sl2) {
+                                                  int n_local, int nqb, int cd_sh, int ls_sh, int fold_tiles, float rcd, float sl2) {
   using C = Tile32<T, D>;
   constexpr int NST = kImpStages;
   extern __shared__ __align__(16) char smem[];
   T* sK = reinterpret_cast<T*>(smem);                                   // [NST][ROW_ELEMS]
-  float* stok = reinterpret_cast<float*>(sK + NST * C::ROW_ELEMS);      // [4][2][32]
-  float* sblk = stok + 4 * kImpQPW * 32;                                 // [8][nsp]
+  float* stok = reinterpret_cast<float*>(sK + NST * C::ROW_ELEMS);      // [4][2][32 F]
+  float* sblk = stok + 4 * kImpQPW * 32 * kImpFoldTiles;                 // [8][nsp]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // long rows first: workgroups go out round-robin, the latest queries first
@@ -127,7 +122,8 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
   };
 
   // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
-  float* my_tok = stok + w * kImpQPW * 32;
+  const int tpq = 32 * fold_tiles;   // token slots per query
+  float* my_tok = stok + w * kImpQPW * tpq;
   float* my_blk = sblk + w * kImpQPW * nsp;
   Frag<T> qf[C::KS];
   float lse2[16];
@@ -150,18 +146,15 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       // absent rows (heads past the group, queries past T) get p = 0
       lse2[r] = ok ? lse[((int64_t)b * Hq + hkv * G + he) * T_ + te] * kLog2e : __builtin_inff();
     }
-  };
-  if (NHC == 1) {
-    load_rows(0);
-    // complete these loads before the walk, whose loads the compiler does
-    // not see (a wait it placed in the loop would drain the tiles in flight);
-    // wider groups load their rows inside the loop, and the compiler's waits
-    // for those only lengthen the walk's
+    // complete these loads here: the walk's own loads are asm the compiler
+    // does not see, so a wait it placed later (e.g. before the first MFMA)
+    // would also drain the K tiles in flight
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) settle(qf[s]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(lse2[r]));
-  }
+  };
+  if (NHC == 1) load_rows(0);
   __syncthreads();   // sblk cleared
   key_pipeline<NST, dma_uniform_loads<256, C::ROW_CHUNKS>()>(ntile, load_tile, [&](int kt) {
     const T* tile = sK + (kt % NST) * C::ROW_ELEMS;
@@ -178,30 +171,35 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       float part[kImpQPW];
 #pragma unroll
       for (int i = 0; i < kImpQPW; ++i) {
-        const bool vis = tok <= hi_q[i];
         float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float p = fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
-          acc += vis ? p : 0.0f;
-        }
-        part[i] = acc;
+        for (int j = 0; j < 8; ++j) acc += fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
+        part[i] = tok <= hi_q[i] ? acc : 0.0f;   // tokens the query cannot see
       }
-      // heads 8h .. 8h+7 of each row are in lane half h: add the other half
+      // heads 8h .. 8h+7 of each row are in lane half h: the half swap gives
+      // both halves part(half 0) and part(half 1); their sum is the same in
+      // every lane
 #pragma unroll
-      for (int i = 0; i < kImpQPW; ++i) part[i] += __shfl_xor(part[i], 32, kWave);
+      for (int i = 0; i < kImpQPW; ++i) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[i]), __float_as_uint(part[i]), false,
+                                                         false);
+        part[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
       // lane half h keeps query h's value for token `tok`
       const float mine = h == 0 ? part[0] : part[1];
+      float* slot = my_tok + h * tpq + (kt % fold_tiles) * 32 + n;
       if (hc == 0)
-        my_tok[h * 32 + n] = mine;
+        *slot = mine;
       else
-        my_tok[h * 32 + n] += mine;
+        *slot += mine;
     }
+    if (kt % fold_tiles != fold_tiles - 1 && kt != ntile - 1) return;
     wave_fence();
-    // fold the tile's tokens into the blocks they overlap, tokens ascending;
-    // lane = (query, block of the tile's span)
-    const int i0 = kt * 32;
-    const int i1 = i0 + 31 < n_cmp - 1 ? i0 + 31 : n_cmp - 1;
+    // fold the last tiles' tokens into the blocks they overlap, tokens
+    // ascending; lane = (query, block of the tokens' span); the block's tokens
+    // are read kImpFold at a time so their LDS reads overlap
+    const int i0 = (kt - kt % fold_tiles) * 32;
+    const int i1 = kt * 32 + 31 < n_cmp - 1 ? kt * 32 + 31 : n_cmp - 1;
     const int jlo = div_sh(i0 * cd, ls, ls_sh);
     int jhi = div_sh(i1 * cd + cl - 1, ls, ls_sh);
     jhi = jhi < n_slc - 1 ? jhi : n_slc - 1;
@@ -209,15 +207,24 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     static_assert(kImpQPW == 2, "lane -> (query, block) split below assumes two queries");
     for (int u = lane; u < kImpQPW * nj; u += kWave) {
       const int qi = u >= nj ? 1 : 0, j = jlo + u - qi * nj;
+      // tokens whose span [i*cd, i*cd+cl) meets [j*ls, (j+1)*ls)
       int a_i = j * ls - cl + 1 <= 0 ? 0 : div_sh(j * ls - cl + 1 + cd - 1, cd, cd_sh);
       int b_i = div_sh((j + 1) * ls - 1, cd, cd_sh);
       a_i = a_i > i0 ? a_i : i0;
       b_i = b_i < i1 ? b_i : i1;
+      const float* tq = my_tok + qi * tpq - i0;
       float sj = my_blk[qi * nsp + j];
-      for (int i = a_i; i <= b_i; ++i) {
-        const int a = i * cd > j * ls ? i * cd : j * ls;
-        const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
-        if (e > a) sj += my_tok[qi * 32 + (i - i0)] * ((float)(e - a) / (float)cd);
+      for (int ib = a_i; ib <= b_i; ib += kImpFold) {
+        float v[kImpFold];
+#pragma unroll
+        for (int x = 0; x < kImpFold; ++x) v[x] = tq[ib + x <= b_i ? ib + x : b_i];
+#pragma unroll
+        for (int x = 0; x < kImpFold; ++x) {
+          const int i = ib + x;
+          const int a = i * cd > j * ls ? i * cd : j * ls;
+          const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
+          if (i <= b_i && e > a) sj += v[x] * ((float)(e - a) * rcd);
+        }
       }
       my_blk[qi * nsp + j] = sj;
     }
@@ -230,36 +237,41 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     const int t = tq0 + qi;
     if (t >= T_) break;
     const int64_t r = (int64_t)bh * T_ + t;
-    float* sc = my_blk + qi * nsp;
+    const float* sc = my_blk + qi * nsp;
     const int tb = t / ls;
-    for (int j = lane; j < n_slc; j += kWave) {
-      const float s = sc[j];
-      if (scores != nullptr) scores[r * n_slc + j] = s;
-      const bool valid = (j + 1) * ls - 1 <= t;
-      const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
-      sc[j] = forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f);
-    }
-    wave_fence();
-    uint64_t removed = 0;
-    auto lane_best = [&]() {
-      uint64_t best = 0;
-      int k = 0;
-      for (int j = lane; j < n_slc; j += kWave, ++k) {
-        if ((removed >> k) & 1ull) continue;
-        const uint64_t key = topn_key(sc[j], j);
-        best = key > best ? key : best;
+    uint32_t key[KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) {
+      const int j = lane + kWave * k;
+      key[k] = 0;
+      if (j < n_slc) {
+        const float s = sc[j];
+        if (scores != nullptr) scores[r * n_slc + j] = s;
+        const bool valid = (j + 1) * ls - 1 <= t;
+        const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
+        key[k] = order_key(forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f));
       }
-      return best;
-    };
-    uint64_t mine = lane_best();
+    }
+    // pick s lands in lane s % 64 and is stored with the group of 64 it ends
     int32_t* orow = out_idx + r * S;
+    int pick = 0;
     for (int s = 0; s < S; ++s) {
-      const uint64_t bk = wave_max_u64(mine);
-      const int jw = (int)(0xFFFFFFFFu - (uint32_t)(bk & 0xFFFFFFFFu));
-      if (lane == 0) orow[s] = jw;
-      if ((jw & (kWave - 1)) == lane) {
-        removed |= 1ull << (jw / kWave);
-        mine = lane_best();
+      uint32_t m = key[0];
+#pragma unroll
+      for (int k = 1; k < KPL; ++k) m = key[k] > m ? key[k] : m;
+      int kb = 0;   // this lane's lowest k holding m
+#pragma unroll
+      for (int k = KPL - 1; k > 0; --k) kb = key[k] == m ? k : kb;
+      kb = key[0] == m ? 0 : kb;
+      const uint32_t top = wave_reduce_u32<true>(m);
+      const int jw = (int)__builtin_amdgcn_readfirstlane(
+          (int)wave_reduce_u32<false>(m == top ? (uint32_t)(lane + kWave * kb) : 0xFFFFFFFFu));
+      pick = lane == (s & (kWave - 1)) ? jw : pick;
+      const bool own = lane == (jw & (kWave - 1));
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) key[k] = own && k == jw / kWave ? 0u : key[k];
+      if ((s & (kWave - 1)) == kWave - 1 || s == S - 1) {
+        if (lane <= (s & (kWave - 1))) orow[(s & ~(kWave - 1)) + lane] = pick;
       }
     }
   }
@@ -284,7 +296,7 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   if (T == 0 || n_slc == 0) return NSA_OK;
   const int nsp = n_slc + 1;   // per-query block-sum pitch (odd: spreads the 8 queries over banks)
   const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)kImpStages * 32 * D;
-  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 + (size_t)kImpQPB * nsp);
+  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 * kImpFoldTiles + (size_t)kImpQPB * nsp);
   NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
   const int nqb = (T + kImpQPB - 1) / kImpQPB;
   const int64_t grid = (int64_t)B * Hkv * nqb;
@@ -292,33 +304,49 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
   const int cd_sh = (cmp_stride & (cmp_stride - 1)) == 0 ? __builtin_ctz(cmp_stride) : -1;
   const int ls_sh = (sel_block & (sel_block - 1)) == 0 ? __builtin_ctz(sel_block) : -1;
+  const float rcd = 1.0f / (float)cmp_stride;
+  // tiles per fold: the most (up to kImpFoldTiles) whose tokens' blocks, for
+  // both queries of a wave, fit the wave's lanes
+  int fold_tiles = 1;
+  for (int f = 2; f <= kImpFoldTiles; ++f) {
+    const int64_t span = (int64_t)(32 * f - 1) * cmp_stride + cmp_block;   // positions the tokens cover
+    if (kImpQPW * ((span - 1) / sel_block + 2) <= 64) fold_tiles = f;
+  }
+  // block keys per lane in the top-S phase
+  const int kpl = n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : 64;
   hipStream_t s = (hipStream_t)stream;
   // more than 64 KB of dynamic LDS must be allowed per kernel
-#define NSA_TOPN_LDS(K) (lds <= 65536 || hipFuncSetAttribute((const void*)(K), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
-  switch (D) {
-#define NSA_TOPN_CASE(DD)                                                                                       \
-  case DD:                                                                                                      \
-    NSA_CHECK(NSA_TOPN_LDS((k_imp_topn<bf16, DD>)) && NSA_TOPN_LDS((k_imp_topn<float, DD>)), NSA_ERR_LAUNCH);  \
-    if (dtype == NSA_BF16)                                                                                      \
-      k_imp_topn<bf16, DD><<<(unsigned)grid, 256, lds, s>>>((const bf16*)q, (const bf16*)k_cmp, lse_cmp,      \
-                                                            block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp, S, \
-                                                            cmp_block, cmp_stride, sel_block, force_init,       \
-                                                            n_local, nqb, cd_sh, ls_sh, sl2);                                 \
-    else                                                                                                        \
-      k_imp_topn<float, DD><<<(unsigned)grid, 256, lds, s>>>((const float*)q, (const float*)k_cmp, lse_cmp,   \
-                                                             block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp,  \
-                                                             S, cmp_block, cmp_stride, sel_block, force_init,   \
-                                                             n_local, nqb, cd_sh, ls_sh, sl2);                                \
+  auto launch = [&](auto kern, auto qp, auto kp) -> int {
+    if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
+                           hipSuccess)
+      return NSA_ERR_LAUNCH;
+    kern<<<(unsigned)grid, 256, lds, s>>>(qp, kp, lse_cmp, block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp, S,
+                                          cmp_block, cmp_stride, sel_block, force_init, n_local, nqb, cd_sh, ls_sh,
+                                          fold_tiles, rcd, sl2);
+    return NSA_OK;
+  };
+  int rc = NSA_ERR_SHAPE;
+#define NSA_TOPN_KPL(DD, KK)                                                                          \
+  if (kpl == KK)                                                                                      \
+    rc = dtype == NSA_BF16 ? launch(k_imp_topn<bf16, DD, KK>, (const bf16*)q, (const bf16*)k_cmp)    \
+                           : launch(k_imp_topn<float, DD, KK>, (const float*)q, (const float*)k_cmp);
+#define NSA_TOPN_CASE(DD) \
+  case DD:                \
+    NSA_TOPN_KPL(DD, 8)   \
+    NSA_TOPN_KPL(DD, 16)  \
+    NSA_TOPN_KPL(DD, 64)  \
     break;
+  switch (D) {
     NSA_TOPN_CASE(16)
     NSA_TOPN_CASE(32)
     NSA_TOPN_CASE(64)
     NSA_TOPN_CASE(128)
-#undef NSA_TOPN_CASE
-#undef NSA_TOPN_LDS
     default:
-      return NSA_ERR_SHAPE;
+      break;
   }
+#undef NSA_TOPN_CASE
+#undef NSA_TOPN_KPL
+  if (rc != NSA_OK) return rc;
   return nsa_launch_status();
 }
 
