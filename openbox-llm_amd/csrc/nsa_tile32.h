@@ -271,6 +271,47 @@ __device__ __forceinline__ void dma_tile_uniform(void* lds, SrcFn src, int tid) 
 template <int NTH, int NCHUNK>
 constexpr int dma_uniform_loads() { return (NCHUNK + NTH - 1) / NTH; }
 
+// dma_tile_uniform for [32][D] row tiles of a [rows][D] source, with the
+// per-thread part of every address (row and chunk inside the tile) computed
+// once by init: a request is a wave-uniform base plus constant per-lane
+// offsets (lds_dma16_sbase), so it costs no per-lane address arithmetic.
+// NAT: natural row order (nrow_chunk), else the permuted order of row_chunk.
+// Rows at or past nrows repeat row nrows - 1.
+template <typename T, int D, int NTH, bool NAT>
+struct RowTileDma {
+  using C = Tile32<T, D>;
+  static constexpr int NL = dma_uniform_loads<NTH, C::ROW_CHUNKS>();
+  int row[NL];
+  uint32_t off[NL];
+  __device__ __forceinline__ void init(int tid) {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int P = (j * NTH + 64 * w) % C::ROW_CHUNKS + lane;
+      int r, c;
+      if constexpr (NAT)
+        nrow_chunk<T, D>(P, r, c);
+      else
+        row_chunk<T, D>(P, r, c);
+      row[j] = r;
+      off[j] = (uint32_t)((r * D + c * C::EPC) * (int)sizeof(T));
+    }
+  }
+  // rows r0 .. r0 + 31 of src -> lds (r0 < nrows)
+  __device__ __forceinline__ void request(void* lds, const T* src, int r0, int nrows, int tid) const {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const T* base = src + (int64_t)r0 * D;
+    const int last = nrows - 1 - r0;   // last row of the tile inside the source
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int first = (j * NTH + 64 * w) % C::ROW_CHUNKS;
+      uint32_t o = off[j];
+      if (last < 31 && row[j] > last) o -= (uint32_t)((row[j] - last) * D * (int)sizeof(T));
+      lds_dma16_sbase(base, o, (char*)lds + 16 * first);
+    }
+  }
+};
+
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Wait for this wave's LDS operations only (lgkmcnt 0; vmcnt and expcnt at

@@ -15,13 +15,14 @@
 //     chunk order), so every sum has a fixed order.
 //  3. every F tiles (and after the last) the tiles' tokens fold into the
 //     selection blocks: imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d,
-//     tokens ascending; F is the most tiles whose blocks (for both queries)
-//     fit one lane each.
+//     tokens ascending, one lane per block for both queries; F is the most
+//     tiles whose blocks fit the wave's lanes.
 //  4. per query: score = +inf for forced blocks, -FLT_MAX for blocks not yet
 //     complete, else imp_slc; the order keys of the scores, KPL per lane in
 //     registers (block lane + 64 k), give S picks, each the highest score by
 //     a wave max and, among equal scores, the lowest block index by a wave
-//     min; a picked key is zeroed.
+//     min; a picked key is zeroed.  The two queries' picks interleave (two
+//     independent dependency chains) when their keys fit the registers.
 #include "nsa_launch.h"
 #include "nsa_tile32.h"
 
@@ -62,8 +63,8 @@ __device__ __forceinline__ void wave_fence() {
 
 constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
 constexpr int kImpFold = 8;               // tokens read per step of a block's fold
-constexpr int kImpFoldTiles = 4;          // most tiles per fold
-constexpr int kImpStages = 4;             // K tiles in flight + 1
+constexpr int kImpFoldTiles = 8;          // most tiles per fold
+constexpr int kImpStages = 3;             // K tiles in flight + 1
 constexpr int kImpQPB = 4 * kImpQPW;      // queries per workgroup
 
 // last pooled token visible to t (-1: none)
@@ -76,8 +77,8 @@ __device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) 
 // x / 2^sh when sh >= 0 (x >= 0), else x / d
 __device__ __forceinline__ int div_sh(int x, int d, int sh) { return sh >= 0 ? x >> sh : x / d; }
 
-// LDS: K tiles [kImpStages][32][D], per-wave token scratch [4][2][32], block
-// sums [8][nsp].  cd_sh / ls_sh: log2 of cd / ls when they are powers of two,
+// LDS: K tiles [kImpStages][32][D], per-wave token scratch [4][32 F][2]
+// (both queries' values of a token side by side), block sums [8][nsp].  cd_sh / ls_sh: log2 of cd / ls when they are powers of two,
 // else -1 (the block fold then divides); rcd = 1 / cd scales the overlap
 // weights; fold_tiles: F above (1 .. kImpFoldTiles).  KPL:
 // block keys per lane in the top-S phase (n_slc <= 64 * KPL).
@@ -91,8 +92,8 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
   constexpr int NST = kImpStages;
   extern __shared__ __align__(16) char smem[];
   T* sK = reinterpret_cast<T*>(smem);                                   // [NST][ROW_ELEMS]
-  float* stok = reinterpret_cast<float*>(sK + NST * C::ROW_ELEMS);      // [4][2][32 F]
-  float* sblk = stok + 4 * kImpQPW * 32 * kImpFoldTiles;                 // [8][nsp]
+  float2* stok = reinterpret_cast<float2*>(sK + NST * C::ROW_ELEMS);    // [4][32 F]
+  float* sblk = reinterpret_cast<float*>(stok + 4 * 32 * kImpFoldTiles); // [8][nsp]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // long rows first: workgroups go out round-robin, the latest queries first
@@ -111,19 +112,12 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
 
   for (int i = tid; i < kImpQPB * nsp; i += 256) sblk[i] = 0.0f;
   const T* kbase = kc + (int64_t)bh * n_cmp * D;
-  auto load_tile = [&](int kt) {
-    dma_tile_uniform<256, C::ROW_CHUNKS>(sK + (kt % NST) * C::ROW_ELEMS, [&](int P) {
-      int r, cc;
-      nrow_chunk<T, D>(P, r, cc);
-      int tok = kt * 32 + r;
-      tok = tok < n_cmp ? tok : n_cmp - 1;
-      return (const void*)(kbase + (int64_t)tok * D + cc * C::EPC);
-    }, tid);
-  };
+  RowTileDma<T, D, 256, true> kdma;
+  kdma.init(tid);
+  auto load_tile = [&](int kt) { kdma.request(sK + (kt % NST) * C::ROW_ELEMS, kbase, kt * 32, n_cmp, tid); };
 
   // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
-  const int tpq = 32 * fold_tiles;   // token slots per query
-  float* my_tok = stok + w * kImpQPW * tpq;
+  float2* my_tok = stok + w * 32 * kImpFoldTiles;
   float* my_blk = sblk + w * kImpQPW * nsp;
   Frag<T> qf[C::KS];
   float lse2[16];
@@ -171,9 +165,9 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       float part[kImpQPW];
 #pragma unroll
       for (int i = 0; i < kImpQPW; ++i) {
-        float acc = 0.0f;
+        float acc = fast_exp2(sacc[8 * i] * sl2 - lse2[8 * i]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc += fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
+        for (int j = 1; j < 8; ++j) acc += fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
         part[i] = tok <= hi_q[i] ? acc : 0.0f;   // tokens the query cannot see
       }
       // heads 8h .. 8h+7 of each row are in lane half h: the half swap gives
@@ -185,37 +179,38 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
                                                          false);
         part[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
       }
-      // lane half h keeps query h's value for token `tok`
-      const float mine = h == 0 ? part[0] : part[1];
-      float* slot = my_tok + h * tpq + (kt % fold_tiles) * 32 + n;
-      if (hc == 0)
-        *slot = mine;
-      else
-        *slot += mine;
+      // lane half 0 keeps both queries' values for token `tok`
+      static_assert(kImpQPW == 2, "a token slot holds two queries");
+      if (h == 0) {
+        float2* slot = my_tok + (kt % fold_tiles) * 32 + n;
+        if (hc == 0) {
+          *slot = make_float2(part[0], part[1]);
+        } else {
+          const float2 o = *slot;
+          *slot = make_float2(o.x + part[0], o.y + part[1]);
+        }
+      }
     }
     if (kt % fold_tiles != fold_tiles - 1 && kt != ntile - 1) return;
     wave_fence();
     // fold the last tiles' tokens into the blocks they overlap, tokens
-    // ascending; lane = (query, block of the tokens' span); the block's tokens
-    // are read kImpFold at a time so their LDS reads overlap
+    // ascending; lane = block of the tokens' span (both queries); the block's
+    // tokens are read kImpFold at a time so their LDS reads overlap
     const int i0 = (kt - kt % fold_tiles) * 32;
     const int i1 = kt * 32 + 31 < n_cmp - 1 ? kt * 32 + 31 : n_cmp - 1;
     const int jlo = div_sh(i0 * cd, ls, ls_sh);
     int jhi = div_sh(i1 * cd + cl - 1, ls, ls_sh);
     jhi = jhi < n_slc - 1 ? jhi : n_slc - 1;
-    const int nj = jhi - jlo + 1;
-    static_assert(kImpQPW == 2, "lane -> (query, block) split below assumes two queries");
-    for (int u = lane; u < kImpQPW * nj; u += kWave) {
-      const int qi = u >= nj ? 1 : 0, j = jlo + u - qi * nj;
+    for (int j = jlo + lane; j <= jhi; j += kWave) {
       // tokens whose span [i*cd, i*cd+cl) meets [j*ls, (j+1)*ls)
       int a_i = j * ls - cl + 1 <= 0 ? 0 : div_sh(j * ls - cl + 1 + cd - 1, cd, cd_sh);
       int b_i = div_sh((j + 1) * ls - 1, cd, cd_sh);
       a_i = a_i > i0 ? a_i : i0;
       b_i = b_i < i1 ? b_i : i1;
-      const float* tq = my_tok + qi * tpq - i0;
-      float sj = my_blk[qi * nsp + j];
+      const float2* tq = my_tok - i0;
+      float s0 = my_blk[j], s1 = my_blk[nsp + j];
       for (int ib = a_i; ib <= b_i; ib += kImpFold) {
-        float v[kImpFold];
+        float2 v[kImpFold];
 #pragma unroll
         for (int x = 0; x < kImpFold; ++x) v[x] = tq[ib + x <= b_i ? ib + x : b_i];
 #pragma unroll
@@ -223,55 +218,72 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
           const int i = ib + x;
           const int a = i * cd > j * ls ? i * cd : j * ls;
           const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
-          if (i <= b_i && e > a) sj += v[x] * ((float)(e - a) * rcd);
+          if (i <= b_i && e > a) {
+            const float wgt = (float)(e - a) * rcd;
+            s0 += v[x].x * wgt;
+            s1 += v[x].y * wgt;
+          }
         }
       }
-      my_blk[qi * nsp + j] = sj;
+      my_blk[j] = s0;
+      my_blk[nsp + j] = s1;
     }
     wave_fence();
   });
   __syncthreads();
 
   // per query of this wave: scores, masking and forcing, then top-S
-  for (int qi = 0; qi < kImpQPW; ++qi) {
-    const int t = tq0 + qi;
-    if (t >= T_) break;
-    const int64_t r = (int64_t)bh * T_ + t;
-    const float* sc = my_blk + qi * nsp;
-    const int tb = t / ls;
-    uint32_t key[KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
+  constexpr int QIL = KPL <= 16 ? kImpQPW : 1;   // queries whose picks interleave
+  for (int q0 = 0; q0 < kImpQPW; q0 += QIL) {
+    uint32_t key[QIL][KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
+    bool live[QIL];
+    int32_t* orow[QIL];
+    int pick[QIL];
 #pragma unroll
-    for (int k = 0; k < KPL; ++k) {
-      const int j = lane + kWave * k;
-      key[k] = 0;
-      if (j < n_slc) {
-        const float s = sc[j];
-        if (scores != nullptr) scores[r * n_slc + j] = s;
-        const bool valid = (j + 1) * ls - 1 <= t;
-        const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
-        key[k] = order_key(forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f));
+    for (int u = 0; u < QIL; ++u) {
+      const int t = tq0 + q0 + u;
+      live[u] = t < T_;
+      const int64_t r = (int64_t)bh * T_ + t;
+      orow[u] = out_idx + r * S;
+      pick[u] = 0;
+      const float* sc = my_blk + (q0 + u) * nsp;
+      const int tb = t / ls;
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) {
+        const int j = lane + kWave * k;
+        key[u][k] = 0;
+        if (live[u] && j < n_slc) {
+          const float s = sc[j];
+          if (scores != nullptr) scores[r * n_slc + j] = s;
+          const bool valid = (j + 1) * ls - 1 <= t;
+          const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
+          key[u][k] = order_key(forced ? __builtin_inff() : (valid ? s : -3.4028234663852886e38f));
+        }
       }
     }
     // pick s lands in lane s % 64 and is stored with the group of 64 it ends
-    int32_t* orow = out_idx + r * S;
-    int pick = 0;
     for (int s = 0; s < S; ++s) {
-      uint32_t m = key[0];
 #pragma unroll
-      for (int k = 1; k < KPL; ++k) m = key[k] > m ? key[k] : m;
-      int kb = 0;   // this lane's lowest k holding m
+      for (int u = 0; u < QIL; ++u) {
+        uint32_t m = key[u][0];
 #pragma unroll
-      for (int k = KPL - 1; k > 0; --k) kb = key[k] == m ? k : kb;
-      kb = key[0] == m ? 0 : kb;
-      const uint32_t top = wave_reduce_u32<true>(m);
-      const int jw = (int)__builtin_amdgcn_readfirstlane(
-          (int)wave_reduce_u32<false>(m == top ? (uint32_t)(lane + kWave * kb) : 0xFFFFFFFFu));
-      pick = lane == (s & (kWave - 1)) ? jw : pick;
-      const bool own = lane == (jw & (kWave - 1));
+        for (int k = 1; k < KPL; ++k) m = key[u][k] > m ? key[u][k] : m;
+        int kb = 0;   // this lane's lowest k holding m
 #pragma unroll
-      for (int k = 0; k < KPL; ++k) key[k] = own && k == jw / kWave ? 0u : key[k];
+        for (int k = KPL - 1; k > 0; --k) kb = key[u][k] == m ? k : kb;
+        kb = key[u][0] == m ? 0 : kb;
+        const uint32_t top = wave_reduce_u32<true>(m);
+        const int jw = (int)__builtin_amdgcn_readfirstlane(
+            (int)wave_reduce_u32<false>(m == top ? (uint32_t)(lane + kWave * kb) : 0xFFFFFFFFu));
+        pick[u] = lane == (s & (kWave - 1)) ? jw : pick[u];
+        const bool own = lane == (jw & (kWave - 1));
+#pragma unroll
+        for (int k = 0; k < KPL; ++k) key[u][k] = own && k == jw / kWave ? 0u : key[u][k];
+      }
       if ((s & (kWave - 1)) == kWave - 1 || s == S - 1) {
-        if (lane <= (s & (kWave - 1))) orow[(s & ~(kWave - 1)) + lane] = pick;
+#pragma unroll
+        for (int u = 0; u < QIL; ++u)
+          if (live[u] && lane <= (s & (kWave - 1))) orow[u][(s & ~(kWave - 1)) + lane] = pick[u];
       }
     }
   }
@@ -297,6 +309,7 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const int nsp = n_slc + 1;   // per-query block-sum pitch (odd: spreads the 8 queries over banks)
   const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)kImpStages * 32 * D;
   const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 * kImpFoldTiles + (size_t)kImpQPB * nsp);
+  static_assert(kImpQPW == 2, "token scratch holds float2 per token");
   NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
   const int nqb = (T + kImpQPB - 1) / kImpQPB;
   const int64_t grid = (int64_t)B * Hkv * nqb;
@@ -305,12 +318,12 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const int cd_sh = (cmp_stride & (cmp_stride - 1)) == 0 ? __builtin_ctz(cmp_stride) : -1;
   const int ls_sh = (sel_block & (sel_block - 1)) == 0 ? __builtin_ctz(sel_block) : -1;
   const float rcd = 1.0f / (float)cmp_stride;
-  // tiles per fold: the most (up to kImpFoldTiles) whose tokens' blocks, for
-  // both queries of a wave, fit the wave's lanes
+  // tiles per fold: the most (up to kImpFoldTiles) whose tokens' blocks fit
+  // the wave's lanes
   int fold_tiles = 1;
   for (int f = 2; f <= kImpFoldTiles; ++f) {
     const int64_t span = (int64_t)(32 * f - 1) * cmp_stride + cmp_block;   // positions the tokens cover
-    if (kImpQPW * ((span - 1) / sel_block + 2) <= 64) fold_tiles = f;
+    if ((span - 1) / sel_block + 2 <= 64) fold_tiles = f;
   }
   // block keys per lane in the top-S phase
   const int kpl = n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : 64;
