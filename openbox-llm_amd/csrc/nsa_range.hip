@@ -51,52 +51,6 @@ __device__ __forceinline__ void visible_range(int mode, int t, int Lk, int windo
   }
 }
 
-// DMA of one 32-key tile into LDS: a row tile of keys kb .. kb+31 from a
-// row-major [Lk][D] tensor (keys past the end read the last key: finite data
-// no row sees) and a column tile from a transposed [D][Lp] copy.
-template <typename T, int D>
-__device__ __forceinline__ void dma_key_rows(T* lds, const T* src, int kb, int Lk, int tid) {
-  using C = Tile32<T, D>;
-  dma_tile<256, C::ROW_CHUNKS>(lds, [&](int P) {
-    int r, c;
-    row_chunk<T, D>(P, r, c);
-    const int key = kb + r < Lk ? kb + r : Lk - 1;
-    return (const void*)(src + (int64_t)key * D + c * C::EPC);
-  }, tid);
-}
-
-template <typename T, int D>
-__device__ __forceinline__ void dma_key_cols(T* lds, const T* src, int kb, int Lp, int tid) {
-  using C = Tile32<T, D>;
-  dma_tile<256, C::COL_CHUNKS>(lds, [&](int P) {
-    int d, c;
-    col_chunk<T, D>(P, d, c);
-    return (const void*)(src + (int64_t)d * Lp + kb + c * C::EPC);
-  }, tid);
-}
-
-// The same tiles through the asm DMA with a uniform per-wave load count
-// (dma_tile_uniform), for partial vmcnt waits over several stages.
-template <typename T, int D>
-__device__ __forceinline__ void dma_key_rows_u(T* lds, const T* src, int kb, int Lk, int tid) {
-  using C = Tile32<T, D>;
-  dma_tile_uniform<256, C::ROW_CHUNKS>(lds, [&](int P) {
-    int r, c;
-    row_chunk<T, D>(P, r, c);
-    const int key = kb + r < Lk ? kb + r : Lk - 1;
-    return (const void*)(src + (int64_t)key * D + c * C::EPC);
-  }, tid);
-}
-template <typename T, int D>
-__device__ __forceinline__ void dma_key_cols_u(T* lds, const T* src, int kb, int Lp, int tid) {
-  using C = Tile32<T, D>;
-  dma_tile_uniform<256, C::COL_CHUNKS>(lds, [&](int P) {
-    int d, c;
-    col_chunk<T, D>(P, d, c);
-    return (const void*)(src + (int64_t)d * Lp + kb + c * C::EPC);
-  }, tid);
-}
-
 // Workgroup / wave query and key ranges of a range launch.
 struct RangeSpan {
   int klo, khi;     // union of visible keys of the workgroup's queries
@@ -301,10 +255,8 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int s = 0; s < 2; ++s) lds_col_frag<T, D>(va[dt][s], tV, dt, n, h, s);
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) st[nt][r] *= sl2;
+  // st holds raw scores: the scale (> 0) is applied to the row maximum and
+  // inside the exponent's fma
   if (mask) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -321,7 +273,7 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
     float v = st[nt][0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) v = fmaxf(v, st[nt][r]);
-    mx[nt] = fmaxf(v, __shfl_xor(v, 32, kWave));
+    mx[nt] = fmaxf(v, __shfl_xor(v, 32, kWave)) * sl2;
     need |= mx[nt] > m_[nt] + kRescale;
   }
   if (__any(need)) {
@@ -342,7 +294,7 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
     float ps = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = fast_exp2(st[nt][r] - m_[nt]);
+      p[r] = fast_exp2(st[nt][r] * sl2 - m_[nt]);
       ps += p[r];
     }
     l_[nt] += ps;
@@ -430,10 +382,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) settle(qf[nt][s]);
-  constexpr int LT = dma_uniform_loads<256, C::ROW_CHUNKS>() + dma_uniform_loads<256, C::COL_CHUNKS>();
+  RowTileDma<T, D, 256, false> kdma;
+  ColTileDma<T, D, 256> vdma;
+  kdma.init(tid);
+  vdma.init(tid, Lp);
+  constexpr int LT = decltype(kdma)::NL + decltype(vdma)::NL;
   key_pipeline<NST, LT>(ntile, [&](int i) {
-    dma_key_rows_u<T, D>(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
-    dma_key_cols_u<T, D>(sV[i % NST], vtbase, kt0 + 32 * i, Lp, tid);
+    kdma.request(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
+    vdma.request(sV[i % NST], vtbase, kt0 + 32 * i, tid);
   }, [&](int it) {
     const int kb = kt0 + 32 * it;
     // every wave takes every tile of the workgroup range (the waves' own ranges
@@ -605,11 +561,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int s = 0; s < C::KS; ++s) settle(qf[nt][s]), settle(df[nt][s]);
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(c[nt]), "+v"(dlt[nt]));
-  constexpr int LT = 2 * dma_uniform_loads<256, C::ROW_CHUNKS>() + dma_uniform_loads<256, C::COL_CHUNKS>();
+  RowTileDma<T, D, 256, false> rdma;   // K and V rows share the per-lane offsets
+  ColTileDma<T, D, 256> ktdma;
+  rdma.init(tid);
+  ktdma.init(tid, Lp);
+  constexpr int LT = 2 * decltype(rdma)::NL + decltype(ktdma)::NL;
   key_pipeline<NST, LT>(ntile, [&](int i) {
-    dma_key_rows_u<T, D>(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
-    dma_key_rows_u<T, D>(sV[i % NST], vbase, kt0 + 32 * i, Lk, tid);
-    dma_key_cols_u<T, D>(sKt[i % NST], ktbase, kt0 + 32 * i, Lp, tid);
+    rdma.request(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
+    rdma.request(sV[i % NST], vbase, kt0 + 32 * i, Lk, tid);
+    ktdma.request(sKt[i % NST], ktbase, kt0 + 32 * i, tid);
   }, [&](int it) {
     const int kb = kt0 + 32 * it;
     const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);

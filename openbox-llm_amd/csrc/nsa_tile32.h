@@ -312,6 +312,33 @@ struct RowTileDma {
   }
 };
 
+// The same for [D][32] column tiles of a transposed [D][Lp] source (keys kb ..
+// kb + 31 of every row d; Lp covers every requested key, no clamping).
+template <typename T, int D, int NTH>
+struct ColTileDma {
+  using C = Tile32<T, D>;
+  static constexpr int NL = dma_uniform_loads<NTH, C::COL_CHUNKS>();
+  uint32_t off[NL];
+  __device__ __forceinline__ void init(int tid, int Lp) {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int P = (j * NTH + 64 * w) % C::COL_CHUNKS + lane;
+      int d, c;
+      col_chunk<T, D>(P, d, c);
+      off[j] = (uint32_t)((d * Lp + c * C::EPC) * (int)sizeof(T));
+    }
+  }
+  __device__ __forceinline__ void request(void* lds, const T* src, int kb, int tid) const {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+      const int first = (j * NTH + 64 * w) % C::COL_CHUNKS;
+      lds_dma16_sbase(src + kb, off[j], (char*)lds + 16 * first);
+    }
+  }
+};
+
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Wait for this wave's LDS operations only (lgkmcnt 0; vmcnt and expcnt at
