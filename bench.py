@@ -153,7 +153,22 @@ def run_gpu(args, w):
     ops.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
     spans = timer.summary_ms()
-    return ms, spans, flops_of, kv, ins, do
+    # untimed: the same steps with the backward's streams serialised, so that
+    # each kernel's duration is its own (the timed steps overlap the selection
+    # dK/dV with the range dK/dV kernels)
+    iso = ops.LaunchTimer()
+    ops.OVERLAP_SEL_BWD = False
+    try:
+        step()
+        torch.cuda.synchronize()
+        ops.set_timer(iso)
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        ops.set_timer(None)
+        ops.OVERLAP_SEL_BWD = True
+    return ms, spans, iso.summary_ms(), flops_of, kv, ins, do
 
 
 def run_cpu_baseline(w, ins_dev, do_dev, rows_n, threads):
@@ -239,7 +254,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     w = WORKLOADS[args.workload]
-    ms, spans, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
+    ms, spans, iso_spans, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
     tokens = w["B"] * w["T"]
     value = tokens / (ms / 1e3)
     total_flops = sum(flops_of.values())
@@ -262,6 +277,13 @@ def main():
                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                     "traffic": MEASURED_TRAFFIC.get((args.workload, name)),
                     "launch_ms": round(per_launch_s * 1e3, 4)}
+        if name in iso_spans:
+            # the same kernel with nothing beside it (untimed serialised steps)
+            icalls, itot = iso_spans[name]
+            iso_s = itot / icalls / 1e3
+            roofline["isolated"] = {"launch_ms": round(iso_s * 1e3, 4),
+                                    "achieved": round(flops_of[name] / iso_s / 1e12, 2),
+                                    "frac": round(flops_of[name] / iso_s / 1e12 / PEAK_BF16_TFLOPS, 4)}
     cpu = None
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)

@@ -138,6 +138,23 @@ def _stream(t):
     return L.stream_of(t)
 
 
+_SIDE_STREAMS = {}
+
+# The fused backward runs the selection dK/dV on a side stream, beside the
+# window and compression key-side kernels; False runs everything in order on
+# the current stream (per-kernel timings then describe each kernel alone).
+OVERLAP_SEL_BWD = True
+
+
+def _side_stream(device):
+    """A second stream per device (default priority) for work that overlaps the
+    current stream's."""
+    key = torch.device(device).index
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=device)
+    return _SIDE_STREAMS[key]
+
+
 def padded_len(n):
     return int(_lib().nsa_padded_len(int(n)))
 
@@ -708,20 +725,40 @@ class NSAFusedHIP(torch.autograd.Function):
         dot, rs, coff, dgate, dop = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w,
                                                   pack_hkv=ks.shape[1] if idx.shape[-1] > 0 else 0)
         dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        # selection dK/dV and dQ partials (block-outer, bound by memory traffic)
+        # run on a side stream beside the window and compression key-side
+        # kernels (bound by MFMA issue) on the current stream
+        main = torch.cuda.current_stream(q.device)
+        dq_part = None
+        if idx.shape[-1] > 0:
+            side = _side_stream(q.device) if OVERLAP_SEL_BWD else main
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
+                                             csr=tuple(csr), want_dq=True, qp=qp, dop=dop)
+            # inputs read on the side stream keep their memory until its work is done
+            for t in (q, ks, vs, dout, coff, dot, idx, qp, dop, *csr):
+                t.record_stream(side)
+        else:
+            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
+            dvs = torch.zeros_like(dks)
         # window
         kt_w = transpose_kv(kw)
         range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
         dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
-        # selection: dK/dV and the dQ partials block-outer
-        dq_part = None
-        if idx.shape[-1] > 0:
-            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                         csr=tuple(csr), want_dq=True, qp=qp, dop=dop)
+        # compression dK/dV
+        if k_cmp.shape[2] > 0:
+            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
+                                  geom.cmp_block, geom.cmp_stride)
         else:
-            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
-            dvs = torch.zeros_like(dks)
-        # compression; its dQ kernel finishes the rows: window dQ + its own +
-        # the selection partials, written in the input dtype
+            dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
+            dvp = torch.zeros_like(dkp)
+        if dq_part is not None and side is not main:
+            main.wait_stream(side)
+            for t in (dks, dvs, dq_part):
+                t.record_stream(main)
+        # compression dQ; it finishes the rows: window dQ + its own + the
+        # selection partials, written in the input dtype
         if k_cmp.shape[2] > 0:
             kt_c = transpose_kv(k_cmp)
             if dq_part is not None:
@@ -732,11 +769,7 @@ class NSAFusedHIP(torch.autograd.Function):
                 range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
                          geom.cmp_block, geom.cmp_stride)
                 dq_out = cast_f32(dq, dtype)
-            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
-                                  geom.cmp_block, geom.cmp_stride)
         else:
-            dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
-            dvp = torch.zeros_like(dkp)
             dq_out = (sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype) if dq_part is not None
                       else cast_f32(dq, dtype))
         if ctx.pooled:

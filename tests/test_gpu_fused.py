@@ -193,6 +193,41 @@ def test_nsa_attention_baseline_geometry(shape, dtype):
         assert_close(x.grad, gr, dtype, f"d{nm}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_nsa_attention_overlapped_backward_matches_serial(dtype):
+    """The backward with the selection dK/dV on a side stream gives the
+    gradients of the backward run in order on one stream (up to the order of
+    the float atomics), over several steps back to back."""
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    import nsa_hip_ops as ops
+    shape = SMALL_BASELINE_SHAPES[1]
+    B, Hq, Hkv, T, D = (shape[x] for x in ("B", "Hq", "Hkv", "T", "D"))
+    geom = ops.NSAGeometry(**BASELINE_GEOM)
+    ins, do = _fused_inputs(B, Hq, Hkv, T, D, dtype, seed=11, head_scale=True)
+    do = do.to(dev)
+
+    def grads(overlap):
+        ops.OVERLAP_SEL_BWD = overlap
+        try:
+            res = []
+            for _ in range(3):
+                xs = [t.to(dev).requires_grad_() for t in ins]
+                out, _ = nfk.nsa_attention(*xs, geom)
+                out.backward(do)
+                res.append([x.grad.float().cpu() for x in xs])
+            torch.cuda.synchronize()
+            return res
+        finally:
+            ops.OVERLAP_SEL_BWD = True
+
+    serial = grads(False)
+    overlapped = grads(True)
+    for step in range(3):
+        for nm, a, b in zip(NAMES, overlapped[step], serial[0]):
+            assert_close(a, b, dtype, f"step {step} d{nm}")
+
+
 def test_csr_bit_exact():
     dev = require_gpu()
     import nsa_fsa
