@@ -493,7 +493,7 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   __shared__ __align__(16) T sdT[2][64 * 32];            // double-buffered by tile parity
   __shared__ int32_t sent[kSelItemMax];                  // the item's CSR entries
   // dQ^T partial stores per post and wave (a lower bound over the waves)
-  constexpr int NSW = D >= 64 ? DTW * 4 : 0;
+  constexpr int NSW = D >= 64 ? DTW * 2 : 0;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, true);   // packed Q / dO
@@ -520,7 +520,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
     for (int i = tid; i < cnt; i += NTH) sent[i] = q_of_block[beg + i];
     KeyAcc<T, D> acc;
     acc.init(k + kvoff, v + kvoff, key_ok ? key : j * L, h);
-    // K^T fragments of the pass's 64 keys for this wave's dQ^T d-tiles
+    // K^T fragments of the pass's 64 keys for this wave's dQ^T d-tiles, rows
+    // in perm32 order (each lane's outputs are then 8 consecutive d: 16-byte
+    // stores)
     Frag<T> ktf[DTW][4];
     if (dq_part != nullptr) {
       const T* ktb = kt + (int64_t)bh * D * Lp;
@@ -528,7 +530,7 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       for (int i = 0; i < DTW; ++i)
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const int d = 32 * (w * DTW + i) + n;
+          const int d = 32 * (w * DTW + i) + perm32(n);
           int c0 = kpass + 16 * kk + 8 * h;
           c0 = c0 < Lp - 8 ? c0 : Lp - 8;
           if (w * DTW + i < DT && (D % 32 == 0 || d < D))
@@ -600,15 +602,17 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       if (t >= 0 && g < G) {
         const int slot = (n < 16 ? sA : sB) * npass + pass;
         T* drow = dq_part + ((((int64_t)bh * T_ + t) * NS + slot) * G + g) * D;
+        // register r of lane half h holds d = 32 (w DTW + d) + acc_elem(h, r)
 #pragma unroll
         for (int d = 0; d < DTW; ++d) {
           if (w * DTW + d >= DT) continue;
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const int dd = 32 * (w * DTW + d) + 8 * g4 + 4 * h;
-            if (D % 32 == 0 || dd < D)
-              store4(drow + dd, dq[d][4 * g4] * scale, dq[d][4 * g4 + 1] * scale, dq[d][4 * g4 + 2] * scale,
-                     dq[d][4 * g4 + 3] * scale);
+          for (int hf = 0; hf < 2; ++hf) {
+            const int dd = 32 * (w * DTW + d) + 16 * hf + 8 * h;
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = dq[d][8 * hf + i] * scale;
+            if (D % 32 == 0 || dd < D) store8(drow + dd, y);
           }
         }
       }

@@ -57,7 +57,7 @@ template <typename T, int D> struct FwdIssuer {
 // float tiles and D < 32 count none, which only lengthens the waits)
 template <typename T, int D>
 constexpr int fwd_bo_stores() {
-  return (sizeof(T) == 2 && D >= 32) ? Tile32<T, D>::DT * 4 + 1 : 0;
+  return (sizeof(T) == 2 && D >= 32) ? Tile32<T, D>::DT * 2 + 1 : 0;
 }
 
 template <typename T, int D>
@@ -91,7 +91,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
     // the item's entries go to LDS once: a global load per tile would be
     // waited for with every tile load in flight
     for (int i = lane; i < cnt; i += 64) sent[i] = q_of_block[beg + i];
-    // block keys: K rows (perm32 order) and V^T, both in registers
+    // block keys: K rows and V^T rows, both in perm32 order and in registers
+    // (the V^T order makes each lane's outputs 8 consecutive d: 16-byte stores)
     Frag<T> kf[2][KS], vf[DT][4];
     const T* kb_ = k + (int64_t)bh * T_ * D;
     const T* vtb = vt + (int64_t)bh * D * Lp;
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        const int d = 32 * dt + n;
+        const int d = 32 * dt + perm32(n);
         int c0 = kbase + 16 * kk + 8 * h;
         c0 = c0 < Lp - 8 ? c0 : Lp - 8;
         if (D % 32 == 0 || d < D)
@@ -223,14 +224,16 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         T* orow = opart + prow * D;
+        // register r of lane half h holds d = 32 dt + acc_elem(h, r)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const int d = 32 * dt + 8 * g4 + 4 * h;
-            if (D % 32 == 0 || d < D)
-              store4(orow + d, acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv, acc[dt][4 * g4 + 2] * inv,
-                     acc[dt][4 * g4 + 3] * inv);
+          for (int hf = 0; hf < 2; ++hf) {
+            const int d = 32 * dt + 16 * hf + 8 * h;
+            float y[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) y[i] = acc[dt][8 * hf + i] * inv;
+            if (D % 32 == 0 || d < D) store8(orow + d, y);
           }
         if (h == 0) mlpart[prow] = make_float2(mx, lt);
       }
