@@ -53,11 +53,12 @@ template <typename T, int D> struct FwdIssuer {
   }
 };
 
-// vector-memory stores of one tile's partials per lane-group (a lower bound:
-// float tiles and D < 32 count none, which only lengthens the waits)
+// vector-memory stores of one tile's partials per wave (a lower bound:
+// float tiles and D < 32 count none, which only lengthens the waits): D / 16
+// staged row stores and the row statistics
 template <typename T, int D>
 constexpr int fwd_bo_stores() {
-  return (sizeof(T) == 2 && D >= 32) ? Tile32<T, D>::DT * 2 + 1 : 0;
+  return (sizeof(T) == 2 && D >= 32) ? D / 16 + 1 : 0;
 }
 
 template <typename T, int D>
@@ -75,6 +76,10 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
   static_assert((NST - 1) * (LT + NSW) < 64, "in-flight operations exceed the vmcnt range");
   __shared__ __align__(16) T sQ[NST][C::ROW_ELEMS];
   __shared__ int32_t sent[kSelItemMax];   // the item's CSR entries
+  // the tile's output rows, staged so that they leave as whole rows (bf16);
+  // 16-byte chunk c of row r sits at chunk c ^ (r % CPR)
+  constexpr int CPR = D * (int)sizeof(T) / 16;
+  __shared__ __align__(16) T sO[sizeof(T) == 2 ? 32 * D : 8];
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
   const int G = Hq / Hkv, NHC = (G + 15) / 16;
   const int NS = S * nsub;
@@ -220,9 +225,56 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       // refill the stage once its reads are complete
       lds_reads_done();
       if (pix < total) request(sQ[ix % NST]);
-      if (rok) {
+      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      if constexpr (sizeof(T) == 2) {
+        // stage the rows (register r of lane half h holds d = 32 dt +
+        // acc_elem(h, r)), then store them as whole rows: 64 lanes write 4
+        // rows of 256 B per instruction.  A row that does not exist takes the
+        // place of row 0 (always a real row: query A, first head of the
+        // chunk) and rewrites its bytes, so every store instruction issues.
+        wave_fence();   // the previous tile's rows are read out
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int c = 4 * dt + 2 * hf + h;
+            if (D % 32 == 0 || c < CPR) {
+              bf16x8 v;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) v[i] = (bf16)(acc[dt][8 * hf + i] * inv);
+              *reinterpret_cast<bf16x8*>(sO + (n * CPR + (c ^ (n % CPR))) * 8) = v;
+            }
+          }
+        wave_fence();
+        // rows 0-15: query A, rows 16-31: query B, each 16 heads of G D
+        // contiguous from the (query, slot) row base.  Rows that do not
+        // exist repeat an existing row's bytes: a missing query B those of
+        // query A, a head past G head 0 of its query.  Every store
+        // instruction then issues, and for D >= 32 each one stays in one
+        // query's rows, so its base address is uniform.
+        const int uA = __builtin_amdgcn_readfirstlane(tA), uB = __builtin_amdgcn_readfirstlane(tB);
+        const int usA = __builtin_amdgcn_readfirstlane(sA), usB = __builtin_amdgcn_readfirstlane(sB);
+        const T* baseA = opart + ((((int64_t)bh * T_ + uA) * NS + usA * nsub + pass) * G + hc * 16) * D;
+        const T* baseB = uB >= 0 ? opart + ((((int64_t)bh * T_ + uB) * NS + usB * nsub + pass) * G + hc * 16) * D
+                                 : baseA;
+        const int grem = G - hc * 16;   // heads of the chunk that exist
+        constexpr int RPI = 64 / CPR;   // rows per store instruction
+        const int c = lane % CPR;
+#pragma unroll
+        for (int i = 0; i < 32 / RPI; ++i) {
+          const int r = RPI * i + lane / CPR;
+          int rr = uB < 0 && r >= 16 ? r - 16 : r;
+          rr = (rr & 15) < grem ? rr : rr & 16;
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+          T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
+          *reinterpret_cast<bf16x8*>(dst) = v;
+        }
+        if (rok && h == 0) {
+          const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
+          mlpart[prow] = make_float2(mx, lt);
+        }
+      } else if (rok) {
         const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         T* orow = opart + prow * D;
         // register r of lane half h holds d = 32 dt + acc_elem(h, r)
 #pragma unroll

@@ -341,6 +341,13 @@ struct ColTileDma {
 
 __device__ __forceinline__ void lds_dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
+// LDS written by some lanes of a wave and read by others: the writes are
+// visible after this (a wave-scope fence and barrier).
+__device__ __forceinline__ void wave_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Wait for this wave's LDS operations only (lgkmcnt 0; vmcnt and expcnt at
 // their maxima): a stage's reads are complete before a DMA refills it.
 __device__ __forceinline__ void lds_reads_done() { __builtin_amdgcn_s_waitcnt(0xC07F); }

@@ -56,11 +56,6 @@ __device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x) {
   return x;
 }
 
-__device__ __forceinline__ void wave_fence() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-}
-
 constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
 constexpr int kImpFold = 8;               // tokens read per step of a block's fold
 constexpr int kImpFoldTiles = 8;          // most tiles per fold
