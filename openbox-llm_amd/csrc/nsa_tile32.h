@@ -20,11 +20,12 @@
 // 16-byte chunks are XOR-swizzled per row so that the fragment reads of a
 // wave hit distinct banks:
 //   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r),
-//                        rkey(r) = 2 (r & 3) + bit 3 of r: the 8 rows perm32
-//                        gives 8 adjacent lanes get 8 distinct keys, and 4
-//                        consecutive rows get keys 2 apart, so the 32-byte
-//                        pieces a transposed read takes from them (lds_tr_frag)
-//                        land on disjoint banks
+//                        rkey(r) = 2 (r & 3) + bit 3 of r + 8 bit 2 of r: the
+//                        16 rows perm32 gives 16 adjacent lanes get 16
+//                        distinct keys (fewer when a row has fewer chunks),
+//                        and 4 consecutive rows get keys 2 apart, so the
+//                        32-byte pieces a transposed read takes from them
+//                        (lds_tr_frag) land on disjoint banks
 //   column tile [D][32]: logical chunk c of row d sits at c ^ ckey(d)
 //
 // Transposed operands (a contraction over the tile's rows) come straight from
@@ -73,10 +74,16 @@ template <typename T, int D> struct Tile32 {
   static constexpr int COL_ELEMS = D * 32;                 // one [D][32] tile
   static constexpr int ROW_CHUNKS = 32 * RCH;
   static constexpr int COL_CHUNKS = D * CCH;
-  static __device__ __forceinline__ int rkey(int r) { return (((r & 3) << 1) | ((r >> 3) & 1)) & (RCH - 1); }
-  // row tiles read in natural row order (lanes 0..7 read rows 0..7)
-  static __device__ __forceinline__ int nkey(int r) { return r & 7 & (RCH - 1); }
-  static __device__ __forceinline__ int ckey(int d) { return (CCH == 4 ? (d >> 1) : d) & (CCH - 1); }
+  // gfx950 serves a 16-byte-per-lane LDS read 16 lanes (256 bytes, every
+  // bank once) at a time: the keys give the rows that 16 adjacent lanes read
+  // distinct chunks (rows sharing a 256-byte line: the same key, different
+  // halves or quarters of the line)
+  static __device__ __forceinline__ int rkey(int r) {
+    return (((r & 3) << 1) | ((r >> 3) & 1) | (((r >> 2) & 1) << 3)) & (RCH - 1);
+  }
+  // row tiles read in natural row order (lanes 0..15 read rows 0..15)
+  static __device__ __forceinline__ int nkey(int r) { return (RCH >= 16 ? r : r / (16 / RCH)) & (RCH - 1); }
+  static __device__ __forceinline__ int ckey(int d) { return (d / (16 / CCH)) & (CCH - 1); }
 };
 
 // A fragment of a [32][D] row tile: permuted row, contraction step s
