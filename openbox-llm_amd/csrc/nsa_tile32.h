@@ -19,13 +19,14 @@
 // (global_load_lds_dwordx4: lane i of a wave writes LDS base + 16 i).  Their
 // 16-byte chunks are XOR-swizzled per row so that the fragment reads of a
 // wave hit distinct banks:
-//   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r),
-//                        rkey(r) = 2 (r & 3) + bit 3 of r + 8 bit 2 of r: the
-//                        16 rows perm32 gives 16 adjacent lanes get 16
-//                        distinct keys (fewer when a row has fewer chunks),
-//                        and 4 consecutive rows get keys 2 apart, so the
-//                        32-byte pieces a transposed read takes from them
-//                        (lds_tr_frag) land on disjoint banks
+//   row tile    [32][D]: logical chunk c of row r sits at c ^ rkey(r).  With
+//                        16 or more chunks per row rkey(r) = 4 (r & 3) +
+//                        ((r >> 2) & 3): the 16 rows 16 adjacent lanes read
+//                        (perm32 or natural order) get 16 distinct keys, and
+//                        the 4 consecutive rows of a transposed read
+//                        (lds_tr_frag, 4 chunks each) keys 4 apart, so its
+//                        16 pieces per 256 bytes are distinct.  Shorter rows:
+//                        rkey(r) = 2 (r & 3) + bit 3 of r, masked
 //   column tile [D][32]: logical chunk c of row d sits at c ^ ckey(d)
 //
 // Transposed operands (a contraction over the tile's rows) come straight from
@@ -79,7 +80,7 @@ template <typename T, int D> struct Tile32 {
   // distinct chunks (rows sharing a 256-byte line: the same key, different
   // halves or quarters of the line)
   static __device__ __forceinline__ int rkey(int r) {
-    return (((r & 3) << 1) | ((r >> 3) & 1) | (((r >> 2) & 1) << 3)) & (RCH - 1);
+    return RCH >= 16 ? 4 * (r & 3) + ((r >> 2) & 3) : (((r & 3) << 1) | ((r >> 3) & 1)) & (RCH - 1);
   }
   // row tiles read in natural row order (lanes 0..15 read rows 0..15)
   static __device__ __forceinline__ int nkey(int r) { return (RCH >= 16 ? r : r / (16 / RCH)) & (RCH - 1); }
