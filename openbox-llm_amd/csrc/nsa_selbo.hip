@@ -189,17 +189,25 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         mma32(st[0], kf[0][s], qb[s]);
         mma32(st[1], kf[1][s], qb[s]);
       }
-      float mx = kNegInfS;
+      // raw scores; the scale (> 0) is applied to the row maximum and inside
+      // the exponent's fma.  Tiles whose 64 keys all exist and precede both
+      // queries (tA <= tB: CSR queries ascend) need no per-element mask.
+      if (!(kbase + 64 <= kend && kbase + 63 <= __builtin_amdgcn_readfirstlane(tA))) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = kbase + 32 * mt + acc_elem(h, r);
+            st[mt][r] = (key < kend && key <= t) ? st[mt][r] : kNegInfS;
+          }
+      }
+      float mr = kNegInfS;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kbase + 32 * mt + acc_elem(h, r);
-          const float x = (key < kend && key <= t) ? st[mt][r] * sl2 : kNegInfS;
-          st[mt][r] = x;
-          mx = fmaxf(mx, x);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        for (int r = 0; r < 16; ++r) mr = fmaxf(mr, st[mt][r]);
+      mr = fmaxf(mr, __shfl_xor(mr, 32, kWave));
+      const float mx = mr == kNegInfS ? kNegInfS : mr * sl2;
       const float ms = mx == kNegInfS ? 0.0f : mx;
       float ps = 0.0f;
       Frag<T> pf[4];
@@ -208,7 +216,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          p[r] = fast_exp2(st[mt][r] - ms);
+          p[r] = fast_exp2(st[mt][r] * sl2 - ms);
           ps += p[r];
         }
         pf[2 * mt].set(p);
