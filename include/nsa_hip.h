@@ -146,8 +146,10 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
  * The FSA forward (replaces _selection_fwd_blockouter_kernel /
  * selection_forward_fsa, nsa_selection_kernel.py:232-365): work items as in
  * nsa_sel_dkdv over a CSR built with pack_slot; for every (query, slot, pass)
- * it writes the block-local output O_j / l_j (input dtype) to o_part and
- * (m_j [log2 units], l_j) float pairs to ml_part, both laid out
+ * it writes the unnormalised block-local output O_j = sum_k p_k v_k (input
+ * dtype; p_k = exp2(s_k - m_j)) to o_part and (m_j [log2 units], l_j = sum_k
+ * p_k) float pairs to ml_part, as the reference's per-pair partials
+ * (nsa_selection_kernel.py:286-290), both laid out
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G] (x D for o_part).
  * q is in the nsa_pack_heads layout [B][Hkv][T][G][D], vt is the
  * nsa_transpose_kv copy of v; chunk <= 512.  Workspace from

@@ -110,7 +110,7 @@ __device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_
 // branch outputs the separate kernels would read.
 template <typename T> struct FwdExtras {
   T* q_packed;             // [B][Hkv][T][G][D] (nullable)
-  const T* opart;          // [B][Hkv][T][NS][G][D] block-local outputs O_j / l_j
+  const T* opart;          // [B][Hkv][T][NS][G][D] unnormalised block-local outputs O_j = sum p v
   const float2* ml;        // [B][Hkv][T][NS][G] (m_j [log2 units], l_j)
   const int32_t* idx;      // [B][Hkv][T][S] selected blocks
   T* o_sel;                // [B][Hq][T][D]
@@ -201,9 +201,11 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T>& f, const f32x16 
       for (int i = 0; i < 8; ++i) acc_s[i] *= rs;
 #pragma unroll
       for (int k2 = 0; k2 < 16; ++k2) {
-        const float wk = ok[k2] ? fast_exp2(ml[k2].x - bm) * ml[k2].y : 0.0f;
+        // the partial is unnormalised; a slot that does not count was maybe
+        // never written, so nothing of it (not even 0 x its l) is used
+        const float wk = ok[k2] ? fast_exp2(ml[k2].x - bm) : 0.0f;
         x[k2].keep_if(ok[k2]);
-        Ls += wk;
+        Ls += ok[k2] ? wk * ml[k2].y : 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc_s[i] += wk * x[k2].get(i);
       }

@@ -233,7 +233,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       // refill the stage once its reads are complete
       lds_reads_done();
       if (pix < total) request(sQ[ix % NST]);
-      const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+      // the partial is the unnormalised block-local output O_j = sum p v; the
+      // merges weight it by exp2(m_j - M) and its l_j by the same
       if constexpr (sizeof(T) == 2) {
         // stage the rows (register r of lane half h holds d = 32 dt +
         // acc_elem(h, r)), then store them as whole rows: 64 lanes write 4
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
             if (D % 32 == 0 || c < CPR) {
               bf16x8 v;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = (bf16)(acc[dt][8 * hf + i] * inv);
+              for (int i = 0; i < 8; ++i) v[i] = (bf16)acc[dt][8 * hf + i];
               *reinterpret_cast<bf16x8*>(sO + (n * CPR + (c ^ (n % CPR))) * 8) = v;
             }
           }
@@ -267,15 +268,26 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
                                  : baseA;
         const int grem = G - hc * 16;   // heads of the chunk that exist
         constexpr int RPI = 64 / CPR;   // rows per store instruction
-        const int c = lane % CPR;
+        const int c = lane % CPR, rl = lane / CPR;
+        if (uB >= 0 && grem >= 16) {
+          // every row exists: the row and its base are fixed per instruction
 #pragma unroll
-        for (int i = 0; i < 32 / RPI; ++i) {
-          const int r = RPI * i + lane / CPR;
-          int rr = uB < 0 && r >= 16 ? r - 16 : r;
-          rr = (rr & 15) < grem ? rr : rr & 16;
-          const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
-          T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
-          *reinterpret_cast<bf16x8*>(dst) = v;
+          for (int i = 0; i < 32 / RPI; ++i) {
+            const int r = RPI * i + rl;
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (r * CPR + (c ^ (r % CPR))) * 8);
+            T* dst = const_cast<T*>(RPI * i < 16 ? baseA : baseB) + ((r & 15) * D + 8 * c);
+            *reinterpret_cast<bf16x8*>(dst) = v;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 32 / RPI; ++i) {
+            const int r = RPI * i + rl;
+            int rr = uB < 0 && r >= 16 ? r - 16 : r;
+            rr = (rr & 15) < grem ? rr : rr & 16;
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+            T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
+            *reinterpret_cast<bf16x8*>(dst) = v;
+          }
         }
         if (rok && h == 0) {
           const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
@@ -292,7 +304,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
             const int d = 32 * dt + 16 * hf + 8 * h;
             float y[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = acc[dt][8 * hf + i] * inv;
+            for (int i = 0; i < 8; ++i) y[i] = acc[dt][8 * hf + i];
             if (D % 32 == 0 || d < D) store8(orow + d, y);
           }
         if (h == 0) mlpart[prow] = make_float2(mx, lt);
@@ -318,7 +330,7 @@ static inline int grid_for(int64_t n) {
 // and weight 0, so whatever an unwritten slot holds never reaches a result.
 constexpr int kSlotBatch = 16;
 
-// o[row] = sum_slots exp2(m - M) l O_slot / sum exp2(m - M) l over the valid
+// o[row] = sum_slots exp2(m - M) O_slot / sum exp2(m - M) l over the valid
 // slots, lse = (M + log2 L) ln 2, with a running maximum M across batches.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const T* __restrict__ opart,
@@ -364,9 +376,11 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
       for (int i = 0; i < 8; ++i) acc[i] *= rs;
 #pragma unroll
       for (int k = 0; k < kSlotBatch; ++k) {
-        const float wk = ok[k] ? fast_exp2(ml[k].x - bm) * ml[k].y : 0.0f;
+        // the partial is unnormalised; a slot that does not count was maybe
+        // never written, so nothing of it (not even 0 x its l) is used
+        const float wk = ok[k] ? fast_exp2(ml[k].x - bm) : 0.0f;
         x[k].keep_if(ok[k]);
-        Ls += wk;
+        Ls += ok[k] ? wk * ml[k].y : 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[i] += wk * x[k].get(i);
       }
