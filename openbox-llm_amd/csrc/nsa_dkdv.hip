@@ -454,15 +454,22 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
                         mode == NSA_MODE_COMPRESS, h);
 }
 
+// x: 16-byte aligned; 16-byte stores for the first n & ~3 elements, the rest one by one
 __global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ x, int64_t n) {
-  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) x[e] = 0.0f;
+  const int64_t n4 = n >> 2;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n4; e += (int64_t)gridDim.x * 256)
+    reinterpret_cast<f32x4*>(x)[e] = zero4();
+  if (blockIdx.x == 0 && threadIdx.x < (n & 3)) x[(n4 << 2) + threadIdx.x] = 0.0f;
 }
 
 // Zero-fill with a kernel (safe inside captured graphs, unlike a memset node).
+// x is the start of a float allocation of this library's callers (16-byte aligned).
 static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
   if (n <= 0) return NSA_OK;
-  int64_t g = (n + 255) / 256;
-  if (g > 65536) g = 65536;
+  if (((uintptr_t)x & 15) != 0) return NSA_ERR_ARG;
+  int64_t g = ((n >> 2) + 255) / 256;
+  if (g > 16384) g = 16384;
+  if (g < 1) g = 1;
   k_fill_zero<<<(unsigned)g, 256, 0, s>>>(x, n);
   return hipGetLastError() == hipSuccess ? NSA_OK : NSA_ERR_LAUNCH;
 }
@@ -658,7 +665,9 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * Lk * D;
   if (mode == NSA_MODE_COMPRESS || T == 0) {
-    if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;
+    int rc = zero_f32(dk, nel, s);
+    if (rc == NSA_OK) rc = zero_f32(dv, nel, s);
+    if (rc != NSA_OK) return rc;
   }
   if (T == 0 || Lk == 0) return NSA_OK;
   const float scale = 1.0f / sqrtf((float)D);
@@ -709,7 +718,11 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
-  if (zero_f32(dk, nel, s) != NSA_OK || zero_f32(dv, nel, s) != NSA_OK) return NSA_ERR_LAUNCH;
+  {
+    int rc = zero_f32(dk, nel, s);
+    if (rc == NSA_OK) rc = zero_f32(dv, nel, s);
+    if (rc != NSA_OK) return rc;
+  }
   const int n_blk = sel_csr_blocks(T, block_size);
   if (T == 0 || S == 0 || n_blk == 0) return NSA_OK;
   const size_t cap = sel_items_cap(B, Hkv, T, S, block_size, chunk);

@@ -15,6 +15,7 @@ namespace nsa {
 // ---------------------------------------------------------------------------
 // transpose_kv: 64 x 64 tiles through LDS
 // ---------------------------------------------------------------------------
+// Any D and Lp: one element per access.
 template <typename T>
 __global__ __launch_bounds__(256) void k_transpose_kv(const T* __restrict__ x, T* __restrict__ xt,
                                                       int L, int D, int Lp) {
@@ -33,6 +34,47 @@ __global__ __launch_bounds__(256) void k_transpose_kv(const T* __restrict__ x, T
     const int r = e / 64, cc = e % 64;          // r: d, cc: key
     const int d = d0 + r, l = l0 + cc;
     if (d < D && l < Lp) yb[(int64_t)d * Lp + l] = from_f32<T>(tile[cc][r]);
+  }
+}
+
+// D % 8 == 0, Lp % 8 == 0, 16-byte aligned rows: 8-element global accesses.
+// A lane moves 8 consecutive d of one key in, 8 consecutive keys of one d out
+// (8 lanes cover a 64-element row piece).  The LDS row pitch (66 bf16 /
+// 65 float) puts the 8 keys x 8 d read by a wave's lanes on distinct banks.
+template <typename T>
+__global__ __launch_bounds__(256) void k_transpose_kv8(const T* __restrict__ x, T* __restrict__ xt,
+                                                       int L, int D, int Lp) {
+  constexpr int P = sizeof(T) == 2 ? 66 : 65;
+  __shared__ T tile[64 * P];
+  const int bh = blockIdx.z;
+  const int l0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const T* xb = x + (int64_t)bh * L * D;
+  T* yb = xt + (int64_t)bh * D * Lp;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i, r = c >> 3, cc = (c & 7) * 8;   // r: key, cc: first d
+    const int l = l0 + r, d = d0 + cc;
+    Frag<T> f;
+    if (l < L && d < D)
+      f.load(xb + (int64_t)l * D + d);
+    else
+      f.zero();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tile[r * P + cc + j] = f.elem(j);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = threadIdx.x + 256 * i, r = c >> 3, kc = (c & 7) * 8;  // r: d, kc: first key
+    const int d = d0 + r, l = l0 + kc;
+    if (d < D && l < Lp) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = to_f32(tile[(kc + j) * P + r]);
+      Frag<T> f;
+      f.set(v);
+      f.store(yb + (int64_t)d * Lp + l);
+    }
   }
 }
 
@@ -56,6 +98,38 @@ __global__ __launch_bounds__(256) void k_pool_fwd(const T* __restrict__ x, T* __
   }
 }
 
+// D % 8 == 0, 16-byte aligned rows: a lane sums 8 consecutive d (same order of
+// additions as k_pool_fwd)
+template <typename T>
+__global__ __launch_bounds__(256) void k_pool_fwd8(const T* __restrict__ x, T* __restrict__ out,
+                                                   int BH, int L, int D, int n, int pl, int pd) {
+  const int dc = D / 8;
+  const int64_t total = (int64_t)BH * n * dc;
+  const float inv = 1.0f / (float)pl;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % dc);
+    const int64_t r = e / dc;
+    const int i = (int)(r % n);
+    const int64_t bh = r / n;
+    const T* src = x + (bh * L + (int64_t)i * pd) * D + 8 * c;
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < pl; ++k) {
+      Frag<T> f;
+      f.load(src + (int64_t)k * D);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] += to_f32(f.elem(j));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] *= inv;
+    Frag<T> o;
+    o.set(s);
+    o.store(out + r * D + 8 * c);
+  }
+}
+
 template <typename TI, typename TO>
 __global__ __launch_bounds__(256) void k_pool_bwd(const TI* __restrict__ dp, TO* __restrict__ dx,
                                                   int BH, int L, int D, int n, int pl, int pd) {
@@ -73,6 +147,39 @@ __global__ __launch_bounds__(256) void k_pool_bwd(const TI* __restrict__ dp, TO*
     float s = 0.0f;
     for (int i = ilo; i <= ihi; ++i) s += to_f32(dp[(bh * n + i) * D + d]);
     dx[e] = from_f32<TO>(s * inv);
+  }
+}
+
+// D % 8 == 0, 16-byte aligned rows: a lane writes 8 consecutive d (same order
+// of additions as k_pool_bwd)
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_pool_bwd8(const TI* __restrict__ dp, TO* __restrict__ dx,
+                                                   int BH, int L, int D, int n, int pl, int pd) {
+  const int dc = D / 8;
+  const int64_t total = (int64_t)BH * L * dc;
+  const float inv = 1.0f / (float)pl;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % dc);
+    const int64_t r = e / dc;
+    const int t = (int)(r % L);
+    const int64_t bh = r / L;
+    int ilo = t - pl + 1 <= 0 ? 0 : (t - pl + 1 + pd - 1) / pd;
+    int ihi = t / pd;
+    if (ihi > n - 1) ihi = n - 1;
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+    for (int i = ilo; i <= ihi; ++i) {
+      Frag<TI> f;
+      f.load(dp + (bh * n + i) * D + 8 * c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] += to_f32(f.elem(j));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] *= inv;
+    Frag<TO> o;
+    o.set(s);
+    o.store(dx + r * D + 8 * c);
   }
 }
 
@@ -195,10 +302,33 @@ __global__ __launch_bounds__(256) void k_pack_heads(const uint4* __restrict__ sr
   }
 }
 
+// x, y 16-byte aligned: 8 elements per access for the first n & ~7, the rest one by one
 template <typename T>
 __global__ __launch_bounds__(256) void k_cast_f32(const float* __restrict__ x, T* __restrict__ y, int64_t n) {
+  const int64_t n8 = n >> 3;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n8; e += (int64_t)gridDim.x * 256) {
+    Frag<float> f;
+    f.load(x + 8 * e);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = f.elem(j);
+    Frag<T> o;
+    o.set(v);
+    o.store(y + 8 * e);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < (n & 7)) {
+    const int64_t e = (n8 << 3) + threadIdx.x;
+    y[e] = from_f32<T>(x[e]);
+  }
+}
+
+// any alignment
+template <typename T>
+__global__ __launch_bounds__(256) void k_cast_f32_1(const float* __restrict__ x, T* __restrict__ y, int64_t n) {
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < n; e += (int64_t)gridDim.x * 256) y[e] = from_f32<T>(x[e]);
 }
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 static inline int grid_for(int64_t n) {
   int64_t g = (n + 255) / 256;
@@ -218,10 +348,18 @@ int nsa_transpose_kv(const void* x, void* xt, int BH, int L, int D, int Lp, int 
   if (L == 0 && Lp == 0) return NSA_OK;
   dim3 grid((Lp + 63) / 64, (D + 63) / 64, BH);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    k_transpose_kv<bf16><<<grid, 256, 0, s>>>((const bf16*)x, (bf16*)xt, L, D, Lp);
-  else
-    k_transpose_kv<float><<<grid, 256, 0, s>>>((const float*)x, (float*)xt, L, D, Lp);
+  const bool vec = D % 8 == 0 && Lp % 8 == 0 && aligned16(x) && aligned16(xt);
+  if (dtype == NSA_BF16) {
+    if (vec)
+      k_transpose_kv8<bf16><<<grid, 256, 0, s>>>((const bf16*)x, (bf16*)xt, L, D, Lp);
+    else
+      k_transpose_kv<bf16><<<grid, 256, 0, s>>>((const bf16*)x, (bf16*)xt, L, D, Lp);
+  } else {
+    if (vec)
+      k_transpose_kv8<float><<<grid, 256, 0, s>>>((const float*)x, (float*)xt, L, D, Lp);
+    else
+      k_transpose_kv<float><<<grid, 256, 0, s>>>((const float*)x, (float*)xt, L, D, Lp);
+  }
   return nsa_launch_status();
 }
 
@@ -233,10 +371,17 @@ int nsa_pool_fwd(const void* x, void* out, int B, int H, int T, int D, int l, in
   const int64_t total = (int64_t)B * H * n * D;
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
+  if (D % 8 == 0 && aligned16(x) && aligned16(out)) {
+    const int g = grid_for(total / 8);
+    if (dtype == NSA_BF16)
+      k_pool_fwd8<bf16><<<g, 256, 0, s>>>((const bf16*)x, (bf16*)out, B * H, T, D, n, l, d);
+    else
+      k_pool_fwd8<float><<<g, 256, 0, s>>>((const float*)x, (float*)out, B * H, T, D, n, l, d);
+  } else if (dtype == NSA_BF16) {
     k_pool_fwd<bf16><<<grid_for(total), 256, 0, s>>>((const bf16*)x, (bf16*)out, B * H, T, D, n, l, d);
-  else
+  } else {
     k_pool_fwd<float><<<grid_for(total), 256, 0, s>>>((const float*)x, (float*)out, B * H, T, D, n, l, d);
+  }
   return nsa_launch_status();
 }
 
@@ -250,6 +395,21 @@ int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int
   const int64_t total = (int64_t)B * H * T * D;
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
+  if (D % 8 == 0 && aligned16(dpool) && aligned16(dx)) {
+    const int g = grid_for(total / 8);
+    if (dpool_dtype == NSA_F32) {
+      if (dtype == NSA_BF16)
+        k_pool_bwd8<float, bf16><<<g, 256, 0, s>>>((const float*)dpool, (bf16*)dx, B * H, T, D, n, l, d);
+      else
+        k_pool_bwd8<float, float><<<g, 256, 0, s>>>((const float*)dpool, (float*)dx, B * H, T, D, n, l, d);
+    } else {
+      if (dtype == NSA_BF16)
+        k_pool_bwd8<bf16, bf16><<<g, 256, 0, s>>>((const bf16*)dpool, (bf16*)dx, B * H, T, D, n, l, d);
+      else
+        k_pool_bwd8<bf16, float><<<g, 256, 0, s>>>((const bf16*)dpool, (float*)dx, B * H, T, D, n, l, d);
+    }
+    return nsa_launch_status();
+  }
   const int grid = grid_for(total);
   if (dpool_dtype == NSA_F32) {
     if (dtype == NSA_BF16)
@@ -336,10 +496,17 @@ int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   if (n == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    k_cast_f32<bf16><<<grid_for(n), 256, 0, s>>>(x, (bf16*)y, n);
-  else
-    k_cast_f32<float><<<grid_for(n), 256, 0, s>>>(x, (float*)y, n);
+  if (aligned16(x) && aligned16(y)) {
+    const int g = grid_for(n / 8);
+    if (dtype == NSA_BF16)
+      k_cast_f32<bf16><<<g, 256, 0, s>>>(x, (bf16*)y, n);
+    else
+      k_cast_f32<float><<<g, 256, 0, s>>>(x, (float*)y, n);
+  } else if (dtype == NSA_BF16) {
+    k_cast_f32_1<bf16><<<grid_for(n), 256, 0, s>>>(x, (bf16*)y, n);
+  } else {
+    k_cast_f32_1<float><<<grid_for(n), 256, 0, s>>>(x, (float*)y, n);
+  }
   return nsa_launch_status();
 }
 

@@ -133,6 +133,30 @@ def test_pool_fwd_bwd(dtype):
     del dy
 
 
+@pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])
+def test_layout_helpers_both_paths(dtype):
+    """transpose_kv and cast_f32 are exact copies: 16-byte-aligned inputs take
+    the 8-element kernels, inputs one element off alignment the per-element ones;
+    lengths that are not multiples of 8 / 64 exercise the tails and the zero pad."""
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    for L_, D_ in ((203, 64), (64, 128), (7, 16)):
+        n = 2 * 3 * L_ * D_
+        flat = randn((n + 1,), 11, dtype).to(dev)
+        for x in (flat[:n].view(2, 3, L_, D_), flat[1:].view(2, 3, L_, D_)):
+            xt = ops.transpose_kv(x)
+            Lp = ops.padded_len(L_)
+            want = torch.zeros(2, 3, D_, Lp, dtype=dtype, device=dev)
+            want[..., :L_] = x.transpose(-1, -2)
+            assert xt.shape == want.shape and torch.equal(xt, want), (L_, D_, x.data_ptr() % 16)
+    for n in (1003, 4096, 5):
+        flat = randn((n + 1,), 12, torch.float32).to(dev)
+        for x in (flat[:n], flat[1:]):
+            y = ops.cast_f32(x, torch.bfloat16)
+            assert torch.equal(y, x.to(torch.bfloat16)), (n, x.data_ptr() % 16)
+    torch.cuda.synchronize()
+
+
 def test_empty_and_tiny_rows():
     """T smaller than a block, all slots -1, and S = 0."""
     dev = require_gpu()
