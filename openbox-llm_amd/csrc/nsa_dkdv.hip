@@ -67,58 +67,72 @@ constexpr int kv_tile_loads() {
 // the row offset +inf, so their P and dS are exactly 0.
 //
 // Everything that depends only on the lane and the head chunk is prepared
-// once (prepare()): each load's 32-bit byte offset below the tile's first
-// row and whether its row is query B's.  Per tile, the base of query A's rows
-// is wave-uniform and every load adds one select to its lane's offset.
+// once per head chunk (prepare()): each load's 32-bit byte offset below the
+// tile's first row, whether its row is query B's, the chunk's element offset
+// and this lane's statistics row.  Per tile, the query ids are made
+// wave-uniform, the operand base is scalar arithmetic, and each load adds
+// query B's row distance to its lane's offset when its rows are B's -- a
+// wave-uniform choice whenever a wave's 64 chunks never straddle the two
+// queries' halves of the tile (16 rows a multiple of 64 chunks).
 template <typename T, int D, int NTH> struct KvIssuer {
   using C = Tile32<T, D>;
   static constexpr int LPT = dma_uniform_loads<NTH, C::ROW_CHUNKS>();   // loads per operand tile
-  uint32_t off[LPT];   // (head * T * D + column) * sizeof(T) of this lane's chunk of load j
-  uint32_t qsel;       // bit j: load j's row belongs to query B
-  uint32_t sbit;       // stats: this lane's row belongs to query B
-  int shead, sreal;    // stats: head of this lane's row (clamped); the head exists
-  int grem;            // heads in the prepared chunk
+  static constexpr bool UNI = (16 * C::RCH) % 64 == 0;
+  uint32_t off[LPT];   // (head * hs + column) * sizeof(T) of this lane's chunk of load j
+  uint32_t qsel;       // bit j: load j's row belongs to query B (per lane; unused when UNI)
+  int64_t qbase;       // element offset of the head chunk's first head, query 0
+  const float* sp;     // statistics row of this lane at query 0 (c for lanes < 32, delta above)
+  int sbit;            // stats: this lane's row belongs to query B
+  int sreal;           // stats: the head exists
 
-  __device__ __forceinline__ void prepare(const QSide<T>& x, int hc, int tid) {
-    grem = x.G - hc * 16;
+  // first physical chunk of load j of wave w (wave-uniform)
+  static __device__ __forceinline__ int first_chunk(int j, int w) {
+    return (int)((uint32_t)(j * NTH + 64 * w) % (uint32_t)C::ROW_CHUNKS);
+  }
+
+  __device__ __forceinline__ void prepare(const QSide<T>& x, int b, int hkv, int hc, int tid) {
+    const int grem = x.G - hc * 16;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     qsel = 0;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       int r, cc;
-      row_chunk<T, D>((j * NTH + 64 * w) % C::ROW_CHUNKS + lane, r, cc);
+      row_chunk<T, D>(first_chunk(j, w) + lane, r, cc);
       const int hd = (r & 15) < grem ? (r & 15) : grem - 1;
       off[j] = (uint32_t)(((uint64_t)hd * x.hs + cc * C::EPC) * sizeof(T));
       qsel |= (uint32_t)(r >> 4) << j;
     }
+    qbase = ((int64_t)b * x.Hkv + hkv) * x.G * x.T_ * D + hc * 16 * x.hs;
     const int r = lane & 31;
     sbit = r >> 4;
-    shead = (r & 15) < grem ? (r & 15) : grem - 1;
+    const int shead = (r & 15) < grem ? (r & 15) : grem - 1;
     sreal = (r & 15) < grem;
+    const int64_t row0 = ((int64_t)b * x.Hq + hkv * x.G + hc * 16 + shead) * x.T_;
+    sp = (lane < 32 ? x.c : x.dot) + row0;
   }
 
-  __device__ __forceinline__ void issue(KvStage<T, D>& s, const QSide<T>& x, int b, int hkv, int hc, int tA,
-                                        int tB, int sA, int sB, int tid) const {
+  __device__ __forceinline__ void issue(KvStage<T, D>& s, const QSide<T>& x, int tA, int tB, int sA, int sB,
+                                        int tid) const {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    tA = __builtin_amdgcn_readfirstlane(tA);
+    tB = __builtin_amdgcn_readfirstlane(tB);
     const int tBq = tB >= 0 ? tB : tA;   // a missing second query re-reads the first
-    const int64_t hbase = (int64_t)b * x.Hq + hkv * x.G + hc * 16;
-    const int64_t rowA = hbase * x.T_ + tA;   // statistics row of query A, head hc * 16
-    const int64_t qoff = ((int64_t)b * x.Hkv + hkv) * x.G * x.T_ * D + hc * 16 * x.hs + tA * x.ts;
+    const int64_t qoff = qbase + (int64_t)tA * x.ts;
     const uint32_t dB = (uint32_t)(tBq - tA) * (uint32_t)(x.ts * sizeof(T));
     const T* qa = x.q + qoff;
     const T* da = x.dout + qoff;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
-      const uint32_t v = off[j] + (((qsel >> j) & 1u) ? dB : 0u);
-      const int first = (j * NTH + 64 * w) % C::ROW_CHUNKS;
+      const int first = first_chunk(j, w);
+      const bool rowB = UNI ? first / C::RCH >= 16 : ((qsel >> j) & 1u) != 0;
+      const uint32_t v = off[j] + (rowB ? dB : 0u);
       lds_dma16_sbase(qa, v, (char*)s.qr + 16 * first);
       lds_dma16_sbase(da, v, (char*)s.dr + 16 * first);
     }
     {
       // lanes 0-31: c of row lane, lanes 32-63: delta of row lane - 32
-      const int64_t ri = rowA + (int64_t)shead * x.T_ + (sbit ? tBq - tA : 0);
-      const bool real = sreal && (!sbit || tB >= 0);
-      lds_dma4(lane < 32 ? (real ? x.c + ri : &kAbsentRow) : x.dot + ri, s.c);
+      const bool real = lane >= 32 || (sreal && (!sbit || tB >= 0));
+      lds_dma4(real ? sp + (sbit ? tBq : tA) : &kAbsentRow, s.c);
     }
     if (tid == 0) {
       s.meta[0] = tA;
@@ -169,8 +183,10 @@ template <typename T, int D> struct KeyAcc {
 
   // First half of a tile: S and dP from the row fragments read earlier, the
   // transposed fragments dO^T (ta) and Q^T (tb) read while those MFMAs run,
-  // then P and dS packed as the operands of the second half.  visA / visB
-  // say whether this lane's key is visible to query A / B.
+  // then P and dS packed as the operands of the second half.  With MASK,
+  // visA / visB say whether this lane's key is visible to query A / B;
+  // without, every key is.
+  template <bool MASK>
   __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, bool visA, bool visB, float sl2,
                                         int lane, Frag<T> (&ta)[C::DT][2], Frag<T> (&tb)[C::DT][2],
                                         Frag<T> (&pf)[2], Frag<T> (&sf)[2]) {
@@ -204,7 +220,7 @@ template <typename T, int D> struct KeyAcc {
     for (int r = 0; r < 16; ++r) {
       const int e = acc_elem(h, r);
       float p = fast_exp2(sacc[r] * sl2 - s.c[e]);
-      p = (r < 8 ? visA : visB) ? p : 0.0f;
+      if (MASK) p = (r < 8 ? visA : visB) ? p : 0.0f;
       P[r] = p;
       dS[r] = p * (pacc[r] - s.dot[e]);
     }
@@ -282,19 +298,20 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   constexpr int LT = kv_tile_loads<T, D, NTH>();
   static_assert(NST >= 3 && (NST - 1) * LT < 64 && (NST - 2) * (LT + NSW) < 64,
                 "in-flight operations exceed the vmcnt range");
-  const int total = ntile * x.NHC;
+  // wave-uniform: every branch on the loop counters below is scalar
+  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
   if (total == 0) return;
   const int lane = tid & 63;
   int iti = 0, ihc = 0;   // next tile to request: tile and head chunk
   KvIssuer<T, D, NTH> iss;
-  iss.prepare(x, 0, tid);
+  iss.prepare(x, b, hkv, 0, tid);
   auto request = [&](KvStage<T, D>& s) {
     int tA, tB, sA, sB;
     qsrc(iti, tA, tB, sA, sB);
-    iss.issue(s, x, b, hkv, ihc, tA, tB, sA, sB, tid);
+    iss.issue(s, x, tA, tB, sA, sB, tid);
     if (++iti == ntile) {
       iti = 0;
-      if (++ihc < x.NHC) iss.prepare(x, ihc, tid);
+      if (++ihc < x.NHC) iss.prepare(x, b, hkv, ihc, tid);
     }
   };
 #pragma unroll
@@ -310,11 +327,15 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   int hc = 0, ti = 0;   // head chunk and tile of iteration `it`
   for (int it = 0; it < total; ++it) {
     const KvStage<T, D>& s = stg[it % NST];
-    const int tA = s.meta[0], tB = s.meta[1], sA = s.meta[2], sB = s.meta[3];
+    const int tA = __builtin_amdgcn_readfirstlane(s.meta[0]), tB = __builtin_amdgcn_readfirstlane(s.meta[1]);
+    const int sA = __builtin_amdgcn_readfirstlane(s.meta[2]), sB = __builtin_amdgcn_readfirstlane(s.meta[3]);
     bool mask, visA, visB;
     vis(tA, tB, mask, visA, visB);
     Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2];
-    acc.front(s, rows, visA || !mask, visB || !mask, sl2, lane, ta, tb, pf, sf);
+    if (mask)
+      acc.template front<true>(s, rows, visA, visB, sl2, lane, ta, tb, pf, sf);
+    else
+      acc.template front<false>(s, rows, true, true, sl2, lane, ta, tb, pf, sf);
     if (WANT_DS) pre(sf, it);
     if (it + NST - 1 < total)
       vm_wait_steps<(NST - 2) * LT, WANT_DS ? NSW : 0, NST - 2>(it);
@@ -367,16 +388,43 @@ __host__ __device__ inline int cmp_active_blocks(int T, int Lk, int chunk, int N
   return n < nkb ? n : nkb;
 }
 
+// xcd_remap for a grid of nlong long workgroups followed by nshort short
+// ones: every XCD takes an equal, contiguous share of each, its long ones
+// first (the few long ones that do not divide evenly go out first, the short
+// ones that do not, last).
+__device__ __forceinline__ int64_t xcd_remap_split(int64_t bid, int64_t nlong, int64_t nshort) {
+  constexpr int64_t kXcd = 8;
+  const int64_t lp = nlong / kXcd, sp = nshort / kXcd, lr = nlong % kXcd;
+  if (bid < lr) return lp * kXcd + bid;
+  bid -= lr;
+  if (bid >= (lp + sp) * kXcd) return nlong + sp * kXcd + (bid - (lp + sp) * kXcd);
+  const int64_t x = bid % kXcd, i = bid / kXcd;
+  return i < lp ? x * lp + i : nlong + x * sp + (i - lp);
+}
+
+__host__ __device__ inline int cmp_blocks_range(int T, int Lk, int chunk, int NW, int cl, int cd, int c0, int c1) {
+  int tot = 0;
+  for (int c = c0; c < c1; ++c) tot += cmp_active_blocks(T, Lk, chunk, NW, cl, cd, c);
+  return tot;
+}
+
 // ---------------------------------------------------------------------------
-// range dK/dV: window: ceil(Lk / (32 NW)) * B*Hkv workgroups; compression:
-// cmp_active_blocks(-1) * B*Hkv
+// range dK/dV: window: ceil(Lk / (32 NW)) * B*Hkv workgroups.  Compression:
+// every (query chunk, key block) pair takes about as long as any other, so a
+// grid of them would end in a partial round of workgroups on an otherwise idle
+// GPU.  Chunks from `chs` on are split into `spl` sub-chunks and launched
+// last, where their short workgroups fill that round.  Logical workgroups
+// (placed on the XCDs by xcd_remap_split):
+//   [0, nbh * big)  chunks < chs, per bh chunk-major
+//   the rest        chunks >= chs, per bh (chunk, sub-chunk)-major
+// (big / small: cmp_blocks_range over the two chunk ranges).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                     const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
                     float* __restrict__ dk, float* __restrict__ dv, int Hq, int Hkv, int T_, int Lk, int chunk,
-                    int window, int cl, int cd, float sl2, float scale) {
+                    int window, int cl, int cd, int nbh, int chs, int spl, float sl2, float scale) {
   constexpr int NTH = 64 * NW;
   __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
@@ -387,18 +435,38 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   // window has one chunk and uniform work per key block.
   const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
   int kblk, ch, bh;
+  int q0 = 0, qlen = chunk;   // compression: the workgroup's queries [q0, q0 + qlen)
   if (mode == NSA_MODE_COMPRESS) {
-    const int per_bh = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, -1);
-    const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
-    bh = (int)(wg / per_bh);
-    int r = (int)(wg % per_bh);
     const int nch = (T_ + chunk - 1) / chunk;
-    for (ch = 0; ch < nch - 1; ++ch) {   // chunk ch holds the first cmp_active_blocks(.., ch) key blocks
+    const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
+    const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
+    const int64_t wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
+    int r, sub = 0;
+    if (wg < (int64_t)big * nbh) {
+      bh = (int)(wg / big);
+      r = (int)(wg % big);
+      for (ch = 0; ch < chs - 1; ++ch) {   // chunk ch holds the first cmp_active_blocks(.., ch) key blocks
+        const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+        if (r < nb) break;
+        r -= nb;
+      }
+    } else {
+      const int64_t w2 = wg - (int64_t)big * nbh;
+      bh = (int)(w2 / per);
+      r = (int)(w2 % per);
+      for (ch = chs; ch < nch - 1; ++ch) {
+        const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch) * spl;
+        if (r < nb) break;
+        r -= nb;
+      }
       const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
-      if (r < nb) break;
-      r -= nb;
+      sub = r / nb;
+      r %= nb;
+      qlen = (chunk + spl - 1) / spl;
     }
     kblk = r;
+    q0 = ch * chunk + sub * qlen;
+    if (q0 + qlen > ch * chunk + chunk) qlen = ch * chunk + chunk - q0;
   } else {
     kblk = (int)(blockIdx.x % nkb);
     ch = 0;
@@ -419,7 +487,7 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   } else {
     tlo = k0 * cd + cl - 1;
     thi = T_ - 1;
-    const int c0 = ch * chunk, c1 = c0 + chunk - 1;
+    const int c0 = q0, c1 = q0 + qlen - 1;
     tlo = tlo > c0 ? tlo : c0;
     thi = thi < c1 ? thi : c1;
   }
@@ -646,7 +714,21 @@ using namespace nsa;
     default: return NSA_ERR_SHAPE;                              \
   }
 
-static constexpr int kCmpChunk = 1024;   // queries per compression dK/dV work item
+static constexpr int kCmpChunk = 2048;   // queries per compression dK/dV work item
+static constexpr int kCmpSplit = 4;      // sub-chunks of the chunks that end the grid
+
+// Compute units of the current device (cached per device).
+static int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
 
 extern "C" {
@@ -674,26 +756,41 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   const float sl2 = scale * kLog2e;
   // 2 waves (64 keys) per workgroup, two workgroups per CU: measured faster than
   // 4 waves sharing each streamed query tile, for both modes
-#define NSA_RANGE_DKDV_LAUNCH(NW_)                                                                               \
-  {                                                                                                            \
-    const int64_t grid = (int64_t)(mode == NSA_MODE_COMPRESS                                                   \
-                                       ? cmp_active_blocks(T, Lk, kCmpChunk, NW_, cmp_block, cmp_stride, -1)  \
-                                       : (Lk + 32 * NW_ - 1) / (32 * NW_)) * B * Hkv;                          \
-    if (grid == 0) return NSA_OK;                                                                              \
-    NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);                                                              \
-    NSA_DISPATCH_D(D, {                                                                                        \
-      if (dtype == NSA_BF16)                                                                                   \
-        k_range_dkdv32<bf16, DD, NW_><<<(unsigned)grid, 64 * NW_, 0, s>>>(                                     \
-            mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, dk, dv, Hq,     \
-            Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, sl2, scale);                                 \
-      else                                                                                                     \
-        k_range_dkdv32<float, DD, NW_><<<(unsigned)grid, 64 * NW_, 0, s>>>(                                    \
-            mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, Hq, \
-            Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, sl2, scale);                                 \
-    });                                                                                                        \
+  constexpr int NW = 2;
+  const int nbh = B * Hkv;
+  int chs = 0, spl = 1;
+  int64_t grid;
+  if (mode == NSA_MODE_COMPRESS) {
+    // split the last chunks while their workgroups fit in one round of the
+    // resident workgroups (two per CU)
+    const int nch = (T + kCmpChunk - 1) / kCmpChunk;
+    const int64_t slots = 2 * (int64_t)device_cu_count();
+    int64_t tail = 0;
+    chs = nch;
+    while (chs > 0) {
+      const int64_t add = (int64_t)cmp_active_blocks(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, chs - 1) * nbh;
+      if (tail + add > slots) break;
+      tail += add;
+      --chs;
+    }
+    spl = chs < nch ? kCmpSplit : 1;
+    grid = ((int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, 0, chs) +
+            (int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, chs, nch) * spl) * nbh;
+  } else {
+    grid = (int64_t)((Lk + 32 * NW - 1) / (32 * NW)) * nbh;
   }
-  NSA_RANGE_DKDV_LAUNCH(2)
-#undef NSA_RANGE_DKDV_LAUNCH
+  if (grid == 0) return NSA_OK;
+  NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  NSA_DISPATCH_D(D, {
+    if (dtype == NSA_BF16)
+      k_range_dkdv32<bf16, DD, NW><<<(unsigned)grid, 64 * NW, 0, s>>>(
+          mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, dk, dv, Hq, Hkv, T,
+          Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
+    else
+      k_range_dkdv32<float, DD, NW><<<(unsigned)grid, 64 * NW, 0, s>>>(
+          mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, Hq, Hkv,
+          T, Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
+  });
   return nsa_launch_status();
 }
 
