@@ -545,7 +545,7 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // ---------------------------------------------------------------------------
 // selection dK/dV over CSR work items (nsa_items.h)
 // ---------------------------------------------------------------------------
-// Persistent grid over the work items; two waves own 64 keys of the item's
+// Persistent grid over the work items (next_item); two waves own 64 keys of the item's
 // block at a time (blocks longer than 64 keys take several passes).  With
 // dq_part, the tile's dS^T (both waves, 64 keys x 32 rows) is staged in LDS
 // before the tile's barrier (double-buffered by tile parity) and dQ^T =
@@ -557,7 +557,7 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                   const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
                   const T* __restrict__ kt, const int32_t* __restrict__ q_of_block, const int4* __restrict__ items,
-                  const int32_t* __restrict__ n_items, float* __restrict__ dk, float* __restrict__ dv,
+                  int32_t* __restrict__ n_items, float* __restrict__ dk, float* __restrict__ dv,
                   T* __restrict__ dq_part, int Hq, int Hkv, int T_, int S, int packed, int n_blk, int L, int Lp,
                   float sl2, float scale) {
   constexpr int NW = 2, NTH = 64 * NW;
@@ -577,7 +577,8 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   const int npass = sel_passes(L);
   const int NS = S * npass;
   const int sbits = sel_slot_bits(S);
-  for (int it = blockIdx.x; it < ni * npass; it += gridDim.x) {
+  __shared__ int next_slot;
+  for (int it = blockIdx.x; it < ni * npass; it = next_item(n_items + 1, &next_slot)) {
     const int4 item = items[it / npass];
     const int pass = it % npass;
     const int bh = item.x / n_blk, j = item.x % n_blk;

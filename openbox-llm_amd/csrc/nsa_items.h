@@ -8,7 +8,8 @@
 
 namespace nsa {
 
-// items[i] = {bh * n_blk + j, begin, end, 0}: pair range [begin, end) of q_of_block
+// items[i] = {bh * n_blk + j, begin, end, 0}: pair range [begin, end) of q_of_block;
+// n_items[0] = item count, n_items[1] = 0 (the work counter of next_item)
 static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __restrict__ offsets, int nb, int n_blk,
                                                            int chunk, int4* __restrict__ items,
                                                            int32_t* __restrict__ n_items) {
@@ -41,7 +42,21 @@ static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __rest
       items[pos++] = make_int4(e, s, se, 0);
     }
   }
-  if (tid == 1023) *n_items = part[1023];
+  if (tid == 1023) {
+    n_items[0] = part[1023];
+    n_items[1] = 0;
+  }
+}
+
+// Next work item of a persistent grid over `total` items: the first
+// gridDim.x go to the workgroups in order, each later one to the workgroup
+// that asks first (the hardware dispatches workgroups as slots free up, so
+// both halves balance dynamically).  Called by every thread of the workgroup
+// after a barrier that follows its last read of *slot.
+__device__ __forceinline__ int next_item(int32_t* counter, int* slot) {
+  if (threadIdx.x == 0) *slot = (int)gridDim.x + atomicAdd(counter, 1);
+  __syncthreads();
+  return *slot;
 }
 
 // Selection blocks of the CSR consumed by the block-outer kernels: every

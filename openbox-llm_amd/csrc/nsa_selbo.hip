@@ -65,7 +65,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ vt, const int32_t* __restrict__ q_of_block,
                                                    const int4* __restrict__ items,
-                                                   const int32_t* __restrict__ n_items, T* __restrict__ opart,
+                                                   int32_t* __restrict__ n_items, T* __restrict__ opart,
                                                    float2* __restrict__ mlpart, int Hq, int Hkv, int T_, int S,
                                                    int n_blk, int L, int Lp, int nsub, float sl2) {
   using C = Tile32<T, D>;
@@ -85,7 +85,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
   const int NS = S * nsub;
   const int sbits = sel_slot_bits(S);
   const int ni = *n_items;
-  for (int it = blockIdx.x; it < ni * nsub; it += gridDim.x) {
+  __shared__ int next_slot;
+  for (int it = blockIdx.x; it < ni * nsub; it = next_item(n_items + 1, &next_slot)) {
     const int4 item = items[it / nsub];
     const int pass = it % nsub;
     const int bh = item.x / n_blk, j = item.x % n_blk;
