@@ -112,6 +112,8 @@ def kernel_flops(w, kv):
 # the same counters read for a plain 1 GiB device copy (x2.0 and x1.0); the
 # commands and counter values are kept under profiles/.  Reported only for
 # the workload and kernel they were measured on.
+ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
+
 MEASURED_TRAFFIC = {("c3", "dkdv[sel]"): 1.955e10 + 9.79e9}
 
 
@@ -142,7 +144,25 @@ def run_gpu(args, w):
         torch.cuda.synchronize()
     kv = keys_visible(w, idx)
     flops_of = kernel_flops(w, kv)
-    timer = ops.LaunchTimer()
+    # untimed, first: every call timed, with the backward's streams serialised
+    # (nsa_hip_ops.OVERLAP_SEL_BWD off), so that each kernel's duration is its
+    # own; this picks the dominant kernel
+    iso = ops.LaunchTimer()
+    overlap = ops.OVERLAP_SEL_BWD
+    ops.OVERLAP_SEL_BWD = False
+    try:
+        ops.set_timer(iso)
+        for _ in range(ISO_STEPS):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        ops.set_timer(None)
+        ops.OVERLAP_SEL_BWD = overlap
+    iso_spans = iso.summary_ms()
+    modeled = {k: v for k, v in iso_spans.items() if k in flops_of}
+    dom = max(modeled, key=lambda k: modeled[k][1]) if modeled else None
+    # timed: HIP events around the dominant kernel's calls only
+    timer = ops.LaunchTimer(only=[dom] if dom else [])
     ops.set_timer(timer)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -152,23 +172,7 @@ def run_gpu(args, w):
     t1 = time.perf_counter()
     ops.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
-    spans = timer.summary_ms()
-    # untimed: the same steps with the backward's streams serialised, so that
-    # each kernel's duration is its own (the timed steps overlap the selection
-    # dK/dV with the range dK/dV kernels)
-    iso = ops.LaunchTimer()
-    ops.OVERLAP_SEL_BWD = False
-    try:
-        step()
-        torch.cuda.synchronize()
-        ops.set_timer(iso)
-        for _ in range(2):
-            step()
-        torch.cuda.synchronize()
-    finally:
-        ops.set_timer(None)
-        ops.OVERLAP_SEL_BWD = True
-    return ms, spans, iso.summary_ms(), flops_of, kv, ins, do
+    return ms, timer.summary_ms(), iso_spans, dom, flops_of, kv, ins, do
 
 
 def run_cpu_baseline(w, ins_dev, do_dev, rows_n, threads):
@@ -254,23 +258,20 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     w = WORKLOADS[args.workload]
-    ms, spans, iso_spans, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
+    ms, spans, iso_spans, dom_name, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
     tokens = w["B"] * w["T"]
     value = tokens / (ms / 1e3)
     total_flops = sum(flops_of.values())
 
-    # dominant kernel: the timed call with the largest total time that has a FLOP model
-    named = {}
-    for name, (calls, tot) in spans.items():
-        named[name] = (calls, tot)
+    # dominant kernel: the call with a FLOP model and the largest total time
+    # in the untimed steps; its launches in the timed steps give `achieved`
     if args.spans:
-        for name, (calls, tot) in sorted(named.items(), key=lambda x: -x[1][1]):
-            log(f"  {name:28s} calls {calls:4d}  total {tot:9.3f} ms  per step {tot / args.steps:8.3f} ms")
-    modeled = {k: v for k, v in named.items() if k in flops_of}
-    dom = max(modeled.items(), key=lambda x: x[1][1]) if modeled else None
+        for name, (calls, tot) in sorted(iso_spans.items(), key=lambda x: -x[1][1]):
+            log(f"  {name:28s} calls {calls:4d}  total {tot:9.3f} ms  per step {tot / ISO_STEPS:8.3f} ms")
     roofline = None
-    if dom is not None:
-        name, (calls, tot) = dom
+    if dom_name is not None and dom_name in spans:
+        name = dom_name
+        calls, tot = spans[name]
         per_launch_s = tot / calls / 1e3
         achieved = flops_of[name] / per_launch_s / 1e12
         roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved, 2),
@@ -278,7 +279,7 @@ def main():
                     "traffic": MEASURED_TRAFFIC.get((args.workload, name)),
                     "launch_ms": round(per_launch_s * 1e3, 4)}
         if name in iso_spans:
-            # the same kernel with nothing beside it (untimed serialised steps)
+            # the same kernel in the untimed steps (backward serialised)
             icalls, itot = iso_spans[name]
             iso_s = itot / icalls / 1e3
             roofline["isolated"] = {"launch_ms": round(iso_s * 1e3, 4),

@@ -60,10 +60,17 @@ class LaunchTimer:
 
     Installed with ``set_timer``; the events are recorded on the current
     stream, which is the stream every kernel of the call is launched on.
+    ``only``: the call names to time (None: all).  Every timing event is a
+    packet in the stream's queue, so a timer meant to leave the timed work
+    undisturbed records only the calls it reports.
     """
 
-    def __init__(self):
+    def __init__(self, only=None):
         self.spans = defaultdict(list)
+        self.only = None if only is None else frozenset(only)
+
+    def wants(self, name):
+        return self.only is None or name in self.only
 
     @contextlib.contextmanager
     def span(self, name):
@@ -90,7 +97,7 @@ def set_timer(timer):
 
 
 def _span(name):
-    return _TIMER.span(name) if _TIMER is not None else contextlib.nullcontext()
+    return _TIMER.span(name) if _TIMER is not None and _TIMER.wants(name) else contextlib.nullcontext()
 
 
 def _span_name(kind, mode):
@@ -140,10 +147,12 @@ def _stream(t):
 
 _SIDE_STREAMS = {}
 
-# The fused backward runs the selection dK/dV on a side stream, beside the
-# window and compression key-side kernels; False runs everything in order on
-# the current stream (per-kernel timings then describe each kernel alone).
-OVERLAP_SEL_BWD = True
+# True: the fused backward runs the selection dK/dV on a side stream, beside
+# the window and compression key-side kernels.  False (default): everything
+# runs in order on the current stream.  At c3 on MI355X both take the same
+# 25.3 ms per fwd+bwd step (the kernels share the CUs without gaining from it),
+# and in order each kernel's timing describes that kernel alone.
+OVERLAP_SEL_BWD = False
 
 
 def _side_stream(device):

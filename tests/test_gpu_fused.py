@@ -207,6 +207,8 @@ def test_nsa_attention_overlapped_backward_matches_serial(dtype):
     ins, do = _fused_inputs(B, Hq, Hkv, T, D, dtype, seed=11, head_scale=True)
     do = do.to(dev)
 
+    default = ops.OVERLAP_SEL_BWD
+
     def grads(overlap):
         ops.OVERLAP_SEL_BWD = overlap
         try:
@@ -219,7 +221,7 @@ def test_nsa_attention_overlapped_backward_matches_serial(dtype):
             torch.cuda.synchronize()
             return res
         finally:
-            ops.OVERLAP_SEL_BWD = True
+            ops.OVERLAP_SEL_BWD = default
 
     serial = grads(False)
     overlapped = grads(True)
