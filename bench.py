@@ -104,6 +104,7 @@ def kernel_flops(w, kv):
         else:
             out[f"dq[{br}]"] = 2 * D * rows_keys
             out[f"dkdv[{br}]"] = 8 * D * rows_keys
+    out["dq[cmp+win]"] = out["dq[cmp]"] + out["dq[win]"]   # both branches in one launch
     return out
 
 

@@ -211,6 +211,22 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
                  const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
                  void* stream);
 
+/* Backward dQ of the compression and window branches in one launch, rows
+ * finished with the selection dQ partials: equal to nsa_range_dq(window,
+ * accumulate = 0) followed by nsa_range_dq(compression, accumulate = 1,
+ * sel_part), without the float32 dQ buffer between them.  The compression
+ * branch takes Lk pooled tokens (kc, vc, ktc), the window branch keys of the
+ * query length (kw, vw, ktw); lse / dot / rowscale per branch as in
+ * nsa_range_dq.  No counterpart in the reference (its two launches are
+ * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426, once per
+ * branch); sel_part, sel_idx and dq_out are required. */
+int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void* vc, const void* ktc,
+                    const float* lse_c, const float* dot_c, const float* rowscale_c, int Lk, int cmp_block,
+                    int cmp_stride, const void* kw, const void* vw, const void* ktw, const float* lse_w,
+                    const float* dot_w, const float* rowscale_w, int window, int B, int Hq, int Hkv, int T, int D,
+                    const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
+                    void* stream);
+
 /* Backward dK/dV of the range branches (key-outer; the key-side half of
  * _range_attn_bwd_qtiled_kernel).  coff / dot: row offsets and deltas from
  * nsa_bwd_prep.  dk/dv float32 [B][Hkv][Lk][D]; the call zero-fills and

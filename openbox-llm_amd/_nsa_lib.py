@@ -60,6 +60,8 @@ SIGNATURES = {
                                   _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _P]),
     "nsa_range_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
+    "nsa_range_dq_cw": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I,
+                             _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
     "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P,
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_importance_topn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,

@@ -431,6 +431,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ---------------------------------------------------------------------------
 // dQ
 // ---------------------------------------------------------------------------
+// Optional second branch of a dQ launch: the window branch over keys of the
+// query length, walked after the launch's compression keys into the same dQ
+// accumulators (k == nullptr: none).
+template <typename T> struct DqWindow {
+  const T* k;
+  const T* v;
+  const T* kt;
+  const float* lse;
+  const float* dot;
+  const float* rowscale;
+  int Lp;
+};
+
 // One 32-key tile of dQ for NT row tiles; c = lse*log2(e) - log2(rowscale) per
 // row, so P = exp2(S*sl2 - c) carries the gate weight.
 template <typename T, int D, int NT, int DT = Tile32<T, D>::DT, int KS = Tile32<T, D>::KS>
@@ -497,7 +510,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                     int accumulate, int Hq, int Hkv, int T_, int Lk, int Lp, int nqt,
                                                     int window, int cl, int cd, float sl2, float scale,
                                                     const T* __restrict__ sel_part, const int32_t* __restrict__ sel_idx,
-                                                    T* __restrict__ dq_out, int S, int sel_L) {
+                                                    T* __restrict__ dq_out, int S, int sel_L, DqWindow<T> w2) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 3;   // key tiles in flight + 1
@@ -517,33 +530,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
   const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
   if (tb0 >= T_) return;
-  const RangeSpan sp = range_span(mode, tb0, QPB, tw0, QPW, T_, Lk, window, cl, cd);
-  const FullSpan fs = full_span(mode, tw0, QPW, T_, Lk, window, cl, cd);
   const int bh = mp.b * Hkv + mp.hkv;
 
   const int hd = n & 15;
   const bool hok = mp.hc * 16 + hd < mp.G;
   const int hsafe = hok ? hd : 0;
   Frag<T> qf[NT][C::KS], df[NT][C::KS];
-  int lo[NT], hi[NT];
-  int64_t row[NT];
+  int64_t row[NT], srow[NT];
   bool rok[NT];
-  float c[NT], dlt[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int t = tw0 + 2 * nt + (n >> 4);
     const int tc = t < T_ ? t : T_ - 1;
     rok[nt] = hok && t < T_;
     row[nt] = ((int64_t)mp.b * Hq + mp.head0 + hd) * T_ + t;
-    const int64_t srow = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + tc;
-    visible_range(mode, tc, Lk, window, cl, cd, lo[nt], hi[nt]);
-    const float rs = rowscale != nullptr ? rowscale[srow] : 1.0f;
-    c[nt] = lse[srow] * kLog2e - __log2f(rs);
-    dlt[nt] = dot[srow];
+    srow[nt] = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + tc;
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) {
-      qf[nt][s].load(q + srow * D + 16 * s + 8 * h);
-      df[nt][s].load(dout + srow * D + 16 * s + 8 * h);
+      qf[nt][s].load(q + srow[nt] * D + 16 * s + 8 * h);
+      df[nt][s].load(dout + srow[nt] * D + 16 * s + 8 * h);
     }
   }
   f32x16 acc[C::DT][NT];
@@ -551,33 +556,54 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) acc[dt][nt] = zero16();
-
-  const int kt0 = sp.klo & ~31;
-  const int ntile = sp.khi >= sp.klo ? (sp.khi - kt0) / 32 + 1 : 0;
-  const T* kbase = k + (int64_t)bh * Lk * D;
-  const T* vbase = v + (int64_t)bh * Lk * D;
-  const T* ktbase = kt + (int64_t)bh * D * Lp;
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) settle(qf[nt][s]), settle(df[nt][s]);
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(c[nt]), "+v"(dlt[nt]));
   RowTileDma<T, D, 256, false> rdma;   // K and V rows share the per-lane offsets
-  ColTileDma<T, D, 256> ktdma;
   rdma.init(tid);
-  ktdma.init(tid, Lp);
-  constexpr int LT = 2 * decltype(rdma)::NL + decltype(ktdma)::NL;
-  key_pipeline<NST, LT>(ntile, [&](int i) {
-    rdma.request(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
-    rdma.request(sV[i % NST], vbase, kt0 + 32 * i, Lk, tid);
-    ktdma.request(sKt[i % NST], ktbase, kt0 + 32 * i, tid);
-  }, [&](int it) {
-    const int kb = kt0 + 32 * it;
-    const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
-    dq_tile<T, D, NT>(acc, qf, df, sK[it % NST], sV[it % NST], sKt[it % NST], kb, mask, lo, hi, c, dlt, sl2, n,
-                      h);
-  });
+
+  // one branch's walk over its keys, accumulating into acc
+  auto walk = [&](int bmode, const T* k_, const T* v_, const T* kt_, const float* lse_, const float* dot_,
+                  const float* rs_, int Lk_, int Lp_) {
+    const RangeSpan sp = range_span(bmode, tb0, QPB, tw0, QPW, T_, Lk_, window, cl, cd);
+    const FullSpan fs = full_span(bmode, tw0, QPW, T_, Lk_, window, cl, cd);
+    int lo[NT], hi[NT];
+    float c[NT], dlt[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int t = tw0 + 2 * nt + (n >> 4);
+      visible_range(bmode, t < T_ ? t : T_ - 1, Lk_, window, cl, cd, lo[nt], hi[nt]);
+      const float rs = rs_ != nullptr ? rs_[srow[nt]] : 1.0f;
+      c[nt] = lse_[srow[nt]] * kLog2e - __log2f(rs);
+      dlt[nt] = dot_[srow[nt]];
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) asm volatile("" : "+v"(c[nt]), "+v"(dlt[nt]));
+    const int kt0 = sp.klo & ~31;
+    const int ntile = sp.khi >= sp.klo ? (sp.khi - kt0) / 32 + 1 : 0;
+    const T* kbase = k_ + (int64_t)bh * Lk_ * D;
+    const T* vbase = v_ + (int64_t)bh * Lk_ * D;
+    const T* ktbase = kt_ + (int64_t)bh * D * Lp_;
+    ColTileDma<T, D, 256> ktdma;
+    ktdma.init(tid, Lp_);
+    constexpr int LT = 2 * decltype(rdma)::NL + decltype(ktdma)::NL;
+    key_pipeline<NST, LT>(ntile, [&](int i) {
+      rdma.request(sK[i % NST], kbase, kt0 + 32 * i, Lk_, tid);
+      rdma.request(sV[i % NST], vbase, kt0 + 32 * i, Lk_, tid);
+      ktdma.request(sKt[i % NST], ktbase, kt0 + 32 * i, tid);
+    }, [&](int it) {
+      const int kb = kt0 + 32 * it;
+      const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
+      dq_tile<T, D, NT>(acc, qf, df, sK[it % NST], sV[it % NST], sKt[it % NST], kb, mask, lo, hi, c, dlt, sl2, n,
+                        h);
+    });
+  };
+  walk(mode, k, v, kt, lse, dot, rowscale, Lk, Lp);
+  if (w2.k != nullptr) {
+    __syncthreads();   // every wave is done with the first walk's stages
+    walk(NSA_MODE_WINDOW, w2.k, w2.v, w2.kt, w2.lse, w2.dot, w2.rowscale, T_, w2.Lp);
+  }
 
   if (sel_part != nullptr) {
     // finish the rows: dq_out = (dq if accumulate) + this branch's dQ + the
@@ -709,6 +735,29 @@ static int range_fwd_launch(int mode, const void* q, const void* k, const void* 
   return nsa_launch_status();
 }
 
+template <typename E>
+static int range_dq_launch(int mode, const void* q, const void* k, const void* v, const void* kt, const void* dout,
+                           const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate,
+                           int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
+                           const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out,
+                           const DqWindow<E>& w2, hipStream_t s) {
+  const int NHC = (Hq / Hkv + 15) / 16;
+  const int Lp = padded_len(Lk);
+  const float scale = 1.0f / sqrtf((float)D);
+  const float sl2 = scale * kLog2e;
+  constexpr int NT = RangeNT<E>::dq;
+  const int nqt = (T + 8 * NT - 1) / (8 * NT);
+  const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
+  NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  NSA_DISPATCH_D(D, {
+    k_range_dq32<E, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
+        mode, (const E*)q, (const E*)k, (const E*)v, (const E*)kt, (const E*)dout, lse, dot, rowscale, dq,
+        accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale, (const E*)sel_part,
+        sel_idx, (E*)dq_out, S, sel_block, w2);
+  });
+  return nsa_launch_status();
+}
+
 extern "C" {
 
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
@@ -769,33 +818,46 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
                                     sel_block % 16 == 0 && (!accumulate || dq != nullptr)),
             NSA_ERR_ARG);
   if (T == 0) return NSA_OK;
-  const int NHC = (Hq / Hkv + 15) / 16;
-  const int Lp = padded_len(Lk);
-  const float scale = 1.0f / sqrtf((float)D);
-  const float sl2 = scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  NSA_DISPATCH_D(D, {
-    if (dtype == NSA_BF16) {
-      constexpr int NT = RangeNT<bf16>::dq;
-      const int nqt = (T + 8 * NT - 1) / (8 * NT);
-      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-      k_range_dq32<bf16, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
-          mode, (const bf16*)q, (const bf16*)k, (const bf16*)v, (const bf16*)kt, (const bf16*)dout, lse, dot,
-          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale,
-          (const bf16*)sel_part, sel_idx, (bf16*)dq_out, S, sel_block);
-    } else {
-      constexpr int NT = RangeNT<float>::dq;
-      const int nqt = (T + 8 * NT - 1) / (8 * NT);
-      const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
-      NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
-      k_range_dq32<float, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
-          mode, (const float*)q, (const float*)k, (const float*)v, (const float*)kt, (const float*)dout, lse, dot,
-          rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale,
-          (const float*)sel_part, sel_idx, (float*)dq_out, S, sel_block);
-    }
-  });
-  return nsa_launch_status();
+  if (dtype == NSA_BF16)
+    return range_dq_launch<bf16>(mode, q, k, v, kt, dout, lse, dot, rowscale, dq, accumulate, B, Hq, Hkv, T, Lk,
+                                 D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block, dq_out,
+                                 DqWindow<bf16>{}, s);
+  return range_dq_launch<float>(mode, q, k, v, kt, dout, lse, dot, rowscale, dq, accumulate, B, Hq, Hkv, T, Lk, D,
+                                window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block, dq_out,
+                                DqWindow<float>{}, s);
+}
+
+int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void* vc, const void* ktc,
+                    const float* lse_c, const float* dot_c, const float* rowscale_c, int Lk, int cmp_block,
+                    int cmp_stride, const void* kw, const void* vw, const void* ktw, const float* lse_w,
+                    const float* dot_w, const float* rowscale_w, int window, int B, int Hq, int Hkv, int T, int D,
+                    const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
+                    void* stream) {
+  NSA_CHECK(range_args_ok(NSA_MODE_COMPRESS, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride) &&
+                range_args_ok(NSA_MODE_WINDOW, B, Hq, Hkv, T, T, D, window, cmp_block, cmp_stride),
+            NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(kw && vw && ktw && lse_w && dot_w && kc && vc && ktc && lse_c && dot_c && dq_out, NSA_ERR_ARG);
+  NSA_CHECK(sel_part == nullptr || (sel_idx != nullptr && S >= 1 && sel_block >= 16 && sel_block % 16 == 0),
+            NSA_ERR_ARG);
+  NSA_CHECK(sel_part != nullptr, NSA_ERR_ARG);   // the rows are finished through the selection epilogue
+  if (T == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int Lpw = padded_len(T);
+  if (dtype == NSA_BF16)
+    return range_dq_launch<bf16>(NSA_MODE_COMPRESS, q, kc, vc, ktc, dout, lse_c, dot_c, rowscale_c, nullptr, 0, B,
+                                 Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block,
+                                 dq_out,
+                                 DqWindow<bf16>{(const bf16*)kw, (const bf16*)vw, (const bf16*)ktw, lse_w, dot_w,
+                                                rowscale_w, Lpw},
+                                 s);
+  return range_dq_launch<float>(NSA_MODE_COMPRESS, q, kc, vc, ktc, dout, lse_c, dot_c, rowscale_c, nullptr, 0, B,
+                                Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block,
+                                dq_out,
+                                DqWindow<float>{(const float*)kw, (const float*)vw, (const float*)ktw, lse_w, dot_w,
+                                                rowscale_w, Lpw},
+                                s);
 }
 
 }  // extern "C"

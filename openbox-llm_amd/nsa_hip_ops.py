@@ -154,6 +154,11 @@ _SIDE_STREAMS = {}
 # and in order each kernel's timing describes that kernel alone.
 OVERLAP_SEL_BWD = False
 
+# True: the fused backward computes the compression and window dQ in one launch
+# (nsa_range_dq_cw) that also finishes the rows; False: one launch per branch
+# through a float32 dQ buffer.
+FUSE_RANGE_DQ = True
+
 
 def _side_stream(device):
     """A second stream per device (default priority) for work that overlaps the
@@ -412,6 +417,21 @@ def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0
           L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
           int(window), int(cmp_block), int(cmp_stride), L.ptr(sel_part), L.ptr(sel_idx), S, int(sel_block),
           L.ptr(out), L.dtype_code(q), _stream(q))
+    return out
+
+
+def range_dq_cw(q, do, kc, vc, ktc, lse_c, dot_c, rs_c, kw, vw, ktw, lse_w, dot_w, rs_w, geom, sel_part, sel_idx):
+    """dQ of the compression and window branches in one launch, rows finished
+    with the selection dQ partials: returns dq_out in q's dtype = compression
+    + window dQ + the partials of the valid slots of ``sel_idx``."""
+    B, Hq, T, D = q.shape
+    Hkv, Lk = kc.shape[1], kc.shape[2]
+    out = torch.empty(B, Hq, T, D, device=q.device, dtype=q.dtype)
+    _call("dq[cmp+win]", _lib().nsa_range_dq_cw, L.ptr(q), L.ptr(do), L.ptr(kc), L.ptr(vc), L.ptr(ktc),
+          L.ptr(lse_c), L.ptr(dot_c), L.ptr(rs_c), Lk, int(geom.cmp_block), int(geom.cmp_stride), L.ptr(kw),
+          L.ptr(vw), L.ptr(ktw), L.ptr(lse_w), L.ptr(dot_w), L.ptr(rs_w), int(geom.window), B, Hq, Hkv, T, D,
+          L.ptr(sel_part), L.ptr(sel_idx), sel_idx.shape[-1], int(geom.sel_block), L.ptr(out), L.dtype_code(q),
+          _stream(q))
     return out
 
 
@@ -733,7 +753,10 @@ class NSAFusedHIP(torch.autograd.Function):
         dtype = q.dtype
         dot, rs, coff, dgate, dop = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w,
                                                   pack_hkv=ks.shape[1] if idx.shape[-1] > 0 else 0)
-        dq = torch.empty(q.shape, device=q.device, dtype=torch.float32)
+        # one launch walks the compression and window keys of every query and
+        # finishes its rows with the selection partials (no float32 dQ buffer)
+        fused_dq = FUSE_RANGE_DQ and idx.shape[-1] > 0 and k_cmp.shape[2] > 0
+        dq = None if fused_dq else torch.empty(q.shape, device=q.device, dtype=torch.float32)
         # selection dK/dV and dQ partials (block-outer, bound by memory traffic)
         # run on a side stream beside the window and compression key-side
         # kernels (bound by MFMA issue) on the current stream
@@ -753,7 +776,8 @@ class NSAFusedHIP(torch.autograd.Function):
             dvs = torch.zeros_like(dks)
         # window
         kt_w = transpose_kv(kw)
-        range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
+        if not fused_dq:
+            range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
         dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
         # compression dK/dV
         if k_cmp.shape[2] > 0:
@@ -770,7 +794,10 @@ class NSAFusedHIP(torch.autograd.Function):
         # selection partials, written in the input dtype
         if k_cmp.shape[2] > 0:
             kt_c = transpose_kv(k_cmp)
-            if dq_part is not None:
+            if fused_dq:
+                dq_out = range_dq_cw(q, dout, k_cmp, v_cmp, kt_c, lse_c, dot[0], rs[0], kw, vw, kt_w, lse_w, dot[2],
+                                     rs[2], geom, dq_part, idx)
+            elif dq_part is not None:
                 dq_out = range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
                                   geom.cmp_block, geom.cmp_stride, sel_part=dq_part, sel_idx=idx,
                                   sel_block=geom.sel_block)

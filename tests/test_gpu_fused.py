@@ -230,6 +230,38 @@ def test_nsa_attention_overlapped_backward_matches_serial(dtype):
             assert_close(a, b, dtype, f"step {step} d{nm}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape_i", [0, 1])
+def test_nsa_attention_fused_range_dq_matches_per_branch(dtype, shape_i):
+    """The compression + window dQ in one launch (nsa_range_dq_cw) gives the
+    gradients of one launch per branch through the float32 dQ buffer."""
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    import nsa_hip_ops as ops
+    shape = SMALL_BASELINE_SHAPES[shape_i]
+    B, Hq, Hkv, T, D = (shape[x] for x in ("B", "Hq", "Hkv", "T", "D"))
+    geom = ops.NSAGeometry(**BASELINE_GEOM)
+    ins, do = _fused_inputs(B, Hq, Hkv, T, D, dtype, seed=12, head_scale=True)
+    do = do.to(dev)
+    default = ops.FUSE_RANGE_DQ
+
+    def grads(fuse):
+        ops.FUSE_RANGE_DQ = fuse
+        try:
+            xs = [t.to(dev).requires_grad_() for t in ins]
+            out, _ = nfk.nsa_attention(*xs, geom)
+            out.backward(do)
+            torch.cuda.synchronize()
+            return [x.grad.float().cpu() for x in xs]
+        finally:
+            ops.FUSE_RANGE_DQ = default
+
+    per_branch = grads(False)
+    fused = grads(True)
+    for nm, a, b in zip(NAMES, fused, per_branch):
+        assert_close(a, b, dtype, f"d{nm}")
+
+
 def test_csr_bit_exact():
     dev = require_gpu()
     import nsa_fsa
