@@ -157,6 +157,38 @@ def test_layout_helpers_both_paths(dtype):
     torch.cuda.synchronize()
 
 
+def test_compression_dkdv_split_grid_long_sequence():
+    """Compression dK/dV at T=32768 over 8 KV heads: a grid longer than one
+    round of resident workgroups, so both the whole-chunk workgroups and the
+    split chunks that end the grid run.  Reference: the same branch in plain
+    float32 torch on the GPU (dense masked softmax; rows with no pooled key
+    give 0), from the same bf16 inputs.  Tolerance: the bf16 bar of TOL."""
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    B, H, T, D, cl, cd = 1, 8, 32768, 64, 32, 16
+    n = O.n_cmp_tokens(T, cl, cd)
+    q = randn((B, H, T, D), 21, torch.bfloat16).to(dev)
+    kp = randn((B, H, n, D), 22, torch.bfloat16).to(dev)
+    vp = randn((B, H, n, D), 23, torch.bfloat16).to(dev)
+    do = randn((B, H, T, D), 24, torch.bfloat16).to(dev)
+    kg, vg = kp.clone().requires_grad_(), vp.clone().requires_grad_()
+    nfk.compression_attn_triton(q, kg, vg, cl, cd).backward(do)
+    torch.cuda.synchronize()
+    t0 = cl - 1   # first query that sees a pooled token
+    qf = q[:, :, t0:].float()
+    kf = kp.float().requires_grad_()
+    vf = vp.float().requires_grad_()
+    s_ = torch.matmul(qf, kf.transpose(-1, -2).contiguous()) * D ** -0.5
+    t = torch.arange(t0, T, device=dev)[:, None]
+    i = torch.arange(n, device=dev)[None, :]
+    s_ = s_.masked_fill(i * cd + cl - 1 > t, float("-inf"))
+    o = torch.matmul(torch.softmax(s_, dim=-1), vf)
+    o.backward(do[:, :, t0:].float())
+    torch.cuda.synchronize()
+    assert_close(kg.grad, kf.grad, torch.bfloat16, "dk")
+    assert_close(vg.grad, vf.grad, torch.bfloat16, "dv")
+
+
 def test_empty_and_tiny_rows():
     """T smaller than a block, all slots -1, and S = 0."""
     dev = require_gpu()
