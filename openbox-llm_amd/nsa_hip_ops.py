@@ -25,6 +25,7 @@ import _nsa_lib as L
 MODE_WINDOW = L.MODE_WINDOW
 MODE_COMPRESS = L.MODE_COMPRESS
 SEL_DKDV_CHUNK = 512          # CSR queries per selection dK/dV work item
+SEL_FWD_CHUNK = 128           # CSR queries per selection forward work item (c3: 128 measured 0.1 ms faster than 512)
 
 
 @dataclass(frozen=True)
@@ -569,10 +570,10 @@ def sel_fwd_partials(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None)
     G = Hq // Hkv
     o_part = torch.empty(B, Hkv, T, ns, G, D, device=q.device, dtype=q.dtype)
     ml_part = torch.empty(B, Hkv, T, ns, G, 2, device=q.device, dtype=torch.float32)
-    ws_bytes = int(_lib().nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
+    ws_bytes = int(_lib().nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, SEL_FWD_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
     _call("fwd[sel]", _lib().nsa_sel_fwd_bo, L.ptr(qp), L.ptr(k), L.ptr(vt), L.ptr(q_of_block), L.ptr(offsets),
-          L.ptr(o_part), L.ptr(ml_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size, SEL_DKDV_CHUNK,
+          L.ptr(o_part), L.ptr(ml_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size, SEL_FWD_CHUNK,
           L.dtype_code(q), _stream(q))
     return (o_part, ml_part), csr
 
