@@ -828,7 +828,9 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   int32_t* n_items = (int32_t*)((char*)workspace + cap * sizeof(int4));
   k_sel_items<<<1, 1024, 0, s>>>(block_offsets, B * Hkv * n_blk, n_blk, chunk, items, n_items);
   if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
-  const size_t grid_cap = cap * sel_passes(block_size) < 4096 ? cap * sel_passes(block_size) : 4096;
+  // one workgroup per resident slot (two per CU); next_item hands out the rest
+  const size_t slots = 2 * (size_t)device_cu_count();
+  const size_t grid_cap = cap * sel_passes(block_size) < slots ? cap * sel_passes(block_size) : slots;
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
   const int Lp = padded_len(T);
