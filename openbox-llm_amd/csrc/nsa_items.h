@@ -72,7 +72,7 @@ static inline size_t sel_items_cap(int B, int Hkv, int T, int S, int block_size,
 
 // Most CSR entries in one selection work item (the kernels stage an item's
 // entries in LDS); the item chunk passed to the entry points is capped here.
-constexpr int kSelItemMax = 512;
+constexpr int kSelItemMax = 1024;
 
 // Keys of a selection block handled per pass of the block-outer kernels; a
 // block longer than this is split into ceil(L / kSelPass) partial slots.
