@@ -127,7 +127,7 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * selection_backward_fsa, nsa_selection_backward.py:207-334).  Consumes the
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
- * work items of at most `chunk` (<= 512) queries; q_of_block holds (t << b) | s
+ * work items of at most `chunk` (<= 1024) queries; q_of_block holds (t << b) | s
  * when `packed`.  q and dout are in the nsa_pack_heads layout
  * [B][Hkv][T][G][D].  coff / dot are the row offsets and deltas of
  * nsa_bwd_prep ([B][Hq][T]), kt the
@@ -152,7 +152,7 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
  * (nsa_selection_kernel.py:286-290), both laid out
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G] (x D for o_part).
  * q is in the nsa_pack_heads layout [B][Hkv][T][G][D], vt is the
- * nsa_transpose_kv copy of v; chunk <= 512.  Workspace from
+ * nsa_transpose_kv copy of v; chunk <= 1024.  Workspace from
  * nsa_sel_fwd_bo_workspace. */
 int nsa_sel_partial_slots(int S, int block_size);
 size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);

@@ -9,8 +9,8 @@
 // S^T = K Q^T, V^T as the A operand of O^T = V^T P^T -- and streams the item's
 // queries two at a time (32 rows = two queries x 16 heads) through LDS.  For
 // every (query, slot, pass) it writes the block-local softmax result: the
-// normalised output O_j / l_j in the input dtype and (m_j, l_j), m in log2
-// units.  k_sel_merge combines the partials of each query into o and lse;
+// unnormalised output O_j = sum_k p_k v_k (p_k = exp2(s_k - m_j)) in the
+// input dtype and (m_j, l_j = sum_k p_k), m in log2 units.  k_sel_merge combines the partials of each query into o and lse;
 // k_sel_dq_reduce sums the dQ partials written by the dK/dV kernel.
 #include "nsa_items.h"
 #include "nsa_launch.h"
