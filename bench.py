@@ -4,18 +4,22 @@ A step is one full NSA attention layer call, forward and backward, over one
 batch of synthetic inputs resident in HBM: compression pooling, compression
 attention, block importance + top-n on the GPU, selection and sliding-window
 attention, gate blend, then the backward of all of it.  The default workload
-is BASELINE config 3 (B1 T32768 Hq64 Hkv4 D128, l=32 d=16 l'=64 top-16 with
-the initial and two local blocks forced, w=512, bf16).
+is BASELINE config 3 as stated there: B1 T32768 Hq64 Hkv4 D128, l=32 d=16
+l'=64, plain top-16 (no forced blocks), w=512, bf16.  The same inputs with the
+initial and two local blocks forced among the 16 are timed beside it
+(``c3_forced``).
 
 Prints ONE JSON line (rank 0): the metric, tokens/s, the dominant kernel's
-roofline (algorithmic FLOPs / its HIP-event-timed launch duration) and a CPU
-baseline (the float32 CPU oracle on a bounded sample of query rows).
+roofline (algorithmic work / its HIP-event-timed launch duration, bound set
+from its measured HBM bytes), per-kernel MFMA fractions, and CPU baselines
+(the float32 CPU oracle on a bounded row sample of c3, and dense on c1).
 """
 
 import argparse
 import json
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -30,16 +34,37 @@ import torch  # noqa: E402
 METRIC = "NSA fused fwd+bwd tokens/s at T=32K bf16; % of MFMA/HBM roofline"
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_F32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
 
+# geometry tuples: (cmp_block, cmp_stride, sel_block, n_sel, window, force_init, n_local)
 WORKLOADS = {
-    "c3": dict(B=1, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, True, 2), head_scale=True,
+    "c3": dict(kind="fused", B=1, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, False, 0),
+               head_scale=True, in_scale=1.0,
                desc="BASELINE config 3: fused 3-branch NSA fwd+bwd, B1 T32768 Hq64 Hkv4 D128, "
-                    "l32/d16 l'64 top-16 (init + 2 local forced) w512, bf16"),
-    "c2": dict(B=4, T=8192, Hq=16, Hkv=1, D=64, geom=(32, 16, 64, 16, 512, False, 0), head_scale=False,
-               desc="BASELINE config 2 shape through the full NSA layer: B4 T8192 Hq16 Hkv1 D64"),
-    "small": dict(B=1, T=4096, Hq=16, Hkv=1, D=128, geom=(32, 16, 64, 16, 512, True, 2), head_scale=True,
-                  desc="reduced c3-like shape for quick checks"),
+                    "l32/d16 l'64 top-16 w512, bf16"),
+    "c3_forced": dict(kind="fused", B=1, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, True, 2),
+                      head_scale=True, in_scale=1.0,
+                      desc="config 3 with the initial block and 2 local blocks forced among the top-16"),
+    "c2": dict(kind="selection", B=4, T=8192, Hq=16, Hkv=1, D=64, geom=(32, 16, 64, 16, 512, False, 0),
+               head_scale=False, in_scale=1.0,
+               desc="BASELINE config 2: selection branch only, fwd+bwd, B4 T8192 Hq16 Hkv1 D64, l'64 top-16, "
+                    "indices from compression importance (l32/d16), bf16"),
+    "c1": dict(kind="fused", B=1, T=1024, Hq=4, Hkv=1, D=64, geom=(32, 16, 64, 16, 512, True, 2),
+               head_scale=False, in_scale=0.125,
+               desc="BASELINE config 1 shape: B1 T1024 Hq4 Hkv1 D64, l32/d16 l'64 top-16 (init + 2 local) w512"),
+    "small": dict(kind="fused", B=1, T=4096, Hq=16, Hkv=1, D=128, geom=(32, 16, 64, 16, 512, False, 0),
+                  head_scale=True, in_scale=1.0, desc="reduced c3-like shape for quick checks"),
 }
+
+# HBM bytes per launch of a kernel, measured with two rocprofv3 PMC passes of
+# this bench (FETCH_SIZE, then WRITE_SIZE) and scaled by what the same
+# counters read for a plain 1 GiB device copy (x2.0 and x1.0); the commands
+# and counter values are kept under profiles/.  Keyed by (workload, kernel).
+MEASURED_TRAFFIC = {
+    ("c3_forced", "dkdv[sel]"): 1.941e10 + 9.30e9,
+}
+
+ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
 
 
 def log(msg):
@@ -47,14 +72,17 @@ def log(msg):
 
 
 def make_inputs(w, dev, dtype, seed=0):
+    """Seeded synthetic inputs of a workload, generated on `dev`: q, kc, vc,
+    ks, vs, kw, vw ~ N(0,1) * in_scale (times a per-head U(0.5, 2) scale when
+    `head_scale`), gate logits N(0,1), dO N(0,1)."""
     g = torch.Generator(device=dev).manual_seed(seed)
     B, T, Hq, Hkv, D = w["B"], w["T"], w["Hq"], w["Hkv"], w["D"]
 
     def rn(*shape):
         return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
 
-    q = rn(B, Hq, T, D)
-    kv = [rn(B, Hkv, T, D) for _ in range(6)]
+    q = rn(B, Hq, T, D) * w["in_scale"]
+    kv = [rn(B, Hkv, T, D) * w["in_scale"] for _ in range(6)]
     if w["head_scale"]:
         sq = torch.rand(Hq, generator=g, device=dev) * 1.5 + 0.5
         skv = torch.rand(6, Hkv, generator=g, device=dev) * 1.5 + 0.5
@@ -82,15 +110,24 @@ def keys_visible(w, idx):
     return int(k_win), int(k_cmp), int(vis.sum())
 
 
+def sel_pairs(w, idx):
+    """(query, selected block) pairs with a visible key: the CSR length."""
+    ls = w["geom"][2]
+    t = torch.arange(w["T"], device=idx.device, dtype=torch.int64)[None, None, :, None]
+    bl = idx.long()
+    return int(((bl >= 0) & (bl * ls <= t)).sum())
+
+
 def kernel_flops(w, kv):
-    """Algorithmic FLOPs of one launch of each timed kernel (span name -> flops).
+    """Algorithmic FLOPs of one launch of each timed library call (span name -> flops).
 
     Per (query head, visible key): forward 4*D (QK^T and PV); range dK/dV
     kernels 8*D (S, dP, dV, dK); range dQ kernels 2*D (dQ only: their S and
     dP are recomputed work, counted once in the dK/dV kernel).  The selection
-    dK/dV kernel also forms the dQ partials (10*D); dq[sel] only sums them
-    and has no FLOP model.  Sum = 14*D per key, the fwd+bwd convention of
-    the metric.
+    dK/dV kernel also forms the dQ partials (10*D).  Every branch sums to
+    14*D per key, the fwd+bwd convention of the metric.  ``dq[cmp+win]`` is
+    the one launch that computes both range dQs; the per-branch ``dq[cmp]`` /
+    ``dq[win]`` entries describe the unfused path and are not added to it.
     """
     G = w["Hq"] // w["Hkv"]
     D = w["D"]
@@ -104,38 +141,85 @@ def kernel_flops(w, kv):
         else:
             out[f"dq[{br}]"] = 2 * D * rows_keys
             out[f"dkdv[{br}]"] = 8 * D * rows_keys
-    out["dq[cmp+win]"] = out["dq[cmp]"] + out["dq[win]"]   # both branches in one launch
+    out["dq[cmp+win]"] = out["dq[cmp]"] + out["dq[win]"]
     return out
 
 
-# HBM bytes per launch of the dominant kernel, measured with two rocprofv3
-# PMC passes of this bench (FETCH_SIZE, then WRITE_SIZE) and scaled by what
-# the same counters read for a plain 1 GiB device copy (x2.0 and x1.0); the
-# commands and counter values are kept under profiles/.  Reported only for
-# the workload and kernel they were measured on.
-ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
-
-MEASURED_TRAFFIC = {("c3", "dkdv[sel]"): 1.941e10 + 9.30e9}
+def step_flops(w, kv):
+    """Algorithmic FLOPs of one fwd+bwd step: 14*D per (query head, visible key)."""
+    G = w["Hq"] // w["Hkv"]
+    ks = kv if w["kind"] == "fused" else (0, 0, kv[2])
+    return 14 * w["D"] * G * sum(ks)
 
 
-def run_gpu(args, w):
+def sel_dkdv_bytes(w, pairs):
+    """Bytes the block-outer selection dK/dV schedule must move per launch,
+    with perfect caching inside one work item: per (query, block) pair the G
+    query rows of Q and dO and the dQ partial written (3*G*D elements) plus
+    the row statistics (2*G float); per selection block K, V and K^T read
+    once and dK, dV written in float32.  And the compulsory bytes: every
+    tensor the kernel touches once."""
+    B, T, Hkv, D = w["B"], w["T"], w["Hkv"], w["D"]
+    G = w["Hq"] // Hkv
+    e = 2
+    per_pair = 3 * G * D * e + 2 * G * 4
+    keys = B * Hkv * T
+    per_key = 3 * D * e + 2 * D * 4
+    algorithmic = pairs * per_pair + keys * per_key
+    rows = B * w["Hq"] * T
+    compulsory = 3 * rows * D * e + 2 * rows * 4 + keys * per_key
+    return algorithmic, compulsory
+
+
+def _setup(w, dev, dtype, seed=0):
+    import nsa_hip_ops as ops
+    geom = ops.NSAGeometry(*w["geom"])
+    ins, do = make_inputs(w, dev, dtype, seed)
+    return geom, ins, do
+
+
+def make_step(w, geom, ins, do):
+    """One fwd+bwd step of the workload -> block indices of the step."""
     import nsa_fused_kernel as nfk
     import nsa_hip_ops as ops
+    import nsa_selection_backward as nsb
 
-    dev = torch.device("cuda:0")
-    dtype = torch.bfloat16
-    geom = ops.NSAGeometry(*w["geom"])
-    ins, do = make_inputs(w, dev, dtype)
-    xs = [t.requires_grad_() for t in ins]
+    if w["kind"] == "fused":
+        xs = [t.requires_grad_() for t in ins]
+
+        def step():
+            for x in xs:
+                x.grad = None
+            out, idx = nfk.nsa_attention(*xs, geom)
+            out.backward(do)
+            return idx
+        return step
+    # selection only: indices from the compression importance (computed once;
+    # they are an input of the selection kernels), keys/values of the
+    # selection branch
+    q, kc, ks, vs = ins[0], ins[1], ins[3], ins[4]
+    with torch.no_grad():
+        k_cmp = ops.pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+        _, lse_c = ops.range_fwd(ops.MODE_COMPRESS, q, k_cmp, k_cmp, 0, geom.cmp_block, geom.cmp_stride)
+        idx = ops.importance_topn(q, k_cmp, lse_c, geom)
+    xs = [t.requires_grad_() for t in (q, ks, vs)]
 
     def step():
         for x in xs:
             x.grad = None
-        out, idx = nfk.nsa_attention(*xs, geom)
-        out.backward(do)
+        o = nsb.selection_attn_triton(*xs, idx, geom.sel_block)
+        o.backward(do)
         return idx
+    return step
 
-    log(f"[bench] warmup {args.warmup} step(s) on {torch.cuda.get_device_name(0)}")
+
+def run_gpu(args, w, name):
+    import nsa_hip_ops as ops
+
+    dev = torch.device("cuda:0")
+    geom, ins, do = _setup(w, dev, torch.bfloat16)
+    step = make_step(w, geom, ins, do)
+    log(f"[bench] {name}: warmup {args.warmup} step(s) on {torch.cuda.get_device_name(0)}")
     idx = None
     for _ in range(args.warmup):
         idx = step()
@@ -144,13 +228,12 @@ def run_gpu(args, w):
         idx = step()
         torch.cuda.synchronize()
     kv = keys_visible(w, idx)
+    pairs = sel_pairs(w, idx)
     flops_of = kernel_flops(w, kv)
-    # untimed, first: every call timed, with the backward's streams serialised
-    # (nsa_hip_ops.OVERLAP_SEL_BWD off), so that each kernel's duration is its
-    # own; this picks the dominant kernel
+    # untimed, first: every call timed (the backward runs in order on one
+    # stream), so that each kernel's duration is its own; picks the dominant
+    # kernel
     iso = ops.LaunchTimer()
-    overlap = ops.OVERLAP_SEL_BWD
-    ops.OVERLAP_SEL_BWD = False
     try:
         ops.set_timer(iso)
         for _ in range(ISO_STEPS):
@@ -158,7 +241,6 @@ def run_gpu(args, w):
         torch.cuda.synchronize()
     finally:
         ops.set_timer(None)
-        ops.OVERLAP_SEL_BWD = overlap
     iso_spans = iso.summary_ms()
     modeled = {k: v for k, v in iso_spans.items() if k in flops_of}
     dom = max(modeled, key=lambda k: modeled[k][1]) if modeled else None
@@ -173,7 +255,25 @@ def run_gpu(args, w):
     t1 = time.perf_counter()
     ops.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
-    return ms, timer.summary_ms(), iso_spans, dom, flops_of, kv, ins, do
+    return dict(ms=ms, spans=timer.summary_ms(), iso_spans=iso_spans, dom=dom, flops_of=flops_of, kv=kv,
+                pairs=pairs, ins=ins, do=do, idx=idx)
+
+
+def time_gpu_only(args, w, name):
+    """Timed steps of a workload, no per-call spans: ms per step."""
+    dev = torch.device("cuda:0")
+    geom, ins, do = _setup(w, dev, torch.bfloat16)
+    step = make_step(w, geom, ins, do)
+    for _ in range(max(1, args.warmup)):
+        idx = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    log(f"[bench] {name}: {ms:.3f} ms per step")
+    return ms, keys_visible(w, idx)
 
 
 def run_cpu_baseline(w, ins_dev, do_dev, rows_n, threads):
@@ -216,6 +316,61 @@ def run_cpu_baseline(w, ins_dev, do_dev, rows_n, threads):
     return rows.numel() * B / secs, secs, rows.numel()
 
 
+def run_cpu_c1(threads, reps=3):
+    """Config 1 on the CPU: the dense float32 oracle (importance, top-n and
+    the three gated branches, forward + backward), median of `reps` runs
+    after one warm-up, for the extended geometry (l32/d16/l'64, init + 2
+    local forced) and the aligned l = d = l' = 64 grid with no forcing
+    (exactly the reference path).  -> {variant: (tokens/s, median s)}."""
+    from oracle import nsa_oracle as O
+
+    torch.set_num_threads(threads)
+    w = WORKLOADS["c1"]
+    ins, do = make_inputs(w, torch.device("cpu"), torch.float32)
+    res = {}
+    for variant, cfg in (("extended", O.NSAConfig(*w["geom"])), ("aligned64", O.NSAConfig.reference(64, 16, 512))):
+        times = []
+        for r in range(reps + 1):
+            xs = [t.clone().requires_grad_() for t in ins]
+            t0 = time.perf_counter()
+            out, _ = O.nsa_forward_reference(*xs, cfg)
+            out.backward(do)
+            dt = time.perf_counter() - t0
+            if r > 0:
+                times.append(dt)
+        med = statistics.median(times)
+        res[variant] = (w["B"] * w["T"] / med, med)
+    return res
+
+
+def time_gpu_c1(reps=20):
+    """Config 1 on the GPU in float32 (the CPU baseline's precision): ms per
+    fwd+bwd step, extended and aligned-64 geometry."""
+    import nsa_hip_ops as ops
+    w = WORKLOADS["c1"]
+    dev = torch.device("cuda:0")
+    ins, do = make_inputs(w, dev, torch.float32)
+    res = {}
+    for variant, geom in (("extended", ops.NSAGeometry(*w["geom"])),
+                          ("aligned64", ops.NSAGeometry.aligned(64, 16, 512))):
+        xs = [t.clone().requires_grad_() for t in ins]
+
+        def step():
+            for x in xs:
+                x.grad = None
+            out, _ = ops.nsa_attention(*xs, geom)
+            out.backward(do)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            step()
+        torch.cuda.synchronize()
+        res[variant] = (time.perf_counter() - t0) * 1e3 / reps
+    return res
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -225,6 +380,43 @@ def cpu_model():
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def per_kernel_table(iso_spans, flops_of, peak):
+    """name -> {ms per step, calls per step, algorithmic TFLOP per launch, MFMA fraction}."""
+    out = {}
+    for name, (calls, tot) in sorted(iso_spans.items(), key=lambda x: -x[1][1]):
+        ent = {"ms_per_step": round(tot / ISO_STEPS, 4), "calls_per_step": calls // ISO_STEPS}
+        if name in flops_of and calls > 0:
+            per = tot / calls / 1e3
+            ent["tflop_per_launch"] = round(flops_of[name] / 1e12, 4)
+            ent["mfma_frac"] = round(flops_of[name] / per / 1e12 / peak, 4)
+        out[name] = ent
+    return out
+
+
+def branch_fractions(iso_spans, flops_of, peak):
+    """MFMA fraction of the selection and sliding-window contractions from
+    the per-call spans.  selection = fwd[sel] + dkdv[sel] (its own
+    launches; the merge of its forward partials runs inside fwd[win] and the
+    sum of its dQ partials inside dq[cmp+win], not counted here); window =
+    fwd[win] + dkdv[win] (fwd[win] includes that merge and the gate blend;
+    the window dQ runs inside dq[cmp+win]); compression = fwd[cmp] +
+    dkdv[cmp]; the combined dQ launch is reported on its own."""
+    def frac(names, flop_names=None):
+        names = [n for n in names if n in iso_spans]
+        if not names:
+            return None
+        t = sum(iso_spans[n][1] for n in names) / ISO_STEPS / 1e3
+        f = sum(flops_of[n] for n in (flop_names or names) if n in flops_of)
+        return {"ms_per_step": round(t * 1e3, 4), "tflop": round(f / 1e12, 4),
+                "mfma_frac": round(f / t / 1e12 / peak, 4) if t > 0 else None}
+    return {
+        "selection": frac(["fwd[sel]", "dkdv[sel]"]),
+        "window": frac(["fwd[win]", "dkdv[win]"]),
+        "compression": frac(["fwd[cmp]", "dkdv[cmp]"]),
+        "range_dq": frac(["dq[cmp+win]"]),
+    }
 
 
 def main():
@@ -237,6 +429,7 @@ def main():
                     help="query rows of the CPU baseline sample (about 10-20 s of CPU work at c3)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, os.cpu_count())")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the forced-block variant and the c1 timings")
     ap.add_argument("--spans", action="store_true", help="print the per-call HIP-event breakdown to stderr")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 times): the known-size kernel that "
@@ -258,43 +451,43 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
-    w = WORKLOADS[args.workload]
-    ms, spans, iso_spans, dom_name, flops_of, kv, ins_dev, do_dev = run_gpu(args, w)
+    name = args.workload
+    w = WORKLOADS[name]
+    r = run_gpu(args, w, name)
+    ms, spans, iso_spans, dom_name, flops_of, kv = r["ms"], r["spans"], r["iso_spans"], r["dom"], r["flops_of"], \
+        r["kv"]
     tokens = w["B"] * w["T"]
     value = tokens / (ms / 1e3)
-    total_flops = sum(flops_of.values())
+    total_flops = step_flops(w, kv)
 
-    # dominant kernel: the call with a FLOP model and the largest total time
-    # in the untimed steps; its launches in the timed steps give `achieved`
     if args.spans:
-        for name, (calls, tot) in sorted(iso_spans.items(), key=lambda x: -x[1][1]):
-            log(f"  {name:28s} calls {calls:4d}  total {tot:9.3f} ms  per step {tot / ISO_STEPS:8.3f} ms")
+        for nm, (calls, tot) in sorted(iso_spans.items(), key=lambda x: -x[1][1]):
+            log(f"  {nm:28s} calls {calls:4d}  total {tot:9.3f} ms  per step {tot / ISO_STEPS:8.3f} ms")
     roofline = None
     if dom_name is not None and dom_name in spans:
-        name = dom_name
-        calls, tot = spans[name]
+        calls, tot = spans[dom_name]
         per_launch_s = tot / calls / 1e3
-        achieved = flops_of[name] / per_launch_s / 1e12
-        roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved, 2),
-                    "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                    "traffic": MEASURED_TRAFFIC.get((args.workload, name)),
-                    "launch_ms": round(per_launch_s * 1e3, 4)}
-        if name in iso_spans:
-            # the same kernel in the untimed steps (backward serialised)
-            icalls, itot = iso_spans[name]
+        tflops = flops_of[dom_name] / per_launch_s / 1e12
+        mfma_frac = tflops / PEAK_BF16_TFLOPS
+        traffic = MEASURED_TRAFFIC.get((name, dom_name))
+        hbm_frac = traffic / per_launch_s / 1e9 / PEAK_HBM_GBS if traffic else None
+        roofline = {"kernel": dom_name, "launch_ms": round(per_launch_s * 1e3, 4), "traffic": traffic,
+                    "mfma_frac": round(mfma_frac, 4),
+                    "hbm_frac": round(hbm_frac, 4) if hbm_frac is not None else None}
+        if hbm_frac is not None and hbm_frac > mfma_frac:
+            # bound by memory traffic: achieved = the schedule's algorithmic bytes per launch / duration
+            alg, comp = sel_dkdv_bytes(w, r["pairs"]) if dom_name == "dkdv[sel]" else (traffic, None)
+            gbs = alg / per_launch_s / 1e9
+            roofline.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                             "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg,
+                             "compulsory_bytes": comp, "measured_gbs": round(traffic / per_launch_s / 1e9, 1)})
+        else:
+            roofline.update({"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(mfma_frac, 4)})
+        if dom_name in iso_spans:
+            icalls, itot = iso_spans[dom_name]
             iso_s = itot / icalls / 1e3
-            roofline["isolated"] = {"launch_ms": round(iso_s * 1e3, 4),
-                                    "achieved": round(flops_of[name] / iso_s / 1e12, 2),
-                                    "frac": round(flops_of[name] / iso_s / 1e12 / PEAK_BF16_TFLOPS, 4)}
-    cpu = None
-    if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        log(f"[bench] CPU baseline: float32 oracle, {args.cpu_rows} rows, {threads} threads")
-        tps, secs, nrows = run_cpu_baseline(w, ins_dev, do_dev, args.cpu_rows, threads)
-        cpu = {"value": round(tps, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-               "sample": f"{nrows} evenly spaced query rows of the same workload (fwd+bwd incl. importance/top-n "
-                         f"for those rows), {secs:.1f} s, extrapolated linearly to tokens/s; CPU {cpu_model()}, "
-                         f"os.cpu_count()={os.cpu_count()}"}
+            roofline["isolated_launch_ms"] = round(iso_s * 1e3, 4)
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -315,9 +508,37 @@ def main():
         "mfu": round(total_flops / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "algorithmic_tflop_per_step": round(total_flops / 1e12, 3),
         "visible_keys": {"win": kv[0], "cmp": kv[1], "sel": kv[2]},
+        "selection_pairs": r["pairs"],
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "branches": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
+        "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS),
     }
+    if not args.no_extras and name == "c3":
+        ms_f, kv_f = time_gpu_only(args, WORKLOADS["c3_forced"], "c3_forced")
+        res["c3_forced"] = {"ms_per_step": round(ms_f, 3), "value": round(tokens / (ms_f / 1e3), 1),
+                            "mfu": round(step_flops(WORKLOADS["c3_forced"], kv_f) / (ms_f / 1e3) / 1e12
+                                         / PEAK_BF16_TFLOPS, 4)}
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    if not args.no_cpu_baseline:
+        log(f"[bench] CPU baseline: float32 oracle, {args.cpu_rows} rows, {threads} threads")
+        tps, secs, nrows = run_cpu_baseline(w, r["ins"], r["do"], args.cpu_rows, threads) \
+            if w["kind"] == "fused" else (None, None, None)
+        if tps is not None:
+            res["cpu_baseline"] = {
+                "value": round(tps, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"{nrows} evenly spaced query rows of the same workload (fwd+bwd incl. importance/top-n "
+                          f"for those rows), {secs:.1f} s, extrapolated linearly to tokens/s; CPU {cpu_model()}, "
+                          f"os.cpu_count()={os.cpu_count()}"}
+        if not args.no_extras:
+            log("[bench] CPU baseline: config 1, dense float32 oracle")
+            c1 = run_cpu_c1(threads)
+            g1 = time_gpu_c1()
+            res["cpu_baseline_c1"] = {
+                v: {"cpu_tokens_per_s": round(tps1, 1), "cpu_ms": round(s1 * 1e3, 2), "gpu_f32_ms": round(g1[v], 3),
+                    "gpu_f32_tokens_per_s": round(WORKLOADS["c1"]["T"] / (g1[v] / 1e3), 1)}
+                for v, (tps1, s1) in c1.items()}
+            res["cpu_baseline_c1"]["note"] = (f"B1 T1024 Hq4 Hkv1 D64 fwd+bwd float32, dense oracle, median of 3 "
+                                              f"after 1 warm-up, {threads} threads; GPU: same inputs, float32")
     print(json.dumps(res), flush=True)
 
 

@@ -68,7 +68,9 @@ int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int
 int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const void* o_win, void* out,
                  int64_t rows, int D, int dtype, void* stream);
 
-/* Backward prep.  nbr == 1: dot[r] = dO[r] . o0[r] (the delta of
+/* Backward prep.  o0 / o1 / o2 are in o_dtype: dtype, or NSA_F32 when the
+ * forward kept the branch outputs unrounded (nsa_range_fwd's o_dtype).
+ * nbr == 1: dot[r] = dO[r] . o0[r] (the delta of
  * nsa_selection_backward.py:168).  nbr == 3: for each branch c,
  * dot[c*rows + r] = dO . o_c, rowscale[c*rows + r] = sigmoid(g_c) and
  * dgate[r][c] = sigmoid'(g_c) dot (autograd of nsa_fused_kernel.py:572-573).
@@ -80,7 +82,7 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
-                 int dtype, void* stream);
+                 int dtype, int o_dtype, void* stream);
 
 /* float32 accumulator -> dtype. */
 int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
@@ -179,10 +181,13 @@ int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float
  * to t iff t-window < p <= t; NSA_MODE_COMPRESS: pooled token i visible iff
  * i*cmp_stride + cmp_block - 1 <= t.  k [B][Hkv][Lk][D], vt transposed v with
  * Lp = nsa_padded_len(Lk).  Writes o and lse; q_packed (nullable) also
- * receives q in the nsa_pack_heads layout (the rows are loaded anyway). */
+ * receives q in the nsa_pack_heads layout (the rows are loaded anyway).
+ * o_dtype: the type of o -- dtype (the reference's convention), or NSA_F32
+ * so that a backward's row dots dO . o see the unrounded output (the fused
+ * layer keeps its branch outputs this way; only its gated sum is returned). */
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, void* q_packed, int dtype,
-                  void* stream);
+                  int o_dtype, void* stream);
 
 /* nsa_range_fwd that also finishes the rows of the gated three-branch layer
  * (no reference counterpart as one call: nsa_sel_merge and nsa_gate_fwd
@@ -190,12 +195,14 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
  * merges the selection partials of nsa_sel_fwd_bo (o_part, ml_part, with the
  * [B][Hkv][T][S] block_idx of block size sel_block) into o_sel / lse_sel
  * and writes out = sigmoid(g0) o_cmp + sigmoid(g1) o_sel + sigmoid(g2) o from
- * the gate logits [B][Hq][T][3], each branch rounded to the dtype first. */
+ * the gate logits [B][Hq][T][3] (out in dtype).  o, o_sel and o_cmp are in
+ * o_dtype (dtype, or NSA_F32 unrounded); the blend uses each branch as
+ * stored. */
 int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                          int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                          const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
                          void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
-                         void* stream);
+                         int o_dtype, void* stream);
 
 /* Backward dQ of the range branches (query-side half of
  * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426): dq (float32)

@@ -186,10 +186,13 @@ template <typename T, int D> struct KeyAcc {
   // then P and dS packed as the operands of the second half.  With MASK,
   // visA / visB say whether this lane's key is visible to query A / B;
   // without, every key is.
-  template <bool MASK>
+  // With SPLIT (16-bit operands only), sl receives the rounding remainder
+  // dS - round(dS) of the dS operand, for a second dK^T product: dS then
+  // enters dK with about twice the significant bits.
+  template <bool MASK, bool SPLIT = false>
   __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, bool visA, bool visB, float sl2,
                                         int lane, Frag<T> (&ta)[C::DT][2], Frag<T> (&tb)[C::DT][2],
-                                        Frag<T> (&pf)[2], Frag<T> (&sf)[2]) {
+                                        Frag<T> (&pf)[2], Frag<T> (&sf)[2], Frag<T> (&sl)[2]) {
     const int h = lane >> 5;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
@@ -228,17 +231,27 @@ template <typename T, int D> struct KeyAcc {
     pf[1].set(P + 8);
     sf[0].set(dS);
     sf[1].set(dS + 8);
+    if constexpr (SPLIT && sizeof(T) == 2) {
+      float lo[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lo[r] = dS[r] - to_f32(from_f32<T>(dS[r]));
+      sl[0].set(lo);
+      sl[1].set(lo + 8);
+    }
   }
 
-  // Second half: dV^T += dO^T P, dK^T += Q^T dS (registers only)
+  // Second half: dV^T += dO^T P, dK^T += Q^T dS (registers only); with
+  // SPLIT also dK^T += Q^T (dS - round(dS))
+  template <bool SPLIT = false>
   __device__ __forceinline__ void back(const Frag<T> (&ta)[C::DT][2], const Frag<T> (&tb)[C::DT][2],
-                                       const Frag<T> (&pf)[2], const Frag<T> (&sf)[2]) {
+                                       const Frag<T> (&pf)[2], const Frag<T> (&sf)[2], const Frag<T> (&sl)[2]) {
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         mma32(dv[dt], ta[dt][k], pf[k]);
         mma32(dk[dt], tb[dt][k], sf[k]);
+        if constexpr (SPLIT && sizeof(T) == 2) mma32(dk[dt], tb[dt][k], sl[k]);
       }
     }
   }
@@ -288,8 +301,8 @@ template <typename T, int D> struct KeyAcc {
 // fragments (element j of fragment k: accumulator register 8 k + j), and
 // post(tA, tB, sA, sB, hc, i) after the back half, so what pre stages in LDS
 // is visible to post without a second barrier.
-template <bool WANT_DS, int NSW, typename T, int D, int NTH, typename QSrc, typename Vis, typename Pre,
-          typename Post>
+template <bool WANT_DS, int NSW, typename T, int D, int NTH, bool SPLIT, typename QSrc, typename Vis,
+          typename Pre, typename Post>
 __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], const QSide<T>& x,
                                         int b, int hkv, int ntile, QSrc qsrc, Vis vis, Pre pre, Post post,
                                         float sl2, int tid) {
@@ -331,11 +344,11 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
     const int sA = __builtin_amdgcn_readfirstlane(s.meta[2]), sB = __builtin_amdgcn_readfirstlane(s.meta[3]);
     bool mask, visA, visB;
     vis(tA, tB, mask, visA, visB);
-    Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2];
+    Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2], sl[2];
     if (mask)
-      acc.template front<true>(s, rows, visA, visB, sl2, lane, ta, tb, pf, sf);
+      acc.template front<true, SPLIT>(s, rows, visA, visB, sl2, lane, ta, tb, pf, sf, sl);
     else
-      acc.template front<false>(s, rows, true, true, sl2, lane, ta, tb, pf, sf);
+      acc.template front<false, SPLIT>(s, rows, true, true, sl2, lane, ta, tb, pf, sf, sl);
     if (WANT_DS) pre(sf, it);
     if (it + NST - 1 < total)
       vm_wait_steps<(NST - 2) * LT, WANT_DS ? NSW : 0, NST - 2>(it);
@@ -343,7 +356,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
       vm_wait<0>();
     __syncthreads();
     if (it + 1 < total) KeyAcc<T, D>::read_rows(rows, stg[(it + 1) % NST], lane);
-    acc.back(ta, tb, pf, sf);
+    acc.template back<SPLIT>(ta, tb, pf, sf, sl);
     if (WANT_DS) post(tA, tB, sA, sB, hc, it);
     if (it + NST < total) request(stg[it % NST]);
     if (++ti == ntile) {
@@ -517,7 +530,7 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   };
   auto no_pre = [](const Frag<T>*, int) {};
   auto no_post = [](int, int, int, int, int, int) {};
-  kv_walk<false, 0, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
+  kv_walk<false, 0, T, D, NTH, false>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -551,7 +564,10 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // before the tile's barrier (double-buffered by tile parity) and dQ^T =
 // K^T dS^T is formed after it for the pass's 64 keys -- each wave covering
 // half of D -- and written, scaled, to the (query, slot, pass) partial that
-// k_sel_dq_reduce sums.
+// k_sel_dq_reduce sums.  dS enters dK^T twice, rounded and as its rounding
+// remainder: a block that every query selects sums tens of thousands of rows
+// into one key's dK, and a single 16-bit dS would leave that sum with an
+// error near the bf16 gradient tolerance.
 template <typename T, int D>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
@@ -694,9 +710,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       }
     };
     if (dq_part != nullptr)
-      kv_walk<true, NSW, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
+      kv_walk<true, NSW, T, D, NTH, true>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     else
-      kv_walk<false, 0, T, D, NTH>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
+      kv_walk<false, 0, T, D, NTH, true>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
     __syncthreads();   // the next item's first tiles reuse stages 0 .. and sent
   }

@@ -232,9 +232,31 @@ __global__ __launch_bounds__(256) void k_gate_fwd(const T* __restrict__ g, const
 // A group of D / N lanes per row (N = elements per 16-byte vector), each
 // lane one vector; 64 / (D / N) rows per wave.  nbr = number of branches
 // (1: plain delta, 3: gated three-branch prep).
-template <typename T>
-__global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, const T* __restrict__ o0,
-                                                  const T* __restrict__ o1, const T* __restrict__ o2,
+// N consecutive branch-output elements as float: TO is the input type (one
+// Vec16) or float kept unrounded by the forward (N / 4 16-byte loads).
+template <typename T, typename TO> struct BranchRow {
+  static constexpr int N = Vec16<T>::N;
+  float x[N];
+  __device__ __forceinline__ void load(const TO* p) {
+    if constexpr (sizeof(TO) == sizeof(T)) {
+      Vec16<T> v;
+      v.load(reinterpret_cast<const T*>(p));
+#pragma unroll
+      for (int i = 0; i < N; ++i) x[i] = v[i];
+    } else {
+#pragma unroll
+      for (int c = 0; c < N / 4; ++c) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[4 * c + i] = v[i];
+      }
+    }
+  }
+};
+
+template <typename T, typename TO>
+__global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, const TO* __restrict__ o0,
+                                                  const TO* __restrict__ o1, const TO* __restrict__ o2,
                                                   const T* __restrict__ gate, T* __restrict__ dgate,
                                                   const float* __restrict__ lse0, const float* __restrict__ lse1,
                                                   const float* __restrict__ lse2, float* __restrict__ dot,
@@ -249,7 +271,8 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   const bool ok = row < rows;
   float acc[3] = {0.f, 0.f, 0.f};
   if (ok) {
-    Vec16<T> d, x;
+    Vec16<T> d;
+    BranchRow<T, TO> x;
     d.load(dout + row * D + sub * N);
     if (dout_packed != nullptr) {
       // row (b, hkv G + g, t) -> packed row ((b Hkv + hkv) T + t) G + g
@@ -257,13 +280,13 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
       const int64_t prow = ((bhq / G) * T_ + (row - bhq * T_)) * G + bhq % G;
       d.store(dout_packed + prow * D + sub * N);
     }
-    const T* os[3] = {o0, o1, o2};
+    const TO* os[3] = {o0, o1, o2};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
       if (c >= nbr) break;
       x.load(os[c] + row * D + sub * N);
 #pragma unroll
-      for (int i = 0; i < N; ++i) acc[c] += d[i] * x[i];
+      for (int i = 0; i < N; ++i) acc[c] += d[i] * x.x[i];
     }
   }
 #pragma unroll
@@ -449,8 +472,9 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
-                 int dtype, void* stream) {
+                 int dtype, int o_dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
   const int vec = dtype == NSA_BF16 ? 8 : 4;
   NSA_CHECK(rows >= 0 && D > 0 && D % vec == 0 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
   const int gs = D / vec;
@@ -464,14 +488,19 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   NSA_CHECK(grid64 < (1ll << 31), NSA_ERR_SHAPE);
   const int grid = (int)grid64;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    k_bwd_prep<bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1, (const bf16*)o2,
-                                          (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2, dot, rowscale,
-                                          coff, (bf16*)dout_packed, G, T, rows, D, nbr);
+  if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
+    k_bwd_prep<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1,
+                                                (const bf16*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2,
+                                                dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr);
+  else if (dtype == NSA_BF16)
+    k_bwd_prep<bf16, float><<<grid, 256, 0, s>>>((const bf16*)dout, (const float*)o0, (const float*)o1,
+                                                 (const float*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1,
+                                                 lse2, dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr);
   else
-    k_bwd_prep<float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
-                                           (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1, lse2,
-                                           dot, rowscale, coff, (float*)dout_packed, G, T, rows, D, nbr);
+    k_bwd_prep<float, float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
+                                                  (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1,
+                                                  lse2, dot, rowscale, coff, (float*)dout_packed, G, T, rows, D,
+                                                  nbr);
   return nsa_launch_status();
 }
 

@@ -108,14 +108,16 @@ __device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_
 // lse_sel (the role of nsa_sel_merge) and blends the three branches through
 // the gate into out (the role of nsa_gate_fwd), each from the same rounded
 // branch outputs the separate kernels would read.
-template <typename T> struct FwdExtras {
+// TO is the type of the branch outputs (o, o_sel, o_cmp): the input type T,
+// or float when the caller keeps them unrounded for the backward's row dots.
+template <typename T, typename TO> struct FwdExtras {
   T* q_packed;             // [B][Hkv][T][G][D] (nullable)
   const T* opart;          // [B][Hkv][T][NS][G][D] unnormalised block-local outputs O_j = sum p v
   const float2* ml;        // [B][Hkv][T][NS][G] (m_j [log2 units], l_j)
   const int32_t* idx;      // [B][Hkv][T][S] selected blocks
-  T* o_sel;                // [B][Hq][T][D]
+  TO* o_sel;               // [B][Hq][T][D]
   float* lse_sel;          // [B][Hq][T]
-  const T* o_cmp;          // [B][Hq][T][D] compression output
+  const TO* o_cmp;         // [B][Hq][T][D] compression output
   const T* gate;           // [B][Hq][T][3] gate logits
   T* out;                  // [B][Hq][T][D]
   int S, sel_L;
@@ -124,9 +126,9 @@ template <typename T> struct FwdExtras {
 // The wave's own output rows (this branch, unnormalised acc with the row
 // statistics l_, m_) go through LDS so that every row is handled in 8-element
 // chunks: lane (row sub-index, chunk) per pass.
-template <typename T, int D>
-__device__ __forceinline__ void finish_rows(const FwdExtras<T>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
-                                            float l_row, float m_row, bool any_key, bool rok, int64_t row, T* o,
+template <typename T, typename TO, int D>
+__device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
+                                            float l_row, float m_row, bool any_key, bool rok, int64_t row, TO* o,
                                             float* lse, char* smem, int w, int lane, int tw0, const RangeMap& mp,
                                             int Hq, int Hkv, int T_) {
   using C = Tile32<T, D>;
@@ -168,7 +170,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T>& f, const f32x16 
       for (int i = 0; i < 4; ++i) ow[i] = a[i], ow[4 + i] = b2[i];
       store8(o + orow * D + 8 * c8, ow);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ow[i] = to_f32(from_f32<T>(ow[i]));
+      for (int i = 0; i < 8; ++i) ow[i] = to_f32(from_f32<TO>(ow[i]));
     }
     // selection: merge the slot partials (running maximum over batches of 16)
     const int64_t qs = bh * T_ + t;
@@ -224,7 +226,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T>& f, const f32x16 
     const float g2 = sigmoidf(to_f32(f.gate[orow * 3 + 2]));
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * to_f32(from_f32<T>(acc_s[i])) + g2 * ow[i];
+    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * to_f32(from_f32<TO>(acc_s[i])) + g2 * ow[i];
     store8(f.out + orow * D + 8 * c8, y);
   }
 }
@@ -311,12 +313,12 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
       for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], va[dt][s], pf[nt][s]);
 }
 
-template <typename T, int D, int NT>
+template <typename T, int D, int NT, typename TO>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_fwd32(int mode, const T* __restrict__ q, const T* __restrict__ k,
-                                                     const T* __restrict__ vt, T* __restrict__ o,
+                                                     const T* __restrict__ vt, TO* __restrict__ o,
                                                      float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
                                                      int Lp, int nqt, int window, int cl, int cd, float sl2,
-                                                     const FwdExtras<T> fin_args) {
+                                                     const FwdExtras<T, TO> fin_args) {
   using C = Tile32<T, D>;
   constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 4;   // key tiles in flight + 1
@@ -403,7 +405,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   if (fin_args.opart != nullptr) {
     static_assert(NT == 1, "one 32-row tile per wave is staged");
-    finish_rows<T, D>(fin_args, acc, l_[0], m_[0], lo[0] <= hi[0], rok[0], row[0], o, lse, smem, w, lane,
+    finish_rows<T, TO, D>(fin_args, acc, l_[0], m_[0], lo[0] <= hi[0], rok[0], row[0], o, lse, smem, w, lane,
                       tw0, mp, Hq, Hkv, T_);
     return;
   }
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!rok[nt]) continue;
     const bool any_key = lo[nt] <= hi[nt];
     const float inv = any_key ? 1.0f / lt : 0.0f;
-    T* orow = o + row[nt] * D;
+    TO* orow = o + row[nt] * D;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
@@ -716,10 +718,10 @@ extern "C" {
 
 }  // extern "C"
 
-template <typename E>
+template <typename E, typename TO>
 static int range_fwd_launch(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                             int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
-                            const FwdExtras<E>& fin, hipStream_t s) {
+                            const FwdExtras<E, TO>& fin, hipStream_t s) {
   const int NHC = (Hq / Hkv + 15) / 16;
   const int Lp = padded_len(Lk);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
@@ -728,7 +730,7 @@ static int range_fwd_launch(int mode, const void* q, const void* k, const void* 
   const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   NSA_DISPATCH_D(D, {
-    k_range_fwd32<E, DD, NT><<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)vt, (E*)o,
+    k_range_fwd32<E, DD, NT, TO><<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)vt, (TO*)o,
                                                             lse, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block,
                                                             cmp_stride, sl2, fin);
   });
@@ -762,47 +764,61 @@ extern "C" {
 
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, void* q_packed, int dtype,
-                  void* stream) {
+                  int o_dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
   if (T == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
   NSA_CHECK(q_packed != q, NSA_ERR_ARG);
-  if (dtype == NSA_BF16) {
-    FwdExtras<bf16> ex{};
+  if (dtype == NSA_BF16 && o_dtype == NSA_BF16) {
+    FwdExtras<bf16, bf16> ex{};
     ex.q_packed = (bf16*)q_packed;
-    return range_fwd_launch<bf16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, ex,
-                                  s);
+    return range_fwd_launch<bf16, bf16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block,
+                                        cmp_stride, ex, s);
   }
-  FwdExtras<float> ex{};
+  if (dtype == NSA_BF16) {
+    FwdExtras<bf16, float> ex{};
+    ex.q_packed = (bf16*)q_packed;
+    return range_fwd_launch<bf16, float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block,
+                                         cmp_stride, ex, s);
+  }
+  FwdExtras<float, float> ex{};
   ex.q_packed = (float*)q_packed;
-  return range_fwd_launch<float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, ex,
-                                 s);
+  return range_fwd_launch<float, float>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block,
+                                        cmp_stride, ex, s);
 }
 
 int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                          int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                          const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
                          void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
-                         void* stream) {
+                         int o_dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
   NSA_CHECK(o_part && ml_part && block_idx && o_sel && lse_sel && o_cmp && gate && out, NSA_ERR_ARG);
   NSA_CHECK(S >= 1 && sel_block >= 16 && sel_block % 16 == 0, NSA_ERR_SHAPE);
   if (T == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16)
-    return range_fwd_launch<bf16>(
+  if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
+    return range_fwd_launch<bf16, bf16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-        FwdExtras<bf16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel, lse_sel,
-                        (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
+        FwdExtras<bf16, bf16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel,
+                              lse_sel, (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
         s);
-  return range_fwd_launch<float>(
+  if (dtype == NSA_BF16)
+    return range_fwd_launch<bf16, float>(
+        mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+        FwdExtras<bf16, float>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
+                               lse_sel, (const float*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
+        s);
+  return range_fwd_launch<float, float>(
       mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-      FwdExtras<float>{nullptr, (const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel, lse_sel,
-                       (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block},
+      FwdExtras<float, float>{nullptr, (const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
+                              lse_sel, (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block},
       s);
 }
 

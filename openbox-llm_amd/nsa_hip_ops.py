@@ -284,10 +284,11 @@ def sel_fwd(q, k, v, block_idx, block_size, vt=None):
     return o, lse
 
 
-def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_packed=None):
+def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_packed=None, o_f32=False):
     """Window (mode 0) or compression (mode 1) forward -> (o, lse[f32]);
     ``q_packed`` (optional, [B, Hkv, T, G, D]) also receives the
-    ``pack_heads`` copy of q."""
+    ``pack_heads`` copy of q.  ``o_f32``: o in float32 (unrounded), else in
+    q's dtype."""
     check_qkv(q, k, v)
     q, k = _contig(q), _contig(k)
     B, Hq, T, D = q.shape
@@ -296,11 +297,11 @@ def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_pac
         assert Lk == T and window >= 1, "window keys must have the query length, window >= 1"
     if vt is None:
         vt = transpose_kv(v)
-    o = torch.empty_like(q)
+    o = torch.empty(q.shape, device=q.device, dtype=torch.float32 if o_f32 else q.dtype)
     lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
     _call(_span_name("fwd", mode), _lib().nsa_range_fwd, mode, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o), L.ptr(lse),
-                                 B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block), int(cmp_stride),
-                                 L.ptr(q_packed), L.dtype_code(q), _stream(q))
+          B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block), int(cmp_stride), L.ptr(q_packed), L.dtype_code(q),
+          L.dtype_code(o), _stream(q))
     return o, lse
 
 
@@ -308,7 +309,8 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     """Window forward that also finishes the gated layer's rows: returns
     (o_w, lse_w, o_s, lse_s, out), with the selection partials ``sel_parts``
     = (o_part, ml_part) of ``sel_fwd_partials`` merged into o_s / lse_s and
-    out = sum_c sigmoid(gate_c) o_c over the three branches."""
+    out = sum_c sigmoid(gate_c) o_c over the three branches.  o_w and o_s
+    take o_c's dtype (q's, or float32 unrounded); out is in q's dtype."""
     check_qkv(q, k, v)
     q, k, gate, o_c = _contig(q), _contig(k), _contig(gate), _contig(o_c)
     B, Hq, T, D = q.shape
@@ -317,15 +319,16 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     if vt is None:
         vt = transpose_kv(v)
     o_part, ml_part = sel_parts
-    o_w = torch.empty_like(q)
+    assert o_c.dtype in (q.dtype, torch.float32), "branch outputs are q's dtype or float32"
+    o_w = torch.empty(q.shape, device=q.device, dtype=o_c.dtype)
     lse_w = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
-    o_s = torch.empty_like(q)
+    o_s = torch.empty_like(o_w)
     lse_s = torch.empty_like(lse_w)
     out = torch.empty_like(q)
     _call("fwd[win]", _lib().nsa_range_fwd_finish, MODE_WINDOW, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o_w),
           L.ptr(lse_w), B, Hq, Hkv, T, T, D, int(window), 1, 1, L.ptr(o_part), L.ptr(ml_part), L.ptr(idx),
           idx.shape[-1], int(sel_block), L.ptr(o_s), L.ptr(lse_s), L.ptr(o_c), L.ptr(gate), L.ptr(out),
-          L.dtype_code(q), _stream(q))
+          L.dtype_code(q), L.dtype_code(o_c), _stream(q))
     return o_w, lse_w, o_s, lse_s, out
 
 
@@ -372,7 +375,8 @@ def delta_of(do, o, lse):
     dot = torch.empty(o.shape[:3], device=o.device, dtype=torch.float32)
     coff = torch.empty_like(dot)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(lse), None, None,
-          L.ptr(dot), None, L.ptr(coff), None, 1, 1, rows, o.shape[3], 1, L.dtype_code(o), _stream(o))
+          L.ptr(dot), None, L.ptr(coff), None, 1, 1, rows, o.shape[3], 1, L.dtype_code(do), L.dtype_code(o),
+          _stream(o))
     return dot, coff
 
 
@@ -380,8 +384,10 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
     """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3], dop); branch
     order compression, selection, window; coff = lse * log2(e) -
     log2(rowscale).  With ``pack_hkv`` > 0, dop is dO packed for that many KV
-    heads (the ``pack_heads`` layout), else None."""
+    heads (the ``pack_heads`` layout), else None.  The branch outputs share
+    one dtype: dO's, or float32 (unrounded)."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
+    assert o_s.dtype == o_c.dtype and o_w.dtype == o_c.dtype, "branch outputs must share one dtype"
     lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
     B, Hq, T, D = o_c.shape
     rows = B * Hq * T
@@ -396,7 +402,7 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
         dop = torch.empty(B, pack_hkv, T, G, D, device=do.device, dtype=do.dtype)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(gate), L.ptr(dgate),
           L.ptr(lse_c), L.ptr(lse_s), L.ptr(lse_w), L.ptr(dot), L.ptr(rs), L.ptr(coff), L.ptr(dop), G, T, rows, D, 3,
-          L.dtype_code(o_c), _stream(o_c))
+          L.dtype_code(do), L.dtype_code(o_c), _stream(o_c))
     return dot, rs, coff, dgate, dop
 
 
@@ -718,11 +724,16 @@ class NSAFusedHIP(torch.autograd.Function):
             assert kc.shape[2] == T, "compression keys must have the query length"
             k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
             v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
-        want_sel = block_idx is None or block_idx.shape[-1] > 0
+        S = min(geom.n_sel, T // geom.sel_block) if block_idx is None else block_idx.shape[-1]
+        want_sel = S > 0
         qp = (torch.empty(q.shape[0], ks.shape[1], T, q.shape[1] // ks.shape[1], q.shape[3], device=q.device,
                           dtype=q.dtype) if want_sel else torch.empty(0, device=q.device, dtype=q.dtype))
+        # the branch outputs stay internal (only their gated sum is returned):
+        # they are kept in float32 so that the backward's row dots dO . o_c
+        # see them unrounded -- with bf16-rounded outputs that dot carries an
+        # error that a peaked softmax row passes on to dS, dQ and dK whole
         o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride,
-                               q_packed=qp if want_sel else None)
+                               q_packed=qp if want_sel else None, o_f32=want_sel)
         if block_idx is None:
             block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
         idx = block_idx.to(torch.int32).contiguous()

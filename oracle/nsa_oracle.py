@@ -407,12 +407,23 @@ def build_block_to_query_csr(block_idx, block_size, n_blk=None):
 # row-sampled evaluation (large T: parity on sampled rows, CPU baseline)
 # ---------------------------------------------------------------------------
 
+def _row_softmax_attention(s, m, vg_fn):
+    """Softmax over the last axis of scaled scores ``s`` restricted to ``m``;
+    ``vg_fn(p)`` contracts the probabilities with the values.  Empty rows
+    give 0 and ``LSE_EMPTY`` (nsa_model.py:70-82)."""
+    s = s.masked_fill(~m, float("-inf"))
+    has = m.any(-1)
+    lse = torch.logsumexp(s, dim=-1)
+    lse = torch.where(has, lse, torch.full_like(lse, LSE_EMPTY))
+    p = torch.exp(s - lse[..., None]).masked_fill(~m, 0.0)
+    return vg_fn(p), lse
+
+
 def _gathered_attention(q_rows, k, v, kidx, kmask, scale):
     """Attention of ``q_rows [B,Hq,R,D]`` over gathered keys ``kidx [B,Hkv,R,K]``."""
     B, Hq, R, D = q_rows.shape
     Hkv = k.shape[1]
     G = Hq // Hkv
-    K = kidx.shape[-1]
     safe = kidx.clamp(min=0)
     bi = torch.arange(B)[:, None, None, None]
     hi = torch.arange(Hkv)[None, :, None, None]
@@ -420,13 +431,23 @@ def _gathered_attention(q_rows, k, v, kidx, kmask, scale):
     vg = v[bi, hi, safe]
     qg = q_rows.reshape(B, Hkv, G, R, D)
     s = torch.einsum("bhgrd,bhrkd->bhgrk", qg, kg) * scale
-    m = kmask[:, :, None]
-    s = s.masked_fill(~m, float("-inf"))
-    has = m.any(-1)
-    lse = torch.logsumexp(s, dim=-1)
-    lse = torch.where(has, lse, torch.full_like(lse, LSE_EMPTY))
-    p = torch.exp(s - lse[..., None]).masked_fill(~m, 0.0)
-    o = torch.einsum("bhgrk,bhrkd->bhgrd", p, vg)
+    o, lse = _row_softmax_attention(s, kmask[:, :, None],
+                                    lambda p: torch.einsum("bhgrk,bhrkd->bhgrd", p, vg))
+    return o.reshape(B, Hq, R, D), lse.reshape(B, Hq, R)
+
+
+def _shared_key_attention(q_rows, k, v, kmask, scale):
+    """Attention of ``q_rows [B,Hq,R,D]`` over all of ``k/v [B,Hkv,n,D]``
+    restricted to ``kmask [R,n]`` (the pooled keys are shared by every row,
+    so no gather is needed)."""
+    B, Hq, R, D = q_rows.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    qg = q_rows.reshape(B, Hkv, G * R, D)
+    s = (qg @ k.transpose(-1, -2)).reshape(B, Hkv, G, R, -1) * scale
+    o, lse = _row_softmax_attention(
+        s, kmask[None, None, None],
+        lambda p: (p.reshape(B, Hkv, G * R, -1) @ v).reshape(B, Hkv, G, R, D))
     return o.reshape(B, Hq, R, D), lse.reshape(B, Hq, R)
 
 
@@ -435,20 +456,31 @@ def nsa_rows(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, cfg: NSAConfig,
     """Three-branch output for the query positions ``rows`` only.
 
     Same function as ``nsa_fused_reference`` restricted to those rows, with
-    the keys of each row gathered explicitly (window range, visible pooled
-    tokens, selected blocks).  Memory is O(rows * keys) instead of O(T^2), so
-    it serves T = 32K parity sampling and the CPU baseline.
+    the keys of each row gathered explicitly (window range, selected blocks;
+    the visible pooled tokens by mask).  Memory is O(rows * keys) instead of
+    O(T^2), so it serves T = 32K parity sampling and the CPU baseline.
     """
-    B, Hq, T, D = q.shape
+    rows = torch.as_tensor(rows, dtype=torch.long)
+    return nsa_rows_gathered(q[:, :, rows], kc, vc, ks, vs, kw, vw, gate_logits[:, :, rows],
+                             block_idx[:, :, rows], cfg, rows, q.shape[2], k_cmp, v_cmp)
+
+
+def nsa_rows_gathered(q_rows, kc, vc, ks, vs, kw, vw, gate_rows, idx_rows, cfg: NSAConfig,
+                      rows, T, k_cmp=None, v_cmp=None):
+    """``nsa_rows`` with the row inputs already gathered: ``q_rows
+    [B,Hq,R,D]``, ``gate_rows [B,Hq,R,3]`` and ``idx_rows [B,Hkv,R,S]`` are
+    the values at the query positions ``rows`` of a length-``T`` sequence
+    (so gradients of ``q_rows`` / ``gate_rows`` are per-row tensors)."""
+    B, Hq, R, D = q_rows.shape
     scale = D ** -0.5
     rows = torch.as_tensor(rows, dtype=torch.long)
-    R = rows.numel()
+    assert rows.numel() == R
     Hkv = kc.shape[1]
     if k_cmp is None:
         k_cmp = pool_mean(kc, cfg.cmp_block, cfg.cmp_stride)
     if v_cmp is None:
         v_cmp = pool_mean(vc, cfg.cmp_block, cfg.cmp_stride)
-    qr = q[:, :, rows]
+    qr = q_rows
     # window
     w = cfg.window
     off = torch.arange(w)
@@ -461,25 +493,39 @@ def nsa_rows(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, cfg: NSAConfig,
     if n > 0:
         ci = torch.arange(n)
         cm = (ci[None, :] * cfg.cmp_stride + cfg.cmp_block - 1) <= rows[:, None]
-        o_c, lse_c = _gathered_attention(qr, k_cmp, v_cmp, ci.expand(B, Hkv, R, n),
-                                         cm.expand(B, Hkv, R, n), scale)
+        o_c, lse_c = _shared_key_attention(qr, k_cmp, v_cmp, cm, scale)
     else:
         o_c = torch.zeros_like(qr)
-        lse_c = torch.full((B, Hq, R), LSE_EMPTY, dtype=q.dtype)
+        lse_c = torch.full((B, Hq, R), LSE_EMPTY, dtype=qr.dtype)
     # selection
-    S = block_idx.shape[-1]
+    S = idx_rows.shape[-1]
     ls = cfg.sel_block
     if S > 0:
-        bl = block_idx[:, :, rows].long()                       # [B,Hkv,R,S]
+        bl = idx_rows.long()                                    # [B,Hkv,R,S]
         pos = bl[..., None] * ls + torch.arange(ls)             # [B,Hkv,R,S,ls]
         pm = (bl[..., None] >= 0) & (pos <= rows[None, None, :, None, None]) & (pos < T)
         o_s, lse_s = _gathered_attention(qr, ks, vs, pos.reshape(B, Hkv, R, S * ls),
                                          pm.reshape(B, Hkv, R, S * ls), scale)
     else:
         o_s = torch.zeros_like(qr)
-        lse_s = torch.full((B, Hq, R), LSE_EMPTY, dtype=q.dtype)
-    out = gate_blend(gate_logits[:, :, rows], o_c, o_s, o_w)
+        lse_s = torch.full((B, Hq, R), LSE_EMPTY, dtype=qr.dtype)
+    out = gate_blend(gate_rows, o_c, o_s, o_w)
     return out, {"cmp": (o_c, lse_c), "slc": (o_s, lse_s), "win": (o_w, lse_w)}
+
+
+def selection_rows(q_rows, k, v, idx_rows, ls, rows, T):
+    """Selection-branch ``(o, lse)`` of the query positions ``rows`` only
+    (the selection part of ``nsa_rows_gathered``; nsa_selection_kernel.py:55-92
+    restricted to those rows)."""
+    B, Hq, R, D = q_rows.shape
+    Hkv = k.shape[1]
+    rows = torch.as_tensor(rows, dtype=torch.long)
+    S = idx_rows.shape[-1]
+    bl = idx_rows.long()
+    pos = bl[..., None] * ls + torch.arange(ls)
+    pm = (bl[..., None] >= 0) & (pos <= rows[None, None, :, None, None]) & (pos < T)
+    return _gathered_attention(q_rows, k, v, pos.reshape(B, Hkv, R, S * ls), pm.reshape(B, Hkv, R, S * ls),
+                               D ** -0.5)
 
 
 def importance_rows(q, k_cmp, cfg: NSAConfig, rows, T):

@@ -102,3 +102,32 @@ def log(msg):
 
 __all__ = ["REF_CONFIGS", "G16_CONFIGS", "cfg_id", "window_for", "randn", "make_block_idx", "TOL",
            "errors", "assert_close", "to64", "require_gpu", "log", "math"]
+
+
+# Strict form of the north-star bound for the full-shape BASELINE checks:
+# elementwise |got - ref| <= atol + ulp * |ref| (atol the north star's
+# absolute bound; ulp one storage unit of the dtype at the value's own
+# magnitude, the representation limit of a bf16 output: 2^-8), and
+# rel-L2 <= rtol.  No scaling by the tensor's largest value.
+STRICT = {torch.bfloat16: (2e-2, 2.0 ** -8, 1e-2), torch.float32: (1e-4, 0.0, 1e-5)}
+
+
+def assert_strict(got, ref, dtype, what=""):
+    atol, ulp, rtol = STRICT[dtype]
+    g = got.detach().double().cpu()
+    r = ref.detach().double().cpu()
+    assert g.shape == r.shape, f"{what}: shape {tuple(g.shape)} vs {tuple(r.shape)}"
+    assert torch.isfinite(g).all(), f"{what}: non-finite values"
+    diff = (g - r).abs()
+    max_abs = float(diff.max()) if diff.numel() else 0.0
+    denom = float(r.norm())
+    rel_l2 = float((g - r).norm()) / denom if denom > 0 else float((g - r).norm())
+    excess = float((diff - (atol + ulp * r.abs())).max()) if diff.numel() else -1.0
+    ref_max = float(r.abs().max()) if r.numel() else 0.0
+    log(f"  {what:12s} max_abs {max_abs:.3e}  rel_l2 {rel_l2:.3e}  |ref|max {ref_max:.3e}")
+    assert excess <= 0.0, f"{what}: max_abs {max_abs:.3e} exceeds {atol:.0e} + {ulp:.1e}|ref| (by {excess:.3e})"
+    assert rel_l2 <= rtol, f"{what}: rel_l2 {rel_l2:.3e} > {rtol:.1e}"
+    return max_abs, rel_l2
+
+
+__all__ += ["STRICT", "assert_strict"]

@@ -56,7 +56,10 @@ def test_bad_shapes_are_rejected_without_launching():
     # D = 48 is not a supported head dim; block 8 is below 16: both fail the checks
     assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 48, 2, 16, 1, None) == -1
     assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 64, 2, 8, 1, None) == -1
-    assert lib.nsa_range_fwd(7, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 1, None) == -3
+    assert lib.nsa_range_fwd(7, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 1, 1, None) == -3
+    # branch outputs are the input type or float32
+    assert lib.nsa_range_fwd(0, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 0, 1, None) == -2
     # the selection chunk is capped at 1024 queries (staged in LDS)
     assert lib.nsa_sel_dkdv(*([None] * 8), 1, *([None] * 6), 1 << 30, 1, 4, 1, 64, 64, 2, 16, 2048, 1, None) == -1
     assert lib.nsa_pool_fwd(None, None, 1, 1, 64, 64, 16, 16, 5, None) == -2
+

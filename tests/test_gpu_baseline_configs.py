@@ -1,0 +1,234 @@
+"""GPU parity at the full shapes of the BASELINE configurations.
+
+c3 -- the metric's workload, B1 T32768 Hq64 Hkv4 D128, l32/d16 l'64 top-16
+w512, bf16, on bench.py's own seeded inputs -- plain top-16 and with the
+initial + 2 local blocks forced:
+
+  (i)   block indices of EVERY row equal the CPU top-n of the GPU's own
+        importance scores, bit for bit, and equal the indices of a second,
+        standalone importance / top-n launch;
+  (ii)  on >= 1024 sampled rows the GPU importance is within float tolerance
+        of the float64 oracle's, and the end-to-end indices equal the
+        oracle's except on near-tie rows (count logged);
+  (iii) with dO zero outside the sampled rows, the output rows and
+  (iv)  all eight input gradients plus dgate match the float64 oracle
+        (nsa_rows_gathered): every gradient is then exactly those rows'
+        contribution, and dq / dgate are exactly zero elsewhere.
+
+c2 -- selection branch only, B4 T8192 Hq16 Hkv1 D64, indices from the
+compression importance (l32/d16): (i), (ii), then selection fwd + bwd on
+sampled rows.  Its selection dK/dV has more work items than the persistent
+grid has workgroups, so the counter path of the item queue runs.
+
+c1 -- B1 T1024 Hq4 Hkv1 D64, inputs N(0,1)/8: the whole dense oracle, float32
+and bfloat16, extended geometry and the aligned l = d = l' = 64 grid.
+
+Tolerances (nsa_testlib.STRICT): bf16 |err| <= 2e-2 + 2^-8 |ref| elementwise
+and rel-L2 <= 1e-2; float32 |err| <= 1e-4 and rel-L2 <= 1e-5.  Raw max-abs
+and rel-L2 of every tensor are printed.  The reference gates its kernels the
+same way on its own matrix (test_kernel_fused.py:53-70).
+"""
+
+import pytest
+import torch
+
+import bench
+from oracle import nsa_oracle as O
+from nsa_testlib import assert_strict, log, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+NAMES = ["q", "kc", "vc", "ks", "vs", "kw", "vw", "gate"]
+
+
+def _sample_rows(T, n=1024):
+    extra = torch.tensor([0, 1, 2, 15, 31, 32, 47, 63, 64, 65, 511, 512, 1023, 1024, 1025, T - 2, T - 1])
+    rows = torch.cat([torch.linspace(0, T - 1, n).round().long(), extra[extra < T]])
+    return torch.unique(rows)
+
+
+def _near_tie_rows(scores, S, eps):
+    if scores.shape[-1] <= S:
+        return torch.zeros(scores.shape[:-1], dtype=torch.bool)
+    top = torch.topk(scores, S + 1, dim=-1).values
+    gap = (top[..., S - 1] - top[..., S]).abs()
+    return gap <= eps * top[..., S - 1].abs().clamp(min=1e-30)
+
+
+def _check_indices(q, kc, geom, cfg, idx_gpu, rows, T, label):
+    """(i) + (ii) for one block choice ``idx_gpu`` made from q and the
+    compression keys kc (both on the GPU)."""
+    import nsa_hip_ops as ops
+    S = idx_gpu.shape[-1]
+    k_cmp = ops.pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+    _, lse_c = ops.range_fwd(ops.MODE_COMPRESS, q, k_cmp, k_cmp, 0, geom.cmp_block, geom.cmp_stride)
+    idx2, scores = ops.importance_topn(q, k_cmp, lse_c, geom, return_scores=True)
+    torch.cuda.synchronize()
+    assert torch.equal(idx2, idx_gpu), f"{label}: standalone importance / top-n launch chose other blocks"
+    idx_c = idx_gpu.cpu()
+    scores_c = scores.cpu()
+    del scores
+    # (i) every row: the CPU top-n of the GPU's scores, bit for bit
+    sel = O.topn_from_scores(O.selection_scores(scores_c.double(), cfg), S)
+    bad_rows = int((sel != idx_c).any(-1).sum())
+    log(f"  {label}: (i) {idx_c.shape[0] * idx_c.shape[1] * idx_c.shape[2]} rows, {bad_rows} differ")
+    assert bad_rows == 0
+    del sel
+    # (ii) sampled rows against the float64 oracle (GPU-pooled keys)
+    q64 = q.double().cpu()
+    kcmp64 = k_cmp.double().cpu()
+    imp_ref = O.importance_rows(q64, kcmp64, cfg, rows, T)
+    got = scores_c[:, :, rows].double()
+    max_abs = float((got - imp_ref).abs().max())
+    scale = max(1.0, float(imp_ref.abs().max()))
+    log(f"  {label}: (ii) importance on {rows.numel()} rows: max_abs {max_abs:.3e} (|ref|max {scale:.2f})")
+    assert max_abs <= 2e-4 * scale
+    sc_ref = O.selection_scores(imp_ref, cfg, t_pos=rows)
+    ref_idx = O.topn_from_scores(sc_ref, S)
+    tie = _near_tie_rows(sc_ref, S, 1e-4)
+    equal = (torch.sort(ref_idx, -1).values == torch.sort(idx_c[:, :, rows], -1).values).all(-1)
+    bad = (~equal) & (~tie)
+    log(f"  {label}: (ii) end-to-end: near-tie rows {int(tie.sum())} / {tie.numel()}, "
+        f"rows differing {int((~equal).sum())}, outside near ties {int(bad.sum())}")
+    assert int(bad.sum()) == 0
+    # the same with the pooled keys kept in float64 (the oracle's own
+    # pooling): logged, not gated -- the product stores pooled keys in the
+    # input dtype, as the reference's block_mean_pool does
+    kcmp_o = O.pool_mean(kc.double().cpu(), geom.cmp_block, geom.cmp_stride)
+    sc_o = O.selection_scores(O.importance_rows(q64, kcmp_o, cfg, rows, T), cfg, t_pos=rows)
+    eq_o = (torch.sort(O.topn_from_scores(sc_o, S), -1).values == torch.sort(idx_c[:, :, rows], -1).values).all(-1)
+    log(f"  {label}: (ii) vs float64 pooling: rows differing {int((~eq_o).sum())} / {eq_o.numel()}, "
+        f"of which outside 1e-2 near ties {int(((~eq_o) & ~_near_tie_rows(sc_o, S, 1e-2)).sum())}")
+    return q64
+
+
+def _oracle_rows_grads(ins, do_rows, idx_rows, cfg, rows, T, chunk=32):
+    """float64 oracle out / grads of the sampled rows: -> (out_rows,
+    grads [dq_rows, dkc, dvc, dks, dvs, dkw, dvw, dgate_rows])."""
+    q_rows = ins[0][:, :, rows.to(ins[0].device)].double().cpu().requires_grad_()
+    g_rows = ins[7][:, :, rows.to(ins[7].device)].double().cpu().requires_grad_()
+    kv = [t.double().cpu().requires_grad_() for t in ins[1:7]]
+    k_cmp = O.pool_mean(kv[0], cfg.cmp_block, cfg.cmp_stride)
+    v_cmp = O.pool_mean(kv[1], cfg.cmp_block, cfg.cmp_stride)
+    outs = []
+    for c0 in range(0, rows.numel(), chunk):
+        sl = slice(c0, c0 + chunk)
+        out, _ = O.nsa_rows_gathered(q_rows[:, :, sl], *kv, g_rows[:, :, sl], idx_rows[:, :, sl], cfg, rows[sl], T,
+                                     k_cmp, v_cmp)
+        out.backward(do_rows[:, :, sl], retain_graph=True)
+        outs.append(out.detach())
+    return torch.cat(outs, dim=2), [q_rows.grad] + [t.grad for t in kv] + [g_rows.grad]
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("workload", ["c3", "c3_forced"])
+def test_c3_full_shape_parity(workload):
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    import nsa_hip_ops as ops
+    w = bench.WORKLOADS[workload]
+    log(f"{workload}: {w['desc']}")
+    T = w["T"]
+    geom = ops.NSAGeometry(*w["geom"])
+    cfg = O.NSAConfig(*w["geom"])
+    torch.set_num_threads(16)
+    ins, do_full = bench.make_inputs(w, dev, torch.bfloat16)
+    rows = _sample_rows(T)
+    rows_d = rows.to(dev)
+    do = torch.zeros_like(do_full)
+    do[:, :, rows_d] = do_full[:, :, rows_d]
+    xs = [t.clone().requires_grad_() for t in ins]
+    out, idx = nfk.nsa_attention(*xs, geom)
+    out.backward(do)
+    torch.cuda.synchronize()
+    log(f"  {workload}: GPU fwd+bwd done, {rows.numel()} sampled rows")
+    _check_indices(ins[0], ins[1], geom, cfg, idx, rows, T, workload)
+    # (iii) + (iv)
+    do_rows = do_full[:, :, rows_d].double().cpu()
+    out_ref, g_ref = _oracle_rows_grads(ins, do_rows, idx[:, :, rows_d].cpu(), cfg, rows, T)
+    assert_strict(out[:, :, rows_d], out_ref, torch.bfloat16, "out")
+    grads = [x.grad for x in xs]
+    assert_strict(grads[0][:, :, rows_d], g_ref[0], torch.bfloat16, "dq")
+    assert_strict(grads[7][:, :, rows_d], g_ref[7], torch.bfloat16, "dgate")
+    for nm, gi, gr in zip(NAMES[1:7], grads[1:7], g_ref[1:7]):
+        assert_strict(gi, gr, torch.bfloat16, f"d{nm}")
+    outside = torch.ones(T, dtype=torch.bool, device=dev)
+    outside[rows_d] = False
+    assert int(torch.count_nonzero(grads[0][:, :, outside])) == 0, "dq nonzero on a row with dO = 0"
+    assert int(torch.count_nonzero(grads[7][:, :, outside])) == 0, "dgate nonzero on a row with dO = 0"
+
+
+@pytest.mark.timeout(600)
+def test_c2_selection_full_shape_parity():
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    import nsa_selection_backward as nsb
+    w = bench.WORKLOADS["c2"]
+    log(f"c2: {w['desc']}")
+    B, T, Hq, Hkv, D = w["B"], w["T"], w["Hq"], w["Hkv"], w["D"]
+    geom = ops.NSAGeometry(*w["geom"])
+    cfg = O.NSAConfig(*w["geom"])
+    torch.set_num_threads(16)
+    ins, do_full = bench.make_inputs(w, dev, torch.bfloat16)
+    q, k, v = ins[0], ins[3], ins[4]
+    k_cmp = ops.pool_fwd(ins[1], geom.cmp_block, geom.cmp_stride)
+    _, lse_c = ops.range_fwd(ops.MODE_COMPRESS, q, k_cmp, k_cmp, 0, geom.cmp_block, geom.cmp_stride)
+    idx = ops.importance_topn(q, k_cmp, lse_c, geom)
+    rows = _sample_rows(T, 512)
+    _check_indices(q, ins[1], geom, cfg, idx, rows, T, "c2")
+    # the selection dK/dV work items outnumber the persistent grid (two
+    # workgroups per CU): items past the grid come from the counter
+    _, offsets, _, _ = ops.csr_device(idx, geom.sel_block, pack_slot=True)
+    cnt = (offsets[..., 1:] - offsets[..., :-1]).long()
+    n_items = int(((cnt + ops.SEL_DKDV_CHUNK - 1) // ops.SEL_DKDV_CHUNK).sum())
+    grid = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    log(f"  c2: selection dK/dV work items {n_items}, persistent grid {grid}")
+    assert n_items > grid
+    rows_d = rows.to(dev)
+    do = torch.zeros_like(do_full)
+    do[:, :, rows_d] = do_full[:, :, rows_d]
+    xs = [t.clone().requires_grad_() for t in (q, k, v)]
+    o = nsb.selection_attn_triton(*xs, idx, geom.sel_block)
+    o.backward(do)
+    torch.cuda.synchronize()
+    q_rows = q[:, :, rows_d].double().cpu().requires_grad_()
+    k64, v64 = (t.double().cpu().requires_grad_() for t in (k, v))
+    idx_rows = idx[:, :, rows_d].cpu()
+    outs = []
+    do_rows = do_full[:, :, rows_d].double().cpu()
+    for c0 in range(0, rows.numel(), 64):
+        sl = slice(c0, c0 + 64)
+        o_r, _ = O.selection_rows(q_rows[:, :, sl], k64, v64, idx_rows[:, :, sl], geom.sel_block, rows[sl], T)
+        o_r.backward(do_rows[:, :, sl])
+        outs.append(o_r.detach())
+    assert_strict(o[:, :, rows_d], torch.cat(outs, 2), torch.bfloat16, "o")
+    assert_strict(xs[0].grad[:, :, rows_d], q_rows.grad, torch.bfloat16, "dq")
+    assert_strict(xs[1].grad, k64.grad, torch.bfloat16, "dk")
+    assert_strict(xs[2].grad, v64.grad, torch.bfloat16, "dv")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("variant", ["extended", "aligned64"])
+def test_c1_dense_parity(variant, dtype):
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    w = bench.WORKLOADS["c1"]
+    T = w["T"]
+    if variant == "extended":
+        geom, cfg = ops.NSAGeometry(*w["geom"]), O.NSAConfig(*w["geom"])
+    else:
+        geom, cfg = ops.NSAGeometry.aligned(64, 16, 512), O.NSAConfig.reference(64, 16, 512)
+    log(f"c1 {variant} {dtype}")
+    ins, do = bench.make_inputs(w, torch.device("cpu"), dtype)
+    xs = [t.to(dev).requires_grad_() for t in ins]
+    out, idx = ops.nsa_attention(*xs, geom)
+    out.backward(do.to(dev))
+    torch.cuda.synchronize()
+    rows = torch.arange(T)
+    _check_indices(xs[0].detach(), xs[1].detach(), geom, cfg, idx, rows, T, f"c1-{variant}")
+    ins64 = [t.double().requires_grad_() for t in ins]
+    ref, _ = O.nsa_fused_reference(*ins64, idx.cpu(), cfg)
+    ref.backward(do.double())
+    assert_strict(out, ref, dtype, "out")
+    for nm, x, r in zip(NAMES, xs, ins64):
+        assert_strict(x.grad, r.grad, dtype, f"d{nm}")

@@ -386,6 +386,36 @@ def test_rows_path_matches_dense_path():
         torch.testing.assert_close(parts_r[key][1], parts[key][1][:, :, rows])
     imp_r = O.importance_rows(q, parts["k_cmp"], cfg, rows, T)
     torch.testing.assert_close(imp_r, parts["importance"][:, :, rows])
+    o_s, lse_s = O.selection_rows(q[:, :, rows], kv[2], kv[3], parts["block_idx"][:, :, rows], 16, rows, T)
+    torch.testing.assert_close(o_s, parts["slc"][0][:, :, rows], rtol=1e-12, atol=1e-12)
+    torch.testing.assert_close(lse_s, parts["slc"][1][:, :, rows])
+
+
+def test_rows_path_gradients_match_dense_path():
+    """Gradients through the row path (row inputs as their own leaves) equal
+    the dense path's with dO zero outside the rows."""
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10)
+    B, Hq, Hkv, T, D = 1, 4, 2, 80, 8
+    q = _rand(B, Hq, T, D, seed=80)
+    kv = [_rand(B, Hkv, T, D, seed=81 + i) for i in range(6)]
+    gate = _rand(B, Hq, T, 3, seed=90)
+    rows = torch.tensor([0, 9, 31, 32, 50, 79])
+    dor = _rand(B, Hq, rows.numel(), D, seed=91)
+    xs = [t.clone().requires_grad_() for t in [q] + kv + [gate]]
+    out, parts = O.nsa_forward_reference(*xs, cfg)
+    do = torch.zeros_like(out)
+    do[:, :, rows] = dor
+    out.backward(do)
+    idx = parts["block_idx"]
+    qr = q[:, :, rows].clone().requires_grad_()
+    gr = gate[:, :, rows].clone().requires_grad_()
+    ys = [t.clone().requires_grad_() for t in kv]
+    out_r, _ = O.nsa_rows_gathered(qr, *ys, gr, idx[:, :, rows], cfg, rows, T)
+    out_r.backward(dor)
+    torch.testing.assert_close(qr.grad, xs[0].grad[:, :, rows], rtol=1e-10, atol=1e-12)
+    torch.testing.assert_close(gr.grad, xs[7].grad[:, :, rows], rtol=1e-10, atol=1e-12)
+    for a, b in zip(ys, xs[1:7]):
+        torch.testing.assert_close(a.grad, b.grad, rtol=1e-10, atol=1e-12)
 
 
 def test_keys_per_row_matches_masks():
