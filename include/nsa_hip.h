@@ -9,7 +9,8 @@
  * with query head h reading KV head h / (Hq / Hkv).  dtype is NSA_F32 or
  * NSA_BF16 for every tensor of the call not marked float.  Every launch goes
  * to `stream` (a hipStream_t); nothing is allocated and nothing synchronises
- * with the host.  Scratch memory is passed in by the caller.
+ * with the host.  Scratch memory is passed in by the caller (one entry point,
+ * nsa_sel_dkdv_noalloc, uses a fixed device array of the library instead).
  *
  * Return value: NSA_OK (0) or a negative NSA_ERR_* code.  Host wrappers map
  * NSA_ERR_SHAPE / NSA_ERR_DTYPE to the reference's assertion failures
@@ -143,6 +144,25 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
                  const float* dot, const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
                  float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq,
                  int Hkv, int T, int D, int S, int block_size, int chunk, int dtype, void* stream);
+
+/* nsa_sel_dkdv without a workspace argument: allocates nothing (no
+ * hipMalloc, no allocating library call).  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  The
+ * work-item list and counters live in a device array of the library,
+ * NSA_SEL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call
+ * whose nsa_sel_dkdv_workspace(...) exceeds it returns NSA_ERR_WORKSPACE
+ * before touching the device (about 65k work items: c3 needs 4.1k).  Every
+ * call on one GPU uses that GPU's array, which keeps the last call's
+ * contents (the call re-initialises what it reads): calls that overlap on
+ * one GPU (two streams, two host threads) race and must be serialised by the
+ * caller.  Arguments otherwise as nsa_sel_dkdv. */
+#define NSA_SEL_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
+int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void* kt, const void* dout,
+                         const float* coff, const float* dot, const int32_t* q_of_block, int packed,
+                         const int32_t* block_offsets, const int32_t* pair_count, float* dk, float* dv,
+                         void* dq_part, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                         int dtype, void* stream);
 
 /* ---- block-outer selection forward and the partial merges ----------------
  * The FSA forward (replaces _selection_fwd_blockouter_kernel /

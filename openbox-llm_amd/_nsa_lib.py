@@ -50,6 +50,8 @@ SIGNATURES = {
     "nsa_sel_dkdv_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
     "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _Z,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_sel_dkdv_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P,
+                                  _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_partial_slots": (_I, [_I, _I]),
     "nsa_sel_fwd_bo_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
     "nsa_sel_fwd_bo": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

@@ -21,6 +21,8 @@
 //                   float atomics; the key blocks of one chunk share an XCD.
 //   * selection   : work items (block, chunk of its CSR query list) built by
 //                   k_sel_items; a persistent grid drains them; chunks merge with atomics.
+#include <mutex>
+
 #include "nsa_launch.h"
 #include "nsa_items.h"
 #include "nsa_tile32.h"
@@ -861,6 +863,58 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
           Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
   });
   return nsa_launch_status();
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// nsa_sel_dkdv without a caller workspace
+// ---------------------------------------------------------------------------
+// The work-item list and the item counters of nsa_sel_dkdv live in this
+// file-scope device array instead of the caller's workspace.  Each GPU holds
+// its own copy until the process ends.  Host code never passes the array's
+// name to a kernel or a copy (on the host it is a stand-in, not a device
+// address): the address comes from hipGetSymbolAddress, looked up once per
+// device with that device current, and kept per device.
+constexpr size_t kSelScratchBytes = NSA_SEL_NOALLOC_SCRATCH_BYTES;   // 65520 work items + the counters
+static __device__ __align__(256) char scratch[kSelScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`, looked up on first use.
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return NSA_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return NSA_ERR_LAUNCH;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSA_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void* kt, const void* dout,
+                         const float* coff, const float* dot, const int32_t* q_of_block, int packed,
+                         const int32_t* block_offsets, const int32_t* pair_count, float* dk, float* dv,
+                         void* dq_part, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                         int dtype, void* stream) {
+  // the size check comes first: it touches no device state
+  const size_t need = nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, chunk);
+  NSA_CHECK(need > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(need <= kSelScratchBytes, NSA_ERR_WORKSPACE);
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != NSA_OK) return rc;
+  return nsa_sel_dkdv(q, k, v, kt, dout, coff, dot, q_of_block, packed, block_offsets, pair_count, dk, dv, dq_part,
+                      ws, kSelScratchBytes, B, Hq, Hkv, T, D, S, block_size, chunk, dtype, stream);
 }
 
 }  // extern "C"

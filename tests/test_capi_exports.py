@@ -63,3 +63,14 @@ def test_bad_shapes_are_rejected_without_launching():
     assert lib.nsa_sel_dkdv(*([None] * 8), 1, *([None] * 6), 1 << 30, 1, 4, 1, 64, 64, 2, 16, 2048, 1, None) == -1
     assert lib.nsa_pool_fwd(None, None, 1, 1, 64, 64, 16, 16, 5, None) == -2
 
+
+def test_noalloc_entry_point_rejects_oversize_without_a_device():
+    mod, lib = _lib()
+    # the work items of this call exceed NSA_SEL_NOALLOC_SCRATCH_BYTES: the size
+    # check runs before any device call, so it answers here without a GPU
+    need = lib.nsa_sel_dkdv_workspace(1, 1, 65536, 16, 64, 2)
+    assert need > (1 << 20)
+    rc = lib.nsa_sel_dkdv_noalloc(*([None] * 8), 1, *([None] * 5), 1, 16, 1, 65536, 64, 16, 64, 2, 1, None)
+    assert rc == mod.NSA_ERR_WORKSPACE
+    # bad arguments are shape errors, also before any device call
+    assert lib.nsa_sel_dkdv_noalloc(*([None] * 8), 1, *([None] * 5), 0, 16, 1, 64, 64, 16, 64, 2, 1, None) == -1
