@@ -60,8 +60,17 @@ WORKLOADS = {
 # this bench (FETCH_SIZE, then WRITE_SIZE) and scaled by what the same
 # counters read for a plain 1 GiB device copy (x2.0 and x1.0); the commands
 # and counter values are kept under profiles/.  Keyed by (workload, kernel).
-MEASURED_TRAFFIC = {
-    ("c3_forced", "dkdv[sel]"): 1.941e10 + 9.30e9,
+MEASURED_TRAFFIC = {   # profiles/nsa_fused_c3_pmc_traffic.md: bytes read + bytes written per launch
+    ("c3", "dkdv[sel]"): 1.956e10 + 9.316e9,
+    ("c3", "fwd[sel]"): 8.593e9 + 8.729e9,
+    ("c3", "dq[cmp+win]"): 1.173e10 + 5.704e8,
+    ("c3", "fwd[win]"): 1.125e10 + 2.714e9,
+    ("c3", "dkdv[win]"): 9.838e9 + 1.344e8,
+    ("c3", "dkdv[cmp]"): 2.872e9 + 6.521e8,
+    ("c3", "fwd[cmp]"): 6.915e8 + 2.242e9,
+    ("c3", "nsa_bwd_prep"): 3.834e9 + 6.263e8,
+    ("c3", "nsa_importance_topn"): 6.073e8 + 8.389e6,
+    ("c3", "nsa_pool_fwd"): 5.886e7 + 2.096e6,
 }
 
 ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
@@ -382,15 +391,21 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
-def per_kernel_table(iso_spans, flops_of, peak):
-    """name -> {ms per step, calls per step, algorithmic TFLOP per launch, MFMA fraction}."""
+def per_kernel_table(iso_spans, flops_of, peak, workload):
+    """name -> {ms per step, calls per step, algorithmic TFLOP per launch,
+    MFMA fraction, and where the PMC traffic was measured for this workload,
+    HBM GB/s and fraction of the HBM peak}."""
     out = {}
     for name, (calls, tot) in sorted(iso_spans.items(), key=lambda x: -x[1][1]):
         ent = {"ms_per_step": round(tot / ISO_STEPS, 4), "calls_per_step": calls // ISO_STEPS}
-        if name in flops_of and calls > 0:
-            per = tot / calls / 1e3
+        per = tot / calls / 1e3 if calls > 0 else None
+        if name in flops_of and per:
             ent["tflop_per_launch"] = round(flops_of[name] / 1e12, 4)
             ent["mfma_frac"] = round(flops_of[name] / per / 1e12 / peak, 4)
+        traffic = MEASURED_TRAFFIC.get((workload, name))
+        if traffic and per:
+            ent["hbm_gbs"] = round(traffic / per / 1e9, 1)
+            ent["hbm_frac"] = round(traffic / per / 1e9 / PEAK_HBM_GBS, 4)
         out[name] = ent
     return out
 
@@ -511,7 +526,7 @@ def main():
         "selection_pairs": r["pairs"],
         "roofline": roofline,
         "branches": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
-        "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS),
+        "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS, name),
     }
     if not args.no_extras and name == "c3":
         ms_f, kv_f = time_gpu_only(args, WORKLOADS["c3_forced"], "c3_forced")
