@@ -54,6 +54,15 @@ WORKLOADS = {
                desc="BASELINE config 1 shape: B1 T1024 Hq4 Hkv1 D64, l32/d16 l'64 top-16 (init + 2 local) w512"),
     "small": dict(kind="fused", B=1, T=4096, Hq=16, Hkv=1, D=128, geom=(32, 16, 64, 16, 512, False, 0),
                   head_scale=True, in_scale=1.0, desc="reduced c3-like shape for quick checks"),
+    "c4": dict(kind="model", B=8, T=4096, Hq=12, Hkv=2, D=64, geom=(32, 16, 64, 16, 512, False, 0),
+               vocab=32000, d_model=768, n_layers=12, ffn_hidden=2048,
+               desc="BASELINE config 4: 12-layer d768 decoder (12q/2kv heads, hd64, SwiGLU 2048, RMSNorm, RoPE 1e4, "
+                    "vocab 32000), NSA l32/d16 l'64 top-16 w512 in every layer, bf16 autocast AdamW step, 8x4096 "
+                    "tokens; dense arm: the same model with causal SDPA attention"),
+    "c5": dict(kind="forward", B=1, T=131072, Hq=32, Hkv=2, D=128, geom=(32, 16, 64, 32, 512, False, 0),
+               head_scale=False, in_scale=1.0, shift_frac=0.01, shift=3.0,
+               desc="BASELINE config 5: NSA forward only, B1 T131072 Hq32 Hkv2 D128, l32/d16 l'64 top-32 w512, bf16, "
+                    "1% of the 64-token key blocks shifted by +3 sigma"),
 }
 
 # HBM bytes per launch of a kernel, measured with two rocprofv3 PMC passes of
@@ -97,6 +106,14 @@ def make_inputs(w, dev, dtype, seed=0):
         skv = torch.rand(6, Hkv, generator=g, device=dev) * 1.5 + 0.5
         q = q * sq[None, :, None, None]
         kv = [x * skv[i][None, :, None, None] for i, x in enumerate(kv)]
+    if w.get("shift_frac"):
+        # a seeded 1% of the 64-token key blocks get a mean shift on every key
+        # of every branch: peaked block scores for the top-n
+        nb = T // 64
+        pick = torch.randperm(nb, generator=g, device=dev)[:max(1, round(w["shift_frac"] * nb))]
+        tok = (pick[:, None] * 64 + torch.arange(64, device=dev)[None, :]).reshape(-1)
+        for i in (0, 2, 4):
+            kv[i][:, :, tok] += w["shift"]
     gate = rn(B, Hq, T, 3)
     do = rn(B, Hq, T, D)
     ins = [t.to(dtype).contiguous() for t in [q] + kv + [gate]]
@@ -380,6 +397,92 @@ def time_gpu_c1(reps=20):
     return res
 
 
+def run_model_bench(args, w):
+    """Config 4: one bf16-autocast AdamW training step of the decoder, NSA
+    (fused HIP attention) against the same model with dense causal SDPA
+    attention; tokens/s and peak device memory per arm."""
+    import nsa_model
+    dev = torch.device("cuda:0")
+    B, T = w["B"], w["T"]
+    l, d, ls, n, win, fi, nl = w["geom"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randint(0, w["vocab"], (B, T), generator=g, device=dev)
+    y = torch.randint(0, w["vocab"], (B, T), generator=g, device=dev)
+    out = {}
+    for arm in ("nsa", "dense"):
+        torch.cuda.empty_cache()
+        torch.manual_seed(0)
+        m = nsa_model.NSATransformer(
+            vocab_size=w["vocab"], d_model=w["d_model"], n_layers=w["n_layers"], n_q_heads=w["Hq"],
+            n_kv_heads=w["Hkv"], max_seq_len=T, ffn_hidden=w["ffn_hidden"], norm="rms", ffn="swiglu", pos="rope",
+            tie_embeddings=False, attn_type="nsa" if arm == "nsa" else "full", attn_impl="fused", dense_impl="sdpa",
+            block_size=l, cmp_stride=d, sel_block=ls, n_selected_blocks=n, window=win, force_init=fi,
+            n_local=nl).to(dev)
+        opt = torch.optim.AdamW(m.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+        losses = []
+
+        def step():
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                _, loss = m(x, y)
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            return loss
+        for _ in range(max(1, args.warmup)):
+            losses.append(float(step()))
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            loss = step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        losses.append(float(loss))
+        out[arm] = {"ms_per_step": round(ms, 2), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+                    "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+                    "params_m": round(sum(p.numel() for p in m.parameters()) / 1e6, 2),
+                    "loss_first_last": [round(losses[0], 4), round(losses[-1], 4)]}
+        log(f"[bench] c4 {arm}: {ms:.1f} ms per step, peak {out[arm]['peak_mem_gib']} GiB")
+        del m, opt
+    return out
+
+
+def run_forward_bench(args, w, name):
+    """Config 5: the NSA forward alone (pooling, compression, importance /
+    top-n, selection, window, gate), no autograd; per-call spans for the
+    roofline of its dominant kernel."""
+    import nsa_hip_ops as ops
+    dev = torch.device("cuda:0")
+    geom, ins, _ = _setup(w, dev, torch.bfloat16)
+
+    def step():
+        with torch.no_grad():
+            return ops.nsa_attention(*ins, geom)
+    for _ in range(max(1, args.warmup)):
+        _, idx = step()
+    torch.cuda.synchronize()
+    kv = keys_visible(w, idx)
+    iso = ops.LaunchTimer()
+    ops.set_timer(iso)
+    for _ in range(ISO_STEPS):
+        step()
+    torch.cuda.synchronize()
+    ops.set_timer(None)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    G, D = w["Hq"] // w["Hkv"], w["D"]
+    fwd_flops = {f"fwd[{br}]": 4 * D * G * k for br, k in zip(("win", "cmp", "sel"), kv)}
+    spans = iso.summary_ms()
+    return {"ms_per_step": round(ms, 3), "tokens_per_s": round(w["B"] * w["T"] / (ms / 1e3), 1),
+            "fwd_tflop": round(sum(fwd_flops.values()) / 1e12, 3),
+            "mfu": round(sum(fwd_flops.values()) / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "visible_keys": {"win": kv[0], "cmp": kv[1], "sel": kv[2]},
+            "per_kernel": per_kernel_table(spans, fwd_flops, PEAK_BF16_TFLOPS, name)}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -468,6 +571,11 @@ def main():
         sys.exit(2)
     name = args.workload
     w = WORKLOADS[name]
+    if w["kind"] in ("model", "forward"):
+        extra = run_model_bench(args, w) if w["kind"] == "model" else run_forward_bench(args, w, name)
+        print(json.dumps({"workload": name, "desc": w["desc"], "steps": args.steps, "warmup": args.warmup,
+                          "result": extra}), flush=True)
+        return
     r = run_gpu(args, w, name)
     ms, spans, iso_spans, dom_name, flops_of, kv = r["ms"], r["spans"], r["iso_spans"], r["dom"], r["flops_of"], \
         r["kv"]

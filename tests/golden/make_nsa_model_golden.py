@@ -11,8 +11,11 @@ sets its parameters with model_params.init_params, runs forward and backward
 on model_params.inputs, and stores the output, the input and parameter
 gradients (rounded to float32) and the block indices its ``torch.topk``
 returned (nsa_model.py:258), in ``nsa_model_golden.npz`` beside this script.
-The inputs are regenerated from their seed by the tests; their float64 sums
-are stored to check that.  Those indices are the one thing
+For every config of model_params.MODEL_CONFIGS it does the same for the
+reference's ``NSATransformer`` (nsa_model.py:455-511): logits, loss, parameter
+gradients, each layer's top-k indices, the state_dict layout and
+``num_params()``.  The inputs are regenerated from their seed by the tests;
+their float64 sums are stored to check that.  Those indices are the one thing
 no closed form pins: the order ``torch.topk`` gives to tied scores.
 """
 
@@ -61,6 +64,37 @@ def main(ref_dir):
         for pname, p in sorted(m.named_parameters()):
             out[f"{name}/grad/{pname}"] = p.grad.numpy().astype(np.float32)
         meta.append(dict(name=name, cfg=cfg, B=B, T=T))
+    # the model around the layer (nsa_model.py:377-556): logits, loss, every
+    # parameter gradient, the state_dict layout and each layer's top-k
+    model_meta = []
+    for name, cfg, B, T in model_params.MODEL_CONFIGS:
+        m = ref.NSATransformer(**cfg, attn_impl="ref").double()
+        model_params.init_params(m, seed=3)
+        x, y = model_params.tokens(cfg, B, T, seed=4)
+        seen = []
+        topk = torch.topk
+
+        def recording_topk(*a, **k):
+            r = topk(*a, **k)
+            seen.append(r.indices.detach().clone())
+            return r
+
+        torch.topk = recording_topk
+        try:
+            logits, loss = m(x, y)
+        finally:
+            torch.topk = topk
+        loss.backward()
+        out[f"{name}/logits"] = logits.detach().numpy().astype(np.float32)
+        out[f"{name}/loss"] = np.array([float(loss)])
+        for i, ix in enumerate(seen):
+            out[f"{name}/topk{i}"] = ix.numpy().astype(np.int32)
+        for pname, p in sorted(m.named_parameters()):
+            out[f"{name}/grad/{pname}"] = p.grad.numpy().astype(np.float32)
+        layout = {k: list(v.shape) for k, v in m.state_dict().items()}
+        model_meta.append(dict(name=name, cfg=cfg, B=B, T=T, n_topk=len(seen), state_dict=layout,
+                               num_params=int(m.num_params())))
+    out["model_meta"] = np.frombuffer(json.dumps(model_meta).encode(), dtype=np.uint8)
     out["meta"] = np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8)
     path = os.path.join(HERE, "nsa_model_golden.npz")
     np.savez_compressed(path, **out)

@@ -33,3 +33,21 @@ def inputs(cfg, B, T, seed, dtype=torch.float64):
     x = torch.randn(B, T, cfg["d_model"], generator=g, dtype=torch.float64)
     dy = torch.randn(B, T, cfg["d_model"], generator=g, dtype=torch.float64)
     return x.to(dtype), dy.to(dtype)
+
+
+# (name, NSATransformer kwargs, B, T): a two-layer model with NSA attention
+# (a trailing partial block, rows with tied fillers) and the same model with
+# the dense control arm.
+MODEL_CONFIGS = [
+    ("tf_nsa", dict(vocab_size=96, d_model=64, n_layers=2, n_q_heads=4, n_kv_heads=2, max_seq_len=80, ffn_mult=2,
+                    block_size=16, n_selected_blocks=3, window=24, attn_type="nsa"), 2, 72),
+    ("tf_full", dict(vocab_size=96, d_model=64, n_layers=2, n_q_heads=4, n_kv_heads=2, max_seq_len=80, ffn_mult=2,
+                     block_size=16, n_selected_blocks=3, window=24, attn_type="full"), 2, 72),
+]
+
+
+def tokens(cfg, B, T, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(0, cfg["vocab_size"], (B, T), generator=g)
+    y = torch.randint(0, cfg["vocab_size"], (B, T), generator=g)
+    return x, y

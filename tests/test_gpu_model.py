@@ -128,3 +128,75 @@ def test_fused_vs_ref_loss_parity(dtype):
     d = max(abs(a - b) for a, b in zip(losses["ref"], losses["fused"]))
     log(f"  losses ref {losses['ref'][0]:.4f}->{losses['ref'][-1]:.4f}, max |delta| {d:.2e}")
     assert d <= LOSS_TOL[dtype]
+
+
+# The reference's model-level gates (test_integration.py:24-30): a two-layer
+# NSATransformer, 8 AdamW steps, loss parity between attn_impl='ref' and
+# 'fused', and one backward's parameter gradients.  Also the Llama-style
+# variant (RMSNorm, SwiGLU, RoPE) with the BASELINE geometry shape
+# (overlapping compression, larger selection blocks, forced blocks).
+TF_CFG = dict(vocab_size=256, d_model=128, n_layers=2, n_q_heads=4, n_kv_heads=2, max_seq_len=128, ffn_mult=2,
+              block_size=16, n_selected_blocks=4, window=32)
+TF_LLAMA = dict(TF_CFG, n_q_heads=8, n_kv_heads=1, block_size=16, n_selected_blocks=5, window=48, norm="rms",
+                ffn="swiglu", ffn_hidden=256, pos="rope", tie_embeddings=False, cmp_stride=8, sel_block=16,
+                force_init=True, n_local=2)
+
+
+def _tf_snapshot(cfg):
+    import nsa_model
+    torch.manual_seed(0)
+    return copy.deepcopy(nsa_model.NSATransformer(attn_type="nsa", attn_impl="ref", **cfg).state_dict())
+
+
+def _tf_build(cfg, impl, snap, dev):
+    import nsa_model
+    m = nsa_model.NSATransformer(attn_type="nsa", attn_impl=impl, **cfg)
+    m.load_state_dict(snap)
+    return m.to(dev)
+
+
+def _tf_batches(cfg, dev, n):
+    g = torch.Generator().manual_seed(1)
+    return [(torch.randint(0, cfg["vocab_size"], (B, T), generator=g).to(dev),
+             torch.randint(0, cfg["vocab_size"], (B, T), generator=g).to(dev)) for _ in range(n)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("variant", ["reference", "llama"])
+def test_transformer_fused_vs_ref(variant, dtype):
+    dev = require_gpu()
+    cfg = TF_CFG if variant == "reference" else TF_LLAMA
+    log(f"transformer {variant} {dtype}")
+    snap = _tf_snapshot(cfg)
+    batches = _tf_batches(cfg, dev, STEPS)
+    amp = dtype == torch.bfloat16
+    # one backward: every parameter gradient
+    grads = {}
+    for impl in ("ref", "fused"):
+        m = _tf_build(cfg, impl, snap, dev)
+        with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+            _, loss = m(*batches[0])
+        loss.backward()
+        grads[impl] = {n: p.grad.detach().float().clone() for n, p in m.named_parameters() if p.grad is not None}
+    assert sorted(grads["ref"]) == sorted(grads["fused"])
+    worst = max(float((grads["ref"][n] - grads["fused"][n]).abs().max()) for n in grads["ref"])
+    log(f"  worst |dgrad| {worst:.3e} over {len(grads['ref'])} params")
+    assert worst <= GRAD_TOL[dtype]
+    # loss over the AdamW steps
+    losses = {}
+    for impl in ("ref", "fused"):
+        m = _tf_build(cfg, impl, snap, dev)
+        opt = torch.optim.AdamW(m.parameters(), lr=1e-3)
+        ls = []
+        for x, y in batches:
+            with torch.autocast("cuda", dtype=torch.bfloat16, enabled=amp):
+                _, loss = m(x, y)
+            opt.zero_grad(set_to_none=True)
+            loss.backward()
+            opt.step()
+            ls.append(float(loss.detach()))
+        losses[impl] = ls
+    torch.cuda.synchronize()
+    d = max(abs(a - b) for a, b in zip(losses["ref"], losses["fused"]))
+    log(f"  losses ref {losses['ref'][0]:.4f}->{losses['ref'][-1]:.4f}, max |delta| {d:.2e}")
+    assert d <= LOSS_TOL[dtype]
