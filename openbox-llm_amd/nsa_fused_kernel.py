@@ -13,16 +13,16 @@ MI355X (drop-in for the reference module nsa_fused_kernel.py).
   by importance + top-n on the GPU and the overlapping compression /
   selection geometry (``NSAGeometry``).
 
-``_range_attn_reference`` and ``nsa_fused_reference`` are the reference's
-dense torch definitions (nsa_fused_kernel.py:576-609), kept for API parity;
-the HIP path never calls them.
+``_range_attn_reference`` and ``nsa_fused_reference`` are dense torch
+definitions of the same functions (nsa_fused_kernel.py:576-609), kept for
+API parity; the HIP path never calls them.
 """
 
 import torch
 
 import nsa_hip_ops as _ops
 from nsa_hip_ops import NSAGeometry  # noqa: F401  (public)
-from nsa_selection_kernel import selection_forward_reference
+from nsa_selection_kernel import dense_branch_attention, selection_forward_reference
 from nsa_selection_backward import selection_attn_hip
 
 MODE_WINDOW = 0
@@ -84,41 +84,30 @@ def nsa_fused_forward_composed(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx
 
 
 # ---------------------------------------------------------------------------
-# the reference's dense definitions (torch, any device)
+# dense definitions (torch, any device): the branches' masks on one helper
 # ---------------------------------------------------------------------------
 
 def _range_attn_reference(q, k, v, mode, window, block_size):
-    B, Hq, T, D = q.shape
-    Hkv = k.shape[1]
-    G = Hq // Hkv
-    Lk = k.shape[2]
-    scale = D ** -0.5
-    kexp = k.float().repeat_interleave(G, dim=1)
-    vexp = v.float().repeat_interleave(G, dim=1)
-    s = torch.matmul(q.float(), kexp.transpose(-1, -2)) * scale
-    tt = torch.arange(T, device=q.device)[:, None]
-    jj = torch.arange(Lk, device=q.device)[None, :]
-    if mode == MODE_WINDOW:
-        keep = (jj <= tt) & (tt - jj < window)
-    else:
-        keep = (jj + 1) * block_size - 1 <= tt
-    keep = keep[None, None].expand(B, Hq, T, Lk)
-    s = s.masked_fill(~keep, torch.finfo(s.dtype).min)
-    p = torch.softmax(s, dim=-1) * keep.any(dim=-1, keepdim=True)
-    return torch.matmul(p, vexp).to(q.dtype)
+    """Dense window (mode 0: keys t - window < p <= t) or compression (mode 1:
+    pooled token j once ``(j + 1) * block_size - 1 <= t``) attention, float32
+    math, output in q's dtype (nsa_fused_kernel.py:576-597)."""
+    t = torch.arange(q.shape[2], device=q.device)[:, None]
+    j = torch.arange(k.shape[2], device=q.device)[None, :]
+    keep = ((j <= t) & (t - j < window)) if mode == MODE_WINDOW else ((j + 1) * block_size - 1 <= t)
+    return dense_branch_attention(q, k, v, keep)
 
 
 def _block_mean_pool_torch(x, block_size):
-    B, H, T, D = x.shape
-    n = T // block_size
-    return x[:, :, :n * block_size].reshape(B, H, n, block_size, D).mean(dim=3)
+    """Mean over the complete non-overlapping blocks of the sequence axis."""
+    return x.unfold(2, block_size, block_size).mean(dim=-1)
 
 
 def nsa_fused_reference(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, block_size, window):
-    k_cmp = _block_mean_pool_torch(kc, block_size)
-    v_cmp = _block_mean_pool_torch(vc, block_size)
-    o_cmp = _range_attn_reference(q, k_cmp, v_cmp, MODE_COMPRESS, 0, block_size)
-    o_slc = selection_forward_reference(q, ks, vs, block_idx, block_size)
-    o_win = _range_attn_reference(q, kw, vw, MODE_WINDOW, window, 0)
+    """The gated three-branch output from the dense definitions
+    (nsa_fused_kernel.py:600-609)."""
+    o = [_range_attn_reference(q, _block_mean_pool_torch(kc, block_size), _block_mean_pool_torch(vc, block_size),
+                               MODE_COMPRESS, 0, block_size),
+         selection_forward_reference(q, ks, vs, block_idx, block_size),
+         _range_attn_reference(q, kw, vw, MODE_WINDOW, window, 0)]
     g = torch.sigmoid(gate_logits)
-    return g[..., 0:1] * o_cmp + g[..., 1:2] * o_slc + g[..., 2:3] * o_win
+    return sum(g[..., c:c + 1] * o[c] for c in range(3))

@@ -11,7 +11,7 @@ it, writing per-(query, block) partials that ``nsa_sel_merge`` combines).  The
 module switch ``USE_FSA_FWD`` is accepted and ignored: the autograd boundary
 always runs block-outer.
 
-``selection_forward_reference`` is the reference's dense torch definition of
+``selection_forward_reference`` is a dense torch definition of
 the branch (nsa_selection_kernel.py:55-92), kept for API parity; the HIP path
 never calls it.
 """
@@ -23,26 +23,41 @@ import nsa_hip_ops as _ops
 USE_FSA_FWD = True
 
 
-def selection_forward_reference(q, k, v, block_idx, block_size):
-    """Dense masked selection attention (float32 math, output in q's dtype)."""
+def dense_branch_attention(q, k, v, keep):
+    """Softmax attention of ``q [B,Hq,T,D]`` over ``k/v [B,Hkv,L,D]``
+    restricted to ``keep`` (bool, broadcastable to ``[B,Hkv,T,L]``): float32
+    math, output in q's dtype, rows with no kept key zero.  Built on
+    ``nsa_model.masked_softmax`` / ``expand_kv``; the dense definitions of
+    the three branches are this function with their masks."""
+    from nsa_model import expand_kv, masked_softmax
     B, Hq, T, D = q.shape
-    Hkv = k.shape[1]
+    Hkv, L = k.shape[1], k.shape[2]
     G = Hq // Hkv
-    dev = q.device
-    scale = D ** -0.5
-    qf = q.float()
-    kexp = k.float().repeat_interleave(G, dim=1)
-    vexp = v.float().repeat_interleave(G, dim=1)
-    s = torch.matmul(qf, kexp.transpose(-1, -2)) * scale
-    p_idx = torch.arange(T, device=dev)
-    blk_of_p = p_idx // block_size
+    keep = expand_kv(torch.as_tensor(keep, device=q.device).expand(B, Hkv, T, L), G)
+    scores = torch.matmul(q.float(), expand_kv(k.float(), G).transpose(-1, -2).contiguous()) * D ** -0.5
+    return (masked_softmax(scores, keep) @ expand_kv(v.float(), G)).to(q.dtype)
+
+
+def selection_keep(block_idx, T, block_size):
+    """``[B,Hkv,T,T]`` mask of the selection branch: key p is kept for query
+    t iff its block ``p // block_size`` is listed in ``block_idx[..., t, :]``
+    (-1 = empty slot) and p <= t; a trailing partial block is reached like any
+    other (nsa_selection_kernel.py:74-85)."""
+    B, Hkv, _, S = block_idx.shape
+    dev = block_idx.device
+    n_blk = -(-T // block_size)
     idx = block_idx.long()
-    chosen = ((idx[..., :, None] == blk_of_p) & (idx[..., :, None] >= 0)).any(dim=3)   # [B,Hkv,T,T]
-    keep = chosen & (p_idx[None, :] <= p_idx[:, None])[None, None]
-    keep = keep.repeat_interleave(G, dim=1)
-    s = s.masked_fill(~keep, torch.finfo(s.dtype).min)
-    p = torch.softmax(s, dim=-1) * keep.any(dim=-1, keepdim=True)
-    return torch.matmul(p, vexp).to(q.dtype)
+    listed = torch.zeros(B, Hkv, T, n_blk + 1, dtype=torch.bool, device=dev)
+    # empty or out-of-range slots land in the spare last column, which no key reads
+    listed.scatter_(-1, torch.where((idx >= 0) & (idx < n_blk), idx, torch.full_like(idx, n_blk)), True)
+    pos = torch.arange(T, device=dev)
+    return listed[..., pos // block_size] & (pos[None, :] <= pos[:, None])
+
+
+def selection_forward_reference(q, k, v, block_idx, block_size):
+    """Dense masked selection attention, float32 math, output in q's dtype
+    (the definition of nsa_selection_kernel.py:55-92)."""
+    return dense_branch_attention(q, k, v, selection_keep(block_idx, q.shape[2], block_size))
 
 
 def selection_forward_hip(q, k, v, block_idx, block_size, return_lse=False):
