@@ -228,6 +228,15 @@ __device__ __forceinline__ void dma_tile(void* lds, SrcFn src, int tid) {
   }
 }
 
+// The 64-bit value whose 32-bit halves came back as int (readfirstlane
+// returns int): each half is taken as uint32_t, so a low half with bit 31 set
+// is zero-extended instead of sign-extended into the high half.
+__host__ __device__ constexpr uint64_t u64_from_halves(int lo, int hi) {
+  return ((uint64_t)(uint32_t)hi << 32) | (uint64_t)(uint32_t)lo;
+}
+static_assert(u64_from_halves((int)0x80001000u, 0x7ffe) == 0x00007ffe80001000ull,
+              "a base address with bit 31 set must survive the split into halves");
+
 // Direct global -> LDS loads as volatile asm (lane i writes lds + SIZE i):
 // the compiler neither tracks them nor adds waits for them, so LDS reads of
 // other stages are not held behind loads still in flight.  The caller owns
@@ -248,11 +257,8 @@ __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
 // offset (the SGPR-base form: no per-lane 64-bit address arithmetic).
 __device__ __forceinline__ void lds_dma16_sbase(const void* sbase, uint32_t voff, void* lds) {
   const uint64_t b = (uint64_t)(uintptr_t)sbase;
-  // readfirstlane returns int: each half goes through uint32_t so that the
-  // low half is zero-extended (a sign-extended low half corrupts the base)
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
-  const uint64_t bu = ((uint64_t)hi << 32) | lo;
+  const uint64_t bu = u64_from_halves(__builtin_amdgcn_readfirstlane((uint32_t)b),
+                                      __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32)));
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :: "s"(lds_addr_uniform(lds)), "v"(voff), "s"(bu) : "memory", "m0");
 }

@@ -339,3 +339,32 @@ def test_selection_trailing_partial_block(dtype):
     for nm, x, r in zip("qkv", xs, (q64, k64, v64)):
         assert_close(x.grad, r.grad, dtype, f"d{nm}")
     assert float(xs[1].grad[:, :, 96:].abs().max()) > 0
+
+
+def test_run_to_run_gradient_difference_is_bounded():
+    """Two identical fwd+bwd steps: block indices, the output and every
+    gradient without float atomics (dq, dgate, window dK/dV) are bit-identical;
+    the compression and selection dK/dV, which merge work-item partials with
+    float atomics, differ at most by float32 rounding of their sums."""
+    dev = require_gpu()
+    import nsa_fused_kernel as nfk
+    import nsa_hip_ops as ops
+    geom = ops.NSAGeometry(**dict(BASELINE_GEOM, force_init=False, n_local=0))
+    ins, do = _fused_inputs(1, 16, 1, 4096, 128, torch.bfloat16, seed=21, head_scale=True)
+    runs = []
+    for _ in range(2):
+        xs = [t.to(dev).requires_grad_() for t in ins]
+        out, idx = nfk.nsa_attention(*xs, geom)
+        out.backward(do.to(dev))
+        torch.cuda.synchronize()
+        runs.append((out.detach().cpu(), idx.cpu(), [x.grad.float().cpu() for x in xs]))
+    (o1, i1, g1), (o2, i2, g2) = runs
+    assert torch.equal(i1, i2) and torch.equal(o1, o2)
+    for nm, a, b in zip(NAMES, g1, g2):
+        d = float((a - b).abs().max())
+        rel = d / max(float(a.abs().max()), 1e-30)
+        log(f"  d{nm}: run-to-run max |diff| {d:.3e} (relative {rel:.2e})")
+        if nm in ("q", "gate", "kw", "vw"):
+            assert d == 0.0, f"d{nm} differs between identical runs"
+        else:
+            assert rel <= 1e-2, f"d{nm}: run-to-run difference {rel:.2e} of its largest value"
