@@ -12,7 +12,8 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libnsa_hip.so")
+# NSA_LIB_PATH: another build of the same library (e.g. for A/B timing)
+LIB_PATH = os.environ.get("NSA_LIB_PATH") or os.path.join(_HERE, "libnsa_hip.so")
 
 NSA_OK = 0
 NSA_ERR_SHAPE = -1

@@ -16,7 +16,10 @@
 //  3. every F tiles (and after the last) the tiles' tokens fold into the
 //     selection blocks: imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d,
 //     tokens ascending, one lane per block for both queries; F is the most
-//     tiles whose blocks fit the wave's lanes.
+//     tiles whose blocks fit the wave's lanes.  The block sums live in
+//     registers: lane L holds blocks L + 64 k (k < KPL) of both queries, the
+//     same layout the top-S phase reads (no LDS array per query, so long
+//     sequences with thousands of blocks keep several workgroups per CU).
 //  4. per query: score = +inf for forced blocks, -FLT_MAX for blocks not yet
 //     complete, else imp_slc; the order keys of the scores, KPL per lane in
 //     registers (block lane + 64 k), give S picks, each the highest score by
@@ -72,23 +75,31 @@ __device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) 
 // x / 2^sh when sh >= 0 (x >= 0), else x / d
 __device__ __forceinline__ int div_sh(int x, int d, int sh) { return sh >= 0 ? x >> sh : x / d; }
 
-// LDS: K tiles [kImpStages][32][D], per-wave token scratch [4][32 F][2]
-// (both queries' values of a token side by side), block sums [8][nsp].  cd_sh / ls_sh: log2 of cd / ls when they are powers of two,
-// else -1 (the block fold then divides); rcd = 1 / cd scales the overlap
-// weights; fold_tiles: F above (1 .. kImpFoldTiles).  KPL:
-// block keys per lane in the top-S phase (n_slc <= 64 * KPL).
+// LDS: K tiles [kImpStages][32][D] and per-wave token scratch [4][32 F][2]
+// (both queries' values of a token side by side).  cd_sh / ls_sh: log2 of
+// cd / ls when they are powers of two, else -1 (the block fold then
+// divides); rcd = 1 / cd scales the overlap weights; fold_tiles: F above
+// (1 .. kImpFoldTiles).  KPL: blocks per lane (n_slc <= 64 * KPL).
+// a[k] += v for a per-lane k, as KPL masked adds: every slot is touched
+// with a static index, so the array stays in registers (adding 0 leaves the
+// non-negative sums unchanged)
+template <int KPL>
+__device__ __forceinline__ void reg_add(float (&a)[KPL], int k, float v) {
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) a[i] += k == i ? v : 0.0f;
+}
+
 template <typename T, int D, int KPL>
 __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
                                                   const float* __restrict__ lse, int32_t* __restrict__ out_idx,
                                                   float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
-                                                  int n_slc, int nsp, int S, int cl, int cd, int ls, int force_init,
+                                                  int n_slc, int S, int cl, int cd, int ls, int force_init,
                                                   int n_local, int nqb, int cd_sh, int ls_sh, int fold_tiles, float rcd, float sl2) {
   using C = Tile32<T, D>;
   constexpr int NST = kImpStages;
   extern __shared__ __align__(16) char smem[];
   T* sK = reinterpret_cast<T*>(smem);                                   // [NST][ROW_ELEMS]
   float2* stok = reinterpret_cast<float2*>(sK + NST * C::ROW_ELEMS);    // [4][32 F]
-  float* sblk = reinterpret_cast<float*>(stok + 4 * 32 * kImpFoldTiles); // [8][nsp]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // long rows first: workgroups go out round-robin, the latest queries first
@@ -105,7 +116,11 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
 #pragma unroll
   for (int i = 0; i < kImpQPW; ++i) hi_q[i] = tq0 + i < T_ ? imp_last_token(tq0 + i, n_cmp, cl, cd) : -1;
 
-  for (int i = tid; i < kImpQPB * nsp; i += 256) sblk[i] = 0.0f;
+  float bsum[kImpQPW][KPL];   // block sums of blocks lane + 64 k, both queries
+#pragma unroll
+  for (int i = 0; i < kImpQPW; ++i)
+#pragma unroll
+    for (int k = 0; k < KPL; ++k) bsum[i][k] = 0.0f;
   const T* kbase = kc + (int64_t)bh * n_cmp * D;
   RowTileDma<T, D, 256, true> kdma;
   kdma.init(tid);
@@ -113,7 +128,6 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
 
   // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
   float2* my_tok = stok + w * 32 * kImpFoldTiles;
-  float* my_blk = sblk + w * kImpQPW * nsp;
   Frag<T> qf[C::KS];
   float lse2[16];
   auto load_rows = [&](int hc) {
@@ -144,7 +158,6 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     for (int r = 0; r < 16; ++r) asm volatile("" : "+v"(lse2[r]));
   };
   if (NHC == 1) load_rows(0);
-  __syncthreads();   // sblk cleared
   key_pipeline<NST, dma_uniform_loads<256, C::ROW_CHUNKS>()>(ntile, load_tile, [&](int kt) {
     const T* tile = sK + (kt % NST) * C::ROW_ELEMS;
     const int tok = kt * 32 + n;
@@ -189,21 +202,25 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
     if (kt % fold_tiles != fold_tiles - 1 && kt != ntile - 1) return;
     wave_fence();
     // fold the last tiles' tokens into the blocks they overlap, tokens
-    // ascending; lane = block of the tokens' span (both queries); the block's
-    // tokens are read kImpFold at a time so their LDS reads overlap
+    // ascending; the blocks touched (at most 64: fold_tiles is chosen so)
+    // go one to a lane, block j to lane j % 64 (its register slot j / 64);
+    // the block's tokens are read kImpFold at a time so their LDS reads
+    // overlap
     const int i0 = (kt - kt % fold_tiles) * 32;
     const int i1 = kt * 32 + 31 < n_cmp - 1 ? kt * 32 + 31 : n_cmp - 1;
     const int jlo = div_sh(i0 * cd, ls, ls_sh);
     int jhi = div_sh(i1 * cd + cl - 1, ls, ls_sh);
     jhi = jhi < n_slc - 1 ? jhi : n_slc - 1;
-    for (int j = jlo + lane; j <= jhi; j += kWave) {
+    const int j = jlo + ((lane - jlo) & (kWave - 1));
+    if (j <= jhi) {
+      const int kj = j / kWave;
       // tokens whose span [i*cd, i*cd+cl) meets [j*ls, (j+1)*ls)
       int a_i = j * ls - cl + 1 <= 0 ? 0 : div_sh(j * ls - cl + 1 + cd - 1, cd, cd_sh);
       int b_i = div_sh((j + 1) * ls - 1, cd, cd_sh);
       a_i = a_i > i0 ? a_i : i0;
       b_i = b_i < i1 ? b_i : i1;
       const float2* tq = my_tok - i0;
-      float s0 = my_blk[j], s1 = my_blk[nsp + j];
+      float s0 = 0.0f, s1 = 0.0f;   // this fold's share of the block's sums
       for (int ib = a_i; ib <= b_i; ib += kImpFold) {
         float2 v[kImpFold];
 #pragma unroll
@@ -220,15 +237,15 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
           }
         }
       }
-      my_blk[j] = s0;
-      my_blk[nsp + j] = s1;
+      reg_add<KPL>(bsum[0], kj, s0);
+      reg_add<KPL>(bsum[1], kj, s1);
     }
     wave_fence();
   });
-  __syncthreads();
 
   // per query of this wave: scores, masking and forcing, then top-S
   constexpr int QIL = KPL <= 16 ? kImpQPW : 1;   // queries whose picks interleave
+#pragma unroll
   for (int q0 = 0; q0 < kImpQPW; q0 += QIL) {
     uint32_t key[QIL][KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
     bool live[QIL];
@@ -241,14 +258,13 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       const int64_t r = (int64_t)bh * T_ + t;
       orow[u] = out_idx + r * S;
       pick[u] = 0;
-      const float* sc = my_blk + (q0 + u) * nsp;
       const int tb = t / ls;
 #pragma unroll
       for (int k = 0; k < KPL; ++k) {
         const int j = lane + kWave * k;
         key[u][k] = 0;
         if (live[u] && j < n_slc) {
-          const float s = sc[j];
+          const float s = bsum[q0 + u][k];
           if (scores != nullptr) scores[r * n_slc + j] = s;
           const bool valid = (j + 1) * ls - 1 <= t;
           const bool forced = (force_init && j == 0) || (j <= tb && j > tb - n_local);
@@ -301,9 +317,8 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const int S = n_sel < n_slc ? n_sel : n_slc;
   NSA_CHECK(n_slc <= 64 * 64, NSA_ERR_SHAPE);
   if (T == 0 || n_slc == 0) return NSA_OK;
-  const int nsp = n_slc + 1;   // per-query block-sum pitch (odd: spreads the 8 queries over banks)
   const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)kImpStages * 32 * D;
-  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 * kImpFoldTiles + (size_t)kImpQPB * nsp);
+  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 * kImpFoldTiles);
   static_assert(kImpQPW == 2, "token scratch holds float2 per token");
   NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
   const int nqb = (T + kImpQPB - 1) / kImpQPB;
@@ -320,15 +335,15 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
     const int64_t span = (int64_t)(32 * f - 1) * cmp_stride + cmp_block;   // positions the tokens cover
     if ((span - 1) / sel_block + 2 <= 64) fold_tiles = f;
   }
-  // block keys per lane in the top-S phase
-  const int kpl = n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : 64;
+  // blocks per lane (registers: block sums, then order keys)
+  const int kpl = n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : n_slc <= 64 * 32 ? 32 : 64;
   hipStream_t s = (hipStream_t)stream;
   // more than 64 KB of dynamic LDS must be allowed per kernel
   auto launch = [&](auto kern, auto qp, auto kp) -> int {
     if (lds > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=
                            hipSuccess)
       return NSA_ERR_LAUNCH;
-    kern<<<(unsigned)grid, 256, lds, s>>>(qp, kp, lse_cmp, block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, nsp, S,
+    kern<<<(unsigned)grid, 256, lds, s>>>(qp, kp, lse_cmp, block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, S,
                                           cmp_block, cmp_stride, sel_block, force_init, n_local, nqb, cd_sh, ls_sh,
                                           fold_tiles, rcd, sl2);
     return NSA_OK;
@@ -342,6 +357,7 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   case DD:                \
     NSA_TOPN_KPL(DD, 8)   \
     NSA_TOPN_KPL(DD, 16)  \
+    NSA_TOPN_KPL(DD, 32)  \
     NSA_TOPN_KPL(DD, 64)  \
     break;
   switch (D) {
