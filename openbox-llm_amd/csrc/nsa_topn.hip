@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
   });
 
   // per query of this wave: scores, masking and forcing, then top-S
-  constexpr int QIL = KPL <= 16 ? kImpQPW : 1;   // queries whose picks interleave
+  constexpr int QIL = KPL <= 32 ? kImpQPW : 1;   // queries whose picks interleave
 #pragma unroll
   for (int q0 = 0; q0 < kImpQPW; q0 += QIL) {
     uint32_t key[QIL][KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
