@@ -11,8 +11,11 @@ initial and two local blocks forced among the 16 are timed beside it
 
 Prints ONE JSON line (rank 0): the metric, tokens/s, the dominant kernel's
 roofline (algorithmic work / its HIP-event-timed launch duration, bound set
-from its measured HBM bytes), per-kernel MFMA fractions, and CPU baselines
-(the float32 CPU oracle on a bounded row sample of c3, and dense on c1).
+from its measured HBM bytes), per-kernel MFMA fractions, the decode step
+(one new query per sequence against 32K caches, B=32 and B=1: tokens/s and
+HBM fraction), and CPU baselines (the float32 CPU oracle on a bounded row
+sample of c3, and dense on c1).  ``--workload dec|dec_b1|dec_c5|c4|c5`` runs
+one of the other workloads alone.
 """
 
 import argparse
@@ -59,6 +62,13 @@ WORKLOADS = {
                desc="BASELINE config 4: 12-layer d768 decoder (12q/2kv heads, hd64, SwiGLU 2048, RMSNorm, RoPE 1e4, "
                     "vocab 32000), NSA l32/d16 l'64 top-16 w512 in every layer, bf16 autocast AdamW step, 8x4096 "
                     "tokens; dense arm: the same model with causal SDPA attention"),
+    "dec": dict(kind="decode", B=32, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, False, 0),
+                desc="decode step (nsa_decode_fwd): 32 sequences, one new query each at position 32767 of "
+                     "32K-token caches, config-3 heads (Hq64 Hkv4 D128) and geometry (l32/d16 l'64 top-16 w512), bf16"),
+    "dec_b1": dict(kind="decode", B=1, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, False, 0),
+                   desc="decode step, one sequence (latency): as dec with B=1"),
+    "dec_c5": dict(kind="decode", B=4, T=131072, Hq=32, Hkv=2, D=128, geom=(32, 16, 64, 32, 512, False, 0),
+                   desc="decode step, 4 sequences at 128K with config-5 heads (Hq32 Hkv2 D128, top-32)"),
     "c5": dict(kind="forward", B=1, T=131072, Hq=32, Hkv=2, D=128, geom=(32, 16, 64, 32, 512, False, 0),
                head_scale=False, in_scale=1.0, shift_frac=0.01, shift=3.0,
                desc="BASELINE config 5: NSA forward only, B1 T131072 Hq32 Hkv2 D128, l32/d16 l'64 top-32 w512, bf16, "
@@ -483,6 +493,52 @@ def run_forward_bench(args, w, name):
             "per_kernel": per_kernel_table(spans, fwd_flops, PEAK_BF16_TFLOPS, name)}
 
 
+def run_decode_bench(w, steps=200, warmup=10):
+    """One decode step per sequence (nsa_decode_fwd) on caches resident in
+    HBM, timed with HIP events over ``steps`` calls.  Algorithmic bytes: every
+    visible cache row read once (pooled tokens, window keys, keys of the
+    picked blocks; K and V) plus q, gate and out."""
+    import nsa_hip_ops as ops
+    dev = torch.device("cuda:0")
+    geom = ops.NSAGeometry(*w["geom"])
+    B, Hq, Hkv, D, T = w["B"], w["Hq"], w["Hkv"], w["D"], w["T"]
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, Hq, D, device=dev, generator=g).bfloat16()
+    gate = torch.randn(B, Hq, 3, device=dev, generator=g).bfloat16()
+    caches = [torch.randn(B, Hkv, T, D, device=dev, generator=g).bfloat16() for _ in range(6)]
+    k_cmp = ops.pool_fwd(caches[0], geom.cmp_block, geom.cmp_stride)
+    v_cmp = ops.pool_fwd(caches[1], geom.cmp_block, geom.cmp_stride)
+    lens = torch.full((B,), T, dtype=torch.int32, device=dev)
+    ws = torch.empty(ops.decode_workspace_bytes(B, Hq, Hkv, D, T, k_cmp.shape[2], geom), device=dev,
+                     dtype=torch.uint8)
+
+    def step():
+        return ops.decode_fwd(q, k_cmp, v_cmp, *caches[2:], gate, lens, geom, workspace=ws)
+    for _ in range(warmup):
+        out, idx = step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    t = T - 1
+    nvis = (t + 1 - geom.cmp_block) // geom.cmp_stride + 1
+    ls = geom.sel_block
+    sel_keys = 0
+    for j in idx.flatten().tolist():
+        if j >= 0:
+            sel_keys += max(0, min((j + 1) * ls, t + 1) - j * ls)
+    kv_rows = B * Hkv * (nvis + min(geom.window, T)) + sel_keys
+    alg = kv_rows * 2 * D * 2 + B * Hq * (2 * D + 3) * 2
+    gbs = alg / (us / 1e6) / 1e9
+    return {"us_per_step": round(us, 2), "tokens_per_s": round(B / (us / 1e6), 1), "steps": steps,
+            "algorithmic_bytes": alg, "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+            "workspace_bytes": ws.numel(), "desc": w["desc"]}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -571,8 +627,11 @@ def main():
         sys.exit(2)
     name = args.workload
     w = WORKLOADS[name]
-    if w["kind"] in ("model", "forward"):
-        extra = run_model_bench(args, w) if w["kind"] == "model" else run_forward_bench(args, w, name)
+    if w["kind"] in ("model", "forward", "decode"):
+        if w["kind"] == "decode":
+            extra = run_decode_bench(w, steps=max(args.steps, 50), warmup=args.warmup)
+        else:
+            extra = run_model_bench(args, w) if w["kind"] == "model" else run_forward_bench(args, w, name)
         print(json.dumps({"workload": name, "desc": w["desc"], "steps": args.steps, "warmup": args.warmup,
                           "result": extra}), flush=True)
         return
@@ -641,6 +700,8 @@ def main():
         res["c3_forced"] = {"ms_per_step": round(ms_f, 3), "value": round(tokens / (ms_f / 1e3), 1),
                             "mfu": round(step_flops(WORKLOADS["c3_forced"], kv_f) / (ms_f / 1e3) / 1e12
                                          / PEAK_BF16_TFLOPS, 4)}
+    if not args.no_extras and name == "c3":
+        res["decode"] = {k: run_decode_bench(WORKLOADS[k]) for k in ("dec", "dec_b1")}
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline: float32 oracle, {args.cpu_rows} rows, {threads} threads")

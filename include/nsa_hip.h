@@ -275,6 +275,46 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
                         int cmp_stride, int sel_block, int n_sel, int force_init, int n_local, int dtype,
                         void* stream);
 
+/* ---- decode: one new query per sequence against its KV caches ---------------
+ * No reference counterpart as an entry point: the reference runs whole
+ * sequences only (NSAAttention.forward, nsa_model.py:196-304).  A decode step
+ * computes that function's row t = lens[b] - 1 for every sequence b, with the
+ * candidate blocks 0 .. t / sel_block (the row of a prefill whose length
+ * reaches the end of t's selection block):
+ *   q, out            [B][Hq][D]
+ *   k_cmp, v_cmp      [B][Hkv][Ncap][D]  pooled caches (nsa_pool_fwd of kc / vc)
+ *   ks vs kw vw       [B][Hkv][Tcap][D]  branch caches; rows >= lens[b] unread
+ *   gate              [B][Hq][3] logits
+ *   lens              [B] int32 on the device, 0 <= lens[b] <= Tcap
+ *   block_idx (out)   [B][Hkv][n_sel] int32, -1 past S = min(n_sel, t/sel_block + 1)
+ *   scores (nullable) float [B][Hkv][(Tcap-1)/sel_block + 1]: raw importance
+ *                     of blocks 0 .. t/sel_block
+ *   o_branch (nullable) float [3][B][Hq][D]: compression, selection, window
+ *   lse_branch (nullable) float [3][B][Hq]
+ * Ncap >= (Tcap - cmp_block)/cmp_stride + 1 and (Tcap-1)/sel_block + 1 <= 4096.
+ * workspace: 256-byte aligned, at least nsa_decode_workspace() bytes (0 =
+ * unsupported shape); it carries the split partials between the launches. */
+size_t nsa_decode_workspace(int B, int Hq, int Hkv, int D, int Tcap, int Ncap, int cmp_block, int cmp_stride,
+                            int sel_block, int n_sel, int window);
+int nsa_decode_fwd(const void* q, const void* k_cmp, const void* v_cmp, const void* ks, const void* vs,
+                   const void* kw, const void* vw, const void* gate, const int32_t* lens, void* out,
+                   int32_t* block_idx, float* scores, float* o_branch, float* lse_branch, void* workspace,
+                   size_t workspace_bytes, int B, int Hq, int Hkv, int D, int Tcap, int Ncap, int cmp_block,
+                   int cmp_stride, int sel_block, int n_sel, int window, int force_init, int n_local, int dtype,
+                   void* stream);
+
+/* Append one token per sequence to the decode caches (no reference
+ * counterpart; the cache update a decode loop needs between steps): the six
+ * new rows [B][Hkv][D] go to position lens_in[b] of kc vc ks vs kw vw, and
+ * when the new length completes a pooled span the pooled token of kc / vc is
+ * written to k_cmp / v_cmp exactly as nsa_pool_fwd computes it.
+ * lens_out[b] = lens_in[b] + 1 (unchanged, and nothing written, when the
+ * cache is full).  lens_in and lens_out must be different buffers. */
+int nsa_decode_append(void* kc, void* vc, void* ks, void* vs, void* kw, void* vw, void* k_cmp, void* v_cmp,
+                      const void* kc_new, const void* vc_new, const void* ks_new, const void* vs_new,
+                      const void* kw_new, const void* vw_new, const int32_t* lens_in, int32_t* lens_out, int B,
+                      int Hkv, int D, int Tcap, int Ncap, int cmp_block, int cmp_stride, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

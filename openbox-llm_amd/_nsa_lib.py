@@ -69,6 +69,9 @@ SIGNATURES = {
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_importance_topn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _P]),
+    "nsa_decode_workspace": (_Z, [_I] * 11),
+    "nsa_decode_fwd": (_I, [_P] * 15 + [_Z] + [_I] * 14 + [_P]),
+    "nsa_decode_append": (_I, [_P] * 16 + [_I] * 8 + [_P]),
 }
 
 _lib = None

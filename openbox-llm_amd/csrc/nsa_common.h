@@ -125,6 +125,34 @@ __device__ __forceinline__ void store4(float* p, float a, float b, float c, floa
   *reinterpret_cast<f32x4*>(p) = (f32x4){a, b, c, d};
 }
 
+// float -> u32 with the same order (+inf highest); every float maps above 0
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Maximum (MAX) or minimum of a u32 over the wave, in every lane: within rows
+// of 16 lanes by DPP (quad swaps, half-row and row mirrors), across rows by
+// the gfx950 row swaps (permlane16: row pairs, permlane32: wave halves) --
+// register moves only, no LDS round trips.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x) {
+  auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x141, 0xF, 0xF, false));   // row_half_mirror
+  x = op(x, (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x140, 0xF, 0xF, false));   // row_mirror
+  {
+    const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = op(p[0], p[1]);   // rows 2r and 2r+1 hold their pair's result
+  }
+  {
+    const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    x = op(p[0], p[1]);   // both halves: the wave's result
+  }
+  return x;
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).
 // Map the hardware block id to a logical one so that logically consecutive
 // workgroups (neighbouring queries / the same KV head) share an XCD.

@@ -838,3 +838,93 @@ def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, blo
     Returns ``(out, block_idx)``.
     """
     return NSAFusedHIP.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom, pooled)
+
+
+# ---------------------------------------------------------------------------
+# decode: one new query per sequence against its KV caches (no reference
+# counterpart; row t = lens[b] - 1 of NSAAttention.forward, nsa_model.py:196-304)
+# ---------------------------------------------------------------------------
+
+def decode_workspace_bytes(B, Hq, Hkv, D, Tcap, Ncap, geom: NSAGeometry):
+    n = int(_lib().nsa_decode_workspace(B, Hq, Hkv, D, Tcap, Ncap, geom.cmp_block, geom.cmp_stride,
+                                        geom.sel_block, geom.n_sel, geom.window))
+    assert n > 0, "decode: unsupported shape (head dim, capacities or candidate blocks)"
+    return n
+
+
+def decode_fwd(q, k_cmp, v_cmp, ks, vs, kw, vw, gate, lens, geom: NSAGeometry, return_scores=False,
+               return_branches=False, workspace=None):
+    """One decode step for every sequence: ``q [B,Hq,D]`` and ``gate
+    [B,Hq,3]`` are the new tokens' query and gate logits, ``lens`` (int32
+    [B], on the device) the cache lengths including the new token.  Caches:
+    ``k_cmp/v_cmp [B,Hkv,Ncap,D]`` pooled, ``ks..vw [B,Hkv,Tcap,D]``.
+
+    Returns ``(out [B,Hq,D], block_idx [B,Hkv,n_sel])`` (-1 past the
+    sequence's S), plus a dict with ``scores`` (raw importance of candidate
+    blocks, float32 ``[B,Hkv,(Tcap-1)//sel_block+1]``, NaN past the
+    candidates) and/or ``o_branch`` ``[3,B,Hq,D]`` / ``lse_branch`` ``[3,B,Hq]``
+    (compression, selection, window) when asked.
+    """
+    assert q.dim() == 3 and q.is_cuda, "decode: q must be [B, Hq, D] on the GPU"
+    B, Hq, D = q.shape
+    caches = [_contig(x) for x in (ks, vs, kw, vw)]
+    assert ks.dim() == 4 and ks.shape[0] == B and ks.shape[3] == D, "decode: caches must be [B, Hkv, Tcap, D]"
+    Hkv, Tcap = ks.shape[1], ks.shape[2]
+    assert Hq % Hkv == 0, "GQA needs n_q_heads divisible by n_kv_heads"
+    for x in caches:
+        assert x.shape == ks.shape and x.dtype == q.dtype, "decode: branch caches differ in shape or dtype"
+    k_cmp, v_cmp = _contig(k_cmp), _contig(v_cmp)
+    Ncap = k_cmp.shape[2]
+    assert k_cmp.shape == (B, Hkv, Ncap, D) and v_cmp.shape == k_cmp.shape, "decode: pooled caches [B, Hkv, Ncap, D]"
+    assert k_cmp.dtype == q.dtype and v_cmp.dtype == q.dtype
+    assert gate.shape == (B, Hq, 3) and gate.dtype == q.dtype, "decode: gate logits [B, Hq, 3] in q's dtype"
+    assert lens.dtype == torch.int32 and lens.shape == (B,) and lens.is_cuda, "decode: lens int32 [B] on the GPU"
+    q, gate, lens = _contig(q), _contig(gate), _contig(lens)
+    nbytes = decode_workspace_bytes(B, Hq, Hkv, D, Tcap, Ncap, geom)
+    if workspace is None:
+        workspace = torch.empty(nbytes, device=q.device, dtype=torch.uint8)
+    assert workspace.numel() * workspace.element_size() >= nbytes and workspace.data_ptr() % 256 == 0, \
+        "decode: workspace too small or not 256-byte aligned"
+    out = torch.empty_like(q)
+    idx = torch.empty(B, Hkv, geom.n_sel, device=q.device, dtype=torch.int32)
+    ncand_cap = (Tcap - 1) // geom.sel_block + 1
+    scores = (torch.full((B, Hkv, ncand_cap), float("nan"), device=q.device, dtype=torch.float32)
+              if return_scores else None)
+    o_br = torch.empty(3, B, Hq, D, device=q.device, dtype=torch.float32) if return_branches else None
+    lse_br = torch.empty(3, B, Hq, device=q.device, dtype=torch.float32) if return_branches else None
+    _call("nsa_decode_fwd", _lib().nsa_decode_fwd, L.ptr(q), L.ptr(k_cmp), L.ptr(v_cmp), *map(L.ptr, caches),
+          L.ptr(gate), L.ptr(lens), L.ptr(out), L.ptr(idx), L.ptr(scores), L.ptr(o_br), L.ptr(lse_br),
+          L.ptr(workspace), workspace.numel() * workspace.element_size(), B, Hq, Hkv, D, Tcap, Ncap,
+          geom.cmp_block, geom.cmp_stride, geom.sel_block, geom.n_sel, geom.window, int(geom.force_init),
+          geom.n_local, L.dtype_code(q), _stream(q))
+    if not (return_scores or return_branches):
+        return out, idx
+    extras = {}
+    if return_scores:
+        extras["scores"] = scores
+    if return_branches:
+        extras["o_branch"], extras["lse_branch"] = o_br, lse_br
+    return out, idx, extras
+
+
+def decode_append(kc, vc, ks, vs, kw, vw, k_cmp, v_cmp, new_rows, lens, geom: NSAGeometry):
+    """Write one token per sequence into the caches (in place): ``new_rows``
+    are the six ``[B,Hkv,D]`` rows (kc vc ks vs kw vw) for position
+    ``lens[b]``; a pooled token is added when the new length completes a
+    span.  Returns the new lengths (a new int32 tensor; full caches keep
+    theirs)."""
+    caches = (kc, vc, ks, vs, kw, vw)
+    B, Hkv, Tcap, D = kc.shape
+    for x in caches + (k_cmp, v_cmp):
+        assert x.is_contiguous() and x.dtype == kc.dtype, "decode_append: caches must be contiguous, one dtype"
+    for x in caches:
+        assert x.shape == kc.shape
+    assert k_cmp.shape[:2] == (B, Hkv) and k_cmp.shape[3] == D and v_cmp.shape == k_cmp.shape
+    rows = [_contig(r) for r in new_rows]
+    assert len(rows) == 6 and all(r.shape == (B, Hkv, D) and r.dtype == kc.dtype for r in rows)
+    assert lens.dtype == torch.int32 and lens.shape == (B,) and lens.is_contiguous()
+    lens_out = torch.empty_like(lens)
+    _call("nsa_decode_append", _lib().nsa_decode_append, *map(L.ptr, caches), L.ptr(k_cmp), L.ptr(v_cmp),
+          *map(L.ptr, rows), L.ptr(lens), L.ptr(lens_out), B, Hkv, D, Tcap, k_cmp.shape[2], geom.cmp_block,
+          geom.cmp_stride, L.dtype_code(kc), _stream(kc))
+    return lens_out

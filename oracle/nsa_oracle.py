@@ -34,6 +34,9 @@ Layout ``q [B,Hq,T,D]``, ``k/v [B,Hkv,T,D]``; query head ``h`` reads KV head
   unspecified).
 * gate: ``out = sum_c sigmoid(gate[...,c]) * o_c`` (nsa_model.py:293-301,
   nsa_fused_kernel.py:572-573).
+* decode (``decode_reference``): row ``t = len-1`` of the above from caches,
+  candidate blocks ``0 .. t // ls``; pinned against the whole-sequence
+  functions in tests/test_oracle_pins.py.
 """
 
 from __future__ import annotations
@@ -424,7 +427,7 @@ def _gathered_attention(q_rows, k, v, kidx, kmask, scale):
     B, Hq, R, D = q_rows.shape
     Hkv = k.shape[1]
     G = Hq // Hkv
-    safe = kidx.clamp(min=0)
+    safe = kidx.clamp(min=0, max=k.shape[2] - 1)   # masked slots may point past the keys
     bi = torch.arange(B)[:, None, None, None]
     hi = torch.arange(Hkv)[None, :, None, None]
     kg = k[bi, hi, safe]                                        # [B,Hkv,R,K,D]
@@ -530,18 +533,70 @@ def selection_rows(q_rows, k, v, idx_rows, ls, rows, T):
 
 def importance_rows(q, k_cmp, cfg: NSAConfig, rows, T):
     """Raw importance ``[B,Hkv,R,n_slc]`` for the query positions ``rows``."""
-    B, Hq, _, D = q.shape
+    rows = torch.as_tensor(rows, dtype=torch.long)
+    return importance_gathered(q[:, :, rows], k_cmp, cfg, rows, T)
+
+
+def importance_gathered(q_rows, k_cmp, cfg: NSAConfig, rows, T):
+    """``importance_rows`` with the query rows already gathered: ``q_rows
+    [B,Hq,R,D]`` are the queries at positions ``rows`` of a length-``T``
+    sequence (nsa_model.py:245-250 restricted to those rows)."""
+    B, Hq, R, D = q_rows.shape
     Hkv = k_cmp.shape[1]
     G = Hq // Hkv
     rows = torch.as_tensor(rows, dtype=torch.long)
     n = k_cmp.shape[2]
     n_slc = n_sel_blocks(T, cfg.sel_block)
-    qr = q[:, :, rows]
     keep = (torch.arange(n)[None, :] * cfg.cmp_stride + cfg.cmp_block - 1) <= rows[:, None]
-    p = attention_probs(qr, k_cmp, keep[None, None])
-    imp_cmp = p.reshape(B, Hkv, G, rows.numel(), n).sum(2)
+    p = attention_probs(q_rows, k_cmp, keep[None, None])
+    imp_cmp = p.reshape(B, Hkv, G, R, n).sum(2)
     W = overlap_weights(n, n_slc, cfg.cmp_block, cfg.cmp_stride, cfg.sel_block)
     return imp_cmp @ W.to(imp_cmp.dtype)
+
+
+# ---------------------------------------------------------------------------
+# decode: one new query per sequence against its caches
+# ---------------------------------------------------------------------------
+
+def decode_reference(q, kc, vc, ks, vs, kw, vw, gate, lens, cfg: NSAConfig):
+    """One decode step: row ``t = lens[b] - 1`` of the three-branch NSA for
+    every sequence ``b`` (nsa_model.py:196-304 at that row).
+
+    ``q [B,Hq,D]`` and ``gate [B,Hq,3]`` are the new query's; the caches
+    ``kc..vw [B,Hkv,Tcap,D]`` are read below ``lens[b]`` only.  The candidate
+    blocks are ``0 .. t // ls`` -- the row of a prefill whose length reaches
+    the end of t's selection block, so a decode step does not depend on how
+    long the sequence will grow.  Returns ``(out [B,Hq,D], block_idx
+    [B,Hkv,n_sel] (-1 past S), parts)``; ``parts`` holds per sequence the raw
+    importance of the candidates and each branch's ``(o, lse)``.
+    """
+    B, Hq, D = q.shape
+    Hkv = kc.shape[1]
+    ls = cfg.sel_block
+    out = torch.zeros_like(q)
+    idx = torch.full((B, Hkv, cfg.n_sel), -1, dtype=torch.int32)
+    parts = []
+    for b in range(B):
+        n = int(lens[b])
+        t = n - 1
+        if t < 0:
+            parts.append(None)
+            continue
+        ncand = t // ls + 1
+        S = min(cfg.n_sel, ncand)
+        sl = slice(b, b + 1)
+        kcb, vcb = kc[sl, :, :n], vc[sl, :, :n]
+        k_cmp = pool_mean(kcb, cfg.cmp_block, cfg.cmp_stride)
+        v_cmp = pool_mean(vcb, cfg.cmp_block, cfg.cmp_stride)
+        qb = q[sl, :, None, :]
+        imp = importance_gathered(qb, k_cmp, cfg, [t], ncand * ls)     # [1,Hkv,1,ncand]
+        pick = topn_from_scores(selection_scores(imp, cfg, t_pos=[t]), S)
+        idx[b, :, :S] = pick[0, :, 0]
+        o, br = nsa_rows_gathered(qb, kcb, vcb, ks[sl, :, :n], vs[sl, :, :n], kw[sl, :, :n], vw[sl, :, :n],
+                                  gate[sl, :, None, :], pick, cfg, [t], n, k_cmp, v_cmp)
+        out[b] = o[0, :, 0]
+        parts.append({"importance": imp[0, :, 0], **{k: (v[0][0, :, 0], v[1][0, :, 0]) for k, v in br.items()}})
+    return out, idx, parts
 
 
 # ---------------------------------------------------------------------------

@@ -74,3 +74,25 @@ def test_noalloc_entry_point_rejects_oversize_without_a_device():
     assert rc == mod.NSA_ERR_WORKSPACE
     # bad arguments are shape errors, also before any device call
     assert lib.nsa_sel_dkdv_noalloc(*([None] * 8), 1, *([None] * 5), 0, 16, 1, 64, 64, 16, 64, 2, 1, None) == -1
+
+
+def test_decode_entry_points_check_before_launching():
+    mod, lib = _lib()
+    # c3 heads, 32K capacity: partials + scores fit in a few tens of MB
+    n = lib.nsa_decode_workspace(16, 64, 4, 128, 32768, 2047, 32, 16, 64, 16, 512)
+    assert 0 < n < 64 << 20
+    # unsupported: head dim 48, a pooled cache too short for the capacity,
+    # more than 4096 candidate blocks
+    assert lib.nsa_decode_workspace(1, 16, 1, 48, 4096, 255, 32, 16, 64, 16, 512) == 0
+    assert lib.nsa_decode_workspace(1, 16, 1, 128, 4096, 100, 32, 16, 64, 16, 512) == 0
+    assert lib.nsa_decode_workspace(1, 16, 1, 128, 64 * 4096 + 1, 1 << 16, 32, 16, 64, 16, 512) == 0
+    fake = 1 << 20   # a non-null, 256-byte aligned address that is never dereferenced
+    args = [fake] * 9 + [fake, fake, None, None, None]
+    # workspace smaller than required: rejected before any launch
+    assert lib.nsa_decode_fwd(*args, fake, 16, 1, 16, 1, 128, 4096, 255, 32, 16, 64, 16, 512, 0, 0, 1,
+                              None) == mod.NSA_ERR_WORKSPACE
+    assert lib.nsa_decode_fwd(*args, fake, 1 << 30, 1, 16, 1, 128, 4096, 255, 32, 16, 64, 16, 512, 0, 0, 7,
+                              None) == mod.NSA_ERR_DTYPE
+    # lens_in and lens_out must differ (the update of one sequence's length
+    # would race with the other KV heads' reads)
+    assert lib.nsa_decode_append(*([fake] * 14), fake, fake, 1, 1, 64, 128, 7, 32, 16, 1, None) == mod.NSA_ERR_ARG

@@ -418,6 +418,49 @@ def test_rows_path_gradients_match_dense_path():
         torch.testing.assert_close(a.grad, b.grad, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("cfg", [
+    O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10, force_init=True, n_local=2),
+    O.NSAConfig(cmp_block=16, cmp_stride=16, sel_block=16, n_sel=2, window=24),
+    O.NSAConfig(cmp_block=8, cmp_stride=8, sel_block=12, n_sel=4, window=7),
+])
+def test_decode_step_is_the_prefill_row(cfg):
+    """A decode step at t (caches holding tokens 0..t, garbage above) equals
+    row t of the whole-sequence NSA of a sequence whose length is a multiple
+    of the selection block: the same block choice and the same output."""
+    B, Hq, Hkv, T, D = 2, 4, 2, 96, 8
+    assert T % cfg.sel_block == 0
+    q = _rand(B, Hq, T, D, seed=100)
+    kv = [_rand(B, Hkv, T, D, seed=101 + i) for i in range(6)]
+    gate = _rand(B, Hq, T, 3, seed=110)
+    out, parts = O.nsa_forward_reference(q, *kv, gate, cfg)
+    idx_full = parts["block_idx"]
+    for t in [0, 3, 7, 8, 15, 16, 17, 31, 40, 47, 48, 63, 95]:
+        lens = torch.tensor([t + 1, max(1, t - 5)])
+        caches = [x.clone() for x in kv]
+        for c in caches:   # rows at or past lens[b] must not matter
+            for b in range(B):
+                c[b, :, int(lens[b]):] = float("nan")
+        qd = torch.stack([q[0, :, t], q[1, :, int(lens[1]) - 1]])
+        gd = torch.stack([gate[0, :, t], gate[1, :, int(lens[1]) - 1]])
+        o_d, i_d, p_d = O.decode_reference(qd, *caches, gd, lens, cfg)
+        for b in range(B):
+            tb = int(lens[b]) - 1
+            torch.testing.assert_close(o_d[b], out[b, :, tb], rtol=1e-12, atol=1e-12)
+            S = min(cfg.n_sel, tb // cfg.sel_block + 1)
+            assert torch.equal(i_d[b, :, :S], idx_full[b, :, tb, :S]), (t, b)
+            assert (i_d[b, :, S:] == -1).all()
+            ncand = tb // cfg.sel_block + 1
+            torch.testing.assert_close(p_d[b]["importance"], parts["importance"][b, :, tb, :ncand])
+
+
+def test_decode_empty_cache_is_zero():
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10)
+    q, gate = _rand(1, 2, 8, seed=1), _rand(1, 2, 3, seed=2)
+    kv = [_rand(1, 1, 16, 8, seed=3 + i) for i in range(6)]
+    o, idx, parts = O.decode_reference(q, *kv, gate, torch.tensor([0]), cfg)
+    assert (o == 0).all() and (idx == -1).all() and parts == [None]
+
+
 def test_keys_per_row_matches_masks():
     cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10)
     T = 96
@@ -464,6 +507,18 @@ def test_pins_catch_planted_mistakes():
     p = O.attention_probs(q, k, keep)
     dq_bad = (8 ** -0.5) * (p * (do @ v.repeat_interleave(2, 1).transpose(-1, -2))) @ k.repeat_interleave(2, 1)
     assert not torch.allclose(dq, dq_bad)
+    # decode offering complete blocks only (ncand = len // ls): differs from
+    # the prefill row where t sits inside a block with local forcing
+    cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=2, window=4, n_local=1)
+    qq = _rand(1, 2, 64, 8, seed=20)
+    kvs = [_rand(1, 1, 64, 8, seed=21 + i) for i in range(6)]
+    gg = _rand(1, 2, 64, 3, seed=30)
+    _, parts = O.nsa_forward_reference(qq, *kvs, gg, cfg)
+    t = 40
+    kcmp = O.pool_mean(kvs[0][:, :, :t + 1], 8, 4)
+    imp = O.importance_gathered(qq[:, :, t:t + 1], kcmp, cfg, [t], t + 1)
+    bad = O.topn_from_scores(O.selection_scores(imp, cfg, t_pos=[t]), min(2, imp.shape[-1]))
+    assert not torch.equal(bad[0, :, 0], parts["block_idx"][0, :, t])
     # top-n tie broken toward the higher index
     sc = torch.tensor([[[[2.0, 2.0, 1.0]]]])
     assert O.topn_from_scores(sc, 1).item() == 0
