@@ -13,7 +13,7 @@ Prints ONE JSON line (rank 0): the metric, tokens/s, the dominant kernel's
 roofline (algorithmic work / its HIP-event-timed launch duration, bound set
 from its measured HBM bytes), per-kernel MFMA fractions, the decode step
 (one new query per sequence against 32K caches, B=32 and B=1: tokens/s and
-HBM fraction), and CPU baselines (the float32 CPU oracle on a bounded row
+HBM fraction), the compression phi's forward / backward time, and CPU baselines (the float32 CPU oracle on a bounded row
 sample of c3, and dense on c1).  ``--workload dec|dec_b1|dec_c5|c4|c5`` runs
 one of the other workloads alone.
 """
@@ -539,6 +539,42 @@ def run_decode_bench(w, steps=200, warmup=10):
             "workspace_bytes": ws.numel(), "desc": w["desc"]}
 
 
+def run_phi_bench(reps=20):
+    """The NSA paper's compression phi (``nsa_hip_ops.phi_compress``) on the
+    config-3 keys of one layer: B1 Hkv4 T32768 D128, span 32 stride 16,
+    hidden 128, bf16; forward and backward timed with HIP events."""
+    import nsa_hip_ops as ops
+    dev = torch.device("cuda:0")
+    B, H, T, D, Hd, l, d = 1, 4, 32768, 128, 128, 32, 16
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(B, H, T, D, device=dev, generator=g).bfloat16().requires_grad_()
+    params = [(0.3 * torch.randn(l, D, device=dev, generator=g)).requires_grad_(),
+              (torch.randn(Hd, l * D, device=dev, generator=g) / 64).requires_grad_(),
+              torch.zeros(Hd, device=dev, requires_grad=True),
+              (torch.randn(D, Hd, device=dev, generator=g) / 11).requires_grad_(),
+              torch.zeros(D, device=dev, requires_grad=True)]
+    n = (T - l) // d + 1
+    dout = torch.randn(B, H, n, D, device=dev, generator=g).bfloat16()
+    for _ in range(3):
+        ops.phi_compress(x, *params, l, d).backward(dout)
+    torch.cuda.synchronize()
+    a, b, c = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    outs = []
+    a.record()
+    for _ in range(reps):
+        outs.append(ops.phi_compress(x, *params, l, d))
+    b.record()
+    for y in outs:
+        y.backward(dout)
+    c.record()
+    torch.cuda.synchronize()
+    fwd_ms, bwd_ms = a.elapsed_time(b) / reps, b.elapsed_time(c) / reps
+    flops = B * H * n * (l * D * Hd + Hd * D) * 2
+    return {"fwd_us": round(fwd_ms * 1e3, 1), "bwd_us": round(bwd_ms * 1e3, 1),
+            "fwd_tflops": round(flops / fwd_ms / 1e9, 1), "fwd_mfma_frac": round(flops / fwd_ms / 1e9 / PEAK_BF16_TFLOPS, 4),
+            "shape": "B1 Hkv4 T32768 D128, l32 d16, hidden 128, bf16 (one of the two compressors of a config-3 layer)"}
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -702,6 +738,7 @@ def main():
                                          / PEAK_BF16_TFLOPS, 4)}
     if not args.no_extras and name == "c3":
         res["decode"] = {k: run_decode_bench(WORKLOADS[k]) for k in ("dec", "dec_b1")}
+        res["phi"] = run_phi_bench()
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline: float32 oracle, {args.cpu_rows} rows, {threads} threads")

@@ -275,6 +275,28 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
                         int cmp_stride, int sel_block, int n_sel, int force_init, int n_local, int dtype,
                         void* stream);
 
+/* ---- compression phi (NSA paper eq. 7) --------------------------------------
+ * Replaces BlockCompressor (nsa_model.py:100-123), the reference's weighted
+ * mean + linear, by the paper's learnable MLP over each span of l tokens at
+ * stride d with an intra-block position encoding P:
+ *   out[i] = W2 silu(W1 vec(x[i d .. i d + l - 1] + P) + b1) + b2
+ * x [BH][L][D] (spans read in place), w1 [H][l D], w2 [D][H] in dtype;
+ * c1 = b1 + W1 vec(P) and b2 float [H] / [D]; out [BH][n][D] in dtype with
+ * n = (L - l)/d + 1; pre (float [BH][n][H]) receives W1 vec(span + P) + b1 for
+ * the backward.  D in {64, 128}, H in {32, 64, 128}. */
+int nsa_phi_fwd(const void* x, const void* w1, const float* c1, const void* w2, const float* b2, void* out,
+                float* pre, int BH, int L, int D, int H, int l, int d, int dtype, void* stream);
+/* Backward of phi's hidden layer: dpre = (W2^T dout) * silu'(pre).  dout
+ * [BH][n][D] and w2t = W2^T [H][D] in dtype; pre / dpre float [BH][n][H]. */
+int nsa_phi_dpre(const void* dout, const void* w2t, const float* pre, float* dpre, int BH, int n, int D, int H,
+                 int dtype, void* stream);
+/* Gradient of the spans back onto the sequence: dx[p] = sum over the spans i
+ * holding p (i d <= p < i d + l) of dspan[i][(p - i d) D ..], spans ascending,
+ * summed in float (deterministic).  dspan [BH][n][l D] in dspan_dtype; dx
+ * [BH][L][D] in dx_dtype. */
+int nsa_phi_fold(const void* dspan, int dspan_dtype, void* dx, int BH, int L, int D, int l, int d, int dx_dtype,
+                 void* stream);
+
 /* ---- decode: one new query per sequence against its KV caches ---------------
  * No reference counterpart as an entry point: the reference runs whole
  * sequences only (NSAAttention.forward, nsa_model.py:196-304).  A decode step

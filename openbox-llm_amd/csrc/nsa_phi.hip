@@ -1,0 +1,280 @@
+// Compression phi of the NSA paper (arXiv:2502.11089, eq. 7): the pooled
+// token of span i is phi(x[i d .. i d + l - 1] + P) with a learnable MLP over
+// the l x D span and an intra-block position encoding P (l x D):
+//
+//   pre_i = W1 vec(x_span_i + P) + b1 = W1 vec(x_span_i) + c1,  c1 = W1 vec(P) + b1
+//   out_i = W2 silu(pre_i) + b2                 (W1: H x lD, W2: D x H)
+//
+// It replaces the reference's weighted mean + linear (BlockCompressor,
+// nsa_model.py:100-123).  The span rows are contiguous in a [T][D] sequence,
+// so span i is the lD-element row starting at x + i d D: the kernels read the
+// overlapping spans in place (no unfolded copy).
+//
+// k_phi_fwd: one wave per 32 pooled tokens.  pre^T = W1 X^T on 32x32x16
+// MFMAs with the hidden units on M (W1 rows, perm32 order) and the tokens on
+// N, so the accumulator of hidden tile mt holds, in registers 8u .. 8u+7 of
+// lane half h, hidden units 32 mt + 16 u + 8 h + j: after bias and SiLU it is
+// the B operand of out^T = W2 silu(pre)^T for contraction step 2 mt + u
+// without moving data between lanes.  pre is kept (float) for the backward.
+// k_phi_dpre: dpre = (W2^T dout) * silu'(pre), the same orientation.
+// k_phi_fold: dx[p] = sum over the spans i that hold p of dspan_i[p - i d]
+// (deterministic gather, no atomics).
+#include "nsa_launch.h"
+#include "nsa_tile32.h"
+
+namespace nsa {
+
+__device__ __forceinline__ float silu_f(float z) { return z / (1.0f + __expf(-z)); }
+__device__ __forceinline__ float silu_grad(float z) {
+  const float s = 1.0f / (1.0f + __expf(-z));
+  return s * (1.0f + z * (1.0f - s));
+}
+
+// 8 consecutive elements starting at an 8-aligned index of a row of T
+template <typename T>
+__device__ __forceinline__ void store_run8(T* p, const float* v) {
+  Frag<T> f;
+  f.set(v);
+  f.store(p);
+}
+
+template <typename T, int D, int H>
+__global__ __launch_bounds__(256) void k_phi_fwd(const T* __restrict__ x, const T* __restrict__ w1,
+                                                 const float* __restrict__ c1, const T* __restrict__ w2,
+                                                 const float* __restrict__ b2, T* __restrict__ out,
+                                                 float* __restrict__ pre_out, int BH, int L, int n, int l, int d,
+                                                 int ntile) {
+  constexpr int MT = H / 32;   // hidden tiles
+  constexpr int DT = D / 32;   // output tiles
+  const int lane = threadIdx.x & 63, h = lane >> 5, nn = lane & 31;
+  const int64_t wt = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wt >= (int64_t)BH * ntile) return;
+  const int bh = (int)(wt / ntile), i0 = (int)(wt % ntile) * 32;
+  const int K = l * D;
+  const int tok = i0 + nn;
+  const bool tok_ok = tok < n;
+  // the B operand: token column nn reads its span row (tokens past n repeat the last)
+  const T* xrow = x + ((int64_t)bh * L + (int64_t)(tok_ok ? tok : n - 1) * d) * D + 8 * h;
+  const T* w1row[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) w1row[mt] = w1 + (int64_t)(32 * mt + perm32(nn)) * K + 8 * h;
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
+#pragma unroll 4
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    Frag<T> bx;
+    bx.load(xrow + k0);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      Frag<T> aw;
+      aw.load(w1row[mt] + k0);
+      mma32(acc[mt], aw, bx);
+    }
+  }
+  // bias, keep pre, SiLU -> B fragments of silu(pre)^T
+  Frag<T> hb[MT][2];
+  float* prow = pre_out + ((int64_t)bh * n + tok) * H;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    float pv[16], hv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      pv[r] = acc[mt][r] + c1[32 * mt + acc_elem(h, r)];
+      hv[r] = silu_f(pv[r]);
+    }
+    if (tok_ok) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float* p = prow + 32 * mt + 16 * u + 8 * h;
+        *reinterpret_cast<f32x4*>(p) = (f32x4){pv[8 * u], pv[8 * u + 1], pv[8 * u + 2], pv[8 * u + 3]};
+        *reinterpret_cast<f32x4*>(p + 4) = (f32x4){pv[8 * u + 4], pv[8 * u + 5], pv[8 * u + 6], pv[8 * u + 7]};
+      }
+    }
+    hb[mt][0].set(hv);
+    hb[mt][1].set(hv + 8);
+  }
+  // out^T = W2 silu(pre)^T: A = W2 rows (perm32), contraction over the hidden units
+  T* orow = out + ((int64_t)bh * n + tok) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    f32x16 o = zero16();
+    const T* w2row = w2 + (int64_t)(32 * dt + perm32(nn)) * H + 8 * h;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        Frag<T> a;
+        a.load(w2row + 32 * mt + 16 * u);
+        mma32(o, a, hb[mt][u]);
+      }
+    if (tok_ok) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int d0 = 32 * dt + 16 * u + 8 * h;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = o[8 * u + j] + b2[d0 + j];
+        store_run8(orow + d0, v);
+      }
+    }
+  }
+}
+
+// dpre = (W2^T dout) * silu'(pre): w2t is W2^T [H][D]; dout [BH][n][D]; dpre float [BH][n][H]
+template <typename T, int D, int H>
+__global__ __launch_bounds__(256) void k_phi_dpre(const T* __restrict__ dout, const T* __restrict__ w2t,
+                                                  const float* __restrict__ pre, float* __restrict__ dpre, int BH,
+                                                  int n, int ntile) {
+  constexpr int MT = H / 32, KS = D / 16;
+  const int lane = threadIdx.x & 63, h = lane >> 5, nn = lane & 31;
+  const int64_t wt = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wt >= (int64_t)BH * ntile) return;
+  const int bh = (int)(wt / ntile), i0 = (int)(wt % ntile) * 32;
+  const int tok = i0 + nn;
+  const bool tok_ok = tok < n;
+  const T* drow = dout + ((int64_t)bh * n + (tok_ok ? tok : n - 1)) * D + 8 * h;
+  Frag<T> bd[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) bd[s].load(drow + 16 * s);
+  const int64_t r0 = ((int64_t)bh * n + tok) * H;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    f32x16 acc = zero16();
+    const T* arow = w2t + (int64_t)(32 * mt + perm32(nn)) * D + 8 * h;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      Frag<T> a;
+      a.load(arow + 16 * s);
+      mma32(acc, a, bd[s]);
+    }
+    if (tok_ok) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int64_t o = r0 + 32 * mt + 16 * u + 8 * h;
+        const f32x4 z0 = *reinterpret_cast<const f32x4*>(pre + o);
+        const f32x4 z1 = *reinterpret_cast<const f32x4*>(pre + o + 4);
+        f32x4 g0, g1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          g0[j] = acc[8 * u + j] * silu_grad(z0[j]);
+          g1[j] = acc[8 * u + 4 + j] * silu_grad(z1[j]);
+        }
+        *reinterpret_cast<f32x4*>(dpre + o) = g0;
+        *reinterpret_cast<f32x4*>(dpre + o + 4) = g1;
+      }
+    }
+  }
+}
+
+// dx[bh][p][c] = sum over spans i with i d <= p < i d + l (i < n) of
+// dspan[bh][i][(p - i d) D + c], spans ascending
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void k_phi_fold(const TI* __restrict__ dspan, TO* __restrict__ dx, int BH,
+                                                  int L, int D, int n, int l, int d) {
+  const int64_t total = (int64_t)BH * L * D;
+  const int64_t K = (int64_t)l * D;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % D);
+    const int64_t r = e / D;
+    const int p = (int)(r % L);
+    const int64_t bh = r / L;
+    int ilo = p - l + 1 <= 0 ? 0 : (p - l + 1 + d - 1) / d;
+    int ihi = p / d;
+    ihi = ihi < n - 1 ? ihi : n - 1;
+    float s = 0.0f;
+    for (int i = ilo; i <= ihi; ++i) s += to_f32(dspan[(bh * n + i) * K + (int64_t)(p - i * d) * D + c]);
+    dx[e] = from_f32<TO>(s);
+  }
+}
+
+}  // namespace nsa
+
+using namespace nsa;
+
+extern "C" {
+
+int nsa_phi_fwd(const void* x, const void* w1, const float* c1, const void* w2, const float* b2, void* out,
+                float* pre, int BH, int L, int D, int H, int l, int d, int dtype, void* stream) {
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(BH > 0 && L >= 0 && l >= 1 && d >= 1, NSA_ERR_SHAPE);
+  NSA_CHECK(D == 64 || D == 128, NSA_ERR_SHAPE);
+  NSA_CHECK(H == 32 || H == 64 || H == 128, NSA_ERR_SHAPE);
+  const int n = L >= l ? (L - l) / d + 1 : 0;
+  if (n == 0) return NSA_OK;
+  NSA_CHECK(x && w1 && c1 && w2 && b2 && out && pre, NSA_ERR_ARG);
+  const int ntile = (n + 31) / 32;
+  const int64_t waves = (int64_t)BH * ntile, grid = (waves + 3) / 4;
+  NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  hipStream_t s = (hipStream_t)stream;
+#define NSA_PHI_FWD(TT, DD, HH)                                                                                \
+  if (D == DD && H == HH)                                                                                      \
+    k_phi_fwd<TT, DD, HH><<<(unsigned)grid, 256, 0, s>>>((const TT*)x, (const TT*)w1, c1, (const TT*)w2, b2, \
+                                                         (TT*)out, pre, BH, L, n, l, d, ntile);
+#define NSA_PHI_FWD_T(TT) \
+  NSA_PHI_FWD(TT, 64, 32) NSA_PHI_FWD(TT, 64, 64) NSA_PHI_FWD(TT, 64, 128) \
+  NSA_PHI_FWD(TT, 128, 32) NSA_PHI_FWD(TT, 128, 64) NSA_PHI_FWD(TT, 128, 128)
+  if (dtype == NSA_BF16) {
+    NSA_PHI_FWD_T(bf16)
+  } else {
+    NSA_PHI_FWD_T(float)
+  }
+#undef NSA_PHI_FWD_T
+#undef NSA_PHI_FWD
+  return nsa_launch_status();
+}
+
+int nsa_phi_dpre(const void* dout, const void* w2t, const float* pre, float* dpre, int BH, int n, int D, int H,
+                 int dtype, void* stream) {
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(BH > 0 && n >= 0, NSA_ERR_SHAPE);
+  NSA_CHECK(D == 64 || D == 128, NSA_ERR_SHAPE);
+  NSA_CHECK(H == 32 || H == 64 || H == 128, NSA_ERR_SHAPE);
+  if (n == 0) return NSA_OK;
+  NSA_CHECK(dout && w2t && pre && dpre, NSA_ERR_ARG);
+  const int ntile = (n + 31) / 32;
+  const int64_t waves = (int64_t)BH * ntile, grid = (waves + 3) / 4;
+  NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  hipStream_t s = (hipStream_t)stream;
+#define NSA_PHI_DPRE(TT, DD, HH)                                                                                   \
+  if (D == DD && H == HH)                                                                                          \
+    k_phi_dpre<TT, DD, HH><<<(unsigned)grid, 256, 0, s>>>((const TT*)dout, (const TT*)w2t, pre, dpre, BH, n, ntile);
+#define NSA_PHI_DPRE_T(TT) \
+  NSA_PHI_DPRE(TT, 64, 32) NSA_PHI_DPRE(TT, 64, 64) NSA_PHI_DPRE(TT, 64, 128) \
+  NSA_PHI_DPRE(TT, 128, 32) NSA_PHI_DPRE(TT, 128, 64) NSA_PHI_DPRE(TT, 128, 128)
+  if (dtype == NSA_BF16) {
+    NSA_PHI_DPRE_T(bf16)
+  } else {
+    NSA_PHI_DPRE_T(float)
+  }
+#undef NSA_PHI_DPRE_T
+#undef NSA_PHI_DPRE
+  return nsa_launch_status();
+}
+
+int nsa_phi_fold(const void* dspan, int dspan_dtype, void* dx, int BH, int L, int D, int l, int d, int dx_dtype,
+                 void* stream) {
+  NSA_CHECK(dx_dtype == NSA_F32 || dx_dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(dspan_dtype == NSA_F32 || dspan_dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(BH > 0 && L >= 0 && D > 0 && l >= 1 && d >= 1, NSA_ERR_SHAPE);
+  const int n = L >= l ? (L - l) / d + 1 : 0;
+  NSA_CHECK(dx != nullptr && (n == 0 || dspan != nullptr), NSA_ERR_ARG);
+  const int64_t total = (int64_t)BH * L * D;
+  if (total == 0) return NSA_OK;
+  int64_t grid = (total + 255) / 256;
+  grid = grid < 65536 ? grid : 65536;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&](auto ti, auto to) {
+    using TI = decltype(ti);
+    using TO = decltype(to);
+    k_phi_fold<TI, TO><<<(unsigned)grid, 256, 0, s>>>((const TI*)dspan, (TO*)dx, BH, L, D, n, l, d);
+  };
+  if (dspan_dtype == NSA_BF16) {
+    if (dx_dtype == NSA_BF16) go(bf16{}, bf16{}); else go(bf16{}, float{});
+  } else {
+    if (dx_dtype == NSA_BF16) go(float{}, bf16{}); else go(float{}, float{});
+  }
+  return nsa_launch_status();
+}
+
+}  // extern "C"

@@ -841,6 +841,80 @@ def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, blo
 
 
 # ---------------------------------------------------------------------------
+# compression phi (NSA paper eq. 7): an MLP over each span of l tokens
+# ---------------------------------------------------------------------------
+
+class PhiCompressHIP(torch.autograd.Function):
+    """``out[b,h,i] = W2 silu(W1 vec(x[b,h,i d : i d + l] + P) + b1) + b2``
+    for ``x [B,H,T,D]``: the forward and the hidden-layer backward on HIP
+    kernels that read the overlapping spans in place; the weight gradients are
+    plain float32 GEMMs.  Parameters may be float32 (autocast): the kernels
+    take W1 / W2 in x's dtype, biases in float32."""
+
+    @staticmethod
+    def forward(ctx, x, pos, w1, b1, w2, b2, l, d):
+        x = _contig(x)
+        B, Hh, T, D = x.shape
+        Hd = w1.shape[0]
+        assert w1.shape == (Hd, l * D) and w2.shape == (D, Hd) and pos.shape == (l, D), "phi: parameter shapes"
+        assert b1.shape == (Hd,) and b2.shape == (D,)
+        n = n_cmp_tokens(T, l, d)
+        dt = x.dtype
+        with torch.autocast("cuda", enabled=False):
+            c1 = (b1.float() + w1.float() @ pos.float().reshape(-1)).contiguous()
+        w1c, w2c = _contig(w1.to(dt)), _contig(w2.to(dt))
+        out = torch.empty(B, Hh, n, D, device=x.device, dtype=dt)
+        pre = torch.empty(B * Hh * n, Hd, device=x.device, dtype=torch.float32)
+        if n > 0:
+            _call("nsa_phi_fwd", _lib().nsa_phi_fwd, L.ptr(x), L.ptr(w1c), L.ptr(c1), L.ptr(w2c),
+                  L.ptr(b2.float().contiguous()), L.ptr(out), L.ptr(pre), B * Hh, T, D, Hd, l, d, L.dtype_code(x),
+                  _stream(x))
+        ctx.save_for_backward(x, pos, w1, b1, w2, b2, pre)
+        ctx.geom = (l, d)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, pos, w1, b1, w2, b2, pre = ctx.saved_tensors
+        l, d = ctx.geom
+        B, Hh, T, D = x.shape
+        Hd = w1.shape[0]
+        n = n_cmp_tokens(T, l, d)
+        BH, M = B * Hh, B * Hh * n
+        dx = torch.zeros_like(x)
+        if n == 0:
+            return (dx, torch.zeros_like(pos), torch.zeros_like(w1), torch.zeros_like(b1), torch.zeros_like(w2),
+                    torch.zeros_like(b2), None, None)
+        dout = _contig(dout.to(x.dtype))
+        w2t = _contig(w2.to(x.dtype).t())
+        dpre = torch.empty(M, Hd, device=x.device, dtype=torch.float32)
+        _call("nsa_phi_dpre", _lib().nsa_phi_dpre, L.ptr(dout), L.ptr(w2t), L.ptr(pre), L.ptr(dpre), BH, n, D, Hd,
+              L.dtype_code(x), _stream(x))
+        # weight gradients in float32 (a bf16 result would round each entry of
+        # a sum over every span); the span gradient, which the fold adds at
+        # most ceil(l / d) at a time in float, runs in x's dtype
+        with torch.autocast("cuda", enabled=False):
+            d2 = dout.reshape(M, D).float()
+            dw2 = d2.t() @ torch.nn.functional.silu(pre)
+            db2 = d2.sum(0)
+            spans = x.as_strided((BH, n, l * D), (T * D, d * D, 1)).reshape(M, l * D).float()
+            db1 = dpre.sum(0)
+            dw1 = dpre.t() @ spans + db1[:, None] * pos.float().reshape(1, -1)
+            del spans
+            dspan = dpre.to(x.dtype) @ w1.to(x.dtype)
+            dpos = (db1 @ w1.float()).view(l, D)   # sum over the spans of dspan, in float
+        _call("nsa_phi_fold", _lib().nsa_phi_fold, L.ptr(dspan), L.dtype_code(dspan), L.ptr(dx), BH, T, D, l, d,
+              L.dtype_code(x), _stream(x))
+        return (dx, dpos.to(pos.dtype), dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype),
+                None, None)
+
+
+def phi_compress(x, pos, w1, b1, w2, b2, l, d):
+    """Pooled tokens ``[B,H,n,D]`` of ``x [B,H,T,D]`` through phi (span l, stride d)."""
+    return PhiCompressHIP.apply(x, pos, w1, b1, w2, b2, l, d)
+
+
+# ---------------------------------------------------------------------------
 # decode: one new query per sequence against its KV caches (no reference
 # counterpart; row t = lens[b] - 1 of NSAAttention.forward, nsa_model.py:196-304)
 # ---------------------------------------------------------------------------

@@ -36,6 +36,10 @@ Keyword-only extensions, off by default (none is in the reference):
   ``sel_block`` (selection block size; block importance collects the pooled
   tokens by span overlap, the NSA paper's eq. 9), ``force_init`` /
   ``n_local`` (block 0 and the ``n_local`` most recent blocks always chosen).
+* ``compressor='mlp'``: the NSA paper's compression phi (``MLPCompressor``,
+  a learnable MLP over each span with an intra-block position encoding) in
+  place of the reference's weighted mean + linear; the fused path runs it on
+  the HIP kernels.
 * model variants for a Llama-style decoder: ``norm='rms'`` (RMSNorm),
   ``ffn='swiglu'`` with ``ffn_hidden``, ``pos='rope'`` (rotary position on
   queries and keys of every branch, keys rotated before pooling),
@@ -49,7 +53,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
-__all__ = ["masked_softmax", "expand_kv", "BlockCompressor", "NSAAttention", "FullAttention", "make_attention",
+__all__ = ["masked_softmax", "expand_kv", "BlockCompressor", "MLPCompressor", "NSAAttention", "FullAttention", "make_attention",
            "Block", "NSATransformer", "branch_of", "param_groups", "REQUIRED_BRANCHES", "Rotary", "SwiGLU"]
 
 
@@ -89,6 +93,37 @@ class BlockCompressor(nn.Module):
         w = torch.softmax(self.pool_logits, dim=0)
         pooled = ((x_blocks + self.intra_pos) * w[:, None]).sum(dim=-2)
         return self.proj(pooled)
+
+
+class MLPCompressor(nn.Module):
+    """The NSA paper's compression phi (arXiv:2502.11089, eq. 7): a learnable
+    MLP with an intra-block position encoding maps a span of ``block_size``
+    tokens to one token, ``fc2(silu(fc1(vec(x_span + intra_pos))))``.  It is
+    the paper-faithful alternative to ``BlockCompressor`` (the reference's
+    weighted mean + linear, nsa_model.py:100-123); ``hidden`` defaults to the
+    head dim.  ``pool_sequence`` computes the same pooled tokens on the MI355X
+    kernels straight from ``[B,Hkv,T,D]`` (the overlapping spans are read in
+    place)."""
+
+    def __init__(self, block_size, d_head, hidden=None):
+        super().__init__()
+        self.block_size = block_size
+        self.hidden = d_head if hidden is None else hidden
+        self.intra_pos = nn.Parameter(torch.zeros(block_size, d_head))
+        self.fc1 = nn.Linear(block_size * d_head, self.hidden)
+        self.fc2 = nn.Linear(self.hidden, d_head)
+
+    def forward(self, x_blocks):
+        """``x_blocks [B,Hkv,n_blk,block_size,D] -> [B,Hkv,n_blk,D]``."""
+        z = (x_blocks + self.intra_pos).flatten(-2)
+        return self.fc2(F.silu(self.fc1(z)))
+
+    def pool_sequence(self, x, stride):
+        """``x [B,Hkv,T,D] -> [B,Hkv,n,D]``, spans ``[i stride, i stride +
+        block_size)``, on the HIP kernels."""
+        import nsa_hip_ops as ops
+        return ops.phi_compress(x, self.intra_pos, self.fc1.weight, self.fc1.bias, self.fc2.weight, self.fc2.bias,
+                                self.block_size, stride)
 
 
 class Rotary(nn.Module):
@@ -147,10 +182,12 @@ class NSAAttention(nn.Module):
     three branches, output projection (nsa_model.py:130-195)."""
 
     def __init__(self, d_model, n_q_heads, n_kv_heads, block_size=16, n_selected_blocks=4, window=32,
-                 attn_impl="ref", *, cmp_stride=None, sel_block=None, force_init=False, n_local=0, rope=None):
+                 attn_impl="ref", *, cmp_stride=None, sel_block=None, force_init=False, n_local=0, rope=None,
+                 compressor="mean", cmp_hidden=None):
         super().__init__()
         assert n_q_heads % n_kv_heads == 0, "GQA needs n_q_heads divisible by n_kv_heads"
         assert attn_impl in ("ref", "fused"), "attn_impl must be 'ref' or 'fused'"
+        assert compressor in ("mean", "mlp"), "compressor must be 'mean' (BlockCompressor) or 'mlp' (phi)"
         self.d_model = d_model
         self.Hq = n_q_heads
         self.Hkv = n_kv_heads
@@ -175,8 +212,13 @@ class NSAAttention(nn.Module):
         self.v_slc = nn.Linear(d_model, kv_dim, bias=False)
         self.k_win = nn.Linear(d_model, kv_dim, bias=False)
         self.v_win = nn.Linear(d_model, kv_dim, bias=False)
-        self.comp_k = BlockCompressor(block_size, self.dh)
-        self.comp_v = BlockCompressor(block_size, self.dh)
+        self.compressor = compressor
+        if compressor == "mlp":
+            self.comp_k = MLPCompressor(block_size, self.dh, cmp_hidden)
+            self.comp_v = MLPCompressor(block_size, self.dh, cmp_hidden)
+        else:
+            self.comp_k = BlockCompressor(block_size, self.dh)
+            self.comp_v = BlockCompressor(block_size, self.dh)
         self.gate = nn.Linear(d_model, self.Hq * 3, bias=True)
         self.out_proj = nn.Linear(self.Hq * self.dh, d_model, bias=False)
 
@@ -198,6 +240,10 @@ class NSAAttention(nn.Module):
     def _pooled(self, kc, vc, n_cmp):
         """Learned pooled tokens of the spans ``[i d, i d + l)``, ``i < n_cmp``."""
         l, d = self.block_size, self.cmp_stride
+        if self.compressor == "mlp" and self.attn_impl == "fused":
+            T = (n_cmp - 1) * d + l
+            return (self.comp_k.pool_sequence(kc[:, :, :T], d).to(kc.dtype),
+                    self.comp_v.pool_sequence(vc[:, :, :T], d).to(vc.dtype))
         if d == l:
             B = kc.shape[0]
             kb = kc[:, :, :n_cmp * l].reshape(B, self.Hkv, n_cmp, l, self.dh)
@@ -383,7 +429,7 @@ def make_attention(attn_type, d_model, n_q_heads, n_kv_heads, **nsa_kw):
 
 
 _NSA_ONLY = ("block_size", "n_selected_blocks", "window", "attn_impl", "cmp_stride", "sel_block", "force_init",
-             "n_local")
+             "n_local", "compressor", "cmp_hidden")
 
 
 class Block(nn.Module):
@@ -429,7 +475,8 @@ class NSATransformer(nn.Module):
     def __init__(self, vocab_size, d_model=512, n_layers=8, n_q_heads=8, n_kv_heads=2, max_seq_len=256,
                  ffn_mult=4, block_size=16, n_selected_blocks=4, window=32, attn_type="nsa", attn_impl="ref", *,
                  norm="layer", ffn="gelu", ffn_hidden=None, pos="learned", rope_base=10000.0, tie_embeddings=True,
-                 dense_impl="ref", cmp_stride=None, sel_block=None, force_init=False, n_local=0):
+                 dense_impl="ref", cmp_stride=None, sel_block=None, force_init=False, n_local=0, compressor="mean",
+                 cmp_hidden=None):
         super().__init__()
         assert pos in ("learned", "rope"), "pos must be 'learned' or 'rope'"
         self.max_seq_len = max_seq_len
@@ -442,7 +489,7 @@ class NSATransformer(nn.Module):
             self.pos_emb = nn.Embedding(max_seq_len, d_model)
         kw = dict(attn_impl=attn_impl, block_size=block_size, n_selected_blocks=n_selected_blocks, window=window,
                   cmp_stride=cmp_stride, sel_block=sel_block, force_init=force_init, n_local=n_local, rope=rope,
-                  dense_impl=dense_impl)
+                  dense_impl=dense_impl, compressor=compressor, cmp_hidden=cmp_hidden)
         self.blocks = nn.ModuleList([Block(d_model, n_q_heads, n_kv_heads, ffn_mult=ffn_mult, attn_type=attn_type,
                                            norm=norm, ffn=ffn, ffn_hidden=ffn_hidden, **kw)
                                      for _ in range(n_layers)])

@@ -34,6 +34,8 @@ Layout ``q [B,Hq,T,D]``, ``k/v [B,Hkv,T,D]``; query head ``h`` reads KV head
   unspecified).
 * gate: ``out = sum_c sigmoid(gate[...,c]) * o_c`` (nsa_model.py:293-301,
   nsa_fused_kernel.py:572-573).
+* compression phi (``phi_compress``): the paper's MLP over each span with
+  an intra-block position encoding (a widening of the reference's pooler).
 * decode (``decode_reference``): row ``t = len-1`` of the above from caches,
   candidate blocks ``0 .. t // ls``; pinned against the whole-sequence
   functions in tests/test_oracle_pins.py.
@@ -110,6 +112,21 @@ def pool_mean(x: torch.Tensor, l: int, d: int) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # masks
 # ---------------------------------------------------------------------------
+
+def phi_compress(x, pos, w1, b1, w2, b2, l: int, d: int, act: str = "silu") -> torch.Tensor:
+    """The NSA paper's compression phi (arXiv:2502.11089, eq. 7), the
+    alternative to the reference's weighted mean + linear
+    (nsa_model.py:100-123): pooled token i of ``x [B,H,T,D]`` is
+    ``w2 act(w1 vec(x[i*d : i*d+l] + pos) + b1) + b2`` (``vec`` flattens the
+    span row-major, position-major), ``act`` SiLU or the identity."""
+    B, H, T, D = x.shape
+    n = n_cmp_tokens(T, l, d)
+    spans = x[:, :, :(n - 1) * d + l].unfold(2, l, d).transpose(-1, -2) if n > 0 else x.new_zeros(B, H, 0, l, D)
+    z = (spans + pos).reshape(B, H, n, l * D)
+    a = z @ w1.transpose(0, 1) + b1
+    hdn = a * torch.sigmoid(a) if act == "silu" else a
+    return hdn @ w2.transpose(0, 1) + b2
+
 
 def window_keep(T: int, w: int) -> torch.Tensor:
     """``[T,T]`` band mask ``p <= t and t - p < w`` (nsa_model.py:287-289)."""

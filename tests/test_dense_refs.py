@@ -61,3 +61,30 @@ def test_selection_reference_edge_rows():
     idx2[0, 1, 70, 1] = idx2[0, 1, 70, 0]
     o2, _ = O.selection_attention(q.double(), k.double(), v.double(), idx2, bs)
     torch.testing.assert_close(nsk.selection_forward_reference(q, k, v, idx2, bs).double(), o2, rtol=1e-5, atol=1e-5)
+
+
+def test_mlp_compressor_matches_oracle():
+    """nsa_model.MLPCompressor on unfolded spans is the oracle's phi (the
+    torch definition the fused path's HIP phi is checked against)."""
+    import nsa_model
+    torch.manual_seed(0)
+    l, d, D = 8, 4, 16
+    m = nsa_model.MLPCompressor(l, D, hidden=12).double()
+    torch.nn.init.normal_(m.intra_pos, std=0.3)
+    x = torch.randn(2, 3, 45, D, dtype=torch.float64)
+    n = (45 - l) // d + 1
+    spans = x[:, :, :(n - 1) * d + l].unfold(2, l, d).transpose(-1, -2)
+    got = m(spans)
+    ref = O.phi_compress(x, m.intra_pos, m.fc1.weight, m.fc1.bias, m.fc2.weight, m.fc2.bias, l, d)
+    torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_nsa_attention_mlp_compressor_ref_runs_on_cpu():
+    import nsa_model
+    torch.manual_seed(0)
+    m = nsa_model.NSAAttention(64, 4, 2, block_size=16, n_selected_blocks=2, window=16, cmp_stride=8,
+                               sel_block=32, compressor="mlp")
+    x = torch.randn(2, 96, 64, requires_grad=True)
+    m(x).sum().backward()
+    assert m.comp_k.fc1.weight.grad is not None and torch.isfinite(m.comp_k.fc1.weight.grad).all()
+    assert nsa_model.branch_of("blocks.0.attn.comp_k.fc1.weight") == "compression"

@@ -461,6 +461,51 @@ def test_decode_empty_cache_is_zero():
     assert (o == 0).all() and (idx == -1).all() and parts == [None]
 
 
+# ------------------------------------------------------------- compression phi
+
+def _phi_params(l, D, Hd, seed):
+    return (0.3 * _rand(l, D, seed=seed), 0.05 * _rand(Hd, l * D, seed=seed + 1), 0.1 * _rand(Hd, seed=seed + 2),
+            0.2 * _rand(D, Hd, seed=seed + 3), 0.1 * _rand(D, seed=seed + 4))
+
+
+def test_phi_identity_mean_is_pool_mean():
+    """With the identity activation, W1 averaging each channel over the span,
+    W2 = I and no position code or bias, phi is the mean pool."""
+    l, d, D = 8, 4, 6
+    x = _rand(2, 3, 41, D, seed=120)
+    w1 = torch.zeros(D, l * D)
+    for p in range(l):
+        w1[:, p * D:(p + 1) * D] = torch.eye(D) / l
+    out = O.phi_compress(x, torch.zeros(l, D), w1, torch.zeros(D), torch.eye(D), torch.zeros(D), l, d,
+                         act="identity")
+    torch.testing.assert_close(out, O.pool_mean(x, l, d), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("l,d", [(8, 4), (4, 4), (6, 3), (5, 7)])
+def test_phi_matches_brute_force(l, d):
+    D, Hd, T = 3, 5, 29
+    x = _rand(1, 2, T, D, seed=130)
+    pos, w1, b1, w2, b2 = _phi_params(l, D, Hd, 131)
+    out = O.phi_compress(x, pos, w1, b1, w2, b2, l, d)
+    n = (T - l) // d + 1
+    assert out.shape == (1, 2, n, D)
+    for h in range(2):
+        for i in range(n):
+            pre = [float(b1[u]) + sum(float(w1[u, p * D + c]) * (float(x[0, h, i * d + p, c]) + float(pos[p, c]))
+                                      for p in range(l) for c in range(D)) for u in range(Hd)]
+            hid = [z / (1.0 + math.exp(-z)) for z in pre]
+            for c in range(D):
+                ref = float(b2[c]) + sum(float(w2[c, u]) * hid[u] for u in range(Hd))
+                assert abs(float(out[0, h, i, c]) - ref) < 1e-12
+
+
+def test_phi_gradcheck():
+    l, d, D, Hd = 4, 2, 3, 4
+    x = _rand(1, 1, 11, D, seed=140).requires_grad_()
+    ps = [t.requires_grad_() for t in _phi_params(l, D, Hd, 141)]
+    assert torch.autograd.gradcheck(lambda *a: O.phi_compress(*a, l, d), (x, *ps))
+
+
 def test_keys_per_row_matches_masks():
     cfg = O.NSAConfig(cmp_block=8, cmp_stride=4, sel_block=16, n_sel=3, window=10)
     T = 96
@@ -519,6 +564,12 @@ def test_pins_catch_planted_mistakes():
     imp = O.importance_gathered(qq[:, :, t:t + 1], kcmp, cfg, [t], t + 1)
     bad = O.topn_from_scores(O.selection_scores(imp, cfg, t_pos=[t]), min(2, imp.shape[-1]))
     assert not torch.equal(bad[0, :, 0], parts["block_idx"][0, :, t])
+    # phi with the spans one token late (x[i*d+1 : i*d+l+1]) fails the brute force
+    xs = _rand(1, 1, 20, 3, seed=150)
+    pos, w1, b1, w2, b2 = _phi_params(4, 3, 5, 151)
+    good_phi = O.phi_compress(xs, pos, w1, b1, w2, b2, 4, 2)
+    bad_phi = O.phi_compress(xs[:, :, 1:], pos, w1, b1, w2, b2, 4, 2)[:, :, :good_phi.shape[2] - 1]
+    assert not torch.allclose(good_phi[:, :, :bad_phi.shape[2]], bad_phi)
     # top-n tie broken toward the higher index
     sc = torch.tensor([[[[2.0, 2.0, 1.0]]]])
     assert O.topn_from_scores(sc, 1).item() == 0
