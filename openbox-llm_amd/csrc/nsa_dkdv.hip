@@ -19,6 +19,8 @@
 //   * window      : a workgroup owns 32*NW keys and walks queries [k0, k0 + 32 NW + w - 2].
 //   * compression : same, over query chunks of kCmpChunk; chunks merge with
 //                   float atomics; the key blocks of one chunk share an XCD.
+//   For 16-bit operands both run the role-split walk (kv_walk's work on two
+//   waves per 32 keys, two waves per SIMD; below).
 //   * selection   : work items (block, chunk of its CSR query list) built by
 //                   k_sel_items; a persistent grid drains them; chunks merge with atomics.
 #include <mutex>
@@ -368,6 +370,257 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
   }
 }
 
+// ---------------------------------------------------------------------------
+// Role-split walk: two waves share a group of 32 keys.  The P-wave keeps the
+// keys' K fragments and dV^T: S = Q K^T, P = exp2(S*scale*log2(e) - c), dV^T
+// += dO^T P, and P (float) goes to LDS.  The dS-wave keeps V and dK^T: dP =
+// dO V^T before the tile's barrier, then, with the P-wave's P of the same
+// tile, dS = P (dP - delta) and dK^T += Q^T dS after it.  Each wave carries
+// about half of a single walker's registers, so two waves run per SIMD
+// (two workgroups per CU) and one's MFMAs cover the other's dependency
+// waits.  Everything a wave reads from a query stage is read before the
+// barrier of that tile, so the stage is refilled after it as in kv_walk.
+// ---------------------------------------------------------------------------
+constexpr int kSplitStages = 3;   // query tiles in flight + 1 (two workgroups per CU)
+
+// P of one tile for the dS-wave: [4][64 lanes][4] floats (register 4 q + j
+// of lane L at (q 64 + L) 4 + j): one 16-byte store / load per quarter, the
+// lanes' pieces consecutive
+typedef f32x4 PTile[4 * 64];
+
+template <typename T, int D> struct PWave {
+  using C = Tile32<T, D>;
+  Frag<T> kf[C::KS];
+  f32x16 dv[C::DT];
+  __device__ __forceinline__ void init(const T* kb, int key_safe, int h) {
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) kf[s].load(kb + (int64_t)key_safe * D + 16 * s + 8 * h);
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) dv[dt] = zero16();
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(kf[s]);
+  }
+  template <bool MASK>
+  __device__ __forceinline__ void tile(const KvStage<T, D>& s, const Frag<T> (&qa)[C::KS], bool visA, bool visB,
+                                       float sl2, int lane, f32x4* pb) {
+    const int h = lane >> 5;
+    Frag<T> ta[C::DT][2];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) lds_tr_frag<T, D>(ta[dt][k], s.dr, dt, lane, k);
+    f32x16 sacc = zero16();
+#pragma unroll
+    for (int k = 0; k < C::KS; ++k) mma32(sacc, qa[k], kf[k]);
+    if constexpr (sizeof(T) == 2) {
+      constexpr int NTR = 2 * C::DT * 2;
+      constexpr int PER = (NTR + C::KS - 1) / C::KS;
+#pragma unroll
+      for (int i = 0; i < C::KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+      }
+    }
+    float P[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(sacc[r] * sl2 - s.c[acc_elem(h, r)]);
+      if (MASK) p = (r < 8 ? visA : visB) ? p : 0.0f;
+      P[r] = p;
+    }
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) pb[64 * q4 + lane] = (f32x4){P[4 * q4], P[4 * q4 + 1], P[4 * q4 + 2], P[4 * q4 + 3]};
+    Frag<T> pf[2];
+    pf[0].set(P);
+    pf[1].set(P + 8);
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) mma32(dv[dt], ta[dt][k], pf[k]);
+  }
+};
+
+template <typename T, int D> struct SWave {
+  using C = Tile32<T, D>;
+  Frag<T> vf[C::KS];
+  f32x16 dk[C::DT];
+  __device__ __forceinline__ void init(const T* vb, int key_safe, int h) {
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) vf[s].load(vb + (int64_t)key_safe * D + 16 * s + 8 * h);
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) dk[dt] = zero16();
+#pragma unroll
+    for (int s = 0; s < C::KS; ++s) settle(vf[s]);
+  }
+  // before the barrier: dP, and the tile's Q^T fragments and deltas
+  __device__ __forceinline__ void front(const KvStage<T, D>& s, const Frag<T> (&da)[C::KS], int lane, f32x16& pacc,
+                                        Frag<T> (&tb)[C::DT][2], float (&dlt)[16]) {
+    const int h = lane >> 5;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) lds_tr_frag<T, D>(tb[dt][k], s.qr, dt, lane, k);
+    pacc = zero16();
+#pragma unroll
+    for (int k = 0; k < C::KS; ++k) mma32(pacc, da[k], vf[k]);
+    if constexpr (sizeof(T) == 2) {
+      constexpr int NTR = 2 * C::DT * 2;
+      constexpr int PER = (NTR + C::KS - 1) / C::KS;
+#pragma unroll
+      for (int i = 0; i < C::KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, PER, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dlt[r] = s.dot[acc_elem(h, r)];
+  }
+  // after: dS from the P-wave's P; dK^T += Q^T dS (with SPLIT also its
+  // rounding remainder); sf receives dS as operand fragments
+  template <bool SPLIT>
+  __device__ __forceinline__ void back(const f32x4* pb, const f32x16& pacc, const Frag<T> (&tb)[C::DT][2],
+                                       const float (&dlt)[16], int lane, Frag<T> (&sf)[2]) {
+    float dS[16];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x4 p = pb[64 * q4 + lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) dS[4 * q4 + j] = p[j] * (pacc[4 * q4 + j] - dlt[4 * q4 + j]);
+    }
+    sf[0].set(dS);
+    sf[1].set(dS + 8);
+    Frag<T> sl[2];
+    if constexpr (SPLIT && sizeof(T) == 2) {
+      float lo[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lo[r] = dS[r] - to_f32(from_f32<T>(dS[r]));
+      sl[0].set(lo);
+      sl[1].set(lo + 8);
+    }
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        mma32(dk[dt], tb[dt][k], sf[k]);
+        if constexpr (SPLIT && sizeof(T) == 2) mma32(dk[dt], tb[dt][k], sl[k]);
+      }
+  }
+};
+
+// The query-tile requests of a split walk: every wave of the workgroup issues
+// its share of each tile (NTH threads), at the same iterations.
+template <typename T, int D, int NTH, typename QSrc> struct SplitReq {
+  KvIssuer<T, D, NTH> iss;
+  int iti, ihc;
+  const int ntile, b, hkv, tid;
+  const QSide<T>& x;
+  QSrc& qsrc;
+  __device__ __forceinline__ SplitReq(const QSide<T>& x_, int b_, int hkv_, int ntile_, QSrc& q, int tid_)
+      : iti(0), ihc(0), ntile(ntile_), b(b_), hkv(hkv_), tid(tid_), x(x_), qsrc(q) {
+    iss.prepare(x, b, hkv, 0, tid);
+  }
+  __device__ __forceinline__ void request(KvStage<T, D>& s) {
+    int tA, tB, sA, sB;
+    qsrc(iti, tA, tB, sA, sB);
+    iss.issue(s, x, tA, tB, sA, sB, tid);
+    if (++iti == ntile) {
+      iti = 0;
+      if (++ihc < x.NHC) iss.prepare(x, b, hkv, ihc, tid);
+    }
+  }
+};
+
+// One walk per role (the roles' registers are then never live at once).
+// Per tile: [role work before the barrier]; wait for tile it+1; barrier;
+// [role work after it]; refill the stage of tile it.  P goes through
+// pbuf[it & 1].
+template <typename T, int D, int NTH, typename QSrc, typename Vis>
+__device__ __forceinline__ void walk_p(PWave<T, D>& pw, KvStage<T, D> (&stg)[kSplitStages], PTile* pbuf,
+                                       const QSide<T>& x, int b, int hkv, int ntile, QSrc qsrc, Vis vis, float sl2,
+                                       int tid) {
+  using C = Tile32<T, D>;
+  constexpr int NST = kSplitStages;
+  constexpr int LT = kv_tile_loads<T, D, NTH>();
+  static_assert((NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
+  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
+  if (total == 0) return;
+  const int lane = tid & 63, h = lane >> 5, n = lane & 31;
+  SplitReq<T, D, NTH, QSrc> rq(x, b, hkv, ntile, qsrc, tid);
+#pragma unroll
+  for (int p = 0; p < NST; ++p)
+    if (p < total) rq.request(stg[p]);
+  if (total >= NST)
+    vm_wait<(NST - 1) * LT>();
+  else
+    vm_wait<0>();
+  __syncthreads();
+  Frag<T> qa[C::KS];
+#pragma unroll
+  for (int k = 0; k < C::KS; ++k) lds_row_frag<T, D>(qa[k], stg[0].qr, n, h, k);
+  for (int it = 0; it < total; ++it) {
+    const KvStage<T, D>& s = stg[it % NST];
+    const int tA = __builtin_amdgcn_readfirstlane(s.meta[0]), tB = __builtin_amdgcn_readfirstlane(s.meta[1]);
+    bool mask, visA, visB;
+    vis(tA, tB, mask, visA, visB);
+    if (mask)
+      pw.template tile<true>(s, qa, visA, visB, sl2, lane, pbuf[it & 1]);
+    else
+      pw.template tile<false>(s, qa, true, true, sl2, lane, pbuf[it & 1]);
+    if (it + NST - 1 < total)
+      vm_wait<(NST - 2) * LT>();
+    else
+      vm_wait<0>();
+    __syncthreads();
+    if (it + 1 < total) {
+#pragma unroll
+      for (int k = 0; k < C::KS; ++k) lds_row_frag<T, D>(qa[k], stg[(it + 1) % NST].qr, n, h, k);
+    }
+    if (it + NST < total) rq.request(stg[it % NST]);
+  }
+}
+
+template <typename T, int D, int NTH, bool SPLIT, typename QSrc>
+__device__ __forceinline__ void walk_s(SWave<T, D>& sw, KvStage<T, D> (&stg)[kSplitStages], const PTile* pbuf,
+                                       const QSide<T>& x, int b, int hkv, int ntile, QSrc qsrc, int tid) {
+  using C = Tile32<T, D>;
+  constexpr int NST = kSplitStages;
+  constexpr int LT = kv_tile_loads<T, D, NTH>();
+  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
+  if (total == 0) return;
+  const int lane = tid & 63, h = lane >> 5, n = lane & 31;
+  SplitReq<T, D, NTH, QSrc> rq(x, b, hkv, ntile, qsrc, tid);
+#pragma unroll
+  for (int p = 0; p < NST; ++p)
+    if (p < total) rq.request(stg[p]);
+  if (total >= NST)
+    vm_wait<(NST - 1) * LT>();
+  else
+    vm_wait<0>();
+  __syncthreads();
+  Frag<T> da[C::KS];
+#pragma unroll
+  for (int k = 0; k < C::KS; ++k) lds_row_frag<T, D>(da[k], stg[0].dr, n, h, k);
+  for (int it = 0; it < total; ++it) {
+    const KvStage<T, D>& s = stg[it % NST];
+    f32x16 pacc;
+    Frag<T> tb[C::DT][2];
+    float dlt[16];
+    sw.front(s, da, lane, pacc, tb, dlt);
+    if (it + NST - 1 < total)
+      vm_wait<(NST - 2) * LT>();
+    else
+      vm_wait<0>();
+    __syncthreads();
+    Frag<T> sf[2];
+    sw.template back<SPLIT>(pbuf[it & 1], pacc, tb, dlt, lane, sf);
+    if (it + 1 < total) {
+#pragma unroll
+      for (int k = 0; k < C::KS; ++k) lds_row_frag<T, D>(da[k], stg[(it + 1) % NST].dr, n, h, k);
+    }
+    if (it + NST < total) rq.request(stg[it % NST]);
+  }
+}
+
 template <typename T, int D>
 __device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const float* c, const float* dot, int Hq,
                                           int Hkv, int T_, bool packed) {
@@ -535,6 +788,143 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   kv_walk<false, 0, T, D, NTH, false>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
+}
+
+// accumulator columns of one key -> a float row (scaled; atomically when
+// several workgroups add into it)
+template <typename T, int D>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[Tile32<T, D>::DT], float* row, float scale,
+                                           bool atomic, int h) {
+  using C = Tile32<T, D>;
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * dt + 8 * g4 + 4 * h;
+      if (!(D % 32 == 0 || d < D)) continue;
+      if (atomic) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) atomicAdd(row + d + i, acc[dt][4 * g4 + i] * scale);
+      } else {
+        *reinterpret_cast<f32x4*>(row + d) =
+            (f32x4){acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]} * scale;
+      }
+    }
+  }
+}
+
+// k_range_dkdv32 with the role-split walk: 2 NW waves, waves < NW the
+// P-waves of key groups 0 .. NW-1, the others their dS-waves.
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(128 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
+                    const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
+                    float* __restrict__ dk, float* __restrict__ dv, int Hq, int Hkv, int T_, int Lk, int chunk,
+                    int window, int cl, int cd, int nbh, int chs, int spl, float sl2, float scale) {
+  constexpr int NTH = 128 * NW;
+  __shared__ __align__(16) KvStage<T, D> stg[kSplitStages];
+  __shared__ __align__(16) PTile pbuf[NW][2];
+  const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool pwave = wv < NW;
+  const int w = pwave ? wv : wv - NW;   // key group (wave-uniform: its masks branch)
+  // 1-D grid over the (key block, query chunk) pairs that have work, per bh,
+  // chunk-major: the workgroups of one chunk (which stream the same queries)
+  // are consecutive, and XCD x takes a contiguous, equal share of them.  The
+  // window has one chunk and uniform work per key block.
+  const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
+  int kblk, ch, bh;
+  int q0 = 0, qlen = chunk;   // compression: the workgroup's queries [q0, q0 + qlen)
+  if (mode == NSA_MODE_COMPRESS) {
+    const int nch = (T_ + chunk - 1) / chunk;
+    const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
+    const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
+    const int64_t wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
+    int r, sub = 0;
+    if (wg < (int64_t)big * nbh) {
+      bh = (int)(wg / big);
+      r = (int)(wg % big);
+      for (ch = 0; ch < chs - 1; ++ch) {   // chunk ch holds the first cmp_active_blocks(.., ch) key blocks
+        const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+        if (r < nb) break;
+        r -= nb;
+      }
+    } else {
+      const int64_t w2 = wg - (int64_t)big * nbh;
+      bh = (int)(w2 / per);
+      r = (int)(w2 % per);
+      for (ch = chs; ch < nch - 1; ++ch) {
+        const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch) * spl;
+        if (r < nb) break;
+        r -= nb;
+      }
+      const int nb = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+      sub = r / nb;
+      r %= nb;
+      qlen = (chunk + spl - 1) / spl;
+    }
+    kblk = r;
+    q0 = ch * chunk + sub * qlen;
+    if (q0 + qlen > ch * chunk + chunk) qlen = ch * chunk + chunk - q0;
+  } else {
+    kblk = (int)(blockIdx.x % nkb);
+    ch = 0;
+    bh = (int)(blockIdx.x / nkb);
+  }
+  const int b = bh / Hkv, hkv = bh % Hkv;
+  const int k0 = kblk * 32 * NW;
+  const int kw = k0 + 32 * w;
+  const int key = kw + n;
+  const bool key_ok = key < Lk;
+  const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, false);
+  // query range of the workgroup
+  int tlo, thi;
+  const int klast = k0 + 32 * NW - 1 < Lk - 1 ? k0 + 32 * NW - 1 : Lk - 1;
+  if (mode == NSA_MODE_WINDOW) {
+    tlo = k0;
+    thi = klast + window - 1;
+  } else {
+    tlo = k0 * cd + cl - 1;
+    thi = T_ - 1;
+    const int c0 = q0, c1 = q0 + qlen - 1;
+    tlo = tlo > c0 ? tlo : c0;
+    thi = thi < c1 ? thi : c1;
+  }
+  thi = thi < T_ - 1 ? thi : T_ - 1;
+  if (tlo > thi) return;   // uniform over the workgroup
+  const int64_t kvoff = (int64_t)bh * Lk * D;
+  const int ntile = (thi - tlo) / 2 + 1;
+  const int wlast = kw + 31;   // last key of the group (may pass Lk: those columns are never stored)
+  auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
+    tA = tlo + 2 * i;
+    tB = tA + 1 <= thi ? tA + 1 : -1;
+    sA = sB = 0;
+  };
+  auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
+    const int tb = tB >= 0 ? tB : tA;
+    if (mode == NSA_MODE_WINDOW) {
+      mask = !(tA >= wlast && tb - window < kw);
+      visA = key <= tA && key > tA - window;
+      visB = key <= tb && key > tb - window;
+    } else {
+      mask = !(wlast * cd + cl - 1 <= tA);
+      visA = key * cd + cl - 1 <= tA;
+      visB = key * cd + cl - 1 <= tb;
+    }
+  };
+  const int key_safe = key_ok ? key : Lk - 1;
+  const bool atomic = mode == NSA_MODE_COMPRESS;
+  if (pwave) {
+    PWave<T, D> pw;
+    pw.init(k + kvoff, key_safe, h);
+    walk_p<T, D, NTH>(pw, stg, pbuf[w], x, b, hkv, ntile, qsrc, vis, sl2, tid);
+    if (key_ok) store_rows<T, D>(pw.dv, dv + kvoff + (int64_t)key * D, 1.0f, atomic, h);
+  } else {
+    SWave<T, D> sw;
+    sw.init(v + kvoff, key_safe, h);
+    walk_s<T, D, NTH, false>(sw, stg, pbuf[w], x, b, hkv, ntile, qsrc, tid);
+    if (key_ok) store_rows<T, D>(sw.dk, dk + kvoff + (int64_t)key * D, scale, atomic, h);
+  }
 }
 
 // x: 16-byte aligned; 16-byte stores for the first n & ~3 elements, the rest one by one
@@ -773,8 +1163,11 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   if (T == 0 || Lk == 0) return NSA_OK;
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
-  // 2 waves (64 keys) per workgroup, two workgroups per CU: measured faster than
-  // 4 waves sharing each streamed query tile, for both modes
+  // 64 keys (NW = 2 groups of 32) per workgroup, two workgroups per CU: 2 waves
+  // (one per group, float) or 4 (P- and dS-wave per group, bf16).  Measured
+  // faster than 128 keys sharing each streamed query tile, for both modes and
+  // both walks; the role-split walk takes config 3's window / compression
+  // dK/dV from 2.03 / 3.89 ms to 1.86 / 3.47 ms.
   constexpr int NW = 2;
   const int nbh = B * Hkv;
   int chs = 0, spl = 1;
@@ -802,7 +1195,7 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16)
-      k_range_dkdv32<bf16, DD, NW><<<(unsigned)grid, 64 * NW, 0, s>>>(
+      k_range_dkdv_split<bf16, DD, NW><<<(unsigned)grid, 128 * NW, 0, s>>>(
           mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, dk, dv, Hq, Hkv, T,
           Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
     else
