@@ -373,7 +373,9 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
 // ---------------------------------------------------------------------------
 // Role-split walk: two waves share a group of 32 keys.  The P-wave keeps the
 // keys' K fragments and dV^T: S = Q K^T, P = exp2(S*scale*log2(e) - c), dV^T
-// += dO^T P, and P (float) goes to LDS.  The dS-wave keeps V and dK^T: dP =
+// += dO^T P, and P goes to LDS as the 16-bit operand it is for dV (rounded
+// once; half the bytes of float, which leaves room for a fourth query stage
+// at two workgroups per CU).  The dS-wave keeps V and dK^T: dP =
 // dO V^T before the tile's barrier, then, with the P-wave's P of the same
 // tile, dS = P (dP - delta) and dK^T += Q^T dS after it.  Each wave carries
 // about half of a single walker's registers, so two waves run per SIMD
@@ -381,12 +383,12 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
 // waits.  Everything a wave reads from a query stage is read before the
 // barrier of that tile, so the stage is refilled after it as in kv_walk.
 // ---------------------------------------------------------------------------
-constexpr int kSplitStages = 3;   // query tiles in flight + 1 (two workgroups per CU)
+constexpr int kSplitStages = 4;   // query tiles in flight + 1 (74 KB: two workgroups per CU)
 
-// P of one tile for the dS-wave: [4][64 lanes][4] floats (register 4 q + j
-// of lane L at (q 64 + L) 4 + j): one 16-byte store / load per quarter, the
-// lanes' pieces consecutive
-typedef f32x4 PTile[4 * 64];
+// P of one tile for the dS-wave, as the two 16-bit operand fragments of the
+// P-wave's dV product: fragment f of lane L at 16-byte slot f 64 + L (each
+// store / load one 16-byte access per lane, the lanes' pieces consecutive)
+typedef uint32_t PTile[4 * 64 * 2];
 
 template <typename T, int D> struct PWave {
   using C = Tile32<T, D>;
@@ -402,7 +404,7 @@ template <typename T, int D> struct PWave {
   }
   template <bool MASK>
   __device__ __forceinline__ void tile(const KvStage<T, D>& s, const Frag<T> (&qa)[C::KS], bool visA, bool visB,
-                                       float sl2, int lane, f32x4* pb) {
+                                       float sl2, int lane, uint32_t* pb) {
     const int h = lane >> 5;
     Frag<T> ta[C::DT][2];
 #pragma unroll
@@ -428,11 +430,15 @@ template <typename T, int D> struct PWave {
       if (MASK) p = (r < 8 ? visA : visB) ? p : 0.0f;
       P[r] = p;
     }
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) pb[64 * q4 + lane] = (f32x4){P[4 * q4], P[4 * q4 + 1], P[4 * q4 + 2], P[4 * q4 + 3]};
     Frag<T> pf[2];
     pf[0].set(P);
     pf[1].set(P + 8);
+    {
+      typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
+      const u32x4_ a = __builtin_bit_cast(u32x4_, pf[0].v), bb = __builtin_bit_cast(u32x4_, pf[1].v);
+      *reinterpret_cast<u32x4_*>(pb + 4 * lane) = a;
+      *reinterpret_cast<u32x4_*>(pb + 256 + 4 * lane) = bb;
+    }
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
@@ -478,15 +484,15 @@ template <typename T, int D> struct SWave {
   // after: dS from the P-wave's P; dK^T += Q^T dS (with SPLIT also its
   // rounding remainder); sf receives dS as operand fragments
   template <bool SPLIT>
-  __device__ __forceinline__ void back(const f32x4* pb, const f32x16& pacc, const Frag<T> (&tb)[C::DT][2],
+  __device__ __forceinline__ void back(const uint32_t* pb, const f32x16& pacc, const Frag<T> (&tb)[C::DT][2],
                                        const float (&dlt)[16], int lane, Frag<T> (&sf)[2]) {
     float dS[16];
+    typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
+    Frag<T> pf[2];
+    pf[0].v = __builtin_bit_cast(decltype(pf[0].v), *reinterpret_cast<const u32x4_*>(pb + 4 * lane));
+    pf[1].v = __builtin_bit_cast(decltype(pf[1].v), *reinterpret_cast<const u32x4_*>(pb + 256 + 4 * lane));
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const f32x4 p = pb[64 * q4 + lane];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) dS[4 * q4 + j] = p[j] * (pacc[4 * q4 + j] - dlt[4 * q4 + j]);
-    }
+    for (int r = 0; r < 16; ++r) dS[r] = to_f32(pf[r >> 3].elem(r & 7)) * (pacc[r] - dlt[r]);
     sf[0].set(dS);
     sf[1].set(dS + 8);
     Frag<T> sl[2];
@@ -1167,7 +1173,7 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   // (one per group, float) or 4 (P- and dS-wave per group, bf16).  Measured
   // faster than 128 keys sharing each streamed query tile, for both modes and
   // both walks; the role-split walk takes config 3's window / compression
-  // dK/dV from 2.03 / 3.89 ms to 1.86 / 3.47 ms.
+  // dK/dV from 2.03 / 3.89 ms to 1.72 / 3.18 ms.
   constexpr int NW = 2;
   const int nbh = B * Hkv;
   int chs = 0, spl = 1;
