@@ -79,7 +79,10 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
  * lse_c[r] * log2(e) - log2(rowscale) (rowscale 1 when nbr == 1) that the
  * dK/dV kernels take; it needs lse_c for every branch c < nbr.  dout_packed
  * (nullable) receives dO in the nsa_pack_heads layout, G heads per KV head
- * and T queries per row block (rows = B Hq T). */
+ * and T queries per row block (rows = B Hq T); the selection branch's dot,
+ * rowscale and coff (nbr == 1: the only branch, nbr == 3: branch 1) are then
+ * written in the same packed row order [B][Hkv][T][G], the layout
+ * nsa_sel_dkdv reads. */
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
@@ -132,8 +135,9 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * partial block, which the forward attends to, gets its gradient), split into
  * work items of at most `chunk` (<= 1024) queries; q_of_block holds (t << b) | s
  * when `packed`.  q and dout are in the nsa_pack_heads layout
- * [B][Hkv][T][G][D].  coff / dot are the row offsets and deltas of
- * nsa_bwd_prep ([B][Hq][T]), kt the
+ * [B][Hkv][T][G][D]; coff / dot, the row offsets and deltas of nsa_bwd_prep,
+ * in the same packed row order [B][Hkv][T][G] (nsa_bwd_prep with
+ * dout_packed writes them so), kt the
  * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
  * zero-fills and then accumulates into.  dq_part (nullable; needs packed and
  * kt): the dQ of every (query, slot, pass), scaled, in the input dtype,

@@ -48,7 +48,10 @@ template <typename T, int D> struct KvStage {
 // Read-only inputs of the query side.  Q and dO are either [B, Hq, T, D]
 // (hs = T D, ts = D) or packed per query [B, Hkv, T, G, D] (hs = D, ts = G D):
 // element (b, hkv, head g of the group, query t) is at
-// (b Hkv + hkv) G T D + g hs + t ts either way.  c and dot are [B, Hq, T].
+// (b Hkv + hkv) G T D + g hs + t ts either way.  The row statistics c and dot
+// follow the same layout without D: [B, Hq, T] (sh = T, st = 1) or packed
+// [B, Hkv, T, G] (sh = 1, st = G), so that a tile of two queries reads them
+// from two 64-byte runs instead of one cache line per row.
 template <typename T> struct QSide {
   const T* q;
   const T* dout;
@@ -56,6 +59,7 @@ template <typename T> struct QSide {
   const float* dot;
   int Hq, Hkv, G, NHC, T_;
   int64_t hs, ts;     // element strides between heads of a group / queries
+  int sh, st;         // the same for the row statistics
 };
 
 // vector-memory loads one wave issues per query tile
@@ -111,7 +115,7 @@ template <typename T, int D, int NTH> struct KvIssuer {
     sbit = r >> 4;
     const int shead = (r & 15) < grem ? (r & 15) : grem - 1;
     sreal = (r & 15) < grem;
-    const int64_t row0 = ((int64_t)b * x.Hq + hkv * x.G + hc * 16 + shead) * x.T_;
+    const int64_t row0 = ((int64_t)b * x.Hkv + hkv) * x.G * x.T_ + (int64_t)(hc * 16 + shead) * x.sh;
     sp = (lane < 32 ? x.c : x.dot) + row0;
   }
 
@@ -136,7 +140,7 @@ template <typename T, int D, int NTH> struct KvIssuer {
     {
       // lanes 0-31: c of row lane, lanes 32-63: delta of row lane - 32
       const bool real = lane >= 32 || (sreal && (!sbit || tB >= 0));
-      lds_dma4(real ? sp + (sbit ? tBq : tA) : &kAbsentRow, s.c);
+      lds_dma4(real ? sp + (int64_t)(sbit ? tBq : tA) * x.st : &kAbsentRow, s.c);
     }
     if (tid == 0) {
       s.meta[0] = tA;
@@ -642,6 +646,8 @@ __device__ __forceinline__ QSide<T> qside(const T* q, const T* dout, const float
   x.T_ = T_;
   x.hs = packed ? (int64_t)D : (int64_t)T_ * D;
   x.ts = packed ? (int64_t)x.G * D : (int64_t)D;
+  x.sh = packed ? 1 : T_;
+  x.st = packed ? x.G : 1;
   return x;
 }
 
@@ -985,7 +991,7 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
   constexpr int NSW = D >= 64 ? DTW * 2 : 0;
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, true);   // packed Q / dO
+  const QSide<T> x = qside<T, D>(q, dout, coff, dot, Hq, Hkv, T_, true);   // packed Q / dO / statistics
   const int G = x.G;
   const int ni = *n_items;
   const int npass = sel_passes(L);

@@ -270,16 +270,17 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   const int sub = lane & (gs - 1);
   const bool ok = row < rows;
   float acc[3] = {0.f, 0.f, 0.f};
+  // row (b, hkv G + g, t) -> packed row ((b Hkv + hkv) T + t) G + g
+  int64_t prow = row;
+  if (dout_packed != nullptr) {
+    const int64_t bhq = row / T_;
+    prow = ((bhq / G) * T_ + (row - bhq * T_)) * G + bhq % G;
+  }
   if (ok) {
     Vec16<T> d;
     BranchRow<T, TO> x;
     d.load(dout + row * D + sub * N);
-    if (dout_packed != nullptr) {
-      // row (b, hkv G + g, t) -> packed row ((b Hkv + hkv) T + t) G + g
-      const int64_t bhq = row / T_;
-      const int64_t prow = ((bhq / G) * T_ + (row - bhq * T_)) * G + bhq % G;
-      d.store(dout_packed + prow * D + sub * N);
-    }
+    if (dout_packed != nullptr) d.store(dout_packed + prow * D + sub * N);
     const TO* os[3] = {o0, o1, o2};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {
@@ -293,17 +294,21 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   for (int c = 0; c < 3; ++c)
     for (int m = 1; m < gs; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
   if (!ok || sub != 0) return;
+  // with dout_packed, the statistics of the selection branch (the only
+  // branch, or branch 1 of 3) go to the packed row, the layout of the
+  // selection dK/dV's query side
   if (nbr == 1) {
-    dot[row] = acc[0];
-    if (coff) coff[row] = lse0[row] * kLog2e;
+    dot[prow] = acc[0];
+    if (coff) coff[prow] = lse0[row] * kLog2e;
     return;
   }
   const float* lse[3] = {lse0, lse1, lse2};
   for (int c = 0; c < nbr; ++c) {
     const float s = sigmoidf(to_f32(gate[row * 3 + c]));
-    dot[(int64_t)c * rows + row] = acc[c];
-    rowscale[(int64_t)c * rows + row] = s;
-    if (coff) coff[(int64_t)c * rows + row] = lse[c][row] * kLog2e - __log2f(s);
+    const int64_t sr = c == 1 ? prow : row;
+    dot[(int64_t)c * rows + sr] = acc[c];
+    rowscale[(int64_t)c * rows + sr] = s;
+    if (coff) coff[(int64_t)c * rows + sr] = lse[c][row] * kLog2e - __log2f(s);
     if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
   }
 }
@@ -469,6 +474,9 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 // rows = B*Hq*T.  nbr == 1 and gate == NULL: dot[r] = dO.o0 (plain delta).
 // nbr == 3: dot[c*rows + r], rowscale[c*rows + r] = sigmoid(gate[r,c]), dgate[r,c].
 // coff (nullable): lse_c * log2(e) - log2(rowscale_c), laid out like dot.
+// dout_packed (nullable): dO in the [B][Hkv][T][G][D] layout; the statistics
+// of the selection branch (nbr == 1: the only branch, nbr == 3: branch 1) are
+// then written at the packed row ((b Hkv + hkv) T + t) G + g instead of r.
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,

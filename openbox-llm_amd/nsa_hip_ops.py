@@ -366,26 +366,37 @@ def importance_topn(q, k_cmp, lse_cmp, geom: NSAGeometry, T=None, return_scores=
 # backward kernels
 # ---------------------------------------------------------------------------
 
-def delta_of(do, o, lse):
+def delta_of(do, o, lse, pack_hkv=0):
     """-> (dot, coff): dot[r] = dO[r] . O[r] in float32
     (nsa_selection_backward.py:168) and the row offset lse[r] * log2(e) that
-    the dK/dV kernels take."""
+    the dK/dV kernels take, both [B, Hq, T].  With ``pack_hkv`` > 0 ->
+    (dot, coff, dop): the statistics in the packed row order [B, Hkv, T, G]
+    and dO in the ``pack_heads`` layout, what ``sel_dkdv`` reads."""
     do, o, lse = _contig(do), _contig(o), _contig(lse)
-    rows = o.shape[0] * o.shape[1] * o.shape[2]
-    dot = torch.empty(o.shape[:3], device=o.device, dtype=torch.float32)
+    B, Hq, T, D = o.shape
+    rows = B * Hq * T
+    G, dop = 1, None
+    shape = (B, Hq, T)
+    if pack_hkv > 0:
+        G = Hq // pack_hkv
+        shape = (B, pack_hkv, T, G)
+        dop = torch.empty(B, pack_hkv, T, G, D, device=do.device, dtype=do.dtype)
+    dot = torch.empty(shape, device=o.device, dtype=torch.float32)
     coff = torch.empty_like(dot)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(lse), None, None,
-          L.ptr(dot), None, L.ptr(coff), None, 1, 1, rows, o.shape[3], 1, L.dtype_code(do), L.dtype_code(o),
+          L.ptr(dot), None, L.ptr(coff), L.ptr(dop), G, T, rows, D, 1, L.dtype_code(do), L.dtype_code(o),
           _stream(o))
-    return dot, coff
+    return (dot, coff) if pack_hkv <= 0 else (dot, coff, dop)
 
 
 def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
     """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3], dop); branch
     order compression, selection, window; coff = lse * log2(e) -
     log2(rowscale).  With ``pack_hkv`` > 0, dop is dO packed for that many KV
-    heads (the ``pack_heads`` layout), else None.  The branch outputs share
-    one dtype: dO's, or float32 (unrounded)."""
+    heads (the ``pack_heads`` layout), else None, and the selection branch's
+    dot[1] / rowscale[1] / coff[1] hold their values in the packed row order
+    [B, Hkv, T, G] (what ``sel_dkdv`` reads with ``stats_packed``).  The
+    branch outputs share one dtype: dO's, or float32 (unrounded)."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
     assert o_s.dtype == o_c.dtype and o_w.dtype == o_c.dtype, "branch outputs must share one dtype"
     lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
@@ -491,18 +502,25 @@ def csr_device(block_idx, block_size, n_blk=None, pack_slot=False):
 
 
 def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, want_dq=False, qp=None,
-             dop=None):
+             dop=None, stats_packed=False):
     """dK, dV (float32) of the selection branch over the block -> query CSR;
     with ``want_dq`` also the dQ partials of every (query, slot, pass) for
     ``sel_dq_reduce`` (the CSR must then be built with ``pack_slot``).
     ``qp`` / ``dop``: ``pack_heads`` copies of q / do (made here when not
-    given)."""
+    given).  ``coff`` / ``dot``: [B, Hq, T], or with ``stats_packed`` already
+    in the packed row order [B, Hkv, T, G] (``delta_of(.., pack_hkv)``,
+    ``gate_bwd_prep(.., pack_hkv)``), the order the kernel reads."""
     B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     if qp is None:
         qp = pack_heads(q, Hkv)
     if dop is None:
         dop = pack_heads(do, Hkv)
+    if not stats_packed:
+        G = Hq // Hkv
+        coff, dot = (t.reshape(B, Hkv, G, T).transpose(2, 3).contiguous() for t in (coff, dot))
+    assert coff.numel() == B * Hq * T and dot.numel() == B * Hq * T, "row statistics must cover B*Hq*T rows"
+    coff, dot = _contig(coff), _contig(dot)
     idx = block_idx.to(torch.int32).contiguous()
     S = idx.shape[-1]
     if csr is None:
@@ -634,8 +652,9 @@ def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None)
     check_qkv(q, k, v)
     q, k, v, do = (_contig(t) for t in (q, k, v, do))
     idx = block_idx.to(torch.int32).contiguous()
-    dot, coff = delta_of(do, o, lse)
-    dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True)
+    dot, coff, dop = delta_of(do, o, lse, pack_hkv=k.shape[1])
+    dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True, dop=dop,
+                               stats_packed=True)
     dq = sel_dq_reduce(idx, dq_part, None, block_size, q.dtype)
     return dq, cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
@@ -779,7 +798,7 @@ class NSAFusedHIP(torch.autograd.Function):
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                             csr=tuple(csr), want_dq=True, qp=qp, dop=dop)
+                                             csr=tuple(csr), want_dq=True, qp=qp, dop=dop, stats_packed=True)
             # inputs read on the side stream keep their memory until its work is done
             for t in (q, ks, vs, dout, coff, dot, idx, qp, dop, *csr):
                 t.record_stream(side)

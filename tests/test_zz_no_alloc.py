@@ -35,14 +35,15 @@ def _run_case(dev, B, Hq, Hkv, T, D, bs, S, seed):
     do = randn((B, Hq, T, D), seed + 4, dtype).to(dev)
     idx = make_block_idx(B, Hkv, T, bs, S, seed=seed).to(dev)
     o, lse = ops.sel_fwd(q, k, v, idx, bs)
-    dot, coff = ops.delta_of(do, o, lse)
-    qp, dop = ops.pack_heads(q, Hkv), ops.pack_heads(do, Hkv)
+    # row statistics in the packed row order [B, Hkv, T, G], dO packed
+    dot, coff, dop = ops.delta_of(do, o, lse, pack_hkv=Hkv)
+    qp = ops.pack_heads(q, Hkv)
     kt = ops.transpose_kv(k)
     csr = ops.csr_device(idx, bs, pack_slot=True)
     chunk = ops.SEL_DKDV_CHUNK
     # caller-workspace entry point
     dk_ref, dv_ref, dq_ref = ops.sel_dkdv(q, k, v, do, coff, dot, idx, bs, csr=csr, kt=kt, want_dq=True,
-                                          qp=qp, dop=dop)
+                                          qp=qp, dop=dop, stats_packed=True)
     # no-alloc entry point: outputs allocated here, nothing inside the call
     dk = torch.full_like(dk_ref, float("nan"))
     dv = torch.full_like(dv_ref, float("nan"))
