@@ -80,16 +80,16 @@ WORKLOADS = {
 # counters read for a plain 1 GiB device copy (x2.0 and x1.0); the commands
 # and counter values are kept under profiles/.  Keyed by (workload, kernel).
 MEASURED_TRAFFIC = {   # profiles/nsa_fused_c3_pmc_traffic.md: bytes read + bytes written per launch
-    ("c3", "dkdv[sel]"): 1.956e10 + 9.316e9,
-    ("c3", "fwd[sel]"): 8.593e9 + 8.729e9,
+    ("c3", "dkdv[sel]"): 1.739e10 + 9.315e9,
+    ("c3", "fwd[sel]"): 8.590e9 + 8.729e9,
     ("c3", "dq[cmp+win]"): 1.173e10 + 5.704e8,
     ("c3", "fwd[win]"): 1.125e10 + 2.714e9,
-    ("c3", "dkdv[win]"): 9.838e9 + 1.344e8,
-    ("c3", "dkdv[cmp]"): 2.872e9 + 6.521e8,
-    ("c3", "fwd[cmp]"): 6.915e8 + 2.242e9,
-    ("c3", "nsa_bwd_prep"): 3.834e9 + 6.263e8,
-    ("c3", "nsa_importance_topn"): 6.073e8 + 8.389e6,
-    ("c3", "nsa_pool_fwd"): 5.886e7 + 2.096e6,
+    ("c3", "dkdv[win]"): 9.893e9 + 1.342e8,
+    ("c3", "dkdv[cmp]"): 2.840e9 + 6.630e8,
+    ("c3", "fwd[cmp]"): 6.907e8 + 2.275e9,
+    ("c3", "nsa_bwd_prep"): 3.834e9 + 8.037e8,
+    ("c3", "nsa_importance_topn"): 6.072e8 + 8.389e6,
+    ("c3", "nsa_pool_fwd"): 5.873e7 + 2.096e6,
 }
 
 ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
