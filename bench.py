@@ -11,7 +11,8 @@ initial and two local blocks forced among the 16 are timed beside it
 
 Prints ONE JSON line (rank 0): the metric, tokens/s, the dominant kernel's
 roofline (algorithmic work / its HIP-event-timed launch duration, bound set
-from its measured HBM bytes), per-kernel MFMA fractions, the decode step
+from its measured HBM bytes), the forward and backward timed apart (medians
+of 20 after 5 warm-up steps), per-kernel MFMA fractions, the decode step
 (one new query per sequence against 32K caches, B=32 and B=1: tokens/s and
 HBM fraction), the compression phi's forward / backward time, and CPU baselines (the float32 CPU oracle on a bounded row
 sample of c3, and dense on c1).  ``--workload dec|dec_b1|dec_c5|c4|c5`` runs
@@ -223,12 +224,17 @@ def make_step(w, geom, ins, do):
     if w["kind"] == "fused":
         xs = [t.requires_grad_() for t in ins]
 
-        def step():
+        def fwd():
             for x in xs:
                 x.grad = None
-            out, idx = nfk.nsa_attention(*xs, geom)
+            return nfk.nsa_attention(*xs, geom)
+
+        def step():
+            out, idx = fwd()
             out.backward(do)
             return idx
+        step.fwd = lambda: fwd()[0]
+        step.bwd = lambda out: out.backward(do)
         return step
     # selection only: indices from the compression importance (computed once;
     # they are an input of the selection kernels), keys/values of the
@@ -240,12 +246,16 @@ def make_step(w, geom, ins, do):
         idx = ops.importance_topn(q, k_cmp, lse_c, geom)
     xs = [t.requires_grad_() for t in (q, ks, vs)]
 
-    def step():
+    def fwd():
         for x in xs:
             x.grad = None
-        o = nsb.selection_attn_triton(*xs, idx, geom.sel_block)
-        o.backward(do)
+        return nsb.selection_attn_triton(*xs, idx, geom.sel_block)
+
+    def step():
+        fwd().backward(do)
         return idx
+    step.fwd = fwd
+    step.bwd = lambda out: out.backward(do)
     return step
 
 
@@ -291,8 +301,32 @@ def run_gpu(args, w, name):
     t1 = time.perf_counter()
     ops.set_timer(None)
     ms = (t1 - t0) * 1e3 / args.steps
+    # forward and backward apart (not the headline: that is the timed steps above)
+    split = time_fwd_bwd(step)
     return dict(ms=ms, spans=timer.summary_ms(), iso_spans=iso_spans, dom=dom, flops_of=flops_of, kv=kv,
-                pairs=pairs, ins=ins, do=do, idx=idx)
+                pairs=pairs, ins=ins, do=do, idx=idx, split=split)
+
+
+def time_fwd_bwd(step, warmup=5, reps=20):
+    """Forward and backward of a step timed apart with HIP events around each
+    call, medians of `reps` after `warmup` steps -> dict (ms)."""
+    for _ in range(warmup):
+        step.bwd(step.fwd())
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    for e in ev:
+        e[0].record()
+        out = step.fwd()
+        e[1].record()
+        step.bwd(out)
+        e[2].record()
+    torch.cuda.synchronize()
+    f = [e[0].elapsed_time(e[1]) for e in ev]
+    b = [e[1].elapsed_time(e[2]) for e in ev]
+    t = [e[0].elapsed_time(e[2]) for e in ev]
+    return {"fwd_ms": round(statistics.median(f), 3), "bwd_ms": round(statistics.median(b), 3),
+            "fwd_bwd_ms": round(statistics.median(t), 3), "warmup": warmup, "reps": reps,
+            "note": "HIP events around each call, medians"}
 
 
 def time_gpu_only(args, w, name):
@@ -728,6 +762,7 @@ def main():
         "visible_keys": {"win": kv[0], "cmp": kv[1], "sel": kv[2]},
         "selection_pairs": r["pairs"],
         "roofline": roofline,
+        "fwd_bwd_split": r["split"],
         "branches": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
         "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS, name),
     }

@@ -391,16 +391,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   kdma.init(tid);
   vdma.init(tid, Lp);
   constexpr int LT = decltype(kdma)::NL + decltype(vdma)::NL;
-  key_pipeline<NST, LT>(ntile, [&](int i) {
-    kdma.request(sK[i % NST], kbase, kt0 + 32 * i, Lk, tid);
-    vdma.request(sV[i % NST], vtbase, kt0 + 32 * i, tid);
-  }, [&](int it) {
+  // unrolled over the stages (immediate stage addresses): 1-2% faster here;
+  // the dQ and the top-n walk measured no gain from it
+  key_pipeline_st<NST, LT>(ntile, [&](int i, auto st) {
+    kdma.request(sK[decltype(st)::value], kbase, kt0 + 32 * i, Lk, tid);
+    vdma.request(sV[decltype(st)::value], vtbase, kt0 + 32 * i, tid);
+  }, [&](int it, auto st) {
     const int kb = kt0 + 32 * it;
     // every wave takes every tile of the workgroup range (the waves' own ranges
     // differ by at most a few queries); tiles inside the wave's fully visible
     // span skip the per-element mask
     const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
-    fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[it % NST], sV[it % NST], kb, mask, lo, hi, sl2, n, h);
+    fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[decltype(st)::value], sV[decltype(st)::value], kb, mask, lo, hi, sl2, n,
+                       h);
   });
 
   if (fin_args.opart != nullptr) {

@@ -35,6 +35,8 @@
 // 4j + (l >> 2), j = 0..3 (measured on gfx950).
 #pragma once
 
+#include <type_traits>
+
 #include "nsa_common.h"
 
 namespace nsa {
@@ -408,6 +410,39 @@ __device__ __forceinline__ void key_pipeline(int ntile, Req request, Body body) 
     __syncthreads();
     if (it + NST - 1 < ntile) request(it + NST - 1);
     body(it);
+  }
+}
+
+// f(integral_constant<int, i>) for i = B .. E-1, unrolled at compile time
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+// key_pipeline unrolled over its NST stages: request(i, st) and body(it, st)
+// also receive the stage as a compile-time constant st (integral_constant),
+// so that stage addresses are immediates rather than per-tile arithmetic.
+template <int NST, int LT, typename Req, typename Body>
+__device__ __forceinline__ void key_pipeline_st(int ntile, Req request, Body body) {
+  static_assert(NST >= 2 && (NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
+  static_for<0, NST - 1>([&](auto p) {
+    if (p.value < ntile) request(p.value, p);
+  });
+  for (int it0 = 0; it0 < ntile; it0 += NST) {
+    static_for<0, NST>([&](auto p) {
+      const int it = it0 + p.value;
+      if (it >= ntile) return;
+      if (it + NST - 2 < ntile)
+        vm_wait<(NST - 2) * LT>();
+      else
+        vm_wait<0>();
+      __syncthreads();
+      if (it + NST - 1 < ntile) request(it + NST - 1, std::integral_constant<int, (p.value + NST - 1) % NST>{});
+      body(it, p);
+    });
   }
 }
 
