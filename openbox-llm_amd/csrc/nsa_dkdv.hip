@@ -125,15 +125,16 @@ template <typename T, int D, int NTH> struct KvIssuer {
     tA = __builtin_amdgcn_readfirstlane(tA);
     tB = __builtin_amdgcn_readfirstlane(tB);
     const int tBq = tB >= 0 ? tB : tA;   // a missing second query re-reads the first
-    const int64_t qoff = qbase + (int64_t)tA * x.ts;
-    const uint32_t dB = (uint32_t)(tBq - tA) * (uint32_t)(x.ts * sizeof(T));
+    // rows addressed upward from the lower query (whatever the entries' order)
+    const PairRows pr = pair_rows(tA, tB, (uint32_t)(x.ts * sizeof(T)));
+    const int64_t qoff = qbase + (int64_t)pr.t0 * x.ts;
     const T* qa = x.q + qoff;
     const T* da = x.dout + qoff;
 #pragma unroll
     for (int j = 0; j < LPT; ++j) {
       const int first = first_chunk(j, w);
       const bool rowB = UNI ? first / C::RCH >= 16 : ((qsel >> j) & 1u) != 0;
-      const uint32_t v = off[j] + (rowB ? dB : 0u);
+      const uint32_t v = off[j] + (rowB ? pr.dB : pr.dA);
       lds_dma16_sbase(qa, v, (char*)s.qr + 16 * first);
       lds_dma16_sbase(da, v, (char*)s.dr + 16 * first);
     }
@@ -1081,7 +1082,10 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
     };
     auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
       const int tb = tB >= 0 ? tB : tA;
-      mask = !(wlast <= tA && wlast < blk_end);
+      // the per-element test is skipped only when every key of the wave
+      // precedes both queries (the earlier of the two: the entries' order is
+      // not relied on)
+      mask = !(wlast <= (tA < tb ? tA : tb) && wlast < blk_end);
       visA = key_ok && key <= tA;
       visB = key_ok && key <= tb;
     };

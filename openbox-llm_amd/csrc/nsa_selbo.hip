@@ -45,11 +45,14 @@ template <typename T, int D> struct FwdIssuer {
       qsel |= (uint32_t)(r >> 4) << j;
     }
   }
-  __device__ __forceinline__ void issue(T* stage, const T* qa, int tA, int tB, int G) const {
-    const uint32_t dB = (uint32_t)((tB >= 0 ? tB : tA) - tA) * (uint32_t)(G * D * sizeof(T));
+  // qbh: the packed Q of the (b, hkv) and head chunk at query 0; rows are
+  // addressed upward from the lower of the two queries
+  __device__ __forceinline__ void issue(T* stage, const T* qbh, int tA, int tB, int G) const {
+    const PairRows pr = pair_rows(tA, tB, (uint32_t)(G * D * sizeof(T)));
+    const T* qa = qbh + (int64_t)pr.t0 * G * D;
 #pragma unroll
     for (int j = 0; j < LPT; ++j)
-      lds_dma16_sbase(qa, off[j] + (((qsel >> j) & 1u) ? dB : 0u), (char*)stage + 1024 * j);
+      lds_dma16_sbase(qa, off[j] + (((qsel >> j) & 1u) ? pr.dB : pr.dA), (char*)stage + 1024 * j);
   }
 };
 
@@ -151,8 +154,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       int tA, sA, tB, sB;
       entry(2 * pti, tA, sA);
       entry(2 * pti + 1, tB, sB);
-      const int64_t qrow = (((int64_t)b * Hkv + hkv) * T_ + tA) * G + phc * 16;   // packed row
-      iss.issue(stage, q + qrow * D, tA, tB, G);
+      const int64_t qrow0 = ((int64_t)b * Hkv + hkv) * T_ * G + phc * 16;   // packed row of query 0
+      iss.issue(stage, q + qrow0 * D, __builtin_amdgcn_readfirstlane(tA), __builtin_amdgcn_readfirstlane(tB), G);
       ++pix;
       if (++pti == ntile) {
         pti = 0;
@@ -192,8 +195,11 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       }
       // raw scores; the scale (> 0) is applied to the row maximum and inside
       // the exponent's fma.  Tiles whose 64 keys all exist and precede both
-      // queries (tA <= tB: CSR queries ascend) need no per-element mask.
-      if (!(kbase + 64 <= kend && kbase + 63 <= __builtin_amdgcn_readfirstlane(tA))) {
+      // queries need no per-element mask (the earlier query decides; the
+      // entries' order is not relied on).
+      const int utA = __builtin_amdgcn_readfirstlane(tA), utB = __builtin_amdgcn_readfirstlane(tB);
+      const int tlow = utB >= 0 && utB < utA ? utB : utA;
+      if (!(kbase + 64 <= kend && kbase + 63 <= tlow)) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll

@@ -239,6 +239,28 @@ __host__ __device__ constexpr uint64_t u64_from_halves(int lo, int hi) {
 static_assert(u64_from_halves((int)0x80001000u, 0x7ffe) == 0x00007ffe80001000ull,
               "a base address with bit 31 set must survive the split into halves");
 
+// The rows of a tile's two queries tA and tB (tB < 0: none; its lanes then
+// read tA's rows) as unsigned byte offsets from the lower of the two rows,
+// t0: the DMA requests add them to unsigned per-lane offsets, so neither may
+// be negative.  CSR entries ascend within a block, but a caller's CSR need
+// not: a difference taken from tA alone would wrap to about 4 GB past the
+// base when tB < tA.
+struct PairRows {
+  int t0;
+  uint32_t dA, dB;
+};
+__host__ __device__ constexpr PairRows pair_rows(int tA, int tB, uint32_t row_bytes) {
+  const int tb = tB >= 0 ? tB : tA;
+  const int t0 = tA < tb ? tA : tb;
+  return PairRows{t0, (uint32_t)(tA - t0) * row_bytes, (uint32_t)(tb - t0) * row_bytes};
+}
+static_assert(pair_rows(7, 3, 4096).t0 == 3 && pair_rows(7, 3, 4096).dA == 4 * 4096 &&
+                  pair_rows(7, 3, 4096).dB == 0,
+              "query B before query A: both offsets from B's row");
+static_assert(pair_rows(3, 7, 256).t0 == 3 && pair_rows(3, 7, 256).dA == 0 && pair_rows(3, 7, 256).dB == 4 * 256,
+              "ascending queries: from A's row");
+static_assert(pair_rows(5, -1, 256).t0 == 5 && pair_rows(5, -1, 256).dB == 0, "no query B: A's row twice");
+
 // Direct global -> LDS loads as volatile asm (lane i writes lds + SIZE i):
 // the compiler neither tracks them nor adds waits for them, so LDS reads of
 // other stages are not held behind loads still in flight.  The caller owns

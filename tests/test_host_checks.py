@@ -4,6 +4,9 @@
   halves by readfirstlane (which returns int) and joined again must survive
   when the low half has bit 31 set -- the fault of an earlier build, whose
   join sign-extended that half (tests/host/check_dma_base.hip).
+* The two query rows of a selection tile (pair_rows): addressed upward from
+  the lower query, so a CSR whose entries do not ascend cannot wrap an
+  unsigned offset (tests/host/check_pair_rows.hip).
 * M0: the inline-asm DMA helpers of nsa_tile32.h write M0 (the LDS address
   of global_load_lds) behind the compiler's back.  That is safe only while
   no compiler-generated instruction keeps a value in M0 across them.  The
@@ -31,6 +34,19 @@ def test_dma_base_address_halves(tmp_path):
     exe = tmp_path / "check_dma_base"
     subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", f"-I{ROOT}/include", f"-I{PKG}/csrc",
                     os.path.join(ROOT, "tests", "host", "check_dma_base.hip"), "-o", str(exe)],
+                   check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout
+
+
+def test_pair_rows_addressing(tmp_path):
+    """The two queries of a selection tile are addressed upward from the lower
+    one, so a CSR whose entries do not ascend cannot produce a wrapped offset
+    (the regression of an out-of-bounds read; tests/host/check_pair_rows.hip)."""
+    exe = tmp_path / "check_pair_rows"
+    subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", f"-I{ROOT}/include", f"-I{PKG}/csrc",
+                    os.path.join(ROOT, "tests", "host", "check_pair_rows.hip"), "-o", str(exe)],
                    check=True, capture_output=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     print(r.stdout)
