@@ -134,7 +134,9 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * CSR above built with n_blk = ceil(T / block_size) (so a selected trailing
  * partial block, which the forward attends to, gets its gradient), split into
  * work items of at most `chunk` (<= 1024) queries; q_of_block holds (t << b) | s
- * when `packed`.  q and dout are in the nsa_pack_heads layout
+ * when `packed`.  The entries of a block may come in any order (one per
+ * (query, slot) pair of that block): nsa_csr_build writes them ascending,
+ * another producer need not.  q and dout are in the nsa_pack_heads layout
  * [B][Hkv][T][G][D]; coff / dot, the row offsets and deltas of nsa_bwd_prep,
  * in the same packed row order [B][Hkv][T][G] (nsa_bwd_prep with
  * dout_packed writes them so), kt the
@@ -171,7 +173,8 @@ int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void
 /* ---- block-outer selection forward and the partial merges ----------------
  * The FSA forward (replaces _selection_fwd_blockouter_kernel /
  * selection_forward_fsa, nsa_selection_kernel.py:232-365): work items as in
- * nsa_sel_dkdv over a CSR built with pack_slot; for every (query, slot, pass)
+ * nsa_sel_dkdv over a CSR built with pack_slot (its entries in any order
+ * within a block); for every (query, slot, pass)
  * it writes the unnormalised block-local output O_j = sum_k p_k v_k (input
  * dtype; p_k = exp2(s_k - m_j)) to o_part and (m_j [log2 units], l_j = sum_k
  * p_k) float pairs to ml_part, as the reference's per-pair partials
