@@ -152,6 +152,20 @@ template <typename T, int D, int NTH> struct KvIssuer {
   }
 };
 
+// Visibility of a lane's key to the rows of a tile, by accumulator register r
+// of KeyAcc::front (register r of lane half h holds row acc_elem(h, r)).
+// Two-query tiles: rows 0-15 are query A's, rows 16-31 query B's.
+struct VisPair {
+  bool a, b;
+  __device__ __forceinline__ bool operator()(int r) const { return r < 8 ? a : b; }
+};
+// Any row layout: bit e of the row mask says whether row e sees the key,
+// stored shifted right by 8 h so that register r tests bit 16 (r >> 3) + (r & 7).
+struct VisBits {
+  uint32_t bits;
+  __device__ __forceinline__ bool operator()(int r) const { return (bits >> (16 * (r >> 3) + (r & 7))) & 1u; }
+};
+
 // Per-wave key state: 32 keys, their K / V fragments and dK^T / dV^T.
 template <typename T, int D> struct KeyAcc {
   using C = Tile32<T, D>;
@@ -193,13 +207,13 @@ template <typename T, int D> struct KeyAcc {
   // First half of a tile: S and dP from the row fragments read earlier, the
   // transposed fragments dO^T (ta) and Q^T (tb) read while those MFMAs run,
   // then P and dS packed as the operands of the second half.  With MASK,
-  // visA / visB say whether this lane's key is visible to query A / B;
-  // without, every key is.
+  // vis(r) says whether this lane's key is visible to the row of accumulator
+  // register r (VisPair, VisBits); without, every key is.
   // With SPLIT (16-bit operands only), sl receives the rounding remainder
   // dS - round(dS) of the dS operand, for a second dK^T product: dS then
   // enters dK with about twice the significant bits.
-  template <bool MASK, bool SPLIT = false>
-  __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, bool visA, bool visB, float sl2,
+  template <bool MASK, bool SPLIT, typename Vis>
+  __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, const Vis& vis, float sl2,
                                         int lane, Frag<T> (&ta)[C::DT][2], Frag<T> (&tb)[C::DT][2],
                                         Frag<T> (&pf)[2], Frag<T> (&sf)[2], Frag<T> (&sl)[2]) {
     const int h = lane >> 5;
@@ -232,7 +246,7 @@ template <typename T, int D> struct KeyAcc {
     for (int r = 0; r < 16; ++r) {
       const int e = acc_elem(h, r);
       float p = fast_exp2(sacc[r] * sl2 - s.c[e]);
-      if (MASK) p = (r < 8 ? visA : visB) ? p : 0.0f;
+      if (MASK) p = vis(r) ? p : 0.0f;
       P[r] = p;
       dS[r] = p * (pacc[r] - s.dot[e]);
     }
@@ -289,9 +303,140 @@ template <typename T, int D> struct KeyAcc {
   }
 };
 
-// Walk `ntile` 2-query tiles (queries and their block_idx slots from
-// qsrc(i, tA, tB, sA, sB); tB = -1: none) over every head chunk, kKvStages
-// tiles deep, one workgroup barrier per tile, in the middle of it:
+// Row tiles of two queries x the 16 heads of a head chunk (KvIssuer), a tile
+// source of kv_walk: the caller's qsrc(i, tA, tB, sA, sB) names tile i's
+// queries and their block_idx slots (tB = -1: none) and vis(tA, tB, mask,
+// visA, visB) fills a tile's mask flags for this wave (tB = -1: query B's rows
+// are absent, whatever visB says).  The consumer reads the tile's queries back
+// from the stage (the ids issue() wrote).
+template <typename T, int D, int NTH, typename QSrc, typename Vis> struct PairTiles {
+  struct Info {
+    int tA, tB, sA, sB;
+  };
+  const QSide<T>& x;
+  int b, hkv;
+  QSrc qsrc;
+  Vis visf;
+  KvIssuer<T, D, NTH> iss;
+  __device__ __forceinline__ void prepare(int hc, int tid) { iss.prepare(x, b, hkv, hc, tid); }
+  __device__ __forceinline__ void issue(KvStage<T, D>& s, int ti, int tid) {
+    int tA, tB, sA, sB;
+    qsrc(ti, tA, tB, sA, sB);
+    iss.issue(s, x, tA, tB, sA, sB, tid);
+  }
+  __device__ __forceinline__ Info info(const KvStage<T, D>& s, int) const {
+    return Info{__builtin_amdgcn_readfirstlane(s.meta[0]), __builtin_amdgcn_readfirstlane(s.meta[1]),
+                __builtin_amdgcn_readfirstlane(s.meta[2]), __builtin_amdgcn_readfirstlane(s.meta[3])};
+  }
+  __device__ __forceinline__ VisPair vis(const Info& i, bool& mask) const {
+    VisPair v;
+    visf(i.tA, i.tB, mask, v.a, v.b);
+    return v;
+  }
+};
+template <typename T, int D, int NTH, typename QSrc, typename Vis>
+__device__ __forceinline__ PairTiles<T, D, NTH, QSrc, Vis> pair_tiles(const QSide<T>& x, int b, int hkv, QSrc qsrc,
+                                                                     Vis vis) {
+  return PairTiles<T, D, NTH, QSrc, Vis>{x, b, hkv, qsrc, vis, {}};
+}
+
+// Row tiles of QPT = floor(32 / G) CSR entries of a selection work item, for
+// GQA groups of G <= 10 heads (a tile of two queries would leave 32 - 2 G of
+// its rows empty): rows q G .. q G + G - 1 are entry q's heads, rows from
+// QPT G on are absent.  Q / dO and the row statistics are in the packed
+// per-query layout, so row (t, g) of the group is row t G + g from the
+// group's base.  A lane's loads are prepared once (the entry q and head g of
+// its chunks' rows); per tile it reads its entries' queries from the item's
+// entries in LDS and adds t G D elements to its offsets.  Absent rows (past
+// QPT G, or of entries past the item's end) read rows of the tile's first
+// entry with the row offset +inf, so their P and dS are exactly 0.  A tile
+// issues the same loads as a KvIssuer tile (kv_tile_loads).
+template <typename T, int D, int NTH> struct GroupTiles {
+  using C = Tile32<T, D>;
+  static constexpr int LPT = dma_uniform_loads<NTH, C::ROW_CHUNKS>();
+  struct Info {
+    int e0;   // the tile's first entry
+  };
+  const int32_t* sent;   // the item's entries (LDS): t, or (t << sbits) | slot when packed
+  int cnt, sbits, packed, G, QPT;
+  const T* qg;           // Q / dO of the group (b, hkv), query 0 head 0
+  const T* dg;
+  const float* sp;       // statistics of the group: c for lanes < 32, delta above
+  uint32_t rowbytes;     // one query's G rows in bytes
+  int key, wlast, blk_end;   // this lane's key, the wave's last key, the block's end
+  bool key_ok;
+  int h;
+  uint32_t off[LPT];     // (g D + column) * sizeof(T) of this lane's chunk of load j
+  int qj[LPT];           // entry (in the tile) of that chunk's row
+  int sq, sg;            // statistics row of this lane: entry and head
+  bool sreal;
+
+  __device__ __forceinline__ int entry_t(int i) const {
+    if (i >= cnt) return -1;
+    const int v = sent[i];
+    return packed ? v >> sbits : v;
+  }
+  __device__ __forceinline__ int entry_s(int i) const {
+    return packed && i < cnt ? sent[i] & ((1 << sbits) - 1) : 0;
+  }
+  __device__ __forceinline__ void prepare(int, int tid) {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int nreal = QPT * G;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int r, cc;
+      row_chunk<T, D>(KvIssuer<T, D, NTH>::first_chunk(j, w) + lane, r, cc);
+      const bool real = r < nreal;
+      qj[j] = real ? r / G : 0;
+      const int g = real ? r % G : 0;
+      off[j] = (uint32_t)((g * D + cc * C::EPC) * (int)sizeof(T));
+    }
+    const int sr = lane & 31;
+    sreal = sr < nreal;
+    sq = sreal ? sr / G : 0;
+    sg = sreal ? sr % G : 0;
+  }
+  __device__ __forceinline__ void issue(KvStage<T, D>& s, int ti, int tid) const {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int e0 = QPT * ti;
+    const int t0 = __builtin_amdgcn_readfirstlane(entry_t(e0));   // a tile's first entry exists
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int t = entry_t(e0 + qj[j]);
+      t = t >= 0 ? t : t0;
+      const uint32_t v = (uint32_t)t * rowbytes + off[j];
+      const int first = KvIssuer<T, D, NTH>::first_chunk(j, w);
+      lds_dma16_sbase(qg, v, (char*)s.qr + 16 * first);
+      lds_dma16_sbase(dg, v, (char*)s.dr + 16 * first);
+    }
+    {
+      // lanes 0-31: c of row lane, lanes 32-63: delta of row lane - 32
+      int t = entry_t(e0 + sq);
+      const bool real = lane >= 32 || (sreal && t >= 0);
+      t = t >= 0 ? t : t0;
+      lds_dma4(real ? sp + (int64_t)t * G + sg : &kAbsentRow, s.c);
+    }
+  }
+  __device__ __forceinline__ Info info(const KvStage<T, D>&, int ti) const { return Info{QPT * ti}; }
+  // the rows of entries whose query the lane's key precedes; the per-element
+  // test is skipped only when every key of the wave precedes every entry's query
+  __device__ __forceinline__ VisBits vis(const Info& i, bool& mask) const {
+    const uint32_t gmask = (1u << G) - 1u;
+    uint32_t bits = 0;
+    int tmin = 0x7fffffff;
+    for (int q = 0; q < QPT; ++q) {
+      const int t = __builtin_amdgcn_readfirstlane(entry_t(i.e0 + q));
+      if (t < 0) break;   // entries past the item's end are the tile's last
+      tmin = t < tmin ? t : tmin;
+      if (key_ok && key <= t) bits |= gmask << (q * G);
+    }
+    mask = !(wlast <= tmin && wlast < blk_end);
+    return VisBits{bits >> (8 * h)};
+  }
+};
+
+// Walk `ntile` row tiles of each of `nhc` head chunks, kKvStages tiles deep,
+// one workgroup barrier per tile, in the middle of it:
 //   front(i)                     S / dP MFMAs, transposed reads, P / dS
 //   wait for tile i+1, barrier   tile i+1 visible; stage i retired by every wave
 //   read rows of tile i+1        LDS reads overlapping ...
@@ -304,36 +449,34 @@ template <typename T, int D> struct KeyAcc {
 // at most that many outstanding operations completes tile i + 1 while the two
 // younger tiles stay in flight (operations complete in issue order; a post
 // that stores more than NSW only makes the wait longer).
-// vis(tA, tB, mask, visA, visB) fills the mask flags of a tile for this wave
-// (tB = -1: query B's rows are absent, whatever visB says).  With WANT_DS,
-// pre(dS, i) runs before the barrier with this lane's dS as two operand-dtype
-// fragments (element j of fragment k: accumulator register 8 k + j), and
-// post(tA, tB, sA, sB, hc, i) after the back half, so what pre stages in LDS
-// is visible to post without a second barrier.
-template <bool WANT_DS, int NSW, typename T, int D, int NTH, bool SPLIT, typename QSrc, typename Vis,
-          typename Pre, typename Post>
-__device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], const QSide<T>& x,
-                                        int b, int hkv, int ntile, QSrc qsrc, Vis vis, Pre pre, Post post,
-                                        float sl2, int tid) {
+// The tile source (PairTiles, GroupTiles) issues a tile's loads into a stage
+// (prepare(hc, tid) once per head chunk, then issue(stage, ti, tid)), names
+// the tile to the consumer (info(stage, ti)) and gives this wave's mask flag
+// and visibility (vis(info, mask)).  With WANT_DS, pre(dS, i) runs before the
+// barrier with this lane's dS as two operand-dtype fragments (element j of
+// fragment k: accumulator register 8 k + j), and post(info, hc, i) after the
+// back half, so what pre stages in LDS is visible to post without a second
+// barrier.
+template <bool WANT_DS, int NSW, typename T, int D, int NTH, bool SPLIT, typename Tiles, typename Pre,
+          typename Post>
+__device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], Tiles& tiles, int nhc,
+                                        int ntile, Pre pre, Post post, float sl2, int tid) {
   using C = Tile32<T, D>;
   constexpr int NST = kKvStages;
   constexpr int LT = kv_tile_loads<T, D, NTH>();
   static_assert(NST >= 3 && (NST - 1) * LT < 64 && (NST - 2) * (LT + NSW) < 64,
                 "in-flight operations exceed the vmcnt range");
   // wave-uniform: every branch on the loop counters below is scalar
-  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
+  const int total = __builtin_amdgcn_readfirstlane(ntile * nhc);
   if (total == 0) return;
   const int lane = tid & 63;
   int iti = 0, ihc = 0;   // next tile to request: tile and head chunk
-  KvIssuer<T, D, NTH> iss;
-  iss.prepare(x, b, hkv, 0, tid);
+  tiles.prepare(0, tid);
   auto request = [&](KvStage<T, D>& s) {
-    int tA, tB, sA, sB;
-    qsrc(iti, tA, tB, sA, sB);
-    iss.issue(s, x, tA, tB, sA, sB, tid);
+    tiles.issue(s, iti, tid);
     if (++iti == ntile) {
       iti = 0;
-      if (++ihc < x.NHC) iss.prepare(x, b, hkv, ihc, tid);
+      if (++ihc < nhc) tiles.prepare(ihc, tid);
     }
   };
 #pragma unroll
@@ -357,15 +500,14 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
       const int it = it0 + p;
       if (it >= total) break;
       const KvStage<T, D>& s = stg[p];
-      const int tA = __builtin_amdgcn_readfirstlane(s.meta[0]), tB = __builtin_amdgcn_readfirstlane(s.meta[1]);
-      const int sA = __builtin_amdgcn_readfirstlane(s.meta[2]), sB = __builtin_amdgcn_readfirstlane(s.meta[3]);
-      bool mask, visA, visB;
-      vis(tA, tB, mask, visA, visB);
+      const auto inf = tiles.info(s, ti);
+      bool mask;
+      const auto v = tiles.vis(inf, mask);
       Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2], sl[2];
       if (mask)
-        acc.template front<true, SPLIT>(s, rows, visA, visB, sl2, lane, ta, tb, pf, sf, sl);
+        acc.template front<true, SPLIT>(s, rows, v, sl2, lane, ta, tb, pf, sf, sl);
       else
-        acc.template front<false, SPLIT>(s, rows, true, true, sl2, lane, ta, tb, pf, sf, sl);
+        acc.template front<false, SPLIT>(s, rows, v, sl2, lane, ta, tb, pf, sf, sl);
       if (WANT_DS) pre(sf, p);
       if (it + NST - 1 < total)
         vm_wait_steps<(NST - 2) * LT, WANT_DS ? NSW : 0, NST - 2>(it);
@@ -374,7 +516,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
       __syncthreads();
       if (it + 1 < total) KeyAcc<T, D>::read_rows(rows, stg[(p + 1) % NST], lane);
       acc.template back<SPLIT>(ta, tb, pf, sf, sl);
-      if (WANT_DS) post(tA, tB, sA, sB, hc, p);
+      if (WANT_DS) post(inf, hc, p);
       if (it + NST < total) request(stg[p]);
       if (++ti == ntile) {
         ti = 0;
@@ -819,8 +961,9 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
     }
   };
   auto no_pre = [](const Frag<T>*, int) {};
-  auto no_post = [](int, int, int, int, int, int) {};
-  kv_walk<false, 0, T, D, NTH, false>(acc, stg, x, b, hkv, ntile, qsrc, vis, no_pre, no_post, sl2, tid);
+  auto no_post = [](const auto&, int, int) {};
+  auto tiles = pair_tiles<T, D, NTH>(x, b, hkv, qsrc, vis);
+  kv_walk<false, 0, T, D, NTH, false>(acc, stg, tiles, x.NHC, ntile, no_pre, no_post, sl2, tid);
   if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
                         mode == NSA_MODE_COMPRESS, h);
 }
@@ -995,7 +1138,9 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // remainder: a block that every query selects sums tens of thousands of rows
 // into one key's dK, and a single 16-bit dS would leave that sum with an
 // error near the bf16 gradient tolerance.
-template <typename T, int D>
+// GP: groups of G <= 10 heads take floor(32 / G) entries per row tile
+// (GroupTiles), the others two queries x 16 heads per head chunk (PairTiles).
+template <typename T, int D, bool GP>
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                   const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
@@ -1064,31 +1209,7 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) settle(ktf[i][kk]);
     }
-    const int ntile = (cnt + 1) / 2;
     __syncthreads();   // sent visible to every wave
-    auto decode = [&](int i, int& t, int& s) {
-      if (i < cnt) {
-        const int val = sent[i];
-        t = packed ? val >> sbits : val;
-        s = packed ? val & ((1 << sbits) - 1) : 0;
-      } else {
-        t = -1;
-        s = 0;
-      }
-    };
-    auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
-      decode(2 * i, tA, sA);
-      decode(2 * i + 1, tB, sB);
-    };
-    auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
-      const int tb = tB >= 0 ? tB : tA;
-      // the per-element test is skipped only when every key of the wave
-      // precedes both queries (the earlier of the two: the entries' order is
-      // not relied on)
-      mask = !(wlast <= (tA < tb ? tA : tb) && wlast < blk_end);
-      visA = key_ok && key <= tA;
-      visB = key_ok && key <= tb;
-    };
     // dS^T (this wave's 32 keys x the tile's 32 rows) -> LDS, two 16-byte
     // pieces per lane: row 32 w + n of sdT, elements 8 h .. and 16 + 8 h ..
     auto pre = [&](const Frag<T>* ds, int i) {
@@ -1106,10 +1227,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
         }
       }
     };
-    // dQ^T = K^T dS^T over the pass's 64 keys, this wave's d-tiles; written
-    // scaled to the (query, slot, pass) partial
-    auto post = [&](int tA, int tB, int sA, int sB, int hc, int i) {
-      f32x16 dq[DTW];
+    // dQ^T = K^T dS^T over the pass's 64 keys, this wave's d-tiles, from the
+    // dS^T that pre staged for tile parity i; lane (h, n) holds row n
+    auto dq_tile = [&](f32x16 (&dq)[DTW], int i) {
 #pragma unroll
       for (int d = 0; d < DTW; ++d) dq[d] = zero16();
 #pragma unroll
@@ -1119,30 +1239,95 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
 #pragma unroll
         for (int d = 0; d < DTW; ++d) mma32(dq[d], ktf[d][kk], bf);
       }
-      const int t = n < 16 ? tA : tB;
-      const int g = hc * 16 + (n & 15);
-      if (t >= 0 && g < G) {
-        const int slot = (n < 16 ? sA : sB) * npass + pass;
-        T* drow = dq_part + ((((int64_t)bh * T_ + t) * NS + slot) * G + g) * D;
-        // register r of lane half h holds d = 32 (w DTW + d) + acc_elem(h, r)
+    };
+    // ... written scaled to head g of the (query t, partial slot) partial
+    auto dq_store = [&](const f32x16 (&dq)[DTW], int t, int slot, int g) {
+      T* drow = dq_part + ((((int64_t)bh * T_ + t) * NS + slot) * G + g) * D;
+      // register r of lane half h holds d = 32 (w DTW + d) + acc_elem(h, r)
 #pragma unroll
-        for (int d = 0; d < DTW; ++d) {
-          if (w * DTW + d >= DT) continue;
+      for (int d = 0; d < DTW; ++d) {
+        if (w * DTW + d >= DT) continue;
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const int dd = 32 * (w * DTW + d) + 16 * hf + 8 * h;
-            float y[8];
+        for (int hf = 0; hf < 2; ++hf) {
+          const int dd = 32 * (w * DTW + d) + 16 * hf + 8 * h;
+          float y[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) y[i] = dq[d][8 * hf + i] * scale;
-            if (D % 32 == 0 || dd < D) store8(drow + dd, y);
-          }
+          for (int i = 0; i < 8; ++i) y[i] = dq[d][8 * hf + i] * scale;
+          if (D % 32 == 0 || dd < D) store8(drow + dd, y);
         }
       }
     };
-    if (dq_part != nullptr)
-      kv_walk<true, NSW, T, D, NTH, true>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
-    else
-      kv_walk<false, 0, T, D, NTH, true>(acc, stg, x, b, hkv, ntile, qsrc, vis, pre, post, sl2, tid);
+    if constexpr (GP) {
+      const int QPT = 32 / G;
+      const int64_t grow = (int64_t)bh * G * T_;   // the group's first packed row
+      GroupTiles<T, D, NTH> tiles;
+      tiles.sent = sent;
+      tiles.cnt = cnt;
+      tiles.sbits = sbits;
+      tiles.packed = packed;
+      tiles.G = G;
+      tiles.QPT = QPT;
+      tiles.qg = x.q + grow * D;
+      tiles.dg = x.dout + grow * D;
+      tiles.sp = (lane < 32 ? x.c : x.dot) + grow;
+      tiles.rowbytes = (uint32_t)(G * D * (int)sizeof(T));
+      tiles.key = key;
+      tiles.wlast = wlast;
+      tiles.blk_end = blk_end;
+      tiles.key_ok = key_ok;
+      tiles.h = h;
+      const int ntile = (cnt + QPT - 1) / QPT;
+      const int pq = n / G, pg = n % G;   // this lane's dQ row: entry and head
+      const bool preal = n < QPT * G;
+      auto post = [&](const typename GroupTiles<T, D, NTH>::Info& inf, int, int i) {
+        f32x16 dq[DTW];
+        dq_tile(dq, i);
+        const int e = inf.e0 + pq;
+        const int t = tiles.entry_t(e);
+        if (preal && t >= 0) dq_store(dq, t, tiles.entry_s(e) * npass + pass, pg);
+      };
+      if (dq_part != nullptr)
+        kv_walk<true, NSW, T, D, NTH, true>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
+      else
+        kv_walk<false, 0, T, D, NTH, true>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
+    } else {
+      const int ntile = (cnt + 1) / 2;
+      auto decode = [&](int i, int& t, int& s) {
+        if (i < cnt) {
+          const int val = sent[i];
+          t = packed ? val >> sbits : val;
+          s = packed ? val & ((1 << sbits) - 1) : 0;
+        } else {
+          t = -1;
+          s = 0;
+        }
+      };
+      auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
+        decode(2 * i, tA, sA);
+        decode(2 * i + 1, tB, sB);
+      };
+      auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
+        const int tb = tB >= 0 ? tB : tA;
+        // the per-element test is skipped only when every key of the wave
+        // precedes both queries (the earlier of the two: the entries' order is
+        // not relied on)
+        mask = !(wlast <= (tA < tb ? tA : tb) && wlast < blk_end);
+        visA = key_ok && key <= tA;
+        visB = key_ok && key <= tb;
+      };
+      auto post = [&](const auto& inf, int hc, int i) {
+        f32x16 dq[DTW];
+        dq_tile(dq, i);
+        const int t = n < 16 ? inf.tA : inf.tB;
+        const int g = hc * 16 + (n & 15);
+        if (t >= 0 && g < G) dq_store(dq, t, (n < 16 ? inf.sA : inf.sB) * npass + pass, g);
+      };
+      auto tiles = pair_tiles<T, D, NTH>(x, b, hkv, qsrc, vis);
+      if (dq_part != nullptr)
+        kv_walk<true, NSW, T, D, NTH, true>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
+      else
+        kv_walk<false, 0, T, D, NTH, true>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
+    }
     if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
     __syncthreads();   // the next item's first tiles reuse stages 0 .. and sent
   }
@@ -1284,15 +1469,21 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
   const int Lp = padded_len(T);
+  // groups of up to 10 heads pack floor(32 / G) >= 3 entries into a row tile
+  const bool gp = Hq / Hkv <= kGroupPackMaxG;
   NSA_DISPATCH_D(D, {
-    if (dtype == NSA_BF16)
-      k_sel_dkdv32<bf16, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
-          (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block, items, n_items, dk, dv, (bf16*)dq_part, Hq,
-          Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
-    else
-      k_sel_dkdv32<float, DD><<<(unsigned)grid_cap, 128, 0, s>>>(
-          (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, (const float*)kt, q_of_block, items, n_items, dk, dv, (float*)dq_part,
-          Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
+    if (dtype == NSA_BF16) {
+      auto kern = gp ? k_sel_dkdv32<bf16, DD, true> : k_sel_dkdv32<bf16, DD, false>;
+      kern<<<(unsigned)grid_cap, 128, 0, s>>>(
+          (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block,
+          items, n_items, dk, dv, (bf16*)dq_part, Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
+    } else {
+      auto kern = gp ? k_sel_dkdv32<float, DD, true> : k_sel_dkdv32<float, DD, false>;
+      kern<<<(unsigned)grid_cap, 128, 0, s>>>(
+          (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, (const float*)kt,
+          q_of_block, items, n_items, dk, dv, (float*)dq_part, Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2,
+          scale);
+    }
   });
   return nsa_launch_status();
 }

@@ -77,6 +77,10 @@ constexpr int kSelItemMax = 1024;
 // Keys of a selection block handled per pass of the block-outer kernels; a
 // block longer than this is split into ceil(L / kSelPass) partial slots.
 constexpr int kSelPass = 64;
+
+// Largest GQA group whose selection row tiles hold floor(32 / G) >= 3 entries
+// (G heads each) instead of two queries x 16 head slots.
+constexpr int kGroupPackMaxG = 10;
 __host__ __device__ inline int sel_passes(int block_size) { return (block_size + kSelPass - 1) / kSelPass; }
 
 // Packed (query, slot) entries of the CSR built with pack_slot:

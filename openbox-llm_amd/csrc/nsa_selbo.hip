@@ -56,6 +56,43 @@ template <typename T, int D> struct FwdIssuer {
   }
 };
 
+// Loads of a tile of QPT = floor(32 / G) entries for groups of G <= 10 heads
+// (a 2-query tile would leave 32 - 2 G rows empty): row r = q G + g is entry
+// q's head g; rows from QPT G on read entry 0's head 0 (finite rows whose
+// output is never stored).  Per load a 32-bit byte offset of the head and
+// column (prepared once) plus t G D elements of the entry's query, read per
+// lane from the item's entries.
+template <typename T, int D> struct FwdIssuerGP {
+  using C = Tile32<T, D>;
+  static constexpr int LPT = C::ROW_CHUNKS / 64;   // loads per tile
+  uint32_t off[LPT];
+  int qj[LPT];   // entry (in the tile) of load j's row
+
+  __device__ __forceinline__ void prepare(int G, int QPT, int lane) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int r, cc;
+      nrow_chunk<T, D>(j * 64 + lane, r, cc);
+      const bool real = r < QPT * G;
+      qj[j] = real ? r / G : 0;
+      const int g = real ? r % G : 0;
+      off[j] = (uint32_t)((g * D + cc * C::EPC) * (int)sizeof(T));
+    }
+  }
+  // qg: the packed Q of the (b, hkv) at query 0; t_of(i): query of entry i
+  // of the item (-1 past its end); e0: the tile's first entry
+  template <typename TOf>
+  __device__ __forceinline__ void issue(T* stage, const T* qg, uint32_t rowbytes, int e0, TOf t_of) const {
+    const int t0 = __builtin_amdgcn_readfirstlane(t_of(e0));   // a tile's first entry exists
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int t = t_of(e0 + qj[j]);
+      t = t >= 0 ? t : t0;
+      lds_dma16_sbase(qg, (uint32_t)t * rowbytes + off[j], (char*)stage + 1024 * j);
+    }
+  }
+};
+
 // vector-memory stores of one tile's partials per wave (a lower bound:
 // float tiles and D < 32 count none, which only lengthens the waits): D / 16
 // staged row stores and the row statistics
@@ -64,7 +101,9 @@ constexpr int fwd_bo_stores() {
   return (sizeof(T) == 2 && D >= 32) ? D / 16 + 1 : 0;
 }
 
-template <typename T, int D>
+// GP: groups of G <= 10 heads take floor(32 / G) entries per tile
+// (FwdIssuerGP), the others two queries x 16 heads per head chunk.
+template <typename T, int D, bool GP>
 __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ vt, const int32_t* __restrict__ q_of_block,
                                                    const int4* __restrict__ items,
@@ -83,6 +122,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
   // 16-byte chunk c of row r sits at chunk c ^ (r % CPR)
   constexpr int CPR = D * (int)sizeof(T) / 16;
   __shared__ __align__(16) T sO[sizeof(T) == 2 ? 32 * D : 8];
+  __shared__ int64_t srow[GP ? 32 : 1];   // GP: each tile row's partial row (element offset / D), -1: none
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
   const int G = Hq / Hkv, NHC = (G + 15) / 16;
   const int NS = S * nsub;
@@ -135,7 +175,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) settle(vf[dt][kk]);
     __syncthreads();   // sent written
-    const int ntile = (cnt + 1) / 2;
+    const int QPT = GP ? 32 / G : 2;   // entries per tile
+    const int ntile = (cnt + QPT - 1) / QPT;
     const int total = ntile * NHC;
     auto entry = [&](int i, int& t, int& s) {
       if (i < cnt) {
@@ -147,21 +188,41 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         s = 0;
       }
     };
+    auto t_of = [&](int i) {
+      int t, s_;
+      entry(i, t, s_);
+      return t;
+    };
+    const int64_t qgrow = ((int64_t)b * Hkv + hkv) * T_ * G;   // packed row of query 0, head 0
     FwdIssuer<T, D> iss;
+    FwdIssuerGP<T, D> issg;
     int pix = 0, phc = 0, pti = 0;   // next tile to request
-    iss.prepare(G, lane);
+    if constexpr (GP)
+      issg.prepare(G, QPT, lane);
+    else
+      iss.prepare(G, lane);
     auto request = [&](T* stage) {
-      int tA, sA, tB, sB;
-      entry(2 * pti, tA, sA);
-      entry(2 * pti + 1, tB, sB);
-      const int64_t qrow0 = ((int64_t)b * Hkv + hkv) * T_ * G + phc * 16;   // packed row of query 0
-      iss.issue(stage, q + qrow0 * D, __builtin_amdgcn_readfirstlane(tA), __builtin_amdgcn_readfirstlane(tB), G);
-      ++pix;
-      if (++pti == ntile) {
-        pti = 0;
-        if (++phc < NHC) iss.prepare(G - phc * 16, lane);
+      if constexpr (GP) {
+        issg.issue(stage, q + qgrow * D, (uint32_t)(G * D * (int)sizeof(T)), QPT * pti, t_of);
+        ++pix;
+        if (++pti == ntile) pti = 0;   // one head chunk
+      } else {
+        int tA, sA, tB, sB;
+        entry(2 * pti, tA, sA);
+        entry(2 * pti + 1, tB, sB);
+        const int64_t qrow0 = qgrow + phc * 16;   // packed row of query 0, the chunk's first head
+        iss.issue(stage, q + qrow0 * D, __builtin_amdgcn_readfirstlane(tA), __builtin_amdgcn_readfirstlane(tB),
+                  G);
+        ++pix;
+        if (++pti == ntile) {
+          pti = 0;
+          if (++phc < NHC) iss.prepare(G - phc * 16, lane);
+        }
       }
     };
+    // GP: this lane's row n is entry n / G of the tile, head n % G (none from QPT G on)
+    const int pq = GP ? n / G : 0, pg = GP ? n % G : 0;
+    const bool preal = GP && n < QPT * G;
 #pragma unroll
     for (int p = 0; p < NST; ++p)
       if (p < total) request(sQ[p]);
@@ -175,12 +236,30 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
       __syncthreads();
       const T* tile = sQ[ix % NST];
       const int hc = ix / ntile, ti = ix % ntile;
-      int tA, sA, tB, sB;
-      entry(2 * ti, tA, sA);
-      entry(2 * ti + 1, tB, sB);
-      const int t = n < 16 ? tA : tB;      // this lane's row: query t, head hc*16 + (n & 15)
-      const int slot = (n < 16 ? sA : sB) * nsub + pass;
-      const int g = hc * 16 + (n & 15);
+      // this lane's row: query t, partial slot, head g; tlow: the tile's earliest query
+      int t, slot, g, tlow;
+      int tA = -1, sA = 0, tB = -1, sB = 0;
+      if constexpr (GP) {
+        int tl, sl;
+        entry(QPT * ti + pq, tl, sl);
+        t = preal ? tl : -1;
+        slot = sl * nsub + pass;
+        g = pg;
+        tlow = 0x7fffffff;
+        for (int e = 0; e < QPT; ++e) {
+          const int te = __builtin_amdgcn_readfirstlane(t_of(QPT * ti + e));
+          if (te < 0) break;   // entries past the item's end are the tile's last
+          tlow = te < tlow ? te : tlow;
+        }
+      } else {
+        entry(2 * ti, tA, sA);
+        entry(2 * ti + 1, tB, sB);
+        t = n < 16 ? tA : tB;   // query t, head hc*16 + (n & 15)
+        slot = (n < 16 ? sA : sB) * nsub + pass;
+        g = hc * 16 + (n & 15);
+        const int utA = __builtin_amdgcn_readfirstlane(tA), utB = __builtin_amdgcn_readfirstlane(tB);
+        tlow = utB >= 0 && utB < utA ? utB : utA;
+      }
       const bool rok = t >= 0 && g < G;
       Frag<T> qb[KS];
 #pragma unroll
@@ -194,11 +273,9 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         mma32(st[1], kf[1][s], qb[s]);
       }
       // raw scores; the scale (> 0) is applied to the row maximum and inside
-      // the exponent's fma.  Tiles whose 64 keys all exist and precede both
-      // queries need no per-element mask (the earlier query decides; the
-      // entries' order is not relied on).
-      const int utA = __builtin_amdgcn_readfirstlane(tA), utB = __builtin_amdgcn_readfirstlane(tB);
-      const int tlow = utB >= 0 && utB < utA ? utB : utA;
+      // the exponent's fma.  Tiles whose 64 keys all exist and precede every
+      // query of the tile need no per-element mask (the earliest query
+      // decides; the entries' order is not relied on).
       if (!(kbase + 64 <= kend && kbase + 63 <= tlow)) {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
@@ -249,6 +326,9 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         // place of row 0 (always a real row: query A, first head of the
         // chunk) and rewrites its bytes, so every store instruction issues.
         wave_fence();   // the previous tile's rows are read out
+        // GP: each row's partial row; a row that does not exist: -1
+        if constexpr (GP)
+          if (h == 0) srow[n] = rok ? (((int64_t)bh * T_ + t) * NS + slot) * G + g : -1;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -262,38 +342,53 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
             }
           }
         wave_fence();
-        // rows 0-15: query A, rows 16-31: query B, each 16 heads of G D
-        // contiguous from the (query, slot) row base.  Rows that do not
-        // exist repeat an existing row's bytes: a missing query B those of
-        // query A, a head past G head 0 of its query.  Every store
-        // instruction then issues, and for D >= 32 each one stays in one
-        // query's rows, so its base address is uniform.
-        const int uA = __builtin_amdgcn_readfirstlane(tA), uB = __builtin_amdgcn_readfirstlane(tB);
-        const int usA = __builtin_amdgcn_readfirstlane(sA), usB = __builtin_amdgcn_readfirstlane(sB);
-        const T* baseA = opart + ((((int64_t)bh * T_ + uA) * NS + usA * nsub + pass) * G + hc * 16) * D;
-        const T* baseB = uB >= 0 ? opart + ((((int64_t)bh * T_ + uB) * NS + usB * nsub + pass) * G + hc * 16) * D
-                                 : baseA;
-        const int grem = G - hc * 16;   // heads of the chunk that exist
         constexpr int RPI = 64 / CPR;   // rows per store instruction
         const int c = lane % CPR, rl = lane / CPR;
-        if (uB >= 0 && grem >= 16) {
-          // every row exists: the row and its base are fixed per instruction
+        if constexpr (GP) {
+          // row r of the tile goes to its own partial row.  A row that does not
+          // exist rewrites row 0's bytes (row 0: the tile's first entry, head 0,
+          // always exists), so every store instruction issues.
+          const int64_t r0 = srow[0];
 #pragma unroll
           for (int i = 0; i < 32 / RPI; ++i) {
             const int r = RPI * i + rl;
-            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (r * CPR + (c ^ (r % CPR))) * 8);
-            T* dst = const_cast<T*>(RPI * i < 16 ? baseA : baseB) + ((r & 15) * D + 8 * c);
-            *reinterpret_cast<bf16x8*>(dst) = v;
+            const int64_t ro = srow[r];
+            const int rr = ro >= 0 ? r : 0;
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+            *reinterpret_cast<bf16x8*>(opart + (ro >= 0 ? ro : r0) * D + 8 * c) = v;
           }
         } else {
+          // rows 0-15: query A, rows 16-31: query B, each 16 heads of G D
+          // contiguous from the (query, slot) row base.  Rows that do not
+          // exist repeat an existing row's bytes: a missing query B those of
+          // query A, a head past G head 0 of its query.  Every store
+          // instruction then issues, and for D >= 32 each one stays in one
+          // query's rows, so its base address is uniform.
+          const int uA = __builtin_amdgcn_readfirstlane(tA), uB = __builtin_amdgcn_readfirstlane(tB);
+          const int usA = __builtin_amdgcn_readfirstlane(sA), usB = __builtin_amdgcn_readfirstlane(sB);
+          const T* baseA = opart + ((((int64_t)bh * T_ + uA) * NS + usA * nsub + pass) * G + hc * 16) * D;
+          const T* baseB = uB >= 0 ? opart + ((((int64_t)bh * T_ + uB) * NS + usB * nsub + pass) * G + hc * 16) * D
+                                   : baseA;
+          const int grem = G - hc * 16;   // heads of the chunk that exist
+          if (uB >= 0 && grem >= 16) {
+            // every row exists: the row and its base are fixed per instruction
 #pragma unroll
-          for (int i = 0; i < 32 / RPI; ++i) {
-            const int r = RPI * i + rl;
-            int rr = uB < 0 && r >= 16 ? r - 16 : r;
-            rr = (rr & 15) < grem ? rr : rr & 16;
-            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
-            T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
-            *reinterpret_cast<bf16x8*>(dst) = v;
+            for (int i = 0; i < 32 / RPI; ++i) {
+              const int r = RPI * i + rl;
+              const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (r * CPR + (c ^ (r % CPR))) * 8);
+              T* dst = const_cast<T*>(RPI * i < 16 ? baseA : baseB) + ((r & 15) * D + 8 * c);
+              *reinterpret_cast<bf16x8*>(dst) = v;
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 32 / RPI; ++i) {
+              const int r = RPI * i + rl;
+              int rr = uB < 0 && r >= 16 ? r - 16 : r;
+              rr = (rr & 15) < grem ? rr : rr & 16;
+              const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+              T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
+              *reinterpret_cast<bf16x8*>(dst) = v;
+            }
           }
         }
         if (rok && h == 0) {
@@ -496,17 +591,20 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
   const size_t grid = cap * nsub < 8192 ? cap * nsub : 8192;
   const int Lp = padded_len(T);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
+  // groups of up to 10 heads pack floor(32 / G) >= 3 entries into a tile
+  const bool gp = Hq / Hkv <= kGroupPackMaxG;
   NSA_DISPATCH_D(D, {
-    if (dtype == NSA_BF16)
-      k_sel_fwd_bo<bf16, DD><<<(unsigned)grid, 64, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)vt,
-                                                           q_of_block, items, n_items, (bf16*)o_part,
-                                                           (float2*)ml_part, Hq, Hkv, T, S, n_blk, block_size, Lp,
-                                                           nsub, sl2);
-    else
-      k_sel_fwd_bo<float, DD><<<(unsigned)grid, 64, 0, s>>>((const float*)q, (const float*)k, (const float*)vt,
-                                                            q_of_block, items, n_items, (float*)o_part,
-                                                            (float2*)ml_part, Hq, Hkv, T, S, n_blk, block_size, Lp,
-                                                            nsub, sl2);
+    if (dtype == NSA_BF16) {
+      auto kern = gp ? k_sel_fwd_bo<bf16, DD, true> : k_sel_fwd_bo<bf16, DD, false>;
+      kern<<<(unsigned)grid, 64, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)vt, q_of_block, items,
+                                         n_items, (bf16*)o_part, (float2*)ml_part, Hq, Hkv, T, S, n_blk,
+                                         block_size, Lp, nsub, sl2);
+    } else {
+      auto kern = gp ? k_sel_fwd_bo<float, DD, true> : k_sel_fwd_bo<float, DD, false>;
+      kern<<<(unsigned)grid, 64, 0, s>>>((const float*)q, (const float*)k, (const float*)vt, q_of_block, items,
+                                         n_items, (float*)o_part, (float2*)ml_part, Hq, Hkv, T, S, n_blk,
+                                         block_size, Lp, nsub, sl2);
+    }
   });
   return nsa_launch_status();
 }

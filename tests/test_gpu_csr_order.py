@@ -26,11 +26,14 @@ def _reversed_blocks(q_of_block, offsets):
     return rev
 
 
+@pytest.mark.parametrize("heads", [(16, 1), (12, 2)], ids=["G16", "G6"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-def test_unsorted_csr_matches_sorted(dtype):
+def test_unsorted_csr_matches_sorted(dtype, heads):
+    """G16: two queries per row tile; G6: five entries per tile, so the
+    reversal also changes which entries share a tile."""
     import nsa_hip_ops as ops
     dev = require_gpu()
-    B, Hq, Hkv, T, D, bs, S = 1, 16, 1, 1024, 64, 64, 8
+    B, Hq, Hkv, T, D, bs, S = 1, heads[0], heads[1], 1024, 64, 64, 8
     log(f"csr order: B{B} Hq{Hq} Hkv{Hkv} T{T} D{D} bs{bs} S{S} {dtype}")
     q = randn((B, Hq, T, D), 1, dtype).to(dev)
     k = randn((B, Hkv, T, D), 2, dtype).to(dev)
