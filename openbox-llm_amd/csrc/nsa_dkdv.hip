@@ -558,8 +558,8 @@ template <typename T, int D> struct PWave {
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) settle(kf[s]);
   }
-  template <bool MASK>
-  __device__ __forceinline__ void tile(const KvStage<T, D>& s, const Frag<T> (&qa)[C::KS], bool visA, bool visB,
+  template <bool MASK, typename Vis>
+  __device__ __forceinline__ void tile(const KvStage<T, D>& s, const Frag<T> (&qa)[C::KS], const Vis& vis,
                                        float sl2, int lane, uint32_t* pb) {
     const int h = lane >> 5;
     Frag<T> ta[C::DT][2];
@@ -583,7 +583,7 @@ template <typename T, int D> struct PWave {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       float p = fast_exp2(sacc[r] * sl2 - s.c[acc_elem(h, r)]);
-      if (MASK) p = (r < 8 ? visA : visB) ? p : 0.0f;
+      if (MASK) p = vis(r) ? p : 0.0f;
       P[r] = p;
     }
     Frag<T> pf[2];
@@ -692,22 +692,98 @@ template <typename T, int D, int NTH, typename QSrc> struct SplitReq {
   }
 };
 
+// The query-tile requests of a split walk over flat rows (groups of G < 16
+// heads, where two queries x 16 head slots would leave 32 - 2 G rows of a
+// tile empty): the rows (t, g) of the group are numbered t G + g and tile i
+// holds rows rlo + 32 i .. rlo + 32 i + 31, read from the [B, Hq, T, D]
+// layout (row (t, g) at (g T + t) D from the group's first row).  Each lane
+// keeps the query and head of its loads' rows and of its statistics row and
+// moves them 32 rows on per request.  Rows of queries past thi (the
+// workgroup's last query) read row (thi, g) with the row offset +inf, so
+// their P and dS are exactly 0.  Same loads per tile as KvIssuer.
+template <typename T, int D, int NTH> struct FlatReq {
+  using C = Tile32<T, D>;
+  static constexpr int LPT = dma_uniform_loads<NTH, C::ROW_CHUNKS>();
+  const T* qg;          // Q / dO of the group: query 0, head 0
+  const T* dg;
+  const float* sp;      // c (lanes < 32) or delta (lanes >= 32) of the group, [G][T]
+  int T_, G, thi, step_g, step_t;   // 32 rows = step_t queries + step_g heads
+  int tid;
+  uint32_t col[LPT];    // column byte offset of this lane's chunk of load j
+  int tj[LPT], gj[LPT];  // query / head of that chunk's row in the next tile
+  int ts, gs;           // query / head of this lane's statistics row in the next tile
+
+  __device__ __forceinline__ void init(const QSide<T>& x, int b, int hkv, int rlo, int thi_, int tid_) {
+    G = x.G;
+    T_ = x.T_;
+    thi = thi_;
+    tid = tid_;
+    step_t = 32 / G;
+    step_g = 32 - step_t * G;
+    const int64_t g0 = (int64_t)b * x.Hq + (int64_t)hkv * G;   // the group's first head
+    qg = x.q + g0 * T_ * D;
+    dg = x.dout + g0 * T_ * D;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    sp = (lane < 32 ? x.c : x.dot) + g0 * T_;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      int r, cc;
+      row_chunk<T, D>(KvIssuer<T, D, NTH>::first_chunk(j, w) + lane, r, cc);
+      col[j] = (uint32_t)(cc * 16);
+      tj[j] = (rlo + r) / G;
+      gj[j] = rlo + r - tj[j] * G;
+    }
+    ts = (rlo + (lane & 31)) / G;
+    gs = rlo + (lane & 31) - ts * G;
+  }
+  __device__ __forceinline__ void advance(int& t, int& g) const {
+    g += step_g;
+    t += step_t;
+    if (g >= G) {
+      g -= G;
+      ++t;
+    }
+  }
+  __device__ __forceinline__ void request(KvStage<T, D>& s) {
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) {
+      const int t = tj[j] <= thi ? tj[j] : thi;
+      const uint32_t v = ((uint32_t)gj[j] * (uint32_t)T_ + (uint32_t)t) * (uint32_t)(D * sizeof(T)) + col[j];
+      const int first = KvIssuer<T, D, NTH>::first_chunk(j, w);
+      lds_dma16_sbase(qg, v, (char*)s.qr + 16 * first);
+      lds_dma16_sbase(dg, v, (char*)s.dr + 16 * first);
+      advance(tj[j], gj[j]);
+    }
+    {
+      // lanes 0-31: c of row lane, lanes 32-63: delta of row lane - 32
+      const bool real = lane >= 32 || ts <= thi;
+      const int t = ts <= thi ? ts : thi;
+      lds_dma4(real ? sp + (int64_t)gs * T_ + t : &kAbsentRow, s.c);
+      advance(ts, gs);
+    }
+  }
+};
+
 // One walk per role (the roles' registers are then never live at once).
 // Per tile: [role work before the barrier]; wait for tile it+1; barrier;
 // [role work after it]; refill the stage of tile it.  P goes through
 // pbuf[it & 1].
-template <typename T, int D, int NTH, typename QSrc, typename Vis>
+// make_rq(): the tile requests (SplitReq, FlatReq), made in the same order
+// by every wave (built inside the walk, whose registers they share); vis(stage,
+// it, mask): the P-wave's visibility of tile it (VisPair, VisBits) and
+// whether it needs the per-element test.
+template <typename T, int D, int NTH, typename MakeReq, typename Vis>
 __device__ __forceinline__ void walk_p(PWave<T, D>& pw, KvStage<T, D> (&stg)[kSplitStages], PTile* pbuf,
-                                       const QSide<T>& x, int b, int hkv, int ntile, QSrc qsrc, Vis vis, float sl2,
-                                       int tid) {
+                                       MakeReq make_rq, int total, Vis vis, float sl2, int tid) {
   using C = Tile32<T, D>;
   constexpr int NST = kSplitStages;
   constexpr int LT = kv_tile_loads<T, D, NTH>();
   static_assert((NST - 1) * LT < 64, "in-flight operations exceed the vmcnt range");
-  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
+  total = __builtin_amdgcn_readfirstlane(total);
   if (total == 0) return;
   const int lane = tid & 63, h = lane >> 5, n = lane & 31;
-  SplitReq<T, D, NTH, QSrc> rq(x, b, hkv, ntile, qsrc, tid);
+  auto rq = make_rq();
 #pragma unroll
   for (int p = 0; p < NST; ++p)
     if (p < total) rq.request(stg[p]);
@@ -727,13 +803,12 @@ __device__ __forceinline__ void walk_p(PWave<T, D>& pw, KvStage<T, D> (&stg)[kSp
       const int it = it0 + p;
       if (it >= total) break;
       const KvStage<T, D>& s = stg[p];
-      const int tA = __builtin_amdgcn_readfirstlane(s.meta[0]), tB = __builtin_amdgcn_readfirstlane(s.meta[1]);
-      bool mask, visA, visB;
-      vis(tA, tB, mask, visA, visB);
+      bool mask;
+      const auto v = vis(s, it, mask);
       if (mask)
-        pw.template tile<true>(s, qa, visA, visB, sl2, lane, pbuf[p & 1]);
+        pw.template tile<true>(s, qa, v, sl2, lane, pbuf[p & 1]);
       else
-        pw.template tile<false>(s, qa, true, true, sl2, lane, pbuf[p & 1]);
+        pw.template tile<false>(s, qa, v, sl2, lane, pbuf[p & 1]);
       if (it + NST - 1 < total)
         vm_wait<(NST - 2) * LT>();
       else
@@ -748,16 +823,16 @@ __device__ __forceinline__ void walk_p(PWave<T, D>& pw, KvStage<T, D> (&stg)[kSp
   }
 }
 
-template <typename T, int D, int NTH, bool SPLIT, typename QSrc>
+template <typename T, int D, int NTH, bool SPLIT, typename MakeReq>
 __device__ __forceinline__ void walk_s(SWave<T, D>& sw, KvStage<T, D> (&stg)[kSplitStages], const PTile* pbuf,
-                                       const QSide<T>& x, int b, int hkv, int ntile, QSrc qsrc, int tid) {
+                                       MakeReq make_rq, int total, int tid) {
   using C = Tile32<T, D>;
   constexpr int NST = kSplitStages;
   constexpr int LT = kv_tile_loads<T, D, NTH>();
-  const int total = __builtin_amdgcn_readfirstlane(ntile * x.NHC);
+  total = __builtin_amdgcn_readfirstlane(total);
   if (total == 0) return;
   const int lane = tid & 63, h = lane >> 5, n = lane & 31;
-  SplitReq<T, D, NTH, QSrc> rq(x, b, hkv, ntile, qsrc, tid);
+  auto rq = make_rq();
 #pragma unroll
   for (int p = 0; p < NST; ++p)
     if (p < total) rq.request(stg[p]);
@@ -992,8 +1067,10 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[Tile32<T, D>::DT]
 }
 
 // k_range_dkdv32 with the role-split walk: 2 NW waves, waves < NW the
-// P-waves of key groups 0 .. NW-1, the others their dS-waves.
-template <typename T, int D, int NW>
+// P-waves of key groups 0 .. NW-1, the others their dS-waves.  FLAT: the
+// query tiles are 32 consecutive rows t G + g of the group (FlatReq, groups
+// of G < 16 heads), else two queries x 16 heads of a head chunk (SplitReq).
+template <typename T, int D, int NW, bool FLAT>
 __global__ __launch_bounds__(128 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                     const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
@@ -1071,37 +1148,77 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
   thi = thi < T_ - 1 ? thi : T_ - 1;
   if (tlo > thi) return;   // uniform over the workgroup
   const int64_t kvoff = (int64_t)bh * Lk * D;
-  const int ntile = (thi - tlo) / 2 + 1;
   const int wlast = kw + 31;   // last key of the group (may pass Lk: those columns are never stored)
-  auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
-    tA = tlo + 2 * i;
-    tB = tA + 1 <= thi ? tA + 1 : -1;
-    sA = sB = 0;
-  };
-  auto vis = [&](int tA, int tB, bool& mask, bool& visA, bool& visB) {
-    const int tb = tB >= 0 ? tB : tA;
-    if (mode == NSA_MODE_WINDOW) {
-      mask = !(tA >= wlast && tb - window < kw);
-      visA = key <= tA && key > tA - window;
-      visB = key <= tb && key > tb - window;
-    } else {
-      mask = !(wlast * cd + cl - 1 <= tA);
-      visA = key * cd + cl - 1 <= tA;
-      visB = key * cd + cl - 1 <= tb;
-    }
-  };
   const int key_safe = key_ok ? key : Lk - 1;
   const bool atomic = mode == NSA_MODE_COMPRESS;
-  if (pwave) {
-    PWave<T, D> pw;
-    pw.init(k + kvoff, key_safe, h);
-    walk_p<T, D, NTH>(pw, stg, pbuf[w], x, b, hkv, ntile, qsrc, vis, sl2, tid);
-    if (key_ok) store_rows<T, D>(pw.dv, dv + kvoff + (int64_t)key * D, 1.0f, atomic, h);
+  // the two roles' walks over the workgroup's query tiles
+  auto run = [&](auto make_rq, int total, auto vis) {
+    if (pwave) {
+      PWave<T, D> pw;
+      pw.init(k + kvoff, key_safe, h);
+      walk_p<T, D, NTH>(pw, stg, pbuf[w], make_rq, total, vis, sl2, tid);
+      if (key_ok) store_rows<T, D>(pw.dv, dv + kvoff + (int64_t)key * D, 1.0f, atomic, h);
+    } else {
+      SWave<T, D> sw;
+      sw.init(v + kvoff, key_safe, h);
+      walk_s<T, D, NTH, false>(sw, stg, pbuf[w], make_rq, total, tid);
+      if (key_ok) store_rows<T, D>(sw.dk, dk + kvoff + (int64_t)key * D, scale, atomic, h);
+    }
+  };
+  if constexpr (FLAT) {
+    // rows tlo G .. thi G + G - 1 of the group; the keys a row's query sees
+    // form a contiguous run of rows for each key: [row_lo, row_hi)
+    const int G = x.G;
+    const int rlo = tlo * G, rhi = thi * G + G - 1;
+    auto make_rq = [&]() {
+      FlatReq<T, D, NTH> rq;
+      rq.init(x, b, hkv, rlo, thi, tid);
+      return rq;
+    };
+    auto vis = [&](const KvStage<T, D>&, int it, bool& mask) {
+      const int R0 = rlo + 32 * it;
+      const int tf = R0 / G;                                   // the tile's first query
+      const int tl = (R0 + 31 < rhi ? R0 + 31 : rhi) / G;      // and last (within the range)
+      int lo, hi;   // rows of the tile that see this lane's key
+      if (mode == NSA_MODE_WINDOW) {
+        mask = !(tf >= wlast && tl - window < kw);
+        lo = key * G - R0;                  // query >= key
+        hi = (key + window) * G - R0;       // query < key + window
+      } else {
+        mask = !(wlast * cd + cl - 1 <= tf);
+        lo = (key * cd + cl - 1) * G - R0;  // query >= key cd + cl - 1
+        hi = 32;
+      }
+      lo = lo < 0 ? 0 : (lo > 32 ? 32 : lo);
+      hi = hi < 0 ? 0 : (hi > 32 ? 32 : hi);
+      const uint64_t bits = key_ok && lo < hi ? ((1ull << hi) - 1ull) & ~((1ull << lo) - 1ull) : 0ull;
+      return VisBits{(uint32_t)bits >> (8 * h)};
+    };
+    run(make_rq, (rhi - rlo) / 32 + 1, vis);
   } else {
-    SWave<T, D> sw;
-    sw.init(v + kvoff, key_safe, h);
-    walk_s<T, D, NTH, false>(sw, stg, pbuf[w], x, b, hkv, ntile, qsrc, tid);
-    if (key_ok) store_rows<T, D>(sw.dk, dk + kvoff + (int64_t)key * D, scale, atomic, h);
+    auto qsrc = [&](int i, int& tA, int& tB, int& sA, int& sB) {
+      tA = tlo + 2 * i;
+      tB = tA + 1 <= thi ? tA + 1 : -1;
+      sA = sB = 0;
+    };
+    auto vis = [&](const KvStage<T, D>& s, int, bool& mask) {
+      const int tA = __builtin_amdgcn_readfirstlane(s.meta[0]), tB = __builtin_amdgcn_readfirstlane(s.meta[1]);
+      const int tb = tB >= 0 ? tB : tA;
+      VisPair v;
+      if (mode == NSA_MODE_WINDOW) {
+        mask = !(tA >= wlast && tb - window < kw);
+        v.a = key <= tA && key > tA - window;
+        v.b = key <= tb && key > tb - window;
+      } else {
+        mask = !(wlast * cd + cl - 1 <= tA);
+        v.a = key * cd + cl - 1 <= tA;
+        v.b = key * cd + cl - 1 <= tb;
+      }
+      return v;
+    };
+    const int ntile = (thi - tlo) / 2 + 1;
+    auto make_rq = [&]() { return SplitReq<T, D, NTH, decltype(qsrc)>(x, b, hkv, ntile, qsrc, tid); };
+    run(make_rq, ntile * x.NHC, vis);
   }
 }
 
@@ -1418,11 +1535,13 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   if (grid == 0) return NSA_OK;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   NSA_DISPATCH_D(D, {
-    if (dtype == NSA_BF16)
-      k_range_dkdv_split<bf16, DD, NW><<<(unsigned)grid, 128 * NW, 0, s>>>(
-          mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, dk, dv, Hq, Hkv, T,
-          Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
-    else
+    if (dtype == NSA_BF16) {
+      // groups of G < 16 heads: query tiles of 32 consecutive (query, head) rows
+      auto kern = Hq / Hkv < 16 ? k_range_dkdv_split<bf16, DD, NW, true> : k_range_dkdv_split<bf16, DD, NW, false>;
+      kern<<<(unsigned)grid, 128 * NW, 0, s>>>(mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k,
+                                               (const bf16*)v, dk, dv, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block,
+                                               cmp_stride, nbh, chs, spl, sl2, scale);
+    } else
       k_range_dkdv32<float, DD, NW><<<(unsigned)grid, 64 * NW, 0, s>>>(
           mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, Hq, Hkv,
           T, Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);

@@ -98,6 +98,62 @@ __device__ __forceinline__ FullSpan full_span(int mode, int tw0, int qpw, int T_
   return f;
 }
 
+// Rows of a range launch.  Head-chunk rows (groups of 16 or more heads): a
+// workgroup owns 8 NT consecutive queries of one head chunk and a wave 2 NT of
+// them; row n of a wave's tile nt is query tw0 + 2 nt + (n >> 4), head
+// hc 16 + (n & 15) of the group.  Flat rows (groups of G < 16 heads, NT = 1):
+// the rows (t, g) of one (b, hkv) are numbered t G + g, a workgroup owns 128
+// consecutive ones and a wave 32 (row n: rw0 + n), so only the sequence's last
+// tile has empty rows where a head chunk would leave 16 - G of every 16 empty.
+// qpb / qpw count the queries the workgroup's / wave's rows touch; a wave past
+// the last row gets tw0 = T (no valid row).
+struct RangeRows {
+  int tb0, qpb, tw0, qpw, rw0;
+};
+template <bool FLAT, int NT>
+__device__ __forceinline__ bool range_rows(RangeRows& r, int qt, int w, int G, int T_) {
+  if constexpr (FLAT) {
+    static_assert(NT == 1, "flat rows: one 32-row tile per wave");
+    const int nrow = T_ * G;
+    const int rb0 = qt * 128;
+    if (rb0 >= nrow) return false;
+    r.tb0 = rb0 / G;
+    r.qpb = (rb0 + 127 < nrow ? rb0 + 127 : nrow - 1) / G - r.tb0 + 1;
+    r.rw0 = rb0 + 32 * w;
+    if (r.rw0 < nrow) {
+      r.tw0 = r.rw0 / G;
+      r.qpw = (r.rw0 + 31 < nrow ? r.rw0 + 31 : nrow - 1) / G - r.tw0 + 1;
+    } else {
+      r.tw0 = T_;
+      r.qpw = 1;
+    }
+  } else {
+    r.tb0 = qt * 8 * NT;
+    if (r.tb0 >= T_) return false;
+    r.qpb = 8 * NT;
+    r.tw0 = r.tb0 + w * 2 * NT;
+    r.qpw = 2 * NT;
+    r.rw0 = 0;
+  }
+  return true;
+}
+// query and head (within the group) of row n of a wave's tile nt
+template <bool FLAT>
+__device__ __forceinline__ void range_row(const RangeRows& r, const RangeMap& mp, int nt, int n, int& t, int& g) {
+  if constexpr (FLAT) {
+    const int R = r.rw0 + n;
+    t = R / mp.G;
+    g = R - t * mp.G;
+  } else {
+    t = r.tw0 + 2 * nt + (n >> 4);
+    g = mp.hc * 16 + (n & 15);
+  }
+}
+// query tiles of a range launch per (b, hkv, head chunk)
+__host__ __device__ inline int range_qtiles(bool flat, int T, int G, int NT) {
+  return flat ? (T * G + 127) / 128 : (T + 8 * NT - 1) / (8 * NT);
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -126,11 +182,11 @@ template <typename T, typename TO> struct FwdExtras {
 // The wave's own output rows (this branch, unnormalised acc with the row
 // statistics l_, m_) go through LDS so that every row is handled in 8-element
 // chunks: lane (row sub-index, chunk) per pass.
-template <typename T, typename TO, int D>
+template <typename T, typename TO, int D, bool FLAT>
 __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32x16 (&acc)[Tile32<T, D>::DT][1],
                                             float l_row, float m_row, bool any_key, bool rok, int64_t row, TO* o,
-                                            float* lse, char* smem, int w, int lane, int tw0, const RangeMap& mp,
-                                            int Hq, int Hkv, int T_) {
+                                            float* lse, char* smem, int w, int lane, const RangeRows& rr,
+                                            const RangeMap& mp, int Hq, int Hkv, int T_) {
   using C = Tile32<T, D>;
   constexpr int FIN_PITCH = D + 4;
   const int h = lane >> 5, n = lane & 31;
@@ -157,8 +213,8 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
   const int64_t bh = (int64_t)mp.b * Hkv + mp.hkv;
   for (int r0 = 0; r0 < 32; r0 += RPI) {
     const int r = r0 + rsub;
-    const int t = tw0 + (r >> 4);
-    const int gl = mp.hc * 16 + (r & 15);   // head within the group
+    int t, gl;   // query and head within the group
+    range_row<FLAT>(rr, mp, 0, r, t, gl);
     if (t >= T_ || gl >= G) continue;
     const int64_t orow = ((int64_t)mp.b * Hq + mp.hkv * G + gl) * T_ + t;
     // this branch's row chunk, rounded as stored
@@ -313,14 +369,13 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
       for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], va[dt][s], pf[nt][s]);
 }
 
-template <typename T, int D, int NT, typename TO>
+template <typename T, int D, int NT, typename TO, bool FLAT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_fwd32(int mode, const T* __restrict__ q, const T* __restrict__ k,
                                                      const T* __restrict__ vt, TO* __restrict__ o,
                                                      float* __restrict__ lse, int Hq, int Hkv, int T_, int Lk,
                                                      int Lp, int nqt, int window, int cl, int cd, float sl2,
                                                      const FwdExtras<T, TO> fin_args) {
   using C = Tile32<T, D>;
-  constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 4;   // key tiles in flight + 1
   // one LDS buffer: the key stages during the walk, then (finishing rows)
   // each wave's float output tile [32][D + 4]
@@ -338,32 +393,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int qt = (int)(wg % nqt);
   if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first
   const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
-  const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
-  if (tb0 >= T_) return;
-  const RangeSpan sp = range_span(mode, tb0, QPB, tw0, QPW, T_, Lk, window, cl, cd);
-  const FullSpan fs = full_span(mode, tw0, QPW, T_, Lk, window, cl, cd);
+  RangeRows rr;
+  if (!range_rows<FLAT, NT>(rr, qt, w, mp.G, T_)) return;
+  const int tw0 = rr.tw0;
+  const RangeSpan sp = range_span(mode, rr.tb0, rr.qpb, tw0, rr.qpw, T_, Lk, window, cl, cd);
+  const FullSpan fs = full_span(mode, tw0, rr.qpw, T_, Lk, window, cl, cd);
   const int bh = mp.b * Hkv + mp.hkv;
   const T* kbase = k + (int64_t)bh * Lk * D;
   const T* vtbase = vt + (int64_t)bh * D * Lp;
 
-  const int hd = n & 15;
-  const bool hok = mp.hc * 16 + hd < mp.G;
-  const int hsafe = hok ? hd : 0;
   Frag<T> qf[NT][C::KS];
   int lo[NT], hi[NT];
   int64_t row[NT];
   bool rok[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int t = tw0 + 2 * nt + (n >> 4);
-    rok[nt] = hok && t < T_;
-    row[nt] = ((int64_t)mp.b * Hq + mp.head0 + hd) * T_ + t;
-    const int64_t srow = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + (t < T_ ? t : T_ - 1);
+    int t, g;   // this lane's row: query t, head g of the group
+    range_row<FLAT>(rr, mp, nt, n, t, g);
+    rok[nt] = g < mp.G && t < T_;
+    const int head = mp.hkv * mp.G + g;
+    row[nt] = ((int64_t)mp.b * Hq + head) * T_ + t;
+    const int64_t srow = ((int64_t)mp.b * Hq + (rok[nt] ? head : mp.hkv * mp.G)) * T_ + (t < T_ ? t : T_ - 1);
     visible_range(mode, t < T_ ? t : T_ - 1, Lk, window, cl, cd, lo[nt], hi[nt]);
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) qf[nt][s].load(q + srow * D + 16 * s + 8 * h);
     if (fin_args.q_packed != nullptr && rok[nt]) {
-      T* dst = fin_args.q_packed + (((int64_t)bh * T_ + t) * mp.G + mp.hc * 16 + hd) * D;
+      T* dst = fin_args.q_packed + (((int64_t)bh * T_ + t) * mp.G + g) * D;
 #pragma unroll
       for (int s = 0; s < C::KS; ++s) qf[nt][s].store(dst + 16 * s + 8 * h);
     }
@@ -408,8 +463,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   if (fin_args.opart != nullptr) {
     static_assert(NT == 1, "one 32-row tile per wave is staged");
-    finish_rows<T, TO, D>(fin_args, acc, l_[0], m_[0], lo[0] <= hi[0], rok[0], row[0], o, lse, smem, w, lane,
-                      tw0, mp, Hq, Hkv, T_);
+    finish_rows<T, TO, D, FLAT>(fin_args, acc, l_[0], m_[0], lo[0] <= hi[0], rok[0], row[0], o, lse, smem, w,
+                                lane, rr, mp, Hq, Hkv, T_);
     return;
   }
 #pragma unroll
@@ -506,7 +561,7 @@ __device__ __forceinline__ void dq_tile(f32x16 (&acc)[DT][NT], const Frag<T> (&q
       for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], ka[dt][s], dsf[nt][s]);
 }
 
-template <typename T, int D, int NT>
+template <typename T, int D, int NT, bool FLAT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_range_dq32(int mode, const T* __restrict__ q, const T* __restrict__ k,
                                                     const T* __restrict__ v, const T* __restrict__ kt,
                                                     const T* __restrict__ dout, const float* __restrict__ lse,
@@ -517,7 +572,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                     const T* __restrict__ sel_part, const int32_t* __restrict__ sel_idx,
                                                     T* __restrict__ dq_out, int S, int sel_L, DqWindow<T> w2) {
   using C = Tile32<T, D>;
-  constexpr int QPW = 2 * NT, QPB = 4 * QPW;
   constexpr int NST = 3;   // key tiles in flight + 1
   // one LDS buffer: the key stages during the walk, then (finishing rows)
   // each wave's float dQ tile [32][D + 4]
@@ -533,23 +587,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int qt = (int)(wg % nqt);
   if (mode == NSA_MODE_COMPRESS) qt = nqt - 1 - qt;   // long rows first, round-robin (as the forward)
   const RangeMap mp = range_map(wg / nqt, Hq, Hkv);
-  const int tb0 = qt * QPB, tw0 = tb0 + w * QPW;
-  if (tb0 >= T_) return;
+  RangeRows rr;
+  if (!range_rows<FLAT, NT>(rr, qt, w, mp.G, T_)) return;
+  const int tw0 = rr.tw0;
   const int bh = mp.b * Hkv + mp.hkv;
 
-  const int hd = n & 15;
-  const bool hok = mp.hc * 16 + hd < mp.G;
-  const int hsafe = hok ? hd : 0;
   Frag<T> qf[NT][C::KS], df[NT][C::KS];
   int64_t row[NT], srow[NT];
+  int trow[NT];   // this lane's query per tile
   bool rok[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int t = tw0 + 2 * nt + (n >> 4);
+    int t, g;   // this lane's row: query t, head g of the group
+    range_row<FLAT>(rr, mp, nt, n, t, g);
     const int tc = t < T_ ? t : T_ - 1;
-    rok[nt] = hok && t < T_;
-    row[nt] = ((int64_t)mp.b * Hq + mp.head0 + hd) * T_ + t;
-    srow[nt] = ((int64_t)mp.b * Hq + mp.head0 + hsafe) * T_ + tc;
+    trow[nt] = t;
+    rok[nt] = g < mp.G && t < T_;
+    const int head = mp.hkv * mp.G + g;
+    row[nt] = ((int64_t)mp.b * Hq + head) * T_ + t;
+    srow[nt] = ((int64_t)mp.b * Hq + (rok[nt] ? head : mp.hkv * mp.G)) * T_ + tc;
 #pragma unroll
     for (int s = 0; s < C::KS; ++s) {
       qf[nt][s].load(q + srow[nt] * D + 16 * s + 8 * h);
@@ -571,13 +627,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // one branch's walk over its keys, accumulating into acc
   auto walk = [&](int bmode, const T* k_, const T* v_, const T* kt_, const float* lse_, const float* dot_,
                   const float* rs_, int Lk_, int Lp_) {
-    const RangeSpan sp = range_span(bmode, tb0, QPB, tw0, QPW, T_, Lk_, window, cl, cd);
-    const FullSpan fs = full_span(bmode, tw0, QPW, T_, Lk_, window, cl, cd);
+    const RangeSpan sp = range_span(bmode, rr.tb0, rr.qpb, tw0, rr.qpw, T_, Lk_, window, cl, cd);
+    const FullSpan fs = full_span(bmode, tw0, rr.qpw, T_, Lk_, window, cl, cd);
     int lo[NT], hi[NT];
     float c[NT], dlt[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const int t = tw0 + 2 * nt + (n >> 4);
+      const int t = trow[nt];
       visible_range(bmode, t < T_ ? t : T_ - 1, Lk_, window, cl, cd, lo[nt], hi[nt]);
       const float rs = rs_ != nullptr ? rs_[srow[nt]] : 1.0f;
       c[nt] = lse_[srow[nt]] * kLog2e - __log2f(rs);
@@ -635,8 +691,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int G = mp.G;
     for (int r0 = 0; r0 < 32; r0 += RPI) {
       const int r = r0 + rsub;
-      const int t = tw0 + (r >> 4);
-      const int gl = mp.hc * 16 + (r & 15);   // head within the group
+      int t, gl;   // query and head within the group
+      range_row<FLAT>(rr, mp, 0, r, t, gl);
       if (t >= T_ || gl >= G) continue;
       const int64_t orow = ((int64_t)mp.b * Hq + mp.hkv * G + gl) * T_ + t;
       float v[8];
@@ -729,13 +785,15 @@ static int range_fwd_launch(int mode, const void* q, const void* k, const void* 
   const int Lp = padded_len(Lk);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
   constexpr int NT = RangeNT<E>::fwd;
-  const int nqt = (T + 8 * NT - 1) / (8 * NT);
+  const bool flat = Hq / Hkv < 16;   // flat rows: no empty head slots
+  NSA_CHECK((int64_t)T * (Hq / Hkv) < (1ll << 31), NSA_ERR_SHAPE);
+  const int nqt = range_qtiles(flat, T, Hq / Hkv, NT);
   const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   NSA_DISPATCH_D(D, {
-    k_range_fwd32<E, DD, NT, TO><<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)vt, (TO*)o,
-                                                            lse, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block,
-                                                            cmp_stride, sl2, fin);
+    auto kern = flat ? k_range_fwd32<E, DD, NT, TO, true> : k_range_fwd32<E, DD, NT, TO, false>;
+    kern<<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)vt, (TO*)o, lse, Hq, Hkv, T, Lk,
+                                        Lp, nqt, window, cmp_block, cmp_stride, sl2, fin);
   });
   return nsa_launch_status();
 }
@@ -751,14 +809,17 @@ static int range_dq_launch(int mode, const void* q, const void* k, const void* v
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
   constexpr int NT = RangeNT<E>::dq;
-  const int nqt = (T + 8 * NT - 1) / (8 * NT);
+  const bool flat = Hq / Hkv < 16;   // flat rows: no empty head slots
+  NSA_CHECK((int64_t)T * (Hq / Hkv) < (1ll << 31), NSA_ERR_SHAPE);
+  const int nqt = range_qtiles(flat, T, Hq / Hkv, NT);
   const int64_t grid = (int64_t)B * Hkv * NHC * nqt;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   NSA_DISPATCH_D(D, {
-    k_range_dq32<E, DD, NT><<<(unsigned)grid, 256, 0, s>>>(
-        mode, (const E*)q, (const E*)k, (const E*)v, (const E*)kt, (const E*)dout, lse, dot, rowscale, dq,
-        accumulate, Hq, Hkv, T, Lk, Lp, nqt, window, cmp_block, cmp_stride, sl2, scale, (const E*)sel_part,
-        sel_idx, (E*)dq_out, S, sel_block, w2);
+    auto kern = flat ? k_range_dq32<E, DD, NT, true> : k_range_dq32<E, DD, NT, false>;
+    kern<<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)v, (const E*)kt, (const E*)dout,
+                                        lse, dot, rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window,
+                                        cmp_block, cmp_stride, sl2, scale, (const E*)sel_part, sel_idx, (E*)dq_out,
+                                        S, sel_block, w2);
   });
   return nsa_launch_status();
 }

@@ -16,7 +16,15 @@ from nsa_testlib import (G16_CONFIGS, REF_CONFIGS, assert_close, cfg_id, log, ma
 pytestmark = pytest.mark.gpu
 
 DTYPES = [torch.float32, torch.bfloat16]
-CONFIGS = REF_CONFIGS + G16_CONFIGS
+# groups of G <= 10 heads: several selection entries per row tile (floor(32 / G)),
+# with partly filled tiles (G = 5, 7, 10), two 64-key passes and ragged passes;
+# the range branches number the rows (t, g) of a group t G + g (flat rows)
+GP_CONFIGS = [dict(B=1, Hq=12, Hkv=2, D=64, T=512, block_size=64, S=8),
+              dict(B=2, Hq=16, Hkv=2, D=32, T=640, block_size=128, S=3),
+              dict(B=1, Hq=10, Hkv=1, D=128, T=384, block_size=48, S=4),
+              dict(B=1, Hq=5, Hkv=1, D=64, T=333, block_size=32, S=5),
+              dict(B=1, Hq=14, Hkv=2, D=64, T=400, block_size=32, S=6)]
+CONFIGS = REF_CONFIGS + G16_CONFIGS + GP_CONFIGS
 
 
 def _inputs(c, dtype, seed=0):
@@ -202,15 +210,8 @@ def test_empty_and_tiny_rows():
         assert (lse == -1e9).all()
 
 
-# groups of G <= 10 heads: several entries per row tile (floor(32 / G)),
-# with partly filled tiles (G = 5, 7, 10), two 64-key passes and ragged passes
-GP_CONFIGS = [dict(B=1, Hq=12, Hkv=2, D=64, T=512, block_size=64, S=8),
-              dict(B=2, Hq=16, Hkv=2, D=32, T=640, block_size=128, S=3),
-              dict(B=1, Hq=10, Hkv=1, D=128, T=384, block_size=48, S=4),
-              dict(B=1, Hq=5, Hkv=1, D=64, T=333, block_size=32, S=5),
-              dict(B=1, Hq=14, Hkv=2, D=64, T=400, block_size=32, S=6)]
 FSA_CONFIGS = CONFIGS + [dict(B=1, Hq=8, Hkv=2, D=64, T=640, block_size=128, S=3),
-                         dict(B=1, Hq=16, Hkv=1, D=128, T=300, block_size=48, S=4)] + GP_CONFIGS
+                         dict(B=1, Hq=16, Hkv=1, D=128, T=300, block_size=48, S=4)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=["f32", "bf16"])

@@ -82,6 +82,8 @@ BASELINE_GEOM = dict(cmp_block=32, cmp_stride=16, sel_block=64, n_sel=16, window
 SMALL_BASELINE_SHAPES = [
     dict(B=1, Hq=16, Hkv=1, T=2048, D=128),
     dict(B=1, Hq=32, Hkv=2, T=1536, D=64),
+    # the c4 model's GQA group (6 heads): group-packed selection tiles, flat range rows
+    dict(B=2, Hq=12, Hkv=2, T=1024, D=64),
 ]
 
 
