@@ -257,6 +257,18 @@ class NSAAttention(nn.Module):
         B, T, _ = x.shape
         return self.gate(x).view(B, T, self.Hq, 3).permute(0, 2, 1, 3)      # [B,Hq,T,3]
 
+    def _projections(self, x):
+        """q, kc, vc, ks, vs, kw, vw and the gate logits of ``x`` ([B, T, .]
+        each) from one GEMM over the eight weights stacked: one launch, one
+        weight cast under autocast, and in the backward one dX GEMM instead of
+        eight plus their sum.  The parameters stay the separate modules of the
+        reference's layout (its state_dict names)."""
+        ws = (self.q_proj.weight, self.k_cmp.weight, self.v_cmp.weight, self.k_slc.weight, self.v_slc.weight,
+              self.k_win.weight, self.v_win.weight, self.gate.weight)
+        w = torch.cat(ws, dim=0)
+        bias = torch.cat([self.gate.bias.new_zeros(w.shape[0] - self.gate.bias.shape[0]), self.gate.bias])
+        return torch.split(F.linear(x, w, bias), [t.shape[0] for t in ws], dim=-1)
+
     def _merge(self, out):
         B, _, T, _ = out.shape
         return self.out_proj(out.transpose(1, 2).reshape(B, T, self.Hq * self.dh))
@@ -344,19 +356,20 @@ class NSAAttention(nn.Module):
 
         B, T, _ = x.shape
         n_cmp = self._n_cmp(T)
-        q = self._rot(self._heads(self.q_proj(x), self.Hq)).contiguous()
-        kc = self._rot(self._heads(self.k_cmp(x), self.Hkv))
-        vc = self._heads(self.v_cmp(x), self.Hkv)
+        yq, ykc, yvc, yks, yvs, ykw, yvw, yg = self._projections(x)
+        q = self._rot(self._heads(yq, self.Hq)).contiguous()
+        kc = self._rot(self._heads(ykc, self.Hkv))
+        vc = self._heads(yvc, self.Hkv)
         if n_cmp > 0:
             k_cmp, v_cmp = self._pooled(kc, vc, n_cmp)
         else:
             k_cmp = q.new_zeros(B, self.Hkv, 0, self.dh)
             v_cmp = q.new_zeros(B, self.Hkv, 0, self.dh)
-        ks = self._rot(self._heads(self.k_slc(x), self.Hkv)).contiguous()
-        vs = self._heads(self.v_slc(x), self.Hkv).contiguous()
-        kw = self._rot(self._heads(self.k_win(x), self.Hkv)).contiguous()
-        vw = self._heads(self.v_win(x), self.Hkv).contiguous()
-        gate_logits = self._gate_logits(x).contiguous()
+        ks = self._rot(self._heads(yks, self.Hkv)).contiguous()
+        vs = self._heads(yvs, self.Hkv).contiguous()
+        kw = self._rot(self._heads(ykw, self.Hkv)).contiguous()
+        vw = self._heads(yvw, self.Hkv).contiguous()
+        gate_logits = yg.view(B, T, self.Hq, 3).permute(0, 2, 1, 3).contiguous()     # [B,Hq,T,3]
         k_cmp, v_cmp, ks, vs, kw, vw, gate_logits = (y.to(q.dtype) for y in (k_cmp, v_cmp, ks, vs, kw, vw,
                                                                              gate_logits))
         geom = ops.NSAGeometry(self.block_size, self.cmp_stride, self.sel_block, self.n_sel, self.window,
@@ -399,9 +412,16 @@ class FullAttention(nn.Module):
 
     def forward(self, x):
         B, T, _ = x.shape
-        q = self._heads(self.q_proj(x), self.Hq)
-        k = self._heads(self.k_proj(x), self.Hkv)
-        v = self._heads(self.v_proj(x), self.Hkv)
+        if self.impl == "sdpa":
+            # the three projections as one GEMM over the stacked weights (as
+            # NSAAttention's fused path does), parameters kept separate
+            ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+            yq, yk, yv = torch.split(F.linear(x, torch.cat(ws, dim=0)), [w.shape[0] for w in ws], dim=-1)
+        else:
+            yq, yk, yv = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        q = self._heads(yq, self.Hq)
+        k = self._heads(yk, self.Hkv)
+        v = self._heads(yv, self.Hkv)
         if self.rope is not None:
             q, k = self.rope(q), self.rope(k)
         k, v = expand_kv(k, self.G), expand_kv(v, self.G)
