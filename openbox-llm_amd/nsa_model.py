@@ -265,9 +265,10 @@ class NSAAttention(nn.Module):
         reference's layout (its state_dict names)."""
         ws = (self.q_proj.weight, self.k_cmp.weight, self.v_cmp.weight, self.k_slc.weight, self.v_slc.weight,
               self.k_win.weight, self.v_win.weight, self.gate.weight)
-        w = torch.cat(ws, dim=0)
-        bias = torch.cat([self.gate.bias.new_zeros(w.shape[0] - self.gate.bias.shape[0]), self.gate.bias])
-        return torch.split(F.linear(x, w, bias), [t.shape[0] for t in ws], dim=-1)
+        *ys, yg = torch.split(F.linear(x, torch.cat(ws, dim=0)), [t.shape[0] for t in ws], dim=-1)
+        # the gate's bias on its own columns only (its gradient then sums 3 Hq
+        # columns, not the whole stacked width)
+        return (*ys, yg + self.gate.bias.to(yg.dtype))
 
     def _merge(self, out):
         B, _, T, _ = out.shape
