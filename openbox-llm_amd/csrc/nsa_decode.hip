@@ -337,29 +337,19 @@ constexpr int kDecTopnThreads = 1024;   // top-n workgroup: candidate blocks tid
 constexpr int kDecKeysPerThread = kDecMaxCand / kDecTopnThreads;
 constexpr int kDecMaxSel = 64;          // picks per query (one lane each in the final sort)
 
-// p_cmp summed over the group's heads for 1024 pooled tokens of one (b, hkv):
-// each workgroup merges the compression splits' (max, sum) into every head's
-// log-sum-exp (a wave per head, lanes over the splits), then a thread sums
-// four tokens (each head's four scores in one 16-byte load; heads 0-7, then
-// 8-15, of each 16-head chunk, as the prefill importance kernel sums them).
-template <typename T>
-__global__ __launch_bounds__(256) void k_dec_toksum(const DecArgs<T> a, int nch) {
-  extern __shared__ __align__(16) float lse2[];
-  const DecGeom& g = a.g;
-  const int tid = threadIdx.x;
-  const int bh = blockIdx.x / nch, ch = blockIdx.x % nch, b = bh / g.Hkv;
-  const DecLen L = dec_len(a.lens[b], g);
-  const int i0 = ch * kDecTokPerWG;
-  if (i0 >= L.nvis) return;
-  const int nsp = g.ncs + g.nws, ncs_len = dec_cmp_splits(L, g);
-  // lph lanes per head (a power of two <= 64, heads side by side), each over
-  // every lph-th split, then combined across the head's lanes
-  int lph = 64;
+// Every head's log-sum-exp (log2 units) over the compression splits of one
+// (b, hkv), into lse2[G]: threads 0 .. 255 of the workgroup, a wave per head
+// (lph lanes per head, heads side by side), lanes over the splits, then
+// combined across the head's lanes.
+__device__ __forceinline__ void dec_head_lse2(const DecGeom& g, const float* __restrict__ p1_ml, int bh,
+                                              int ncs_len, float* lse2, int tid) {
+  const int nsp = g.ncs + g.nws;
+  int lph = 64;   // lanes per head: a power of two <= 64
   while (lph > 1 && lph * g.G > 256) lph >>= 1;
   for (int h0 = 0; h0 < g.G; h0 += 256 / lph) {
     const int hd = h0 + tid / lph, sub = tid % lph;
     const int hs = hd < g.G ? hd : g.G - 1;
-    const float* ml = a.p1_ml + 2 * (((int64_t)(bh * g.NHC + hs / 32) * nsp) * 32 + hs % 32);
+    const float* ml = p1_ml + 2 * (((int64_t)(bh * g.NHC + hs / 32) * nsp) * 32 + hs % 32);
     float m = kDecNegInf, l = 0.0f;
     for (int k0 = sub; k0 < ncs_len; k0 += 4 * lph) {
       float2 v[4];
@@ -380,15 +370,20 @@ __global__ __launch_bounds__(256) void k_dec_toksum(const DecArgs<T> a, int nch)
     for (int off = 1; off < lph; off <<= 1) S += __shfl_xor(S, off, kWave);
     if (sub == 0 && hd < g.G) lse2[hd] = M + __log2f(S);
   }
-  __syncthreads();
-  const int i4 = i0 + 4 * tid;
-  if (i4 >= L.nvis) return;
-  const float* sc = a.s_cmp + (int64_t)bh * g.G * g.NcapP;
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// p_cmp of pooled tokens i4 .. i4 + 3 of one (b, hkv) summed over the group's
+// heads (each head's four scores in one 16-byte load; heads 0-7, then 8-15,
+// of each 16-head chunk, as the prefill importance kernel sums them)
+__device__ __forceinline__ void dec_token_sums4(const DecGeom& g, const float* __restrict__ s_cmp, int bh, int i4,
+                                                const float* lse2, float sl2, float (&v)[4]) {
+  const float* sc = s_cmp + (int64_t)bh * g.G * g.NcapP;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = 0.0f;
   for (int c0 = 0; c0 < g.G; c0 += 16) {
     f32x4 x[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)   // past nvis (inside the row pitch) the values are never stored
+    for (int j = 0; j < 16; ++j)   // past nvis (inside the row pitch) the values are never used
       x[j] = c0 + j < g.G ? *reinterpret_cast<const f32x4*>(sc + (int64_t)(c0 + j) * g.NcapP + i4)
                           : (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -400,13 +395,32 @@ __global__ __launch_bounds__(256) void k_dec_toksum(const DecArgs<T> a, int nch)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int hd = c0 + 8 * hh + j;
-          if (hd < g.G) sum += fast_exp2(x[8 * hh + j][e] * a.sl2 - lse2[hd]);
+          if (hd < g.G) sum += fast_exp2(x[8 * hh + j][e] * sl2 - lse2[hd]);
         }
         half[hh] = sum;
       }
       v[e] = c0 == 0 ? half[0] + half[1] : v[e] + (half[0] + half[1]);
     }
   }
+}
+
+// p_cmp summed over the group's heads for 1024 pooled tokens of one (b, hkv)
+// (dec_head_lse2, then four tokens per thread: dec_token_sums4).
+template <typename T>
+__global__ __launch_bounds__(256) void k_dec_toksum(const DecArgs<T> a, int nch) {
+  extern __shared__ __align__(16) float lse2[];
+  const DecGeom& g = a.g;
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x / nch, ch = blockIdx.x % nch, b = bh / g.Hkv;
+  const DecLen L = dec_len(a.lens[b], g);
+  const int i0 = ch * kDecTokPerWG;
+  if (i0 >= L.nvis) return;
+  dec_head_lse2(g, a.p1_ml, bh, dec_cmp_splits(L, g), lse2, tid);
+  __syncthreads();
+  const int i4 = i0 + 4 * tid;
+  if (i4 >= L.nvis) return;
+  float v[4];
+  dec_token_sums4(g, a.s_cmp, bh, i4, lse2, a.sl2, v);
   float* dst = a.tok + (int64_t)bh * g.NcapP + i4;
   if (i4 + 3 < L.nvis) {
     *reinterpret_cast<f32x4*>(dst) = (f32x4){v[0], v[1], v[2], v[3]};
@@ -425,11 +439,17 @@ __global__ __launch_bounds__(256) void k_dec_toksum(const DecArgs<T> a, int nch)
 // by radix selection (eight 8-bit digits from the top: a histogram of the
 // keys that match the digits fixed so far, and the digit at which the count
 // from the top reaches the picks still needed), gathered, and sorted
-// descending across the lanes of one wave.
+// descending across the lanes of one wave.  FUSE: the workgroup forms the
+// token sums itself (k_dec_toksum's arithmetic, so the same bits) instead of
+// reading them, one launch and one round trip less when the pooled sequence
+// is short.
+template <bool FUSE>
 __global__ __launch_bounds__(kDecTopnThreads) void k_dec_topn(const int32_t* __restrict__ lens,
                                                              const float* __restrict__ tok,
                                                              int32_t* __restrict__ idx, float* __restrict__ scores,
-                                                             int ncand_cap, DecGeom g, float rcd) {
+                                                             int ncand_cap, DecGeom g, float rcd,
+                                                             const float* __restrict__ p1_ml,
+                                                             const float* __restrict__ s_cmp, float sl2) {
   __shared__ uint32_t hist[2][256];
   __shared__ uint64_t ctl_prefix;
   __shared__ int ctl_need;
@@ -439,10 +459,21 @@ __global__ __launch_bounds__(kDecTopnThreads) void k_dec_topn(const int32_t* __r
   const int bh = blockIdx.x, b = bh / g.Hkv;
   const DecLen L = dec_len(lens[b], g);
   int32_t* orow = idx + (int64_t)bh * g.n_sel;
-  extern __shared__ __align__(16) float tk[];   // token sums [NcapP]
+  extern __shared__ __align__(16) float tk[];   // token sums [NcapP] (FUSE: then lse2 [G])
   if (tid < 256) hist[0][tid] = 0;
   if (tid == 0) npicked = 0;
-  {
+  if constexpr (FUSE) {
+    float* lse2 = tk + g.NcapP;
+    if (L.nvis > 0) {   // uniform
+      if (tid < 256) dec_head_lse2(g, p1_ml, bh, dec_cmp_splits(L, g), lse2, tid);
+      __syncthreads();
+      for (int i4 = 4 * tid; i4 < L.nvis; i4 += 4 * kDecTopnThreads) {
+        float v[4];
+        dec_token_sums4(g, s_cmp, bh, i4, lse2, sl2, v);
+        *reinterpret_cast<f32x4*>(tk + i4) = (f32x4){v[0], v[1], v[2], v[3]};   // inside the row pitch
+      }
+    }
+  } else {
     const float* src = tok + (int64_t)bh * g.NcapP;
     for (int i = 4 * tid; i < L.nvis; i += 4 * kDecTopnThreads)   // rows are 32-float aligned
       *reinterpret_cast<f32x4*>(tk + i) = *reinterpret_cast<const f32x4*>(src + i);
@@ -775,14 +806,18 @@ static int dec_launch(const DecArgs<T>& a, const DecPlan& P, hipStream_t s) {
   const int nch = (g.NcapP + kDecTokPerWG - 1) / kDecTokPerWG;
   const int64_t gt = (int64_t)g.B * g.Hkv * nch;
   NSA_CHECK(gt < (1ll << 31), NSA_ERR_SHAPE);
-  if (g.ncs > 0) k_dec_toksum<T><<<(unsigned)gt, 256, sizeof(float) * g.G, s>>>(a, nch);
-  const size_t topn_lds = sizeof(float) * g.NcapP;
+  // short pooled sequences (two token-sum chunks at most): the top-n
+  // workgroup forms the token sums itself
+  const bool fuse = nch <= 2;
+  if (g.ncs > 0 && !fuse) k_dec_toksum<T><<<(unsigned)gt, 256, sizeof(float) * g.G, s>>>(a, nch);
+  const size_t topn_lds = sizeof(float) * (g.NcapP + (fuse ? g.G : 0));
+  const void* topn = fuse ? (const void*)k_dec_topn<true> : (const void*)k_dec_topn<false>;
   if (topn_lds > 48 * 1024 &&
-      hipFuncSetAttribute((const void*)k_dec_topn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)topn_lds) !=
-          hipSuccess)
+      hipFuncSetAttribute(topn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)topn_lds) != hipSuccess)
     return NSA_ERR_LAUNCH;
-  k_dec_topn<<<(unsigned)(g.B * g.Hkv), kDecTopnThreads, topn_lds, s>>>(a.lens, a.tok, a.idx, a.scores,
-                                                                       a.ncand_cap, g, 1.0f / (float)g.cd);
+  auto topn_kern = fuse ? k_dec_topn<true> : k_dec_topn<false>;
+  topn_kern<<<(unsigned)(g.B * g.Hkv), kDecTopnThreads, topn_lds, s>>>(
+      a.lens, a.tok, a.idx, a.scores, a.ncand_cap, g, 1.0f / (float)g.cd, a.p1_ml, a.s_cmp, a.sl2);
   k_dec_part<T, D, NST><<<(unsigned)g3, 64, 0, s>>>(a, 1);
   const int64_t rows = (int64_t)g.B * g.Hq;
   NSA_CHECK(rows < (1ll << 31), NSA_ERR_SHAPE);
