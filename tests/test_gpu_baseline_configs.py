@@ -15,6 +15,9 @@ initial + 2 local blocks forced:
         (nsa_rows_gathered): every gradient is then exactly those rows'
         contribution, and dq / dgate are exactly zero elsewhere.
 
+The c4 model's attention layer (B8 T4096 Hq12 Hkv2 D64, a GQA group of 6
+heads) is checked the same way (i)-(iv).
+
 c2 -- selection branch only, B4 T8192 Hq16 Hkv1 D64, indices from the
 compression importance (l32/d16): (i), (ii), then selection fwd + bwd on
 sampled rows.  Its selection dK/dV has more work items than the persistent
@@ -124,13 +127,21 @@ def _oracle_rows_grads(ins, do_rows, idx_rows, cfg, rows, T, chunk=32):
     return torch.cat(outs, dim=2), [q_rows.grad] + [t.grad for t in kv] + [g_rows.grad]
 
 
+# the attention layer of the c4 model at its full shape: a GQA group of 6
+# heads (group-packed selection tiles, flat range rows) over 8 sequences
+C4_LAYER = dict(kind="fused", B=8, T=4096, Hq=12, Hkv=2, D=64, geom=(32, 16, 64, 16, 512, False, 0),
+                head_scale=True, in_scale=1.0,
+                desc="config-4 attention layer: B8 T4096 Hq12 Hkv2 D64, l32/d16 l'64 top-16 w512, bf16")
+
+
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("workload", ["c3", "c3_forced"])
+@pytest.mark.parametrize("workload", ["c3", "c3_forced", "c4_layer"])
 def test_c3_full_shape_parity(workload):
+    """c3 (plain and forced) and the c4 model's attention layer."""
     dev = require_gpu()
     import nsa_fused_kernel as nfk
     import nsa_hip_ops as ops
-    w = bench.WORKLOADS[workload]
+    w = C4_LAYER if workload == "c4_layer" else bench.WORKLOADS[workload]
     log(f"{workload}: {w['desc']}")
     T = w["T"]
     geom = ops.NSAGeometry(*w["geom"])
