@@ -5,7 +5,9 @@
 // A wave owns 32 keys: their K and V fragments stay in registers and their
 // dK^T / dV^T accumulate in registers for the whole walk.  The queries that
 // see those keys stream through LDS two at a time (32 rows = two queries x 16
-// heads of a head chunk): row tiles of Q and dO (direct global -> LDS loads,
+// heads of a head chunk; groups of fewer heads fill a tile with more queries:
+// GroupTiles for the selection, FlatReq for the range branches): row tiles of
+// Q and dO (direct global -> LDS loads,
 // kKvStages deep) and per-row statistics c = lse*log2(e) - log2(rowscale)
 // and delta, shared by the workgroup's waves.
 //   S = Q K^T, dP = dO V^T                     (rows on M, keys on N)

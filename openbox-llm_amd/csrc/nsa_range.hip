@@ -5,6 +5,8 @@
 // chunk of a query form 16 consecutive rows, so a 32-row MFMA tile holds two
 // queries.  A wave owns NT such tiles (2*NT consecutive queries) and a
 // workgroup of four waves owns 8*NT consecutive queries of one KV head chunk.
+// Groups of G < 16 heads number their rows t G + g instead and take 32
+// consecutive rows per wave (flat rows, range_rows).
 // The workgroup walks the union of its queries' visible key range in 32-key
 // tiles; each tile of K (row-major) and V^T (or K, V and K^T for dQ) is
 // staged once in LDS by direct global -> LDS loads, double-buffered, and read
@@ -23,7 +25,7 @@
 namespace nsa {
 
 struct RangeMap {
-  int b, hkv, hc, head0, G, NHC;
+  int b, hkv, hc, G, NHC;
 };
 
 __device__ __forceinline__ RangeMap range_map(int64_t r, int Hq, int Hkv) {
@@ -34,7 +36,6 @@ __device__ __forceinline__ RangeMap range_map(int64_t r, int Hq, int Hkv) {
   const int bh = (int)(r / m.NHC);
   m.b = bh / Hkv;
   m.hkv = bh % Hkv;
-  m.head0 = m.hkv * m.G + m.hc * 16;
   return m;
 }
 
