@@ -1168,8 +1168,8 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
     }
   };
   if constexpr (FLAT) {
-    // rows tlo G .. thi G + G - 1 of the group; the keys a row's query sees
-    // form a contiguous run of rows for each key: [row_lo, row_hi)
+    // rows tlo G .. thi G + G - 1 of the group; the rows that see a key are
+    // one run (flat_rows_seeing)
     const int G = x.G;
     const int rlo = tlo * G, rhi = thi * G + G - 1;
     auto make_rq = [&]() {
@@ -1177,24 +1177,12 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
       rq.init(x, b, hkv, rlo, thi, tid);
       return rq;
     };
+    const int wmode = mode == NSA_MODE_WINDOW ? window : 0;
     auto vis = [&](const KvStage<T, D>&, int it, bool& mask) {
       const int R0 = rlo + 32 * it;
-      const int tf = R0 / G;                                   // the tile's first query
-      const int tl = (R0 + 31 < rhi ? R0 + 31 : rhi) / G;      // and last (within the range)
-      int lo, hi;   // rows of the tile that see this lane's key
-      if (mode == NSA_MODE_WINDOW) {
-        mask = !(tf >= wlast && tl - window < kw);
-        lo = key * G - R0;                  // query >= key
-        hi = (key + window) * G - R0;       // query < key + window
-      } else {
-        mask = !(wlast * cd + cl - 1 <= tf);
-        lo = (key * cd + cl - 1) * G - R0;  // query >= key cd + cl - 1
-        hi = 32;
-      }
-      lo = lo < 0 ? 0 : (lo > 32 ? 32 : lo);
-      hi = hi < 0 ? 0 : (hi > 32 ? 32 : hi);
-      const uint64_t bits = key_ok && lo < hi ? ((1ull << hi) - 1ull) & ~((1ull << lo) - 1ull) : 0ull;
-      return VisBits{(uint32_t)bits >> (8 * h)};
+      mask = flat_tile_needs_mask(kw, R0, rhi, G, wmode, cl, cd);
+      const uint32_t bits = key_ok ? flat_rows_seeing(key, R0, G, wmode, cl, cd) : 0u;
+      return VisBits{bits >> (8 * h)};
     };
     run(make_rq, (rhi - rlo) / 32 + 1, vis);
   } else {

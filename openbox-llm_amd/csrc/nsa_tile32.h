@@ -261,6 +261,36 @@ static_assert(pair_rows(3, 7, 256).t0 == 3 && pair_rows(3, 7, 256).dA == 0 && pa
               "ascending queries: from A's row");
 static_assert(pair_rows(5, -1, 256).t0 == 5 && pair_rows(5, -1, 256).dB == 0, "no query B: A's row twice");
 
+// Flat rows (groups of G < 16 heads): row R of a group is query R / G, head
+// R % G, and a tile is rows R0 .. R0 + 31.  The queries that see key `key`
+// form one run, so its rows are one run too:
+//   window (window > 0): key <= t < key + window  <=>  key G <= R < (key + window) G
+//   compression (window = 0): t >= key cd + cl - 1  <=>  R >= (key cd + cl - 1) G
+// (t = floor(R / G) >= m  <=>  R >= m G, and t < m  <=>  R < m G).
+// Returns bit r set for the tile rows r that see the key.
+__host__ __device__ constexpr uint32_t flat_rows_seeing(int key, int R0, int G, int window, int cl, int cd) {
+  int lo = window > 0 ? key * G - R0 : (key * cd + cl - 1) * G - R0;
+  int hi = window > 0 ? (key + window) * G - R0 : 32;
+  lo = lo < 0 ? 0 : (lo > 32 ? 32 : lo);
+  hi = hi < 0 ? 0 : (hi > 32 ? 32 : hi);
+  return lo < hi ? (uint32_t)(((1ull << hi) - 1ull) & ~((1ull << lo) - 1ull)) : 0u;
+}
+// Whether a flat tile needs the per-element test for the 32 keys kw ..
+// kw + 31: false only when every one of them is seen by every row of the
+// tile up to row rhi (the last present row).
+__host__ __device__ constexpr bool flat_tile_needs_mask(int kw, int R0, int rhi, int G, int window, int cl,
+                                                        int cd) {
+  const int tf = R0 / G;                                 // the tile's first query
+  const int tl = (R0 + 31 < rhi ? R0 + 31 : rhi) / G;    // and its last present one
+  const int wlast = kw + 31;
+  return window > 0 ? !(tf >= wlast && tl - window < kw) : !(wlast * cd + cl - 1 <= tf);
+}
+static_assert(flat_rows_seeing(5, 0, 6, 512, 0, 0) == ~((1u << 30) - 1u), "window: rows of queries >= 5");
+static_assert(flat_rows_seeing(0, 0, 6, 3, 0, 0) == (1u << 18) - 1u, "window of 3: queries 0 .. 2");
+static_assert(flat_rows_seeing(1, 270, 6, 0, 32, 16) == ~((1u << 12) - 1u),
+              "compression, l 32 / d 16: key 1 seen by queries >= 47, rows >= 282");
+static_assert(flat_rows_seeing(1, 60, 6, 0, 32, 16) == 0u, "compression: no row of queries 10 .. 15 sees key 1");
+
 // Direct global -> LDS loads as volatile asm (lane i writes lds + SIZE i):
 // the compiler neither tracks them nor adds waits for them, so LDS reads of
 // other stages are not held behind loads still in flight.  The caller owns

@@ -80,3 +80,16 @@ def test_m0_is_written_only_by_the_dma_helpers():
             elif ln.startswith("global_load_lds_dword"):
                 assert lines[i - 2].startswith("s_mov_b32 m0,"), f"{name}: DMA without its M0 write: {ln}"
     assert checked > 0
+
+
+def test_flat_row_visibility(tmp_path):
+    """The range dK/dV's flat-row masks (groups of G < 16 heads, row R =
+    query R / G) against brute force over every row of a tile, window and
+    compression (tests/host/check_flat_rows.hip)."""
+    exe = tmp_path / "check_flat_rows"
+    subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", f"-I{ROOT}/include", f"-I{PKG}/csrc",
+                    os.path.join(ROOT, "tests", "host", "check_flat_rows.hip"), "-o", str(exe)],
+                   check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout
