@@ -10,12 +10,16 @@
 // so span i is the lD-element row starting at x + i d D: the kernels read the
 // overlapping spans in place (no unfolded copy).
 //
-// k_phi_fwd: one wave per 32 pooled tokens.  pre^T = W1 X^T on 32x32x16
-// MFMAs with the hidden units on M (W1 rows, perm32 order) and the tokens on
-// N, so the accumulator of hidden tile mt holds, in registers 8u .. 8u+7 of
-// lane half h, hidden units 32 mt + 16 u + 8 h + j: after bias and SiLU it is
-// the B operand of out^T = W2 silu(pre)^T for contraction step 2 mt + u
-// without moving data between lanes.  pre is kept (float) for the backward.
+// k_phi_fwd: one workgroup of four waves per 32 pooled tokens.  pre^T = W1
+// X^T on 32x32x16 MFMAs with the hidden units on M (W1 rows, perm32 order)
+// and the tokens on N; the waves split the lD contraction in quarters (one
+// wave alone, streaming W1 and the spans from memory, is bound by the
+// latency of its loads).  The quarters meet in LDS and are summed in wave
+// order; wave mt then holds hidden tile mt, whose registers 8u .. 8u+7 of lane
+// half h are hidden units 32 mt + 16 u + 8 h + j: after bias and SiLU they are
+// the B operand of out^T = W2 silu(pre)^T for contraction step 2 mt + u, handed
+// to the other waves through LDS in that same lane layout.  Wave dt computes
+// output tile dt.  pre is kept (float) for the backward.
 // k_phi_dpre: dpre = (W2^T dout) * silu'(pre), the same orientation.
 // k_phi_fold: dx[p] = sum over the spans i that hold p of dspan_i[p - i d]
 // (deterministic gather, no atomics).
@@ -38,19 +42,25 @@ __device__ __forceinline__ void store_run8(T* p, const float* v) {
   f.store(p);
 }
 
+constexpr int kPhiFwdWaves = 4;   // waves per 32 pooled tokens, each a quarter of the contraction
+
 template <typename T, int D, int H>
-__global__ __launch_bounds__(256) void k_phi_fwd(const T* __restrict__ x, const T* __restrict__ w1,
-                                                 const float* __restrict__ c1, const T* __restrict__ w2,
-                                                 const float* __restrict__ b2, T* __restrict__ out,
-                                                 float* __restrict__ pre_out, int BH, int L, int n, int l, int d,
-                                                 int ntile) {
+__global__ __launch_bounds__(64 * kPhiFwdWaves) void k_phi_fwd(const T* __restrict__ x, const T* __restrict__ w1,
+                                                               const float* __restrict__ c1,
+                                                               const T* __restrict__ w2, const float* __restrict__ b2,
+                                                               T* __restrict__ out, float* __restrict__ pre_out,
+                                                               int BH, int L, int n, int l, int d, int ntile) {
+  constexpr int NW = kPhiFwdWaves;
   constexpr int MT = H / 32;   // hidden tiles
   constexpr int DT = D / 32;   // output tiles
-  const int lane = threadIdx.x & 63, h = lane >> 5, nn = lane & 31;
-  const int64_t wt = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wt >= (int64_t)BH * ntile) return;
+  static_assert(MT <= NW && DT <= NW, "one hidden / output tile per wave");
+  __shared__ float part[NW][MT][16][64];              // each wave's partial pre^T, [register][lane]
+  __shared__ __align__(16) T hbs[MT][2][64 * 8];      // silu(pre)^T B fragments, [lane][8]
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, nn = lane & 31;
+  const int64_t wt = blockIdx.x;
+  if (wt >= (int64_t)BH * ntile) return;   // uniform over the workgroup
   const int bh = (int)(wt / ntile), i0 = (int)(wt % ntile) * 32;
-  const int K = l * D;
+  const int K = l * D, KW = K / NW;        // D >= 64: KW is a multiple of 16
   const int tok = i0 + nn;
   const bool tok_ok = tok < n;
   // the B operand: token column nn reads its span row (tokens past n repeat the last)
@@ -62,7 +72,7 @@ __global__ __launch_bounds__(256) void k_phi_fwd(const T* __restrict__ x, const 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
 #pragma unroll 4
-  for (int k0 = 0; k0 < K; k0 += 16) {
+  for (int k0 = w * KW; k0 < (w + 1) * KW; k0 += 16) {
     Frag<T> bx;
     bx.load(xrow + k0);
 #pragma unroll
@@ -72,18 +82,26 @@ __global__ __launch_bounds__(256) void k_phi_fwd(const T* __restrict__ x, const 
       mma32(acc[mt], aw, bx);
     }
   }
-  // bias, keep pre, SiLU -> B fragments of silu(pre)^T
-  Frag<T> hb[MT][2];
-  float* prow = pre_out + ((int64_t)bh * n + tok) * H;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[w][mt][r][lane] = acc[mt][r];
+  __syncthreads();
+  // wave mt: the quarters of hidden tile mt summed in wave order, bias, keep
+  // pre, SiLU -> B fragments of silu(pre)^T
+  if (w < MT) {
+    const int mt = w;
     float pv[16], hv[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pv[r] = acc[mt][r] + c1[32 * mt + acc_elem(h, r)];
+      float a = part[0][mt][r][lane];
+#pragma unroll
+      for (int q = 1; q < NW; ++q) a += part[q][mt][r][lane];
+      pv[r] = a + c1[32 * mt + acc_elem(h, r)];
       hv[r] = silu_f(pv[r]);
     }
     if (tok_ok) {
+      float* prow = pre_out + ((int64_t)bh * n + tok) * H;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         float* p = prow + 32 * mt + 16 * u + 8 * h;
@@ -91,24 +109,31 @@ __global__ __launch_bounds__(256) void k_phi_fwd(const T* __restrict__ x, const 
         *reinterpret_cast<f32x4*>(p + 4) = (f32x4){pv[8 * u + 4], pv[8 * u + 5], pv[8 * u + 6], pv[8 * u + 7]};
       }
     }
-    hb[mt][0].set(hv);
-    hb[mt][1].set(hv + 8);
-  }
-  // out^T = W2 silu(pre)^T: A = W2 rows (perm32), contraction over the hidden units
-  T* orow = out + ((int64_t)bh * n + tok) * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
+    for (int u = 0; u < 2; ++u) {
+      Frag<T> f;
+      f.set(hv + 8 * u);
+      f.store(&hbs[mt][u][lane * 8]);
+    }
+  }
+  __syncthreads();
+  // wave dt: out^T tile dt = W2 silu(pre)^T (A = W2 rows in perm32 order,
+  // contraction over the hidden units)
+  if (w < DT) {
+    const int dt = w;
     f32x16 o = zero16();
     const T* w2row = w2 + (int64_t)(32 * dt + perm32(nn)) * H + 8 * h;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        Frag<T> a;
+        Frag<T> a, hb;
         a.load(w2row + 32 * mt + 16 * u);
-        mma32(o, a, hb[mt][u]);
+        hb.load(&hbs[mt][u][lane * 8]);
+        mma32(o, a, hb);
       }
     if (tok_ok) {
+      T* orow = out + ((int64_t)bh * n + tok) * D;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int d0 = 32 * dt + 16 * u + 8 * h;
@@ -204,13 +229,14 @@ int nsa_phi_fwd(const void* x, const void* w1, const float* c1, const void* w2, 
   if (n == 0) return NSA_OK;
   NSA_CHECK(x && w1 && c1 && w2 && b2 && out && pre, NSA_ERR_ARG);
   const int ntile = (n + 31) / 32;
-  const int64_t waves = (int64_t)BH * ntile, grid = (waves + 3) / 4;
+  const int64_t grid = (int64_t)BH * ntile;   // one workgroup per 32 pooled tokens
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
-#define NSA_PHI_FWD(TT, DD, HH)                                                                                \
-  if (D == DD && H == HH)                                                                                      \
-    k_phi_fwd<TT, DD, HH><<<(unsigned)grid, 256, 0, s>>>((const TT*)x, (const TT*)w1, c1, (const TT*)w2, b2, \
-                                                         (TT*)out, pre, BH, L, n, l, d, ntile);
+#define NSA_PHI_FWD(TT, DD, HH)                                                                                    \
+  if (D == DD && H == HH)                                                                                          \
+    k_phi_fwd<TT, DD, HH><<<(unsigned)grid, 64 * kPhiFwdWaves, 0, s>>>((const TT*)x, (const TT*)w1, c1,           \
+                                                                       (const TT*)w2, b2, (TT*)out, pre, BH, L, n, \
+                                                                       l, d, ntile);
 #define NSA_PHI_FWD_T(TT) \
   NSA_PHI_FWD(TT, 64, 32) NSA_PHI_FWD(TT, 64, 64) NSA_PHI_FWD(TT, 64, 128) \
   NSA_PHI_FWD(TT, 128, 32) NSA_PHI_FWD(TT, 128, 64) NSA_PHI_FWD(TT, 128, 128)
