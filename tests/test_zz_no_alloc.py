@@ -19,9 +19,10 @@ from nsa_testlib import log, make_block_idx, randn, require_gpu
 
 pytestmark = pytest.mark.gpu
 
-CASES = [  # (B, Hq, Hkv, T, D, block_size, S): the second is smaller
-    (2, 16, 2, 2048, 64, 64, 8),
+CASES = [  # (B, Hq, Hkv, T, D, block_size, S): each call smaller than the one before
+    (2, 16, 2, 2048, 64, 64, 8),   # G = 8: group-packed row tiles
     (1, 8, 1, 512, 32, 32, 4),
+    (1, 16, 1, 384, 32, 32, 4),    # G = 16: two queries x 16 heads per tile
 ]
 
 
