@@ -63,6 +63,22 @@ int nsa_pool_fwd(const void* x, void* out, int B, int H, int T, int D, int l, in
 int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int T, int D, int l, int d,
                  int dtype, void* stream);
 
+/* Learned weighted pool over the same overlapping spans: the arithmetic of
+ * BlockCompressor's pooling (nsa_model.py:100-123, before its projection),
+ * sum_p w[p] (x[i*d + p] + P[p]), taken as sum_p w[p] x[i*d + p] + cvec with
+ * cvec = w^T P.  w: the l softmax weights, float32; out [B][H][n][D] float32.
+ * D % 8 == 0; x and out 16-byte aligned. */
+int nsa_wpool_fwd(const void* x, const float* w, const float* cvec, float* out, int B, int H, int T, int D, int l,
+                  int d, int dtype, void* stream);
+/* Its gradient for x: dx[t] = sum over the spans i holding t of
+ * w[t - i*d] dpool[i] (dpool float32 [B][H][n][D]); dx in dtype. */
+int nsa_wpool_bwd(const float* dpool, const float* w, void* dx, int B, int H, int T, int D, int l, int d, int dtype,
+                  void* stream);
+/* Its gradient for the weights (the x part): dw[p] = sum over (b, h, i, c) of
+ * x[b][h][i*d + p][c] dpool[b][h][i][c], float32 [l], summed in a fixed order. */
+int nsa_wpool_dw(const void* x, const float* dpool, float* dw, int B, int H, int T, int D, int l, int d, int dtype,
+                 void* stream);
+
 /* ---- gate ------------------------------------------------------------------
  * Replaces the gate blend of nsa_fused_forward (nsa_fused_kernel.py:572-573):
  * out = sigmoid(g0) o_cmp + sigmoid(g1) o_slc + sigmoid(g2) o_win. rows = B*Hq*T. */

@@ -184,6 +184,109 @@ __global__ __launch_bounds__(256) void k_pool_bwd8(const TI* __restrict__ dp, TO
 }
 
 // ---------------------------------------------------------------------------
+// learned weighted pool (BlockCompressor, nsa_model.py:100-123)
+// ---------------------------------------------------------------------------
+// The pooled token of span i is sum_p w[p] (x[i d + p] + P[p]) for softmax
+// weights w and a position code P; here sum_p w[p] x[i d + p] + cv with cv =
+// w^T P, over the overlapping spans in place (no unfolded copy), in float32 as
+// the module computes it.  D % 8 == 0: a lane takes 8 consecutive channels.
+
+// out[bh][i][c] = sum_p w[p] x[bh][i d + p][c] + cv[c]   (p ascending)
+template <typename T>
+__global__ __launch_bounds__(256) void k_wpool_fwd8(const T* __restrict__ x, const float* __restrict__ w,
+                                                    const float* __restrict__ cv, float* __restrict__ out, int BH,
+                                                    int L, int D, int n, int pl, int pd) {
+  const int dc = D / 8;
+  const int64_t total = (int64_t)BH * n * dc;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % dc);
+    const int64_t r = e / dc;
+    const int i = (int)(r % n);
+    const int64_t bh = r / n;
+    const T* src = x + (bh * L + (int64_t)i * pd) * D + 8 * c;
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < pl; ++k) {
+      Frag<T> f;
+      f.load(src + (int64_t)k * D);
+      const float wk = w[k];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] += wk * to_f32(f.elem(j));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] += cv[8 * c + j];
+    float* o = out + r * D + 8 * c;
+    *reinterpret_cast<f32x4*>(o) = (f32x4){s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4*>(o + 4) = (f32x4){s[4], s[5], s[6], s[7]};
+  }
+}
+
+// dx[bh][t][c] = sum over the spans i that hold t (ascending) of w[t - i d] dp[bh][i][c]
+template <typename TO>
+__global__ __launch_bounds__(256) void k_wpool_bwd8(const float* __restrict__ dp, const float* __restrict__ w,
+                                                    TO* __restrict__ dx, int BH, int L, int D, int n, int pl,
+                                                    int pd) {
+  const int dc = D / 8;
+  const int64_t total = (int64_t)BH * L * dc;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e % dc);
+    const int64_t r = e / dc;
+    const int t = (int)(r % L);
+    const int64_t bh = r / L;
+    int ilo = t - pl + 1 <= 0 ? 0 : (t - pl + 1 + pd - 1) / pd;
+    int ihi = t / pd;
+    if (ihi > n - 1) ihi = n - 1;
+    float s[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f;
+    for (int i = ilo; i <= ihi; ++i) {
+      Frag<float> g;
+      g.load(dp + (bh * n + i) * D + 8 * c);
+      const float wk = w[t - i * pd];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] += wk * g.elem(j);
+    }
+    Frag<TO> o;
+    o.set(s);
+    o.store(dx + r * D + 8 * c);
+  }
+}
+
+// dw[p] = sum over (bh, i, c) of x[bh][i d + p][c] dp[bh][i][c]: workgroup p;
+// each thread a strided share of the 8-channel chunks, then a tree over the
+// workgroup's threads (a fixed order: the same bits every run)
+template <typename T>
+__global__ __launch_bounds__(256) void k_wpool_dw(const T* __restrict__ x, const float* __restrict__ dp,
+                                                  float* __restrict__ dw, int BH, int L, int D, int n, int pd) {
+  __shared__ float red[256];
+  const int p = blockIdx.x, tid = threadIdx.x;
+  const int dc = D / 8;
+  const int64_t total = (int64_t)BH * n * dc;
+  float acc = 0.0f;
+  for (int64_t e = tid; e < total; e += 256) {
+    const int c = (int)(e % dc);
+    const int64_t r = e / dc;
+    const int i = (int)(r % n);
+    const int64_t bh = r / n;
+    Frag<T> f;
+    f.load(x + (bh * L + (int64_t)i * pd + p) * D + 8 * c);
+    Frag<float> g;
+    g.load(dp + r * D + 8 * c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += to_f32(f.elem(j)) * g.elem(j);
+  }
+  red[tid] = acc;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (tid < off) red[tid] += red[tid + off];
+    __syncthreads();
+  }
+  if (tid == 0) dw[p] = red[0];
+}
+
+// ---------------------------------------------------------------------------
 // gate
 // ---------------------------------------------------------------------------
 
@@ -450,6 +553,55 @@ int nsa_pool_bwd(const void* dpool, int dpool_dtype, void* dx, int B, int H, int
     else
       k_pool_bwd<bf16, float><<<grid, 256, 0, s>>>((const bf16*)dpool, (float*)dx, B * H, T, D, n, l, d);
   }
+  return nsa_launch_status();
+}
+
+int nsa_wpool_fwd(const void* x, const float* w, const float* cvec, float* out, int B, int H, int T, int D, int l,
+                  int d, int dtype, void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && D % 8 == 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int n = T >= l ? (T - l) / d + 1 : 0;
+  const int64_t total = (int64_t)B * H * n * D;
+  if (total == 0) return NSA_OK;
+  NSA_CHECK(x && w && cvec && out && aligned16(x) && aligned16(out), NSA_ERR_ARG);
+  hipStream_t s = (hipStream_t)stream;
+  const int g = grid_for(total / 8);
+  if (dtype == NSA_BF16)
+    k_wpool_fwd8<bf16><<<g, 256, 0, s>>>((const bf16*)x, w, cvec, out, B * H, T, D, n, l, d);
+  else
+    k_wpool_fwd8<float><<<g, 256, 0, s>>>((const float*)x, w, cvec, out, B * H, T, D, n, l, d);
+  return nsa_launch_status();
+}
+
+int nsa_wpool_bwd(const float* dpool, const float* w, void* dx, int B, int H, int T, int D, int l, int d, int dtype,
+                  void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && D % 8 == 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int n = T >= l ? (T - l) / d + 1 : 0;
+  const int64_t total = (int64_t)B * H * T * D;
+  if (total == 0) return NSA_OK;
+  NSA_CHECK(w && dx && aligned16(dx) && (n == 0 || (dpool && aligned16(dpool))), NSA_ERR_ARG);
+  hipStream_t s = (hipStream_t)stream;
+  const int g = grid_for(total / 8);
+  if (dtype == NSA_BF16)
+    k_wpool_bwd8<bf16><<<g, 256, 0, s>>>(dpool, w, (bf16*)dx, B * H, T, D, n, l, d);
+  else
+    k_wpool_bwd8<float><<<g, 256, 0, s>>>(dpool, w, (float*)dx, B * H, T, D, n, l, d);
+  return nsa_launch_status();
+}
+
+int nsa_wpool_dw(const void* x, const float* dpool, float* dw, int B, int H, int T, int D, int l, int d, int dtype,
+                 void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && D % 8 == 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  const int n = T >= l ? (T - l) / d + 1 : 0;
+  NSA_CHECK(x && dw && aligned16(x) && (n == 0 || (dpool && aligned16(dpool))), NSA_ERR_ARG);
+  hipStream_t s = (hipStream_t)stream;
+  // n == 0: every dw[p] is an empty sum, written as 0 by the kernel's loop
+  if (dtype == NSA_BF16)
+    k_wpool_dw<bf16><<<l, 256, 0, s>>>((const bf16*)x, dpool, dw, B * H, T, D, n, d);
+  else
+    k_wpool_dw<float><<<l, 256, 0, s>>>((const float*)x, dpool, dw, B * H, T, D, n, d);
   return nsa_launch_status();
 }
 

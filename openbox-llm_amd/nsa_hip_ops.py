@@ -242,6 +242,54 @@ def pool_bwd(dpool, T, l, d, dtype):
     return dx
 
 
+class WeightedPoolHIP(torch.autograd.Function):
+    """``out[b,h,i] = sum_p w[p] (x[b,h,i d + p] + pos[p])`` (float32
+    ``[B,H,n,D]``): the pooling of BlockCompressor (nsa_model.py:100-123,
+    before its projection) on the HIP kernels, over the overlapping spans in
+    place.  Gradients for x (in x's dtype), w and pos (float32 sums)."""
+
+    @staticmethod
+    def forward(ctx, x, w, pos, l, d):
+        x = _contig(x)
+        B, H, T, D = x.shape
+        assert w.shape == (l,) and pos.shape == (l, D), "weighted pool: w [l], pos [l, D]"
+        n = n_cmp_tokens(T, l, d)
+        with torch.autocast("cuda", enabled=False):
+            wf = w.float().contiguous()
+            cvec = (wf @ pos.float()).contiguous()
+        out = torch.empty(B, H, n, D, device=x.device, dtype=torch.float32)
+        if n > 0:
+            _call("nsa_wpool_fwd", _lib().nsa_wpool_fwd, L.ptr(x), L.ptr(wf), L.ptr(cvec), L.ptr(out), B, H, T, D,
+                  l, d, L.dtype_code(x), _stream(x))
+        ctx.save_for_backward(x, wf, pos)
+        ctx.meta = (l, d, w.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        x, wf, pos = ctx.saved_tensors
+        l, d, w_dtype = ctx.meta
+        B, H, T, D = x.shape
+        dout = _contig(dout.float())
+        dx = torch.empty_like(x)
+        dw = torch.empty(l, device=x.device, dtype=torch.float32)
+        _call("nsa_wpool_bwd", _lib().nsa_wpool_bwd, L.ptr(dout), L.ptr(wf), L.ptr(dx), B, H, T, D, l, d,
+              L.dtype_code(x), _stream(x))
+        _call("nsa_wpool_dw", _lib().nsa_wpool_dw, L.ptr(x), L.ptr(dout), L.ptr(dw), B, H, T, D, l, d,
+              L.dtype_code(x), _stream(x))
+        with torch.autocast("cuda", enabled=False):
+            dc = dout.sum(dim=(0, 1, 2))                  # the gradient of cvec = w^T pos
+            dw = dw + pos.float() @ dc
+            dpos = wf[:, None] * dc[None, :]
+        return dx, dw.to(w_dtype), dpos.to(pos.dtype), None, None
+
+
+def weighted_pool(x, w, pos, l, d):
+    """BlockCompressor's pooled tokens before the projection, ``sum_p w[p]
+    (x[i d + p] + pos[p])`` for the spans [i d, i d + l) of ``x [B,H,T,D]``."""
+    return WeightedPoolHIP.apply(x, w, pos, l, d)
+
+
 class _PoolMean(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, l, d):

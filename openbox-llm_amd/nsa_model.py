@@ -94,6 +94,16 @@ class BlockCompressor(nn.Module):
         pooled = ((x_blocks + self.intra_pos) * w[:, None]).sum(dim=-2)
         return self.proj(pooled)
 
+    def pool_sequence(self, x, stride):
+        """The same pooled tokens straight from ``x [B,Hkv,T,D]`` (spans
+        ``[i stride, i stride + block_size)``) on the HIP kernels, which read
+        the overlapping spans in place; the weighted sum in float32, as the
+        unfolded form computes it, the projection under the caller's
+        autocast."""
+        import nsa_hip_ops as ops
+        w = torch.softmax(self.pool_logits, dim=0)
+        return self.proj(ops.weighted_pool(x, w, self.intra_pos, self.block_size, stride))
+
 
 class MLPCompressor(nn.Module):
     """The NSA paper's compression phi (arXiv:2502.11089, eq. 7): a learnable
@@ -244,6 +254,10 @@ class NSAAttention(nn.Module):
             T = (n_cmp - 1) * d + l
             return (self.comp_k.pool_sequence(kc[:, :, :T], d).to(kc.dtype),
                     self.comp_v.pool_sequence(vc[:, :, :T], d).to(vc.dtype))
+        if self.attn_impl == "fused":
+            # the learned mean on the HIP kernels (spans read in place); the
+            # sequences are passed whole: their pooled tokens are the same n_cmp
+            return self.comp_k.pool_sequence(kc, d), self.comp_v.pool_sequence(vc, d)
         if d == l:
             B = kc.shape[0]
             kb = kc[:, :, :n_cmp * l].reshape(B, self.Hkv, n_cmp, l, self.dh)
