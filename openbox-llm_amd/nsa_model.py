@@ -439,14 +439,16 @@ class FullAttention(nn.Module):
         v = self._heads(yv, self.Hkv)
         if self.rope is not None:
             q, k = self.rope(q), self.rope(k)
-        k, v = expand_kv(k, self.G), expand_kv(v, self.G)
         if self.impl == "sdpa":
-            # fused kernels only: the unfused math fallback forms batched
-            # products with transposed operands, avoided on this GPU
+            # fused kernels only (the unfused math fallback forms batched
+            # products with transposed operands, avoided on this GPU), with
+            # the KV heads shared by their query groups inside the kernel
             from torch.nn.attention import SDPBackend, sdpa_kernel
             with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-                o = F.scaled_dot_product_attention(q.contiguous(), k.contiguous(), v.contiguous(), is_causal=True)
+                o = F.scaled_dot_product_attention(q.contiguous(), k.contiguous(), v.contiguous(), is_causal=True,
+                                                   enable_gqa=self.G > 1)
         else:
+            k, v = expand_kv(k, self.G), expand_kv(v, self.G)
             causal = torch.ones(T, T, dtype=torch.bool, device=x.device).tril()
             o = masked_softmax(_scores(q, k, self.scale), causal[None, None]) @ v
         return self.out_proj(o.transpose(1, 2).reshape(B, T, self.Hq * self.dh))

@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 import torch
 
-from nsa_testlib import log, require_gpu
+from nsa_testlib import assert_close, log, require_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -200,3 +200,32 @@ def test_transformer_fused_vs_ref(variant, dtype):
     d = max(abs(a - b) for a, b in zip(losses["ref"], losses["fused"]))
     log(f"  losses ref {losses['ref'][0]:.4f}->{losses['ref'][-1]:.4f}, max |delta| {d:.2e}")
     assert d <= LOSS_TOL[dtype]
+
+
+@pytest.mark.parametrize("heads", [(12, 2), (8, 8)], ids=["gqa6", "mha"])
+def test_dense_arm_sdpa_matches_ref(heads):
+    """The c4 dense arm (FullAttention impl='sdpa': stacked q/k/v projection,
+    flash kernels with the KV heads shared by their query groups) against the
+    module's materialised causal attention (impl='ref') on the same weights,
+    bf16 autocast; output and every parameter gradient."""
+    import nsa_model
+    dev = require_gpu()
+    Hq, Hkv = heads
+    torch.manual_seed(0)
+    rope = nsa_model.Rotary(64)
+    ref = nsa_model.FullAttention(64 * Hq, Hq, Hkv, rope=rope, impl="ref").to(dev)
+    sdpa = nsa_model.FullAttention(64 * Hq, Hq, Hkv, rope=rope, impl="sdpa").to(dev)
+    sdpa.load_state_dict(ref.state_dict())
+    x = torch.randn(2, 256, 64 * Hq, device=dev)
+    outs, grads = [], []
+    for m in (ref, sdpa):
+        xm = x.clone().requires_grad_()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            o = m(xm)
+        o.float().square().mean().backward()
+        outs.append(o.float())
+        grads.append([xm.grad] + [p.grad for p in m.parameters()])
+    torch.cuda.synchronize()
+    assert_close(outs[1], outs[0], torch.bfloat16, "out")
+    for i, (a, b) in enumerate(zip(grads[1], grads[0])):
+        assert_close(a.float(), b.float(), torch.bfloat16, f"grad {i}")
