@@ -74,10 +74,12 @@ int nsa_wpool_fwd(const void* x, const float* w, const float* cvec, float* out, 
  * w[t - i*d] dpool[i] (dpool float32 [B][H][n][D]); dx in dtype. */
 int nsa_wpool_bwd(const float* dpool, const float* w, void* dx, int B, int H, int T, int D, int l, int d, int dtype,
                   void* stream);
-/* Its gradient for the weights (the x part): dw[p] = sum over (b, h, i, c) of
- * x[b][h][i*d + p][c] dpool[b][h][i][c], float32 [l], summed in a fixed order. */
-int nsa_wpool_dw(const void* x, const float* dpool, float* dw, int B, int H, int T, int D, int l, int d, int dtype,
-                 void* stream);
+/* Its gradient for the weights (the x part), per (b, h): dw_part[p][b*H + h] =
+ * sum over (i, c) of x[b][h][i*d + p][c] dpool[b][h][i][c], float32 [l][B*H],
+ * each summed in a fixed order; dw[p] is the sum of row p (the caller's, so
+ * the library needs no scratch).  D % 8 == 0, D <= 2048, B*H < 65536. */
+int nsa_wpool_dw(const void* x, const float* dpool, float* dw_part, int B, int H, int T, int D, int l, int d,
+                 int dtype, void* stream);
 
 /* ---- gate ------------------------------------------------------------------
  * Replaces the gate blend of nsa_fused_forward (nsa_fused_kernel.py:572-573):

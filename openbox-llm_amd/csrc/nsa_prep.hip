@@ -254,26 +254,23 @@ __global__ __launch_bounds__(256) void k_wpool_bwd8(const float* __restrict__ dp
   }
 }
 
-// dw[p] = sum over (bh, i, c) of x[bh][i d + p][c] dp[bh][i][c]: workgroup p;
-// each thread a strided share of the 8-channel chunks, then a tree over the
-// workgroup's threads (a fixed order: the same bits every run)
+// dwp[p][bh] = sum over (i, c) of x[bh][i d + p][c] dp[bh][i][c]: workgroup
+// (p, bh); thread (row lane, channel chunk) strides over the spans, then a
+// tree over the workgroup (a fixed order: the same bits every run)
 template <typename T>
 __global__ __launch_bounds__(256) void k_wpool_dw(const T* __restrict__ x, const float* __restrict__ dp,
-                                                  float* __restrict__ dw, int BH, int L, int D, int n, int pd) {
+                                                  float* __restrict__ dwp, int BH, int L, int D, int n, int pd) {
   __shared__ float red[256];
-  const int p = blockIdx.x, tid = threadIdx.x;
-  const int dc = D / 8;
-  const int64_t total = (int64_t)BH * n * dc;
+  const int p = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  const int dc = D / 8, cl = tid % dc, rpi = 256 / dc;   // D / 8 divides 256 (D <= 2048)
+  const T* xb = x + ((int64_t)bh * L + p) * D + 8 * cl;
+  const float* gb = dp + (int64_t)bh * n * D + 8 * cl;
   float acc = 0.0f;
-  for (int64_t e = tid; e < total; e += 256) {
-    const int c = (int)(e % dc);
-    const int64_t r = e / dc;
-    const int i = (int)(r % n);
-    const int64_t bh = r / n;
+  for (int i = tid / dc; i < n; i += rpi) {
     Frag<T> f;
-    f.load(x + (bh * L + (int64_t)i * pd + p) * D + 8 * c);
+    f.load(xb + (int64_t)i * pd * D);
     Frag<float> g;
-    g.load(dp + r * D + 8 * c);
+    g.load(gb + (int64_t)i * D);
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc += to_f32(f.elem(j)) * g.elem(j);
   }
@@ -283,7 +280,7 @@ __global__ __launch_bounds__(256) void k_wpool_dw(const T* __restrict__ x, const
     if (tid < off) red[tid] += red[tid + off];
     __syncthreads();
   }
-  if (tid == 0) dw[p] = red[0];
+  if (tid == 0) dwp[(int64_t)p * BH + bh] = red[0];
 }
 
 // ---------------------------------------------------------------------------
@@ -590,18 +587,20 @@ int nsa_wpool_bwd(const float* dpool, const float* w, void* dx, int B, int H, in
   return nsa_launch_status();
 }
 
-int nsa_wpool_dw(const void* x, const float* dpool, float* dw, int B, int H, int T, int D, int l, int d, int dtype,
-                 void* stream) {
-  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && D % 8 == 0 && l > 0 && d > 0, NSA_ERR_SHAPE);
+int nsa_wpool_dw(const void* x, const float* dpool, float* dw_part, int B, int H, int T, int D, int l, int d,
+                 int dtype, void* stream) {
+  NSA_CHECK(B > 0 && H > 0 && T >= 0 && D > 0 && D % 8 == 0 && D <= 2048 && l > 0 && d > 0, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK((int64_t)B * H < 65536, NSA_ERR_SHAPE);   // the grid's second dimension
   const int n = T >= l ? (T - l) / d + 1 : 0;
-  NSA_CHECK(x && dw && aligned16(x) && (n == 0 || (dpool && aligned16(dpool))), NSA_ERR_ARG);
+  NSA_CHECK(x && dw_part && aligned16(x) && (n == 0 || (dpool && aligned16(dpool))), NSA_ERR_ARG);
   hipStream_t s = (hipStream_t)stream;
-  // n == 0: every dw[p] is an empty sum, written as 0 by the kernel's loop
+  // n == 0: every part is an empty sum, written as 0 by the kernel's loop
+  const dim3 grid((unsigned)l, (unsigned)(B * H));
   if (dtype == NSA_BF16)
-    k_wpool_dw<bf16><<<l, 256, 0, s>>>((const bf16*)x, dpool, dw, B * H, T, D, n, d);
+    k_wpool_dw<bf16><<<grid, 256, 0, s>>>((const bf16*)x, dpool, dw_part, B * H, T, D, n, d);
   else
-    k_wpool_dw<float><<<l, 256, 0, s>>>((const float*)x, dpool, dw, B * H, T, D, n, d);
+    k_wpool_dw<float><<<grid, 256, 0, s>>>((const float*)x, dpool, dw_part, B * H, T, D, n, d);
   return nsa_launch_status();
 }
 

@@ -272,14 +272,14 @@ class WeightedPoolHIP(torch.autograd.Function):
         B, H, T, D = x.shape
         dout = _contig(dout.float())
         dx = torch.empty_like(x)
-        dw = torch.empty(l, device=x.device, dtype=torch.float32)
+        dw_part = torch.empty(l, B * H, device=x.device, dtype=torch.float32)
         _call("nsa_wpool_bwd", _lib().nsa_wpool_bwd, L.ptr(dout), L.ptr(wf), L.ptr(dx), B, H, T, D, l, d,
               L.dtype_code(x), _stream(x))
-        _call("nsa_wpool_dw", _lib().nsa_wpool_dw, L.ptr(x), L.ptr(dout), L.ptr(dw), B, H, T, D, l, d,
+        _call("nsa_wpool_dw", _lib().nsa_wpool_dw, L.ptr(x), L.ptr(dout), L.ptr(dw_part), B, H, T, D, l, d,
               L.dtype_code(x), _stream(x))
         with torch.autocast("cuda", enabled=False):
             dc = dout.sum(dim=(0, 1, 2))                  # the gradient of cvec = w^T pos
-            dw = dw + pos.float() @ dc
+            dw = dw_part.sum(dim=1) + pos.float() @ dc
             dpos = wf[:, None] * dc[None, :]
         return dx, dw.to(w_dtype), dpos.to(pos.dtype), None, None
 
