@@ -41,6 +41,8 @@ SIGNATURES = {
     "nsa_wpool_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_wpool_bwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_wpool_dw": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_heads_split": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
+    "nsa_heads_merge_grad": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
     "nsa_pool_bwd": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_gate_fwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _P]),
     "nsa_bwd_prep": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _I, _P]),

@@ -7,6 +7,9 @@
 //                     dgate_c = sigmoid'(g_c) dot_c        (autograd of nsa_model.py:297-301),
 //                     coff_c = lse_c log2(e) - log2(rowscale_c) for the dK/dV kernels
 //  * cast_f32       : fp32 accumulator -> output dtype
+//  * wpool_*        : BlockCompressor's learned weighted pool and its gradients
+//  * heads_split    : stacked projection -> head-major branch inputs (+ RoPE,
+//                     bias), and the gradient scatter back (nsa_model.py:192-194)
 #include "nsa_common.h"
 #include "nsa_launch.h"
 
@@ -284,6 +287,187 @@ __global__ __launch_bounds__(256) void k_wpool_dw(const T* __restrict__ x, const
 }
 
 // ---------------------------------------------------------------------------
+// head split of a stacked projection (nsa_model.py:192-194, 325-335)
+// ---------------------------------------------------------------------------
+// A row of the stacked projection y [B][L][W] holds the segments one after
+// another: segment k (H_k heads of hd_k channels) starts at column
+// col0_k = sum_{j<k} H_j hd_j.  The split writes segment k head-major,
+// out_k [B][H_k][L][hd_k], adds its bias (if any), and rotates it (if marked)
+// by the half-split rotary: with h = hd / 2 and channel pairs (j, j + h),
+//   o[j] = a c - b s,   o[j + h] = b c + a s,     a = x[j], b = x[j + h],
+// c, s = cos, sin [t][j] from the caller's tables.  float32 arithmetic, one
+// rounding to T per output.  The gradient kernel is the transpose,
+//   dy[j] = g[j] c + g[j + h] s,   dy[j + h] = g[j + h] c - g[j] s,
+// scattered back into the stacked row (zeros for a segment without gradient).
+// Work item = (b, h, t, channel chunk), chunks fastest: head-major side
+// written / read contiguously, the stacked side in 16-byte pieces per token.
+
+constexpr int kMaxHeadSegs = 8;
+struct HeadSeg {
+  void* buf;            // split: out_k; gradient: d out_k or null
+  const float* bias;    // split only: [H hd] float32, or null
+  int col0, H, hd, rot, vec;   // vec: 8 channels per lane (else 1)
+};
+struct HeadSegs {
+  HeadSeg s[kMaxHeadSegs];
+};
+
+// segment k (uniform over the workgroup) by constant indices into the kernel
+// argument: a dynamic index would copy the table to scratch memory
+__device__ __forceinline__ HeadSeg head_seg(const HeadSegs& sg, int k) {
+  static_assert(kMaxHeadSegs == 8, "one case per segment");
+  switch (k) {
+    case 0: return sg.s[0];
+    case 1: return sg.s[1];
+    case 2: return sg.s[2];
+    case 3: return sg.s[3];
+    case 4: return sg.s[4];
+    case 5: return sg.s[5];
+    case 6: return sg.s[6];
+    default: return sg.s[7];
+  }
+}
+
+struct HeadItem {
+  int64_t r, b;   // r = (b H + h) L + t
+  int h, t, j0;   // j0: first channel of the item
+};
+
+__device__ __forceinline__ HeadItem head_item(int64_t e, const HeadSeg& g, int L, int nc, int step) {
+  HeadItem it;
+  const int c = (int)(e % nc);
+  it.r = e / nc;
+  it.t = (int)(it.r % L);
+  const int64_t bh = it.r / L;
+  it.h = (int)(bh % g.H);
+  it.b = bh / g.H;
+  it.j0 = c * step;
+  return it;
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* x) {
+  const f32x4 lo = *reinterpret_cast<const f32x4*>(p), hi = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[j] = lo[j];
+    x[4 + j] = hi[j];
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_heads_split(const T* __restrict__ y, HeadSegs sg,
+                                                     const float* __restrict__ cs, const float* __restrict__ sn,
+                                                     int L, int W, int B) {
+  const HeadSeg g = head_seg(sg, blockIdx.y);
+  T* out = (T*)g.buf;
+  const int h2 = g.hd / 2, step = g.vec ? 8 : 1;
+  const int nc = (g.rot ? h2 : g.hd) / step;
+  const int64_t total = (int64_t)B * g.H * L * nc;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const HeadItem it = head_item(e, g, L, nc, step);
+    const T* src = y + (it.b * L + it.t) * W + g.col0 + it.h * g.hd;
+    T* dst = out + it.r * g.hd;
+    const float* bias = g.bias ? g.bias + it.h * g.hd : nullptr;
+    if (g.vec) {
+      float a[8], b[8], c[8], s[8];
+      Frag<T> fa;
+      fa.load(src + it.j0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = to_f32(fa.elem(j)) + (bias ? bias[it.j0 + j] : 0.0f);
+      if (g.rot) {
+        Frag<T> fb;
+        fb.load(src + h2 + it.j0);
+        load8f(cs + (int64_t)it.t * h2 + it.j0, c);
+        load8f(sn + (int64_t)it.t * h2 + it.j0, s);
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          b[j] = to_f32(fb.elem(j)) + (bias ? bias[h2 + it.j0 + j] : 0.0f);
+          o[j] = a[j] * c[j] - b[j] * s[j];
+          b[j] = b[j] * c[j] + a[j] * s[j];
+        }
+        fa.set(o);
+        fa.store(dst + it.j0);
+        fb.set(b);
+        fb.store(dst + h2 + it.j0);
+      } else {
+        fa.set(a);
+        fa.store(dst + it.j0);
+      }
+    } else {
+      const int j = it.j0;
+      const float a = to_f32(src[j]) + (bias ? bias[j] : 0.0f);
+      if (g.rot) {
+        const float b = to_f32(src[h2 + j]) + (bias ? bias[h2 + j] : 0.0f);
+        const float c = cs[(int64_t)it.t * h2 + j], s = sn[(int64_t)it.t * h2 + j];
+        dst[j] = from_f32<T>(a * c - b * s);
+        dst[h2 + j] = from_f32<T>(b * c + a * s);
+      } else {
+        dst[j] = from_f32<T>(a);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void k_heads_merge_grad(T* __restrict__ dy, HeadSegs sg,
+                                                          const float* __restrict__ cs,
+                                                          const float* __restrict__ sn, int L, int W, int B) {
+  const HeadSeg g = head_seg(sg, blockIdx.y);
+  const T* gin = (const T*)g.buf;
+  const int h2 = g.hd / 2, step = g.vec ? 8 : 1;
+  const int nc = (g.rot ? h2 : g.hd) / step;
+  const int64_t total = (int64_t)B * g.H * L * nc;
+  for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const HeadItem it = head_item(e, g, L, nc, step);
+    T* dst = dy + (it.b * L + it.t) * W + g.col0 + it.h * g.hd;
+    const T* src = gin ? gin + it.r * g.hd : nullptr;
+    if (g.vec) {
+      float a[8], b[8], c[8], s[8];
+      Frag<T> fa, fb;
+      if (src) {
+        fa.load(src + it.j0);
+        if (g.rot) fb.load(src + h2 + it.j0);
+      } else {
+        fa.zero();
+        fb.zero();
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) a[j] = to_f32(fa.elem(j));
+      if (g.rot) {
+        load8f(cs + (int64_t)it.t * h2 + it.j0, c);
+        load8f(sn + (int64_t)it.t * h2 + it.j0, s);
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          b[j] = to_f32(fb.elem(j));
+          o[j] = a[j] * c[j] + b[j] * s[j];
+          b[j] = b[j] * c[j] - a[j] * s[j];
+        }
+        fa.set(o);
+        fa.store(dst + it.j0);
+        fb.set(b);
+        fb.store(dst + h2 + it.j0);
+      } else {
+        fa.set(a);
+        fa.store(dst + it.j0);
+      }
+    } else {
+      const int j = it.j0;
+      const float a = src ? to_f32(src[j]) : 0.0f;
+      if (g.rot) {
+        const float b = src ? to_f32(src[h2 + j]) : 0.0f;
+        const float c = cs[(int64_t)it.t * h2 + j], s = sn[(int64_t)it.t * h2 + j];
+        dst[j] = from_f32<T>(a * c + b * s);
+        dst[h2 + j] = from_f32<T>(b * c - a * s);
+      } else {
+        dst[j] = from_f32<T>(a);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // gate
 // ---------------------------------------------------------------------------
 
@@ -464,6 +648,48 @@ static inline int grid_for(int64_t n) {
   return (int)(g < 1 ? 1 : g);
 }
 
+// The segment table of a split / gradient call, checked: segments tile the
+// row exactly, rotated ones share one even head dim (the tables' width),
+// buffers on the vector path 16-byte aligned.  Returns NSA_OK or an error;
+// *items = the largest segment's work items (the grid's x extent).
+static int head_segs(HeadSegs& sg, void* const* bufs, const float* const* biases, const int* heads,
+                     const int* head_dim, const int* rotate, int nseg, const float* cos_t, const float* sin_t,
+                     int B, int T, int W, const void* stacked, bool need_bufs, int64_t* items) {
+  NSA_CHECK(nseg >= 1 && nseg <= kMaxHeadSegs && heads && head_dim && rotate && bufs, NSA_ERR_ARG);
+  NSA_CHECK(B > 0 && T >= 0 && W > 0, NSA_ERR_SHAPE);
+  NSA_CHECK(T == 0 || stacked, NSA_ERR_ARG);   // empty tensors may hold null pointers
+  int64_t col = 0;
+  int rot_hd = 0;
+  *items = 0;
+  for (int k = 0; k < nseg; ++k) {
+    const int H = heads[k], hd = head_dim[k], rot = rotate[k] ? 1 : 0;
+    NSA_CHECK(H > 0 && hd > 0, NSA_ERR_SHAPE);
+    NSA_CHECK(!need_bufs || T == 0 || bufs[k], NSA_ERR_ARG);
+    if (rot) {
+      NSA_CHECK(hd % 2 == 0 && (rot_hd == 0 || rot_hd == hd), NSA_ERR_SHAPE);
+      NSA_CHECK(cos_t && sin_t, NSA_ERR_ARG);
+      rot_hd = hd;
+    }
+    HeadSeg& g = sg.s[k];
+    g.buf = bufs[k];
+    g.bias = biases ? biases[k] : nullptr;
+    g.col0 = (int)col;
+    g.H = H;
+    g.hd = hd;
+    g.rot = rot;
+    g.vec = hd % (rot ? 16 : 8) == 0 && col % 8 == 0 && W % 8 == 0 && aligned16(stacked) &&
+            (!bufs[k] || aligned16(bufs[k])) && (!rot || (aligned16(cos_t) && aligned16(sin_t)));
+    const int64_t per = (rot ? hd / 2 : hd) / (g.vec ? 8 : 1);
+    const int64_t n = (int64_t)B * H * T * per;
+    if (n > *items) *items = n;
+    col += (int64_t)H * hd;
+    NSA_CHECK(col <= W, NSA_ERR_SHAPE);
+  }
+  NSA_CHECK(col == W, NSA_ERR_SHAPE);
+  for (int k = nseg; k < kMaxHeadSegs; ++k) sg.s[k] = sg.s[0];
+  return NSA_OK;
+}
+
 }  // namespace nsa
 
 using namespace nsa;
@@ -601,6 +827,43 @@ int nsa_wpool_dw(const void* x, const float* dpool, float* dw_part, int B, int H
     k_wpool_dw<bf16><<<grid, 256, 0, s>>>((const bf16*)x, dpool, dw_part, B * H, T, D, n, d);
   else
     k_wpool_dw<float><<<grid, 256, 0, s>>>((const float*)x, dpool, dw_part, B * H, T, D, n, d);
+  return nsa_launch_status();
+}
+
+int nsa_heads_split(const void* y, void* const* outs, const float* const* biases, const int* heads,
+                    const int* head_dim, const int* rotate, int nseg, const float* cos_t, const float* sin_t, int B,
+                    int T, int W, int dtype, void* stream) {
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  HeadSegs sg;
+  int64_t items = 0;
+  const int rc = head_segs(sg, outs, biases, heads, head_dim, rotate, nseg, cos_t, sin_t, B, T, W, y, true, &items);
+  if (rc != NSA_OK) return rc;
+  if (items == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)grid_for(items), (unsigned)nseg);
+  if (dtype == NSA_BF16)
+    k_heads_split<bf16><<<grid, 256, 0, s>>>((const bf16*)y, sg, cos_t, sin_t, T, W, B);
+  else
+    k_heads_split<float><<<grid, 256, 0, s>>>((const float*)y, sg, cos_t, sin_t, T, W, B);
+  return nsa_launch_status();
+}
+
+int nsa_heads_merge_grad(const void* const* douts, void* dy, const int* heads, const int* head_dim,
+                         const int* rotate, int nseg, const float* cos_t, const float* sin_t, int B, int T, int W,
+                         int dtype, void* stream) {
+  NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  HeadSegs sg;
+  int64_t items = 0;
+  const int rc = head_segs(sg, const_cast<void* const*>(douts), nullptr, heads, head_dim, rotate, nseg, cos_t, sin_t,
+                           B, T, W, dy, false, &items);
+  if (rc != NSA_OK) return rc;
+  if (items == 0) return NSA_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)grid_for(items), (unsigned)nseg);
+  if (dtype == NSA_BF16)
+    k_heads_merge_grad<bf16><<<grid, 256, 0, s>>>((bf16*)dy, sg, cos_t, sin_t, T, W, B);
+  else
+    k_heads_merge_grad<float><<<grid, 256, 0, s>>>((float*)dy, sg, cos_t, sin_t, T, W, B);
   return nsa_launch_status();
 }
 

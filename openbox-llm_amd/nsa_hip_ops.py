@@ -290,6 +290,105 @@ def weighted_pool(x, w, pos, l, d):
     return WeightedPoolHIP.apply(x, w, pos, l, d)
 
 
+def _seg_table(segs, bufs):
+    """ctypes arrays (kept alive by the caller) for a segment table."""
+    import ctypes
+    n = len(segs)
+    ints = ctypes.c_int * n
+    heads = ints(*[int(s[0]) for s in segs])
+    dims = ints(*[int(s[1]) for s in segs])
+    rot = ints(*[1 if s[2] else 0 for s in segs])
+    ptrs = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for b in bufs])
+    return heads, dims, rot, ptrs
+
+
+def _addr(arr):
+    import ctypes
+    return None if arr is None else ctypes.cast(arr, ctypes.c_void_p)
+
+
+class HeadSplitHIP(torch.autograd.Function):
+    """The stacked projection ``y [B,T,W]`` split into head-major tensors
+    ``[B,H_k,T,hd_k]``, one per segment ``(H_k, hd_k, rotate_k)``, in one
+    kernel: the model's ``_split_heads(proj(x)).contiguous()`` per branch
+    (nsa_model.py:192-194, 325-335), with the rotary embedding of a RoPE model
+    (half-split pairs, factors ``cos``/``sin`` [T, hd/2] float32) and one
+    segment's bias folded in.  The backward scatters the outputs' gradients
+    back into the stacked row (inverse rotation) in one kernel."""
+
+    @staticmethod
+    def forward(ctx, y, bias, cos, sin, segs, bias_seg):
+        y = _contig(y)
+        B, T, W = y.shape
+        assert len(segs) <= 8 and sum(h * d for h, d, _ in segs) == W, "segments must tile the stacked row"
+        rot = any(s[2] for s in segs)
+        if rot:
+            hd = {s[1] for s in segs if s[2]}
+            assert len(hd) == 1 and cos is not None and sin is not None, "rotated segments share one head dim"
+            assert cos.shape == (T, next(iter(hd)) // 2) and sin.shape == cos.shape, "rotary tables [T, hd/2]"
+            cos = _contig(cos.float())
+            sin = _contig(sin.float())
+        outs = [torch.empty(B, h, T, d, device=y.device, dtype=y.dtype) for h, d, _ in segs]
+        biases = None
+        bf = None
+        if bias is not None:
+            H, d, _ = segs[bias_seg]
+            assert bias.numel() == H * d, "the bias covers its segment"
+            with torch.autocast("cuda", enabled=False):
+                bf = bias.detach().float().contiguous()
+            biases = [None] * len(segs)
+            biases[bias_seg] = bf
+        heads, dims, rots, ptrs = _seg_table(segs, outs)
+        bptrs = None if biases is None else _seg_table(segs, biases)[3]
+        _call("nsa_heads_split", _lib().nsa_heads_split, L.ptr(y), _addr(ptrs), _addr(bptrs), _addr(heads),
+              _addr(dims), _addr(rots), len(segs), L.ptr(cos) if rot else None, L.ptr(sin) if rot else None, B, T, W,
+              L.dtype_code(y), _stream(y))
+        ctx.set_materialize_grads(False)
+        ctx.save_for_backward(cos if rot else None, sin if rot else None)
+        ctx.meta = (segs, bias_seg, B, T, W, y.dtype, None if bias is None else bias.dtype)
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *gouts):
+        cos, sin = ctx.saved_tensors
+        segs, bias_seg, B, T, W, dtype, bias_dtype = ctx.meta
+        gs = [None if g is None else _contig(g.to(dtype)) for g in gouts]
+        dy = torch.empty(B, T, W, device=next(g for g in gs if g is not None).device, dtype=dtype) \
+            if any(g is not None for g in gs) else None
+        if dy is None:
+            return (None,) * 6
+        heads, dims, rots, ptrs = _seg_table(segs, gs)
+        _call("nsa_heads_merge_grad", _lib().nsa_heads_merge_grad, _addr(ptrs), L.ptr(dy), _addr(heads),
+              _addr(dims), _addr(rots), len(segs), L.ptr(cos), L.ptr(sin), B, T, W, L.dtype_code(dy), _stream(dy))
+        dbias = None
+        if bias_dtype is not None and ctx.needs_input_grad[1]:
+            # float32 sums over B and T of the segment's gradient; the bias is
+            # added before the rotation, so a rotated segment's gradient is
+            # rotated back first (per t, after the sum over B)
+            H, d, rot = segs[bias_seg]
+            g = gouts[bias_seg]
+            with torch.autocast("cuda", enabled=False):
+                if g is None:
+                    dbias = torch.zeros(H * d, device=dy.device, dtype=torch.float32)
+                else:
+                    gs = g.float().sum(dim=0)                           # [H, T, d]
+                    if rot:
+                        h = d // 2
+                        a, b = gs[..., :h], gs[..., h:]
+                        gs = torch.cat([a * cos + b * sin, b * cos - a * sin], dim=-1)
+                    dbias = gs.sum(dim=1).reshape(-1)
+            dbias = dbias.to(bias_dtype)
+        return dy, dbias, None, None, None, None
+
+
+def split_heads(y, segs, cos=None, sin=None, bias=None, bias_seg=None):
+    """Head-major tensors of the stacked projection ``y [B,T,W]`` per segment
+    ``(heads, head_dim, rotate)``, rotated segments by the rotary factors
+    ``cos``/``sin`` [T, head_dim/2], ``bias`` added to segment ``bias_seg``."""
+    assert y.is_cuda, "the head split runs on the GPU"
+    return HeadSplitHIP.apply(y, bias, cos, sin, tuple(tuple(s) for s in segs), bias_seg)
+
+
 class _PoolMean(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, l, d):

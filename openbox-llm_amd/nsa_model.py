@@ -146,6 +146,23 @@ class Rotary(nn.Module):
         assert dim % 2 == 0, "rotary needs an even head dim"
         inv = base ** (-torch.arange(0, dim, 2, dtype=torch.float64) / dim)
         self.register_buffer("inv_freq", inv.float(), persistent=False)
+        self._tables = {}
+
+    def tables(self, T, device, dtype):
+        """The factors ``forward`` multiplies by, ``cos, sin [T, dim/2]`` with
+        the values of ``dtype``, held as float32 (the fused head split's
+        tables); cached per length, device, dtype and frequency buffer."""
+        inv = self.inv_freq
+        key = (T, str(device), dtype, inv.dtype, inv.data_ptr(), inv._version)
+        hit = self._tables.get(key)
+        if hit is None:
+            with torch.no_grad(), torch.autocast(device_type=torch.device(device).type, enabled=False):
+                ang = torch.arange(T, device=device, dtype=torch.float32)[:, None] * inv.to(device)[None, :]
+                hit = (ang.cos().to(dtype).float().contiguous(), ang.sin().to(dtype).float().contiguous())
+            if len(self._tables) > 8:
+                self._tables.clear()
+            self._tables[key] = hit
+        return hit
 
     def forward(self, x):
         """``x [B,H,T,D]`` rotated by position ``t``."""
@@ -271,18 +288,35 @@ class NSAAttention(nn.Module):
         B, T, _ = x.shape
         return self.gate(x).view(B, T, self.Hq, 3).permute(0, 2, 1, 3)      # [B,Hq,T,3]
 
+    def _stacked_weights(self):
+        return (self.q_proj.weight, self.k_cmp.weight, self.v_cmp.weight, self.k_slc.weight, self.v_slc.weight,
+                self.k_win.weight, self.v_win.weight, self.gate.weight)
+
     def _projections(self, x):
         """q, kc, vc, ks, vs, kw, vw and the gate logits of ``x`` ([B, T, .]
         each) from one GEMM over the eight weights stacked: one launch, one
         weight cast under autocast, and in the backward one dX GEMM instead of
         eight plus their sum.  The parameters stay the separate modules of the
         reference's layout (its state_dict names)."""
-        ws = (self.q_proj.weight, self.k_cmp.weight, self.v_cmp.weight, self.k_slc.weight, self.v_slc.weight,
-              self.k_win.weight, self.v_win.weight, self.gate.weight)
+        ws = self._stacked_weights()
         *ys, yg = torch.split(F.linear(x, torch.cat(ws, dim=0)), [t.shape[0] for t in ws], dim=-1)
         # the gate's bias on its own columns only (its gradient then sums 3 Hq
         # columns, not the whole stacked width)
         return (*ys, yg + self.gate.bias.to(yg.dtype))
+
+    def _split_fused(self, x):
+        """The fused path's inputs from the stacked projection of ``x`` in one
+        head-split kernel: q, kc, vc, ks, vs, kw, vw head-major ([B, H, T, dh],
+        q and the keys rotated when the model uses RoPE) and the gate logits
+        [B, Hq, T, 3] with the gate's bias."""
+        import nsa_hip_ops as ops
+        y = F.linear(x, torch.cat(self._stacked_weights(), dim=0))
+        r = self.rope is not None
+        cos, sin = self.rope.tables(x.shape[1], y.device, y.dtype) if r else (None, None)
+        kv = (self.Hkv, self.dh)
+        segs = ((self.Hq, self.dh, r), (*kv, r), (*kv, False), (*kv, r), (*kv, False), (*kv, r), (*kv, False),
+                (self.Hq, 3, False))
+        return ops.split_heads(y, segs, cos, sin, bias=self.gate.bias, bias_seg=7)
 
     def _merge(self, out):
         B, _, T, _ = out.shape
@@ -371,20 +405,12 @@ class NSAAttention(nn.Module):
 
         B, T, _ = x.shape
         n_cmp = self._n_cmp(T)
-        yq, ykc, yvc, yks, yvs, ykw, yvw, yg = self._projections(x)
-        q = self._rot(self._heads(yq, self.Hq)).contiguous()
-        kc = self._rot(self._heads(ykc, self.Hkv))
-        vc = self._heads(yvc, self.Hkv)
+        q, kc, vc, ks, vs, kw, vw, gate_logits = self._split_fused(x)
         if n_cmp > 0:
             k_cmp, v_cmp = self._pooled(kc, vc, n_cmp)
         else:
             k_cmp = q.new_zeros(B, self.Hkv, 0, self.dh)
             v_cmp = q.new_zeros(B, self.Hkv, 0, self.dh)
-        ks = self._rot(self._heads(yks, self.Hkv)).contiguous()
-        vs = self._heads(yvs, self.Hkv).contiguous()
-        kw = self._rot(self._heads(ykw, self.Hkv)).contiguous()
-        vw = self._heads(yvw, self.Hkv).contiguous()
-        gate_logits = yg.view(B, T, self.Hq, 3).permute(0, 2, 1, 3).contiguous()     # [B,Hq,T,3]
         k_cmp, v_cmp, ks, vs, kw, vw, gate_logits = (y.to(q.dtype) for y in (k_cmp, v_cmp, ks, vs, kw, vw,
                                                                              gate_logits))
         geom = ops.NSAGeometry(self.block_size, self.cmp_stride, self.sel_block, self.n_sel, self.window,
@@ -427,18 +453,27 @@ class FullAttention(nn.Module):
 
     def forward(self, x):
         B, T, _ = x.shape
-        if self.impl == "sdpa":
-            # the three projections as one GEMM over the stacked weights (as
-            # NSAAttention's fused path does), parameters kept separate
-            ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
-            yq, yk, yv = torch.split(F.linear(x, torch.cat(ws, dim=0)), [w.shape[0] for w in ws], dim=-1)
+        ws = (self.q_proj.weight, self.k_proj.weight, self.v_proj.weight)
+        if self.impl == "sdpa" and x.is_cuda:
+            # the plumbing of NSAAttention's fused path: one GEMM over the
+            # stacked weights (parameters kept separate), then one head-split
+            # kernel (RoPE folded in) for q, k, v
+            import nsa_hip_ops as ops
+            y = F.linear(x, torch.cat(ws, dim=0))
+            r = self.rope is not None
+            cos, sin = self.rope.tables(T, y.device, y.dtype) if r else (None, None)
+            q, k, v = ops.split_heads(y, ((self.Hq, self.dh, r), (self.Hkv, self.dh, r), (self.Hkv, self.dh, False)),
+                                      cos, sin)
         else:
-            yq, yk, yv = self.q_proj(x), self.k_proj(x), self.v_proj(x)
-        q = self._heads(yq, self.Hq)
-        k = self._heads(yk, self.Hkv)
-        v = self._heads(yv, self.Hkv)
-        if self.rope is not None:
-            q, k = self.rope(q), self.rope(k)
+            if self.impl == "sdpa":
+                yq, yk, yv = torch.split(F.linear(x, torch.cat(ws, dim=0)), [w.shape[0] for w in ws], dim=-1)
+            else:
+                yq, yk, yv = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+            q = self._heads(yq, self.Hq)
+            k = self._heads(yk, self.Hkv)
+            v = self._heads(yv, self.Hkv)
+            if self.rope is not None:
+                q, k = self.rope(q), self.rope(k)
         if self.impl == "sdpa":
             # fused kernels only (the unfused math fallback forms batched
             # products with transposed operands, avoided on this GPU), with
