@@ -85,8 +85,10 @@ int nsa_wpool_dw(const void* x, const float* dpool, float* dw_part, int B, int H
  * Replaces the model's per-branch `_split_heads(proj(x)).contiguous()`
  * (nsa_model.py:192-194, 325-335), and the rotary embedding of a RoPE model,
  * for all branches in one pass.  y [B][T][W] is the row-major output of the
- * stacked projection; its columns hold nseg segments in order, segment k being
- * heads[k] heads of head_dim[k] channels (sum heads*head_dim == W, nseg <= 8).
+ * stacked projection; its columns hold nseg segments in order from column 0,
+ * segment k being heads[k] heads of head_dim[k] channels (nseg <= 8); columns
+ * past sum heads*head_dim <= W are padding (a pitch W % 8 == 0 lets 16-byte
+ * pieces of every aligned segment move in one access).
  * outs[k] [B][heads[k]][T][head_dim[k]] gets segment k plus biases[k][h*hd+j]
  * (float32, or null; biases itself may be null), rotated when rotate[k] by the
  * half-split rotary with cos_t, sin_t float32 [T][hd/2] (all rotated segments
@@ -97,8 +99,8 @@ int nsa_heads_split(const void* y, void* const* outs, const float* const* biases
                     int T, int W, int dtype, void* stream);
 /* Gradient of nsa_heads_split for y: dy [B][T][W] from the outputs' gradients
  * douts[k] (same layout as outs[k]; a null entry is a zero gradient), the
- * inverse rotation applied to rotated segments.  Bias gradients are the
- * caller's (sums of douts[k] over B and T). */
+ * inverse rotation applied to rotated segments, zeros in the padding columns.
+ * Bias gradients are the caller's (sums over B and T). */
 int nsa_heads_merge_grad(const void* const* douts, void* dy, const int* heads, const int* head_dim,
                          const int* rotate, int nseg, const float* cos_t, const float* sin_t, int B, int T, int W,
                          int dtype, void* stream);

@@ -412,7 +412,15 @@ __global__ __launch_bounds__(256) void k_heads_split(const T* __restrict__ y, He
 template <typename T>
 __global__ __launch_bounds__(256) void k_heads_merge_grad(T* __restrict__ dy, HeadSegs sg,
                                                           const float* __restrict__ cs,
-                                                          const float* __restrict__ sn, int L, int W, int B) {
+                                                          const float* __restrict__ sn, int L, int W, int B,
+                                                          int nseg, int wseg) {
+  if ((int)blockIdx.y == nseg) {   // padding columns [wseg, W): zero gradient
+    const int pw = W - wseg;
+    const int64_t total = (int64_t)B * L * pw;
+    for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256)
+      dy[(e / pw) * W + wseg + (int)(e % pw)] = from_f32<T>(0.0f);
+    return;
+  }
   const HeadSeg g = head_seg(sg, blockIdx.y);
   const T* gin = (const T*)g.buf;
   const int h2 = g.hd / 2, step = g.vec ? 8 : 1;
@@ -648,13 +656,14 @@ static inline int grid_for(int64_t n) {
   return (int)(g < 1 ? 1 : g);
 }
 
-// The segment table of a split / gradient call, checked: segments tile the
-// row exactly, rotated ones share one even head dim (the tables' width),
-// buffers on the vector path 16-byte aligned.  Returns NSA_OK or an error;
+// The segment table of a split / gradient call, checked: segments fill the
+// row from column 0 (*wseg columns; the rest of the W-column pitch is
+// padding), rotated ones share one even head dim (the tables' width).  The
+// vector path needs 16-byte aligned pieces.  Returns NSA_OK or an error;
 // *items = the largest segment's work items (the grid's x extent).
 static int head_segs(HeadSegs& sg, void* const* bufs, const float* const* biases, const int* heads,
                      const int* head_dim, const int* rotate, int nseg, const float* cos_t, const float* sin_t,
-                     int B, int T, int W, const void* stacked, bool need_bufs, int64_t* items) {
+                     int B, int T, int W, const void* stacked, bool need_bufs, int64_t* items, int* wseg) {
   NSA_CHECK(nseg >= 1 && nseg <= kMaxHeadSegs && heads && head_dim && rotate && bufs, NSA_ERR_ARG);
   NSA_CHECK(B > 0 && T >= 0 && W > 0, NSA_ERR_SHAPE);
   NSA_CHECK(T == 0 || stacked, NSA_ERR_ARG);   // empty tensors may hold null pointers
@@ -685,7 +694,7 @@ static int head_segs(HeadSegs& sg, void* const* bufs, const float* const* biases
     col += (int64_t)H * hd;
     NSA_CHECK(col <= W, NSA_ERR_SHAPE);
   }
-  NSA_CHECK(col == W, NSA_ERR_SHAPE);
+  *wseg = (int)col;   // columns [col, W) are padding
   for (int k = nseg; k < kMaxHeadSegs; ++k) sg.s[k] = sg.s[0];
   return NSA_OK;
 }
@@ -836,7 +845,9 @@ int nsa_heads_split(const void* y, void* const* outs, const float* const* biases
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   HeadSegs sg;
   int64_t items = 0;
-  const int rc = head_segs(sg, outs, biases, heads, head_dim, rotate, nseg, cos_t, sin_t, B, T, W, y, true, &items);
+  int wseg = 0;
+  const int rc =
+      head_segs(sg, outs, biases, heads, head_dim, rotate, nseg, cos_t, sin_t, B, T, W, y, true, &items, &wseg);
   if (rc != NSA_OK) return rc;
   if (items == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -854,16 +865,20 @@ int nsa_heads_merge_grad(const void* const* douts, void* dy, const int* heads, c
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   HeadSegs sg;
   int64_t items = 0;
+  int wseg = 0;
   const int rc = head_segs(sg, const_cast<void* const*>(douts), nullptr, heads, head_dim, rotate, nseg, cos_t, sin_t,
-                           B, T, W, dy, false, &items);
+                           B, T, W, dy, false, &items, &wseg);
   if (rc != NSA_OK) return rc;
   if (items == 0) return NSA_OK;
+  const int64_t pad_items = (int64_t)B * T * (W - wseg);
+  if (pad_items > items) items = pad_items;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)grid_for(items), (unsigned)nseg);
+  // one more workgroup row zeroes the padding columns
+  const dim3 grid((unsigned)grid_for(items), (unsigned)(nseg + (W > wseg ? 1 : 0)));
   if (dtype == NSA_BF16)
-    k_heads_merge_grad<bf16><<<grid, 256, 0, s>>>((bf16*)dy, sg, cos_t, sin_t, T, W, B);
+    k_heads_merge_grad<bf16><<<grid, 256, 0, s>>>((bf16*)dy, sg, cos_t, sin_t, T, W, B, nseg, wseg);
   else
-    k_heads_merge_grad<float><<<grid, 256, 0, s>>>((float*)dy, sg, cos_t, sin_t, T, W, B);
+    k_heads_merge_grad<float><<<grid, 256, 0, s>>>((float*)dy, sg, cos_t, sin_t, T, W, B, nseg, wseg);
   return nsa_launch_status();
 }
 

@@ -309,7 +309,8 @@ def _addr(arr):
 
 class HeadSplitHIP(torch.autograd.Function):
     """The stacked projection ``y [B,T,W]`` split into head-major tensors
-    ``[B,H_k,T,hd_k]``, one per segment ``(H_k, hd_k, rotate_k)``, in one
+    ``[B,H_k,T,hd_k]``, one per segment ``(H_k, hd_k, rotate_k)`` from column
+    0 (columns past the segments are padding: ignored, zero gradient), in one
     kernel: the model's ``_split_heads(proj(x)).contiguous()`` per branch
     (nsa_model.py:192-194, 325-335), with the rotary embedding of a RoPE model
     (half-split pairs, factors ``cos``/``sin`` [T, hd/2] float32) and one
@@ -320,7 +321,7 @@ class HeadSplitHIP(torch.autograd.Function):
     def forward(ctx, y, bias, cos, sin, segs, bias_seg):
         y = _contig(y)
         B, T, W = y.shape
-        assert len(segs) <= 8 and sum(h * d for h, d, _ in segs) == W, "segments must tile the stacked row"
+        assert len(segs) <= 8 and sum(h * d for h, d, _ in segs) <= W, "segments must fit the stacked row"
         rot = any(s[2] for s in segs)
         if rot:
             hd = {s[1] for s in segs if s[2]}

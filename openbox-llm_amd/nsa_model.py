@@ -197,6 +197,16 @@ def _overlap_weights(n_cmp, n_slc, l, d, ls, device):
     return (hi - lo).clamp(min=0) / d
 
 
+def _stacked_padded(ws):
+    """The weights stacked for one GEMM, with zero rows up to a multiple of 8
+    outputs: the head split then moves 16-byte pieces of every output row
+    (the padding columns come out 0, their gradient is written 0)."""
+    pad = -sum(w.shape[0] for w in ws) % 8
+    if pad:
+        ws = tuple(ws) + (ws[0].new_zeros(pad, ws[0].shape[1]),)
+    return torch.cat(ws, dim=0)
+
+
 def _top_blocks(imp, k):
     """Top-k block indices per row, descending score then ascending index."""
     order = torch.sort(imp, dim=-1, descending=True, stable=True).indices
@@ -310,7 +320,7 @@ class NSAAttention(nn.Module):
         q and the keys rotated when the model uses RoPE) and the gate logits
         [B, Hq, T, 3] with the gate's bias."""
         import nsa_hip_ops as ops
-        y = F.linear(x, torch.cat(self._stacked_weights(), dim=0))
+        y = F.linear(x, _stacked_padded(self._stacked_weights()))
         r = self.rope is not None
         cos, sin = self.rope.tables(x.shape[1], y.device, y.dtype) if r else (None, None)
         kv = (self.Hkv, self.dh)
@@ -459,7 +469,7 @@ class FullAttention(nn.Module):
             # stacked weights (parameters kept separate), then one head-split
             # kernel (RoPE folded in) for q, k, v
             import nsa_hip_ops as ops
-            y = F.linear(x, torch.cat(ws, dim=0))
+            y = F.linear(x, _stacked_padded(ws))
             r = self.rope is not None
             cos, sin = self.rope.tables(T, y.device, y.dtype) if r else (None, None)
             q, k, v = ops.split_heads(y, ((self.Hq, self.dh, r), (self.Hkv, self.dh, r), (self.Hkv, self.dh, False)),

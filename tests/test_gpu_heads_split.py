@@ -22,6 +22,8 @@ CASES = [
     (2, 41, [(3, 24, 1), (1, 24, 1), (1, 24, 0)], None),
     # one segment
     (2, 19, [(4, 32, 1)], 0),
+    # the c4 layer with the row padded to a multiple of 8 (1572 -> 1576), as the model stacks it
+    (2, 64, [(12, 64, 1), (2, 64, 1), (2, 64, 0), (2, 64, 1), (2, 64, 0), (2, 64, 1), (2, 64, 0), (12, 3, 0), 4], 7),
 ]
 
 
@@ -64,8 +66,10 @@ def _check(got, ref, dtype):
 def test_heads_split_matches_definition(case, dtype):
     import nsa_hip_ops as ops
     B, T, segs, bias_seg = CASES[case]
+    pad = segs[-1] if isinstance(segs[-1], int) else 0
+    segs = segs[:-1] if pad else segs
     torch.manual_seed(case)
-    W = sum(h * d for h, d, _ in segs)
+    W = sum(h * d for h, d, _ in segs) + pad
     y = torch.randn(B, T, W, device="cuda").to(dtype).requires_grad_()
     bias = None
     if bias_seg is not None:
@@ -92,6 +96,8 @@ def test_heads_split_matches_definition(case, dtype):
     loss64 = sum((r * c.double()).sum() for i, (r, c) in enumerate(zip(refs, cots)) if i != skip)
     g64 = torch.autograd.grad(loss64, [y64] + ([b64] if b64 is not None else []))
     _check(grads[0], g64[0], dtype)
+    if pad:
+        assert bool((grads[0][..., W - pad:] == 0).all()), "padding columns get a zero gradient"
     if bias is not None:
         torch.testing.assert_close(grads[1].double(), g64[1], rtol=1e-4, atol=1e-4)
 
@@ -103,14 +109,14 @@ def test_heads_split_empty_sequence():
     assert q.shape == (2, 2, 0, 32) and k.shape == (2, 1, 0, 32)
 
 
-def test_heads_split_rejects_a_table_that_does_not_tile_the_row():
+def test_heads_split_rejects_a_table_wider_than_the_row():
     import _nsa_lib as L
     import nsa_hip_ops as ops
     y = torch.zeros(1, 4, 96, device="cuda", dtype=torch.bfloat16)
     with pytest.raises(AssertionError):
-        ops.split_heads(y, [(2, 32, 0)])
+        ops.split_heads(y, [(2, 32, 0), (1, 40, 0)])
     # the library's own check, past the Python one
-    heads, dims, rots, ptrs = ops._seg_table([(2, 32, 0)], [torch.empty(1, 2, 4, 32, device="cuda",
+    heads, dims, rots, ptrs = ops._seg_table([(2, 64, 0)], [torch.empty(1, 2, 4, 64, device="cuda",
                                                                          dtype=torch.bfloat16)])
     rc = L.load().nsa_heads_split(L.ptr(y), ops._addr(ptrs), None, ops._addr(heads), ops._addr(dims),
                                   ops._addr(rots), 1, None, None, 1, 4, 96, L.dtype_code(y), L.stream_of(y))
