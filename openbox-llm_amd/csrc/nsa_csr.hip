@@ -5,7 +5,7 @@
 // otherwise; a stable LSD radix sort of (key, t) then groups the pairs by
 // block with queries ascending, exactly like the reference's stable argsort.
 // Offsets are lower bounds of every block key in the sorted keys.
-#include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_radix_sort.hpp>
 
 #include "nsa_launch.h"
 #include "nsa_items.h"
@@ -61,6 +61,19 @@ __global__ __launch_bounds__(256) void k_csr_pair_bh(const uint32_t* __restrict_
     pair_bh[e] = e < P ? (int32_t)(skeys[e] / (uint32_t)n_blk) : -1;
 }
 
+// The stable radix sort of the (key, value) pairs.  rocprim sorts up to
+// MergeSortLimit items by block sort + merge passes (about 10 passes at 2^20
+// pairs); past the limit by onesweep LSD passes over the few key bits.  The
+// limit is lowered so that the CSR's sizes (2^17 pairs and up) take onesweep.
+// Both algorithms are stable: equal keys keep the input order.
+using CsrSortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::default_config,
+                                                 rocprim::default_config, (size_t)1 << 17>;
+
+static inline hipError_t csr_sort(void* temp, size_t& bytes, const uint32_t* kin, uint32_t* kout, const int32_t* vin,
+                                  int32_t* vout, int n, int end_bit, hipStream_t s) {
+  return rocprim::radix_sort_pairs<CsrSortConfig>(temp, bytes, kin, kout, vin, vout, n, 0u, (unsigned)end_bit, s);
+}
+
 struct CsrLayout {
   int64_t n;
   size_t keys_in, vals_in, keys_out, temp, temp_bytes, total;
@@ -77,9 +90,7 @@ static CsrLayout csr_layout(int B, int Hkv, int T, int S, int n_blk) {
   while (bits < 32 && (1ull << bits) <= sentinel) ++bits;
   c.end_bit = bits;
   c.temp_bytes = 0;
-  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, c.temp_bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)c.n, 0, c.end_bit,
-                                     (hipStream_t)0);
+  (void)csr_sort(nullptr, c.temp_bytes, nullptr, nullptr, nullptr, nullptr, (int)c.n, c.end_bit, (hipStream_t)0);
   c.keys_in = 0;
   c.vals_in = c.keys_in + align256(c.n * sizeof(uint32_t));
   c.keys_out = c.vals_in + align256(c.n * sizeof(int32_t));
@@ -126,9 +137,7 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
                                              (uint32_t)((int64_t)nbh * n_blk), pack_slot);
     if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
     size_t tb = c.temp_bytes;
-    if (hipcub::DeviceRadixSort::SortPairs(temp, tb, kin, kout, vin, q_of_block, (int)c.n, 0, c.end_bit, s) !=
-        hipSuccess)
-      return NSA_ERR_LAUNCH;
+    if (csr_sort(temp, tb, kin, kout, vin, q_of_block, (int)c.n, c.end_bit, s) != hipSuccess) return NSA_ERR_LAUNCH;
   }
   k_csr_offsets<<<grid_for((int64_t)nbh * (n_blk + 1)), 256, 0, s>>>(kout, c.n, nbh, n_blk, block_offsets,
                                                                      pair_count);
