@@ -164,8 +164,10 @@ int nsa_sel_dq(const void* q, const void* k, const void* v, const void* kt, cons
  * ceil(T / block_size) to include the trailing partial block.  Outputs:
  * q_of_block [cap] (the query t, or (t << b) | s with b = ceil(log2 S) -- s the pair's slot in block_idx --
  * when pack_slot != 0), block_offsets [B][Hkv][n_blk+1] (global offsets),
- * pair_bh [cap], *pair_count (device int).  cap = B*Hkv*T*S.  Scratch from
- * nsa_csr_workspace. */
+ * pair_bh [cap] (nullable), *pair_count (device int); entries past
+ * *pair_count are unspecified.  cap = B*Hkv*T*S.  Pairs of one (b, hkv, j)
+ * keep the input order ((t, slot) ascending, a block held twice by a row
+ * twice).  Deterministic.  Scratch from nsa_csr_workspace. */
 size_t nsa_csr_workspace(int B, int Hkv, int T, int S, int n_blk);
 int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_offsets, int32_t* pair_bh,
                   int32_t* pair_count, void* workspace, size_t workspace_bytes, int B, int Hkv, int T, int S,
