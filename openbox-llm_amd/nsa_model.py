@@ -99,10 +99,10 @@ class BlockCompressor(nn.Module):
         ``[i stride, i stride + block_size)``) on the HIP kernels, which read
         the overlapping spans in place; the weighted sum in float32, as the
         unfolded form computes it, the projection under the caller's
-        autocast."""
+        autocast (its weight gradient as batched float32 products)."""
         import nsa_hip_ops as ops
         w = torch.softmax(self.pool_logits, dim=0)
-        return self.proj(ops.weighted_pool(x, w, self.intra_pos, self.block_size, stride))
+        return ops.linear_split_dw(ops.weighted_pool(x, w, self.intra_pos, self.block_size, stride), self.proj.weight)
 
 
 class MLPCompressor(nn.Module):
