@@ -76,6 +76,75 @@ def _scores(q, k, scale):
     return torch.matmul(q, k.transpose(-1, -2).contiguous()) * scale
 
 
+_SPLITK_PARTS = 16
+_SPLITK_MAX_BYTES = 256 << 20    # float32 partial weight gradients of one split-K product
+
+
+def _weight_grad(g2, x2):
+    """``g2^T x2`` for the rows of a linear layer ([M, out], [M, in]).  On the
+    GPU in 16 bits, with M in the tens of thousands, one GEMM of a small
+    [out, in] result over M runs on a few dozen workgroups; the rows are taken
+    instead as 16 batched products with float32 outputs (bmm's out_dtype),
+    summed in float32: 2.5-3x faster at the c4 shapes.  Either way the weight
+    gradient comes out in float32, with no bf16 rounding."""
+    M, P = g2.shape[0], _SPLITK_PARTS
+    if not (g2.is_cuda and g2.dtype in (torch.bfloat16, torch.float16)):
+        return g2.t() @ x2
+    if M % P == 0 and M >= P * 256 and P * g2.shape[1] * x2.shape[1] * 4 <= _SPLITK_MAX_BYTES:
+        return torch.bmm(g2.view(P, M // P, -1).transpose(1, 2), x2.view(P, M // P, -1),
+                         out_dtype=torch.float32).sum(0)
+    return torch.mm(g2.t(), x2, out_dtype=torch.float32)
+
+
+class _SplitKLinear(torch.autograd.Function):
+    """``F.linear`` in the compute dtype ``cdt`` (inputs cast as autocast
+    would), with the weight gradient through ``_weight_grad``.  Saves the cast
+    input and weight, as autocast's linear does."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, cdt):
+        xc, wc = x.to(cdt), w.to(cdt)
+        ctx.save_for_backward(xc, wc)
+        ctx.meta = (x.dtype, w.dtype, None if b is None else b.dtype)
+        with torch.autocast("cuda", enabled=False):
+            return F.linear(xc, wc, None if b is None else b.to(cdt))
+
+    @staticmethod
+    def backward(ctx, g):
+        xc, wc = ctx.saved_tensors
+        x_dt, w_dt, b_dt = ctx.meta
+        g2 = g.reshape(-1, g.shape[-1]).to(wc.dtype)
+        dx = dw = db = None
+        if ctx.needs_input_grad[0]:
+            dx = (g2 @ wc).view(*xc.shape[:-1], wc.shape[1]).to(x_dt)
+        if ctx.needs_input_grad[1]:
+            dw = _weight_grad(g2, xc.reshape(-1, xc.shape[-1])).to(w_dt)
+        if b_dt is not None and ctx.needs_input_grad[2]:
+            db = g2.float().sum(0).to(b_dt)
+        return dx, dw, db, None
+
+
+def _linear(x, w, b=None):
+    """``F.linear(x, w, b)``; on the GPU with a 16-bit compute dtype (autocast,
+    or 16-bit x and w) through ``_SplitKLinear``."""
+    if x.is_cuda:
+        if torch.is_autocast_enabled("cuda"):
+            cdt = torch.get_autocast_dtype("cuda")
+            if cdt in (torch.bfloat16, torch.float16):
+                return _SplitKLinear.apply(x, w, b, cdt)
+        elif x.dtype in (torch.bfloat16, torch.float16) and w.dtype == x.dtype:
+            return _SplitKLinear.apply(x, w, b, x.dtype)
+    return F.linear(x, w, b)
+
+
+class Linear(nn.Linear):
+    """``nn.Linear`` (same parameters and state_dict names) computed by
+    ``_linear``."""
+
+    def forward(self, x):
+        return _linear(x, self.weight, self.bias)
+
+
 class BlockCompressor(nn.Module):
     """Learned pooling of one span of ``block_size`` tokens into one token:
     ``proj(sum_p softmax(pool_logits)_p * (x_p + intra_pos_p))``
@@ -86,7 +155,7 @@ class BlockCompressor(nn.Module):
         self.block_size = block_size
         self.intra_pos = nn.Parameter(torch.zeros(block_size, d_head))
         self.pool_logits = nn.Parameter(torch.zeros(block_size))
-        self.proj = nn.Linear(d_head, d_head, bias=False)
+        self.proj = Linear(d_head, d_head, bias=False)
 
     def forward(self, x_blocks):
         """``x_blocks [B,Hkv,n_blk,block_size,D] -> [B,Hkv,n_blk,D]``."""
@@ -120,8 +189,8 @@ class MLPCompressor(nn.Module):
         self.block_size = block_size
         self.hidden = d_head if hidden is None else hidden
         self.intra_pos = nn.Parameter(torch.zeros(block_size, d_head))
-        self.fc1 = nn.Linear(block_size * d_head, self.hidden)
-        self.fc2 = nn.Linear(self.hidden, d_head)
+        self.fc1 = Linear(block_size * d_head, self.hidden)
+        self.fc2 = Linear(self.hidden, d_head)
 
     def forward(self, x_blocks):
         """``x_blocks [B,Hkv,n_blk,block_size,D] -> [B,Hkv,n_blk,D]``."""
@@ -179,9 +248,9 @@ class SwiGLU(nn.Module):
 
     def __init__(self, d_model, hidden):
         super().__init__()
-        self.w_gate = nn.Linear(d_model, hidden, bias=False)
-        self.w_up = nn.Linear(d_model, hidden, bias=False)
-        self.w_down = nn.Linear(hidden, d_model, bias=False)
+        self.w_gate = Linear(d_model, hidden, bias=False)
+        self.w_up = Linear(d_model, hidden, bias=False)
+        self.w_down = Linear(hidden, d_model, bias=False)
 
     def forward(self, x):
         return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
@@ -242,13 +311,13 @@ class NSAAttention(nn.Module):
         self.register_buffer("scale", torch.tensor(self.dh ** -0.5), persistent=False)
 
         kv_dim = self.Hkv * self.dh
-        self.q_proj = nn.Linear(d_model, self.Hq * self.dh, bias=False)
-        self.k_cmp = nn.Linear(d_model, kv_dim, bias=False)
-        self.v_cmp = nn.Linear(d_model, kv_dim, bias=False)
-        self.k_slc = nn.Linear(d_model, kv_dim, bias=False)
-        self.v_slc = nn.Linear(d_model, kv_dim, bias=False)
-        self.k_win = nn.Linear(d_model, kv_dim, bias=False)
-        self.v_win = nn.Linear(d_model, kv_dim, bias=False)
+        self.q_proj = Linear(d_model, self.Hq * self.dh, bias=False)
+        self.k_cmp = Linear(d_model, kv_dim, bias=False)
+        self.v_cmp = Linear(d_model, kv_dim, bias=False)
+        self.k_slc = Linear(d_model, kv_dim, bias=False)
+        self.v_slc = Linear(d_model, kv_dim, bias=False)
+        self.k_win = Linear(d_model, kv_dim, bias=False)
+        self.v_win = Linear(d_model, kv_dim, bias=False)
         self.compressor = compressor
         if compressor == "mlp":
             self.comp_k = MLPCompressor(block_size, self.dh, cmp_hidden)
@@ -256,8 +325,8 @@ class NSAAttention(nn.Module):
         else:
             self.comp_k = BlockCompressor(block_size, self.dh)
             self.comp_v = BlockCompressor(block_size, self.dh)
-        self.gate = nn.Linear(d_model, self.Hq * 3, bias=True)
-        self.out_proj = nn.Linear(self.Hq * self.dh, d_model, bias=False)
+        self.gate = Linear(d_model, self.Hq * 3, bias=True)
+        self.out_proj = Linear(self.Hq * self.dh, d_model, bias=False)
 
     @property
     def aligned(self):
@@ -320,7 +389,7 @@ class NSAAttention(nn.Module):
         q and the keys rotated when the model uses RoPE) and the gate logits
         [B, Hq, T, 3] with the gate's bias."""
         import nsa_hip_ops as ops
-        y = F.linear(x, _stacked_padded(self._stacked_weights()))
+        y = _linear(x, _stacked_padded(self._stacked_weights()))
         r = self.rope is not None
         cos, sin = self.rope.tables(x.shape[1], y.device, y.dtype) if r else (None, None)
         kv = (self.Hkv, self.dh)
@@ -452,10 +521,10 @@ class FullAttention(nn.Module):
         self.rope = rope
         self.impl = impl
         self.register_buffer("scale", torch.tensor(self.dh ** -0.5), persistent=False)
-        self.q_proj = nn.Linear(d_model, self.Hq * self.dh, bias=False)
-        self.k_proj = nn.Linear(d_model, self.Hkv * self.dh, bias=False)
-        self.v_proj = nn.Linear(d_model, self.Hkv * self.dh, bias=False)
-        self.out_proj = nn.Linear(self.Hq * self.dh, d_model, bias=False)
+        self.q_proj = Linear(d_model, self.Hq * self.dh, bias=False)
+        self.k_proj = Linear(d_model, self.Hkv * self.dh, bias=False)
+        self.v_proj = Linear(d_model, self.Hkv * self.dh, bias=False)
+        self.out_proj = Linear(self.Hq * self.dh, d_model, bias=False)
 
     def _heads(self, y, n_heads):
         B, T, _ = y.shape
@@ -469,7 +538,7 @@ class FullAttention(nn.Module):
             # stacked weights (parameters kept separate), then one head-split
             # kernel (RoPE folded in) for q, k, v
             import nsa_hip_ops as ops
-            y = F.linear(x, _stacked_padded(ws))
+            y = _linear(x, _stacked_padded(ws))
             r = self.rope is not None
             cos, sin = self.rope.tables(T, y.device, y.dtype) if r else (None, None)
             q, k, v = ops.split_heads(y, ((self.Hq, self.dh, r), (self.Hkv, self.dh, r), (self.Hkv, self.dh, False)),
@@ -535,7 +604,7 @@ class Block(nn.Module):
             self.ffn = SwiGLU(d_model, hidden)
         else:
             assert ffn == "gelu", "ffn must be 'gelu' or 'swiglu'"
-            self.ffn = nn.Sequential(nn.Linear(d_model, hidden), nn.GELU(), nn.Linear(hidden, d_model))
+            self.ffn = nn.Sequential(Linear(d_model, hidden), nn.GELU(), Linear(hidden, d_model))
 
     def forward(self, x):
         x = x + self.attn(self.ln1(x))
@@ -576,7 +645,7 @@ class NSATransformer(nn.Module):
                                            norm=norm, ffn=ffn, ffn_hidden=ffn_hidden, **kw)
                                      for _ in range(n_layers)])
         self.ln_f = _norm(norm, d_model)
-        self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
+        self.lm_head = Linear(d_model, vocab_size, bias=False)
         if tie_embeddings:
             self.lm_head.weight = self.tok_emb.weight
         self.apply(self._init)

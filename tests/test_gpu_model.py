@@ -229,3 +229,37 @@ def test_dense_arm_sdpa_matches_ref(heads):
     assert_close(outs[1], outs[0], torch.bfloat16, "out")
     for i, (a, b) in enumerate(zip(grads[1], grads[0])):
         assert_close(a.float(), b.float(), torch.bfloat16, f"grad {i}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,d_in,d_out,bias", [(8192, 768, 1576, False), (4096, 2048, 768, True),
+                                                  (1000, 96, 40, True)])
+def test_split_k_linear_matches_linear(rows, d_in, d_out, bias):
+    """The model's GPU linear under bf16 autocast: forward bit-identical to
+    F.linear, dX within bf16 rounding, and the weight (and bias) gradient
+    within 1e-4 of the float64 product: the split-K sum keeps float32 (rows
+    not a multiple of 16 x 256 take the single product)."""
+    import nsa_model
+    torch.manual_seed(rows)
+    x = torch.randn(2, rows // 2, d_in, device="cuda", requires_grad=True)
+    lin = nsa_model.Linear(d_in, d_out, bias=bias).cuda()
+    g = torch.randn(2, rows // 2, d_out, device="cuda").bfloat16()
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = lin(x)
+        y_ref = torch.nn.functional.linear(x, lin.weight, lin.bias)
+    assert y.dtype == torch.bfloat16 and torch.equal(y, y_ref)
+    y.backward(g)
+    dx, dw = x.grad.clone(), lin.weight.grad.clone()
+    db = lin.bias.grad.clone() if bias else None
+    x.grad = None
+    lin.weight.grad = None
+    y_ref.backward(g)
+    assert_close(dx, x.grad, torch.bfloat16, "dx")
+    xb = x.detach().bfloat16().double().reshape(-1, d_in)
+    g64 = g.double().reshape(-1, d_out)
+    dw64 = g64.t() @ xb
+    err = (dw.double() - dw64).abs().max().item()
+    print(f"[split-k linear] rows {rows} {d_in}->{d_out}: dW max err {err:.3e} of {dw64.abs().max().item():.3e}")
+    assert err <= 1e-4 * dw64.abs().max().item()
+    if bias:
+        assert (db.double() - g64.sum(0)).abs().max().item() <= 1e-4 * g64.sum(0).abs().max().item()
