@@ -371,12 +371,13 @@ class HeadSplitHIP(torch.autograd.Function):
             with torch.autocast("cuda", enabled=False):
                 if g is None:
                     dbias = torch.zeros(H * d, device=dy.device, dtype=torch.float32)
+                elif not rot:
+                    dbias = g.float().sum(dim=(0, 2)).reshape(-1)       # [H, d] summed over B and T
                 else:
                     gs = g.float().sum(dim=0)                           # [H, T, d]
-                    if rot:
-                        h = d // 2
-                        a, b = gs[..., :h], gs[..., h:]
-                        gs = torch.cat([a * cos + b * sin, b * cos - a * sin], dim=-1)
+                    h = d // 2
+                    a, b = gs[..., :h], gs[..., h:]
+                    gs = torch.cat([a * cos + b * sin, b * cos - a * sin], dim=-1)
                     dbias = gs.sum(dim=1).reshape(-1)
             dbias = dbias.to(bias_dtype)
         return dy, dbias, None, None, None, None
