@@ -263,3 +263,30 @@ def test_split_k_linear_matches_linear(rows, d_in, d_out, bias):
     assert err <= 1e-4 * dw64.abs().max().item()
     if bias:
         assert (db.double() - g64.sum(0)).abs().max().item() <= 1e-4 * g64.sum(0).abs().max().item()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("arm", ["nsa", "full"])
+def test_model_is_causal(arm):
+    """Tokens at and after t0 cannot change the logits before t0: a small
+    c4-like decoder (G = 6, RoPE, RMSNorm, SwiGLU, l32/d16 l'64, fused NSA or
+    SDPA), bf16 autocast, every token from t0 on replaced.  t0 sits inside a
+    selection block, so queries before it see that block with its later keys
+    masked.  The forward's reductions never mix rows, so the logits before t0
+    must be bit-identical; the ones after must change."""
+    import nsa_model
+    torch.manual_seed(0)
+    B, T, V, t0 = 2, 1024, 512, 700
+    m = nsa_model.NSATransformer(
+        vocab_size=V, d_model=384, n_layers=2, n_q_heads=6, n_kv_heads=1, max_seq_len=T, ffn_hidden=768,
+        norm="rms", ffn="swiglu", pos="rope", tie_embeddings=False, attn_type=arm, attn_impl="fused",
+        dense_impl="sdpa", block_size=32, cmp_stride=16, sel_block=64, n_selected_blocks=4, window=128).cuda()
+    x = torch.randint(0, V, (B, T), device="cuda")
+    x2 = x.clone()
+    x2[:, t0:] = torch.randint(0, V, (B, T - t0), device="cuda")
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        a, _ = m(x)
+        b, _ = m(x2)
+    assert torch.equal(a[:, :t0], b[:, :t0]), \
+        f"{arm}: logits before t0 moved by {(a[:, :t0].float() - b[:, :t0].float()).abs().max().item():.3e}"
+    assert not torch.equal(a[:, t0:], b[:, t0:])
