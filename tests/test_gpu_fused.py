@@ -268,10 +268,10 @@ def test_csr_bit_exact():
     dev = require_gpu()
     import nsa_fsa
     import nsa_hip_ops as ops
-    # the last case has 6000 one-token blocks: past the counting build's LDS
-    # budget, it takes the radix-sort build
+    # (T 10, block 16): no complete block, an empty count matrix; 6000
+    # one-token blocks: past the counting build's LDS budget, the radix sort
     for (B, Hkv, T, bs, S, seed) in ((2, 2, 256, 16, 5, 0), (1, 4, 1024, 64, 16, 1), (1, 1, 100, 32, 4, 2),
-                                     (1, 2, 6000, 1, 4, 3)):
+                                     (1, 2, 10, 16, 3, 4), (1, 2, 6000, 1, 4, 3)):
         idx = make_block_idx(B, Hkv, T, bs, S, seed=seed)
         # -1 padding becomes block 2: non-causal (future) for early rows, causal later
         idx[..., -1] = torch.where(idx[..., -1] < 0, torch.full_like(idx[..., -1], 2), idx[..., -1])
