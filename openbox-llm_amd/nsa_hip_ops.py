@@ -1088,38 +1088,6 @@ def _sum_of_products(a, b, parts=16):
     return torch.bmm(a3, b.view(parts, mc, b.shape[1])).sum(0)
 
 
-class LinearSplitDW(torch.autograd.Function):
-    """``x @ w^T`` (no bias) for a small weight applied to many rows (the
-    compressors' projection of every pooled token).  Forward and dX are
-    ``F.linear`` under the caller's autocast.  The weight gradient, a small
-    [out, in] sum over all rows, is taken as 16 batched float32 products
-    summed: as one GEMM it runs on a single workgroup."""
-
-    @staticmethod
-    @torch.amp.custom_fwd(device_type="cuda")
-    def forward(ctx, x, w):
-        ctx.save_for_backward(x, w)
-        return torch.nn.functional.linear(x, w)
-
-    @staticmethod
-    @torch.amp.custom_bwd(device_type="cuda")
-    def backward(ctx, g):
-        x, w = ctx.saved_tensors
-        dx = dw = None
-        if ctx.needs_input_grad[0]:
-            dx = torch.matmul(g, w.to(g.dtype)).to(x.dtype)
-        if ctx.needs_input_grad[1]:
-            with torch.autocast("cuda", enabled=False):
-                dw = _sum_of_products(g.reshape(-1, g.shape[-1]).float(), x.reshape(-1, x.shape[-1]).float())
-            dw = dw.to(w.dtype)
-        return dx, dw
-
-
-def linear_split_dw(x, w):
-    """``x @ w^T`` with the weight gradient spread over the GPU (LinearSplitDW)."""
-    return LinearSplitDW.apply(x, w)
-
-
 def _phi_dw1(x, dpre, BH, n, l, d):
     """dW1 = sum over spans of dpre_i^T vec(span_i), float32 ([H, l D]).  When
     d divides l, span i is the l / d consecutive d-row chunks i .. i + l/d - 1

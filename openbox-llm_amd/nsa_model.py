@@ -90,7 +90,7 @@ def _weight_grad(g2, x2):
     M, P = g2.shape[0], _SPLITK_PARTS
     if not (g2.is_cuda and g2.dtype in (torch.bfloat16, torch.float16)):
         return g2.t() @ x2
-    if M % P == 0 and M >= P * 256 and P * g2.shape[1] * x2.shape[1] * 4 <= _SPLITK_MAX_BYTES:
+    if M % P == 0 and M >= P * 64 and P * g2.shape[1] * x2.shape[1] * 4 <= _SPLITK_MAX_BYTES:
         return torch.bmm(g2.view(P, M // P, -1).transpose(1, 2), x2.view(P, M // P, -1),
                          out_dtype=torch.float32).sum(0)
     return torch.mm(g2.t(), x2, out_dtype=torch.float32)
@@ -168,10 +168,10 @@ class BlockCompressor(nn.Module):
         ``[i stride, i stride + block_size)``) on the HIP kernels, which read
         the overlapping spans in place; the weighted sum in float32, as the
         unfolded form computes it, the projection under the caller's
-        autocast (its weight gradient as batched float32 products)."""
+        autocast (its weight gradient split over the pooled tokens)."""
         import nsa_hip_ops as ops
         w = torch.softmax(self.pool_logits, dim=0)
-        return ops.linear_split_dw(ops.weighted_pool(x, w, self.intra_pos, self.block_size, stride), self.proj.weight)
+        return _linear(ops.weighted_pool(x, w, self.intra_pos, self.block_size, stride), self.proj.weight)
 
 
 class MLPCompressor(nn.Module):

@@ -233,12 +233,13 @@ def test_dense_arm_sdpa_matches_ref(heads):
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("rows,d_in,d_out,bias", [(8192, 768, 1576, False), (4096, 2048, 768, True),
-                                                  (1000, 96, 40, True)])
+                                                  (4080, 64, 64, False), (1000, 96, 40, True)])
 def test_split_k_linear_matches_linear(rows, d_in, d_out, bias):
     """The model's GPU linear under bf16 autocast: forward bit-identical to
     F.linear, dX within bf16 rounding, and the weight (and bias) gradient
-    within 1e-4 of the float64 product: the split-K sum keeps float32 (rows
-    not a multiple of 16 x 256 take the single product)."""
+    within 1e-4 of the float64 product: the split-K sum keeps float32 (4080
+    rows: the compressors' projection at c4; rows not a multiple of 16, or
+    fewer than 16 x 64, take one product with a float32 output)."""
     import nsa_model
     torch.manual_seed(rows)
     x = torch.randn(2, rows // 2, d_in, device="cuda", requires_grad=True)
