@@ -77,7 +77,8 @@ def _scores(q, k, scale):
 
 
 _SPLITK_PARTS = 16
-_SPLITK_MAX_BYTES = 256 << 20    # float32 partial weight gradients of one split-K product
+_SPLITK_PART_BYTES = 80 << 20    # float32 partials of one split-K product: fewer parts past this
+_SPLITK_MAX_BYTES = 256 << 20    # ... and no split past this
 
 
 def _weight_grad(g2, x2):
@@ -85,11 +86,15 @@ def _weight_grad(g2, x2):
     GPU in 16 bits, with M in the tens of thousands, one GEMM of a small
     [out, in] result over M runs on a few dozen workgroups; the rows are taken
     instead as 16 batched products with float32 outputs (bmm's out_dtype),
-    summed in float32: 2.5-3x faster at the c4 shapes.  Either way the weight
-    gradient comes out in float32, with no bf16 rounding."""
+    summed in float32: 2.5-3x faster at the c4 shapes.  Large outputs take 8
+    parts, as the extra partials' sum costs more than the parallelism gains
+    there ([2048, 768]: 118 us at 8 parts, 145 at 16, 229 as one GEMM).  Either
+    way the weight gradient comes out in float32, with no bf16 rounding."""
     M, P = g2.shape[0], _SPLITK_PARTS
     if not (g2.is_cuda and g2.dtype in (torch.bfloat16, torch.float16)):
         return g2.t() @ x2
+    while P > 8 and P * g2.shape[1] * x2.shape[1] * 4 > _SPLITK_PART_BYTES:
+        P //= 2
     if M % P == 0 and M >= P * 64 and P * g2.shape[1] * x2.shape[1] * 4 <= _SPLITK_MAX_BYTES:
         return torch.bmm(g2.view(P, M // P, -1).transpose(1, 2), x2.view(P, M // P, -1),
                          out_dtype=torch.float32).sum(0)
