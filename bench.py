@@ -208,6 +208,54 @@ def sel_dkdv_bytes(w, pairs):
     return algorithmic, compulsory
 
 
+def compulsory_bytes(w, kernel, kv, pairs):
+    """Bytes a kernel must move at least: every tensor of its operation read or
+    written once (inputs at their sizes, outputs once per row), or None where
+    no formula is kept.  The selection dK/dV: Q, dO and dQ rows (one per query
+    row), the row statistics, and per key K, V, K^T read and dK, dV written in
+    float32."""
+    if kernel == "dkdv[sel]":
+        return sel_dkdv_bytes(w, pairs)[1]
+    return None
+
+
+def roofline_of(w, name, flops, per_launch_s, traffic, kv, pairs):
+    """Roofline entry of one kernel: the bound is set by its arithmetic
+    intensity over its compulsory bytes against the ridge point of the peaks
+    (bf16 MFMA FLOP/s over HBM B/s); `frac` is the algorithmic work per launch
+    (FLOPs, or the compulsory bytes when HBM-bound) / launch duration / peak.
+    `traffic` is the counter-measured HBM bytes per launch and
+    `traffic_ratio` its multiple of the compulsory bytes."""
+    tflops = flops / per_launch_s / 1e12
+    comp = compulsory_bytes(w, name, kv, pairs)
+    ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+    ent = {"kernel": name, "launch_ms": round(per_launch_s * 1e3, 4), "algorithmic_tflop": round(flops / 1e12, 4),
+           "traffic": traffic, "compulsory_bytes": comp}
+    hbm_frac = comp / per_launch_s / 1e9 / PEAK_HBM_GBS if comp else None
+    intensity = flops / comp if comp else None
+    if intensity is None or intensity >= ridge:
+        ent.update({"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(tflops / PEAK_BF16_TFLOPS, 4)})
+    else:
+        gbs = comp / per_launch_s / 1e9
+        ent.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4)})
+    ent.update({"mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                "hbm_frac": round(hbm_frac, 4) if hbm_frac is not None else None,
+                "intensity_flop_per_byte": round(intensity, 1) if intensity else None,
+                "ridge_flop_per_byte": round(ridge, 1)})
+    if traffic:
+        ent["measured_gbs"] = round(traffic / per_launch_s / 1e9, 1)
+        ent["traffic_ratio"] = round(traffic / comp, 2) if comp else None
+    if name == "dkdv[sel]":
+        # the bytes of its block-outer schedule (Q, dO and dQ-partial rows per
+        # (query, block) pair): what the kernel can move at best as built
+        sched = sel_dkdv_bytes(w, pairs)[0]
+        ent["schedule_bytes"] = sched
+        ent["achieved_gbs"] = round(sched / per_launch_s / 1e9, 1)
+    return ent
+
+
 def _setup(w, dev, dtype, seed=0):
     import nsa_hip_ops as ops
     geom = ops.NSAGeometry(*w["geom"])
@@ -303,8 +351,16 @@ def run_gpu(args, w, name):
     ms = (t1 - t0) * 1e3 / args.steps
     # forward and backward apart (not the headline: that is the timed steps above)
     split = time_fwd_bwd(step)
+    # peak device memory of one step (inputs resident, as in the timed steps)
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    step()
+    torch.cuda.synchronize()
+    mem = {"peak_gib": round(torch.cuda.max_memory_allocated() / 2**30, 3),
+           "peak_above_inputs_gib": round((torch.cuda.max_memory_allocated() - base) / 2**30, 3)}
     return dict(ms=ms, spans=timer.summary_ms(), iso_spans=iso_spans, dom=dom, flops_of=flops_of, kv=kv,
-                pairs=pairs, ins=ins, do=do, idx=idx, split=split)
+                pairs=pairs, ins=ins, do=do, idx=idx, split=split, geom=geom, mem=mem)
 
 
 def time_fwd_bwd(step, warmup=5, reps=20):
@@ -455,6 +511,7 @@ def run_model_bench(args, w):
     out = {}
     for arm in ("nsa", "dense"):
         torch.cuda.empty_cache()
+        base = torch.cuda.memory_allocated()   # other workloads' tensors still held by the caller
         torch.manual_seed(0)
         m = nsa_model.NSATransformer(
             vocab_size=w["vocab"], d_model=w["d_model"], n_layers=w["n_layers"], n_q_heads=w["Hq"],
@@ -483,7 +540,7 @@ def run_model_bench(args, w):
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         losses.append(float(loss))
         out[arm] = {"ms_per_step": round(ms, 2), "tokens_per_s": round(B * T / (ms / 1e3), 1),
-                    "peak_mem_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+                    "peak_mem_gib": round((torch.cuda.max_memory_allocated() - base) / 2**30, 2),
                     "params_m": round(sum(p.numel() for p in m.parameters()) / 1e6, 2),
                     "loss_first_last": [round(losses[0], 4), round(losses[-1], 4)]}
         log(f"[bench] c4 {arm}: {ms:.1f} ms per step, peak {out[arm]['peak_mem_gib']} GiB")
@@ -609,6 +666,32 @@ def run_phi_bench(reps=20):
             "shape": "B1 Hkv4 T32768 D128, l32 d16, hidden 128, bf16 (one of the two compressors of a config-3 layer)"}
 
 
+def run_other_configs(args):
+    """The other BASELINE configs beside the c3 line: c2 (selection branch
+    fwd+bwd), c5 (long-context forward) and c4 (the 150M training step, NSA
+    against dense attention, time and peak memory of each arm)."""
+    small = argparse.Namespace(steps=min(args.steps, 10), warmup=min(args.warmup, 3))
+    out = {}
+    w2 = WORKLOADS["c2"]
+    ms2, kv2 = time_gpu_only(small, w2, "c2")
+    f2 = step_flops(w2, kv2)
+    out["c2"] = {"ms_per_step": round(ms2, 3), "tokens_per_s": round(w2["B"] * w2["T"] / (ms2 / 1e3), 1),
+                 "tflop": round(f2 / 1e12, 4), "mfma_frac": round(f2 / (ms2 / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                 "desc": w2["desc"]}
+    torch.cuda.empty_cache()
+    c5 = run_forward_bench(small, WORKLOADS["c5"], "c5")
+    out["c5"] = {k: c5[k] for k in ("ms_per_step", "tokens_per_s", "fwd_tflop", "mfu")}
+    out["c5"]["desc"] = WORKLOADS["c5"]["desc"]
+    torch.cuda.empty_cache()
+    c4 = run_model_bench(small, WORKLOADS["c4"])
+    c4["nsa_vs_dense_time"] = round(c4["dense"]["ms_per_step"] / c4["nsa"]["ms_per_step"], 4)
+    c4["nsa_vs_dense_memory"] = round(c4["nsa"]["peak_mem_gib"] / c4["dense"]["peak_mem_gib"], 4)
+    c4["desc"] = WORKLOADS["c4"]["desc"]
+    out["c4"] = c4
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -639,14 +722,89 @@ def per_kernel_table(iso_spans, flops_of, peak, workload):
     return out
 
 
+def measure_branches(w, geom, ins, do, kv, reps=2):
+    """Each branch's work as launches of its own, so that every launch is one
+    branch: the forward through the per-branch calls (compression; selection
+    partials, then their merge as its own launch; the window alone; the gate
+    blend), the backward with one dQ launch per branch
+    (``FUSE_RANGE_DQ = False``, ``SEPARATE_SEL_DQ = True``).  The timed step
+    fuses these launches (the merge and the gate into the window forward, the
+    three dQs into one launch); this split only attributes time to branches.
+    Per branch: its launches (ms per step), their sum, the branch's
+    algorithmic FLOPs (14 D per visible (query head, key), fwd + bwd) and the
+    MFMA fraction; the gate blend and the backward's row statistics are
+    reported as `gate`."""
+    import nsa_fused_kernel as nfk
+    import nsa_hip_ops as ops
+    q, kc, vc, ks, vs, kw, vw, gate = (t.detach() for t in ins)
+    Hkv = ks.shape[1]
+    fwd = ops.LaunchTimer()
+    ops.set_timer(fwd)
+    try:
+        with torch.no_grad():
+            for _ in range(reps):
+                k_cmp = ops.pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+                v_cmp = ops.pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
+                o_c, lse_c = ops.range_fwd(ops.MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride)
+                idx = ops.importance_topn(q, k_cmp, lse_c, geom)
+                parts, _ = ops.sel_fwd_partials(q, ks, vs, idx, geom.sel_block)
+                o_s, _ = ops.sel_merge(idx, parts, q.shape, Hkv, geom.sel_block)
+                del parts
+                o_w, _ = ops.range_fwd(ops.MODE_WINDOW, q, kw, vw, geom.window)
+                ops.gate_fwd(gate, o_c, o_s, o_w)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_timer(None)
+    saved = (ops.FUSE_RANGE_DQ, ops.SEPARATE_SEL_DQ)
+    bwd_names = ["dq[win]", "dq[cmp]", "dq[sel]", "dkdv[sel]", "dkdv[win]", "dkdv[cmp]", "nsa_bwd_prep"]
+    bwd = ops.LaunchTimer(only=bwd_names)
+    ops.FUSE_RANGE_DQ, ops.SEPARATE_SEL_DQ = False, True
+    try:
+        xs = [t.requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw, gate)]
+        for i in range(reps + 1):
+            out, _ = nfk.nsa_attention(*xs, geom)
+            if i > 0:
+                ops.set_timer(bwd)
+            out.backward(do)
+            ops.set_timer(None)
+            del out
+        torch.cuda.synchronize()
+    finally:
+        ops.set_timer(None)
+        ops.FUSE_RANGE_DQ, ops.SEPARATE_SEL_DQ = saved
+        for t in (q, kc, vc, ks, vs, kw, vw, gate):
+            t.requires_grad_(False)
+            t.grad = None
+    spans = {**{k: v for k, v in fwd.summary_ms().items()}, **bwd.summary_ms()}
+    G, D = w["Hq"] // w["Hkv"], w["D"]
+    k_win, k_cmp_n, k_sel = kv
+
+    def branch(names, keys):
+        launches = {n: round(spans[n][1] / reps, 4) for n in names if n in spans}
+        ms = sum(launches.values())
+        ent = {"launches_ms": launches, "ms_per_step": round(ms, 4)}
+        if keys is not None:
+            flops = 14 * D * G * keys
+            ent.update({"tflop": round(flops / 1e12, 4),
+                        "mfma_frac": round(flops / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4) if ms > 0 else None})
+        return ent
+    return {
+        "selection": branch(["fwd[sel]", "nsa_sel_merge", "dkdv[sel]", "dq[sel]"], k_sel),
+        "window": branch(["fwd[win]", "dq[win]", "dkdv[win]"], k_win),
+        "compression": branch(["fwd[cmp]", "dq[cmp]", "dkdv[cmp]"], k_cmp_n),
+        "gate": branch(["nsa_gate_fwd", "nsa_bwd_prep"], None),
+        "note": "each branch's launches run apart (merge, gate and dQs unfused) in an untimed pass; "
+                "mfma_frac = 14 D per visible (query head, key) / their summed time / 2.5 PFLOP/s",
+    }
+
+
 def branch_fractions(iso_spans, flops_of, peak):
-    """MFMA fraction of the selection and sliding-window contractions from
-    the per-call spans.  selection = fwd[sel] + dkdv[sel] (its own
-    launches; the merge of its forward partials runs inside fwd[win] and the
-    sum of its dQ partials inside dq[cmp+win], not counted here); window =
-    fwd[win] + dkdv[win] (fwd[win] includes that merge and the gate blend;
-    the window dQ runs inside dq[cmp+win]); compression = fwd[cmp] +
-    dkdv[cmp]; the combined dQ launch is reported on its own."""
+    """MFMA fraction of the fused step's launches grouped by branch.
+    selection = fwd[sel] + dkdv[sel] (the merge of its forward partials runs
+    inside fwd[win] and the sum of its dQ partials inside dq[cmp+win]);
+    window = fwd[win] + dkdv[win] (fwd[win] carries that merge and the gate
+    blend); compression = fwd[cmp] + dkdv[cmp]; the combined dQ launch on its
+    own.  `measure_branches` gives the per-branch split."""
     def frac(names, flop_names=None):
         names = [n for n in names if n in iso_spans]
         if not names:
@@ -719,27 +877,11 @@ def main():
     if dom_name is not None and dom_name in spans:
         calls, tot = spans[dom_name]
         per_launch_s = tot / calls / 1e3
-        tflops = flops_of[dom_name] / per_launch_s / 1e12
-        mfma_frac = tflops / PEAK_BF16_TFLOPS
-        traffic = MEASURED_TRAFFIC.get((name, dom_name))
-        hbm_frac = traffic / per_launch_s / 1e9 / PEAK_HBM_GBS if traffic else None
-        roofline = {"kernel": dom_name, "launch_ms": round(per_launch_s * 1e3, 4), "traffic": traffic,
-                    "mfma_frac": round(mfma_frac, 4),
-                    "hbm_frac": round(hbm_frac, 4) if hbm_frac is not None else None}
-        if hbm_frac is not None and hbm_frac > mfma_frac:
-            # bound by memory traffic: achieved = the schedule's algorithmic bytes per launch / duration
-            alg, comp = sel_dkdv_bytes(w, r["pairs"]) if dom_name == "dkdv[sel]" else (traffic, None)
-            gbs = alg / per_launch_s / 1e9
-            roofline.update({"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                             "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": alg,
-                             "compulsory_bytes": comp, "measured_gbs": round(traffic / per_launch_s / 1e9, 1)})
-        else:
-            roofline.update({"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-                             "unit": "TFLOP/s", "frac": round(mfma_frac, 4)})
+        roofline = roofline_of(w, dom_name, flops_of[dom_name], per_launch_s, MEASURED_TRAFFIC.get((name, dom_name)),
+                               kv, r["pairs"])
         if dom_name in iso_spans:
             icalls, itot = iso_spans[dom_name]
-            iso_s = itot / icalls / 1e3
-            roofline["isolated_launch_ms"] = round(iso_s * 1e3, 4)
+            roofline["isolated_launch_ms"] = round(itot / icalls, 4)
     res = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -763,8 +905,10 @@ def main():
         "selection_pairs": r["pairs"],
         "roofline": roofline,
         "fwd_bwd_split": r["split"],
-        "branches": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
+        "branches": (measure_branches(w, r["geom"], r["ins"], r["do"], kv) if w["kind"] == "fused" else None),
+        "fused_launches_by_branch": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
         "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS, name),
+        "memory": r["mem"],
     }
     if not args.no_extras and name == "c3":
         ms_f, kv_f = time_gpu_only(args, WORKLOADS["c3_forced"], "c3_forced")
@@ -774,6 +918,7 @@ def main():
     if not args.no_extras and name == "c3":
         res["decode"] = {k: run_decode_bench(WORKLOADS[k]) for k in ("dec", "dec_b1")}
         res["phi"] = run_phi_bench()
+        res.update(run_other_configs(args))
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline: float32 oracle, {args.cpu_rows} rows, {threads} threads")

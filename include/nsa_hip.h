@@ -184,16 +184,24 @@ int nsa_csr_build(const int32_t* block_idx, int32_t* q_of_block, int32_t* block_
  * [B][Hkv][T][G][D]; coff / dot, the row offsets and deltas of nsa_bwd_prep,
  * in the same packed row order [B][Hkv][T][G] (nsa_bwd_prep with
  * dout_packed writes them so), kt the
- * nsa_transpose_kv copy of k.  dk/dv are float32 accumulators that the call
- * zero-fills and then accumulates into.  dq_part (nullable; needs packed and
- * kt): the dQ of every (query, slot, pass), scaled, in the input dtype,
+ * nsa_transpose_kv copy of k.  dk/dv: float32 [B][Hkv][T][D], every key
+ * written.  dkdv_part (nullable, part_bytes >= nsa_sel_dkdv_partial_bytes):
+ * each work item writes its dK/dV rows there and one more launch sums a
+ * block's items in item order, so dk/dv are bit-identical run to run, as
+ * the reference's disjoint per-block writes are
+ * (nsa_selection_backward.py:207-275); without it the items merge with
+ * float atomics into zero-filled dk/dv and the last bits may differ run to
+ * run.  dq_part (nullable; needs packed and kt): the dQ of every (query,
+ * slot, pass), scaled, in the input dtype,
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G][D] -- summed by
  * nsa_sel_dq_reduce. */
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
+size_t nsa_sel_dkdv_partial_bytes(int B, int Hkv, int T, int S, int D, int block_size, int chunk);
 int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const float* coff,
                  const float* dot, const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
-                 float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq,
-                 int Hkv, int T, int D, int S, int block_size, int chunk, int dtype, void* stream);
+                 float* dk, float* dv, float* dkdv_part, size_t part_bytes, void* dq_part, void* workspace,
+                 size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                 int dtype, void* stream);
 
 /* nsa_sel_dkdv without a workspace argument: allocates nothing (no
  * hipMalloc, no allocating library call).  No counterpart in the reference:
@@ -203,8 +211,8 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
  * NSA_SEL_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends; a call
  * whose nsa_sel_dkdv_workspace(...) exceeds it returns NSA_ERR_WORKSPACE
  * before touching the device (about 65k work items: c3 needs 4.1k).  Every
- * call on one GPU uses that GPU's array, which keeps the last call's
- * contents (the call re-initialises what it reads): calls that overlap on
+ * call uses the array of its stream's device (the null stream: the current
+ * device), which keeps the last call's contents (the call re-initialises what it reads): calls that overlap on
  * one GPU (two streams, two host threads) race and must be serialised by the
  * caller.  Arguments otherwise as nsa_sel_dkdv. */
 #define NSA_SEL_NOALLOC_SCRATCH_BYTES ((size_t)1 << 20)
@@ -307,11 +315,17 @@ int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void*
 
 /* Backward dK/dV of the range branches (key-outer; the key-side half of
  * _range_attn_bwd_qtiled_kernel).  coff / dot: row offsets and deltas from
- * nsa_bwd_prep.  dk/dv float32 [B][Hkv][Lk][D]; the call zero-fills and
- * accumulates into them. */
+ * nsa_bwd_prep.  dk/dv float32 [B][Hkv][Lk][D], every key written.  The
+ * window has one writer per key.  Compression splits each key's queries into
+ * chunks: with dkdv_part (nullable, part_bytes >=
+ * nsa_range_dkdv_partial_bytes for the same stream's device) the chunks write
+ * partial rows that one more launch sums in chunk order (bit-identical run
+ * to run); without it they merge with float atomics into zero-filled dk/dv. */
+size_t nsa_range_dkdv_partial_bytes(int mode, int B, int Hkv, int T, int Lk, int D, int cmp_block, int cmp_stride,
+                                    void* stream);
 int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const float* coff,
-                   const float* dot, float* dk, float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window,
-                   int cmp_block, int cmp_stride, int dtype, void* stream);
+                   const float* dot, float* dk, float* dv, float* dkdv_part, size_t part_bytes, int B, int Hq,
+                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype, void* stream);
 
 /* ---- block importance + top-n ----------------------------------------------
  * Replaces the importance / topk block of NSAAttention._forward_fused

@@ -54,7 +54,8 @@ SIGNATURES = {
     "nsa_csr_workspace": (_Z, [_I, _I, _I, _I, _I]),
     "nsa_csr_build": (_I, [_P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dkdv_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
-    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _Z,
+    "nsa_sel_dkdv_partial_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I]),
+    "nsa_sel_dkdv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _Z, _P, _P, _Z,
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dkdv_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P,
                                   _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -70,7 +71,8 @@ SIGNATURES = {
                           _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
     "nsa_range_dq_cw": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I,
                              _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
-    "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P,
+    "nsa_range_dkdv_partial_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z,
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_importance_topn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _P]),

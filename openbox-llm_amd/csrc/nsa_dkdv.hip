@@ -25,6 +25,7 @@
 //   waves per 32 keys, two waves per SIMD; below).
 //   * selection   : work items (block, chunk of its CSR query list) built by
 //                   k_sel_items; a persistent grid drains them; chunks merge with atomics.
+#include <atomic>
 #include <mutex>
 
 #include "nsa_launch.h"
@@ -930,6 +931,17 @@ __host__ __device__ inline int cmp_blocks_range(int T, int Lk, int chunk, int NW
   return tot;
 }
 
+// Zeros over one key's float rows of dK and dV: the two lanes of a key
+// (h = 0, 1) write one half of each row.
+template <int D>
+__device__ __forceinline__ void zero_rows(float* dkrow, float* dvrow, int h) {
+#pragma unroll
+  for (int d = h * (D / 2); d < (h + 1) * (D / 2); d += 4) {
+    *reinterpret_cast<f32x4*>(dkrow + d) = zero4();
+    *reinterpret_cast<f32x4*>(dvrow + d) = zero4();
+  }
+}
+
 // ---------------------------------------------------------------------------
 // range dK/dV: window: ceil(Lk / (32 NW)) * B*Hkv workgroups.  Compression:
 // every (query chunk, key block) pair takes about as long as any other, so a
@@ -945,8 +957,9 @@ template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                     const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
-                    float* __restrict__ dk, float* __restrict__ dv, int Hq, int Hkv, int T_, int Lk, int chunk,
-                    int window, int cl, int cd, int nbh, int chs, int spl, float sl2, float scale) {
+                    float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ part, int64_t part_half,
+                    int Hq, int Hkv, int T_, int Lk, int chunk, int window, int cl, int cd, int nbh, int chs, int spl,
+                    float sl2, float scale) {
   constexpr int NTH = 64 * NW;
   __shared__ __align__(16) KvStage<T, D> stg[kKvStages];
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
@@ -958,11 +971,12 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
   int kblk, ch, bh;
   int q0 = 0, qlen = chunk;   // compression: the workgroup's queries [q0, q0 + qlen)
+  int64_t wg = blockIdx.x;    // logical workgroup (compression: its rows of the partial buffer)
   if (mode == NSA_MODE_COMPRESS) {
     const int nch = (T_ + chunk - 1) / chunk;
     const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
     const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
-    const int64_t wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
+    wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
     int r, sub = 0;
     if (wg < (int64_t)big * nbh) {
       bh = (int)(wg / big);
@@ -1014,7 +1028,13 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
     thi = thi < c1 ? thi : c1;
   }
   thi = thi < T_ - 1 ? thi : T_ - 1;
-  if (tlo > thi) return;   // uniform over the workgroup
+  // compression with a partial buffer: this workgroup's 32 NW rows of it
+  // (every logical workgroup writes them, zeros when it has no query)
+  float* prow = part != nullptr && mode == NSA_MODE_COMPRESS ? part + (wg * 32 * NW + (key - k0)) * D : nullptr;
+  if (tlo > thi) {   // uniform over the workgroup
+    if (prow != nullptr && key_ok) zero_rows<D>(prow, prow + part_half, h);
+    return;
+  }
   KeyAcc<T, D> acc;
   const int64_t kvoff = (int64_t)bh * Lk * D;
   acc.init(k + kvoff, v + kvoff, key_ok ? key : Lk - 1, h);
@@ -1041,8 +1061,12 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   auto no_post = [](const auto&, int, int) {};
   auto tiles = pair_tiles<T, D, NTH>(x, b, hkv, qsrc, vis);
   kv_walk<false, 0, T, D, NTH, false>(acc, stg, tiles, x.NHC, ntile, no_pre, no_post, sl2, tid);
-  if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale,
-                        mode == NSA_MODE_COMPRESS, h);
+  if (key_ok) {
+    if (prow != nullptr)
+      acc.write(prow, prow + part_half, scale, false, h);
+    else
+      acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, mode == NSA_MODE_COMPRESS, h);
+  }
 }
 
 // accumulator columns of one key -> a float row (scaled; atomically when
@@ -1076,8 +1100,9 @@ template <typename T, int D, int NW, bool FLAT>
 __global__ __launch_bounds__(128 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__ dout, const float* __restrict__ coff,
                     const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
-                    float* __restrict__ dk, float* __restrict__ dv, int Hq, int Hkv, int T_, int Lk, int chunk,
-                    int window, int cl, int cd, int nbh, int chs, int spl, float sl2, float scale) {
+                    float* __restrict__ dk, float* __restrict__ dv, float* __restrict__ part, int64_t part_half,
+                    int Hq, int Hkv, int T_, int Lk, int chunk, int window, int cl, int cd, int nbh, int chs, int spl,
+                    float sl2, float scale) {
   constexpr int NTH = 128 * NW;
   __shared__ __align__(16) KvStage<T, D> stg[kSplitStages];
   __shared__ __align__(16) PTile pbuf[NW][2];
@@ -1092,11 +1117,12 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
   const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
   int kblk, ch, bh;
   int q0 = 0, qlen = chunk;   // compression: the workgroup's queries [q0, q0 + qlen)
+  int64_t wg = blockIdx.x;    // logical workgroup (compression: its rows of the partial buffer)
   if (mode == NSA_MODE_COMPRESS) {
     const int nch = (T_ + chunk - 1) / chunk;
     const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
     const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
-    const int64_t wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
+    wg = xcd_remap_split(blockIdx.x, (int64_t)big * nbh, (int64_t)per * nbh);
     int r, sub = 0;
     if (wg < (int64_t)big * nbh) {
       bh = (int)(wg / big);
@@ -1148,23 +1174,29 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
     thi = thi < c1 ? thi : c1;
   }
   thi = thi < T_ - 1 ? thi : T_ - 1;
-  if (tlo > thi) return;   // uniform over the workgroup
+  // compression with a partial buffer: this workgroup's 32 NW rows of it
+  // (every logical workgroup writes them, zeros when it has no query)
+  float* prow = part != nullptr && mode == NSA_MODE_COMPRESS ? part + (wg * 32 * NW + (key - k0)) * D : nullptr;
+  if (tlo > thi) {   // uniform over the workgroup
+    if (prow != nullptr && key_ok) zero_rows<D>(prow, prow + part_half, h);
+    return;
+  }
   const int64_t kvoff = (int64_t)bh * Lk * D;
   const int wlast = kw + 31;   // last key of the group (may pass Lk: those columns are never stored)
   const int key_safe = key_ok ? key : Lk - 1;
-  const bool atomic = mode == NSA_MODE_COMPRESS;
+  const bool atomic = mode == NSA_MODE_COMPRESS && prow == nullptr;
   // the two roles' walks over the workgroup's query tiles
   auto run = [&](auto make_rq, int total, auto vis) {
     if (pwave) {
       PWave<T, D> pw;
       pw.init(k + kvoff, key_safe, h);
       walk_p<T, D, NTH>(pw, stg, pbuf[w], make_rq, total, vis, sl2, tid);
-      if (key_ok) store_rows<T, D>(pw.dv, dv + kvoff + (int64_t)key * D, 1.0f, atomic, h);
+      if (key_ok) store_rows<T, D>(pw.dv, prow ? prow + part_half : dv + kvoff + (int64_t)key * D, 1.0f, atomic, h);
     } else {
       SWave<T, D> sw;
       sw.init(v + kvoff, key_safe, h);
       walk_s<T, D, NTH, false>(sw, stg, pbuf[w], make_rq, total, tid);
-      if (key_ok) store_rows<T, D>(sw.dk, dk + kvoff + (int64_t)key * D, scale, atomic, h);
+      if (key_ok) store_rows<T, D>(sw.dk, prow ? prow : dk + kvoff + (int64_t)key * D, scale, atomic, h);
     }
   };
   if constexpr (FLAT) {
@@ -1253,8 +1285,8 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
                   const float* __restrict__ dot, const T* __restrict__ k, const T* __restrict__ v,
                   const T* __restrict__ kt, const int32_t* __restrict__ q_of_block, const int4* __restrict__ items,
                   int32_t* __restrict__ n_items, float* __restrict__ dk, float* __restrict__ dv,
-                  T* __restrict__ dq_part, int Hq, int Hkv, int T_, int S, int packed, int n_blk, int L, int Lp,
-                  float sl2, float scale) {
+                  float* __restrict__ part, int64_t part_half, T* __restrict__ dq_part, int Hq, int Hkv, int T_,
+                  int S, int packed, int n_blk, int L, int Lp, float sl2, float scale) {
   constexpr int NW = 2, NTH = 64 * NW;
   using C = Tile32<T, D>;
   constexpr int DT = C::DT, DTW = (DT + 1) / 2;          // dQ^T d-tiles per wave
@@ -1435,8 +1467,95 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       else
         kv_walk<false, 0, T, D, NTH, true>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
     }
-    if (key_ok) acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
+    if (key_ok) {
+      if (part != nullptr) {
+        // this item's rows of the partial buffer (k_sel_dkdv_reduce sums them
+        // in item order)
+        float* pr = part + ((int64_t)it * kSelPass + (key - kpass)) * D;
+        acc.write(pr, pr + part_half, scale, false, h);
+      } else {
+        acc.write(dk + kvoff + (int64_t)key * D, dv + kvoff + (int64_t)key * D, scale, true, h);
+      }
+    }
     __syncthreads();   // the next item's first tiles reuse stages 0 .. and sent
+  }
+}
+
+// dK / dV of every key of the selection blocks from the work items'
+// partials: one workgroup per (block, pass), each output element summed by
+// one thread over the block's items in item order (the items of a block are
+// consecutive and ascend in query order), so the result does not depend on
+// which workgroup finished first.  A block no query selected gets zeros.
+template <int D>
+__global__ __launch_bounds__(256) void k_sel_dkdv_reduce(const float* __restrict__ part, int64_t part_half,
+                                                         const int32_t* __restrict__ first, float* __restrict__ dk,
+                                                         float* __restrict__ dv, int T_, int n_blk, int L,
+                                                         int npass) {
+  const int e = blockIdx.x / npass, pass = blockIdx.x % npass;   // e = bh * n_blk + j
+  const int bh = e / n_blk, j = e % n_blk;
+  const int k0 = j * L + kSelPass * pass;
+  const int kend = j * L + L < T_ ? j * L + L : T_;
+  const int nk = kend - k0 < kSelPass ? kend - k0 : kSelPass;   // keys of this pass
+  if (nk <= 0) return;
+  const int i0 = first[e], i1 = first[e + 1];
+  constexpr int V4 = D / 4;   // float4 per key row
+  for (int f = threadIdx.x; f < nk * V4; f += 256) {
+    const int kk = f / V4, c = f % V4;
+    f32x4 a = zero4(), b = zero4();
+    for (int i = i0; i < i1; ++i) {
+      const int64_t row = ((int64_t)i * npass + pass) * kSelPass + kk;
+      a += reinterpret_cast<const f32x4*>(part + row * D)[c];
+      b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
+    }
+    const int64_t orow = ((int64_t)bh * T_ + k0 + kk) * D;
+    reinterpret_cast<f32x4*>(dk + orow)[c] = a;
+    reinterpret_cast<f32x4*>(dv + orow)[c] = b;
+  }
+}
+
+// dK / dV of the pooled keys from the compression workgroups' partial rows:
+// one workgroup per (bh, block of 32 NW keys), each output element summed by
+// one thread over the block's chunks in chunk (then sub-chunk) order -- the
+// logical workgroup numbering of k_range_dkdv32 / k_range_dkdv_split -- so the
+// result does not depend on which workgroup finished first.
+template <int D, int NW>
+__global__ __launch_bounds__(256) void k_cmp_dkdv_reduce(const float* __restrict__ part, int64_t part_half,
+                                                         float* __restrict__ dk, float* __restrict__ dv, int T_,
+                                                         int Lk, int chunk, int cl, int cd, int nbh, int chs,
+                                                         int spl) {
+  constexpr int KB = 32 * NW;
+  const int nkb = (Lk + KB - 1) / KB;
+  const int bh = blockIdx.x / nkb, kblk = blockIdx.x % nkb;
+  const int nch = (T_ + chunk - 1) / chunk;
+  const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
+  const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
+  const int k0 = kblk * KB;
+  const int nk = Lk - k0 < KB ? Lk - k0 : KB;
+  constexpr int V4 = D / 4;   // float4 per key row
+  for (int f = threadIdx.x; f < nk * V4; f += 256) {
+    const int kk = f / V4, c = f % V4;
+    f32x4 a = zero4(), b = zero4();
+    auto add = [&](int64_t wgi) {
+      const int64_t row = wgi * KB + kk;
+      a += reinterpret_cast<const f32x4*>(part + row * D)[c];
+      b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
+    };
+    int64_t base = (int64_t)bh * big;   // chunks < chs: per bh, chunk-major
+    for (int ch = 0; ch < chs; ++ch) {
+      const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+      if (kblk < na) add(base + kblk);
+      base += na;
+    }
+    base = (int64_t)big * nbh + (int64_t)bh * per;   // the split chunks: (chunk, sub-chunk)-major
+    for (int ch = chs; ch < nch; ++ch) {
+      const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+      if (kblk < na)
+        for (int sub = 0; sub < spl; ++sub) add(base + (int64_t)sub * na + kblk);
+      base += (int64_t)na * spl;
+    }
+    const int64_t orow = ((int64_t)bh * Lk + k0 + kk) * D;
+    reinterpret_cast<f32x4*>(dk + orow)[c] = a;
+    reinterpret_cast<f32x4*>(dv + orow)[c] = b;
   }
 }
 
@@ -1456,25 +1575,66 @@ using namespace nsa;
 static constexpr int kCmpChunk = 2048;   // queries per compression dK/dV work item
 static constexpr int kCmpSplit = 4;      // sub-chunks of the chunks that end the grid
 
-// Compute units of the current device (cached per device).
-static int device_cu_count() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
+// Device of a stream (the null stream: the current device), or -1.
+static int stream_device(hipStream_t s) {
+  hipDevice_t dev = -1;
+  if (hipStreamGetDevice(s, &dev) != hipSuccess) return -1;
+  return (int)dev;
+}
+
+// Compute units of the stream's device, cached per device.  The cache is
+// written with relaxed atomics: two threads that race on a first lookup store
+// the same value.
+static int device_cu_count(hipStream_t s) {
+  static std::atomic<int> cache[64];
+  const int dev = stream_device(s);
+  if (dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return n;
 }
 
 
+// Compression dK/dV grid: logical workgroups over (key block, query chunk),
+// the chunks from *chs on split into *spl sub-chunks while their workgroups fit
+// in one round of the resident workgroups (two per CU of the stream's device).
+static int64_t cmp_grid(int T, int Lk, int cl, int cd, int nbh, hipStream_t s, int* chs_out, int* spl_out) {
+  constexpr int NW = 2;
+  const int nch = (T + kCmpChunk - 1) / kCmpChunk;
+  const int64_t slots = 2 * (int64_t)device_cu_count(s);
+  int64_t tail = 0;
+  int chs = nch;
+  while (chs > 0) {
+    const int64_t add = (int64_t)cmp_active_blocks(T, Lk, kCmpChunk, NW, cl, cd, chs - 1) * nbh;
+    if (tail + add > slots) break;
+    tail += add;
+    --chs;
+  }
+  const int spl = chs < nch ? kCmpSplit : 1;
+  *chs_out = chs;
+  *spl_out = spl;
+  return ((int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cl, cd, 0, chs) +
+          (int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cl, cd, chs, nch) * spl) * nbh;
+}
+
 extern "C" {
 
+size_t nsa_range_dkdv_partial_bytes(int mode, int B, int Hkv, int T, int Lk, int D, int cmp_block, int cmp_stride,
+                                    void* stream) {
+  if (mode != NSA_MODE_COMPRESS || B <= 0 || Hkv <= 0 || T <= 0 || Lk <= 0 || D <= 0 || cmp_block < 1 ||
+      cmp_stride < 1)
+    return 0;
+  int chs = 0, spl = 1;
+  const int64_t grid = cmp_grid(T, Lk, cmp_block, cmp_stride, B * Hkv, (hipStream_t)stream, &chs, &spl);
+  return (size_t)grid * 64 * (size_t)D * 2 * sizeof(float);
+}
+
 int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const void* dout, const float* coff,
-                   const float* dot, float* dk, float* dv, int B, int Hq, int Hkv, int T, int Lk, int D, int window,
-                   int cmp_block, int cmp_stride, int dtype, void* stream) {
+                   const float* dot, float* dk, float* dv, float* dkdv_part, size_t part_bytes, int B, int Hq, int Hkv,
+                   int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && Lk >= 0, NSA_ERR_SHAPE);
   NSA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, NSA_ERR_SHAPE);
@@ -1485,14 +1645,6 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * Lk * D;
-  if (mode == NSA_MODE_COMPRESS || T == 0) {
-    int rc = zero_f32(dk, nel, s);
-    if (rc == NSA_OK) rc = zero_f32(dv, nel, s);
-    if (rc != NSA_OK) return rc;
-  }
-  if (T == 0 || Lk == 0) return NSA_OK;
-  const float scale = 1.0f / sqrtf((float)D);
-  const float sl2 = scale * kLog2e;
   // 64 keys (NW = 2 groups of 32) per workgroup, two workgroups per CU: 2 waves
   // (one per group, float) or 4 (P- and dS-wave per group, bf16).  Measured
   // faster than 128 keys sharing each streamed query tile, for both modes and
@@ -1502,78 +1654,96 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
   constexpr int NW = 2;
   const int nbh = B * Hkv;
   int chs = 0, spl = 1;
-  int64_t grid;
-  if (mode == NSA_MODE_COMPRESS) {
-    // split the last chunks while their workgroups fit in one round of the
-    // resident workgroups (two per CU)
-    const int nch = (T + kCmpChunk - 1) / kCmpChunk;
-    const int64_t slots = 2 * (int64_t)device_cu_count();
-    int64_t tail = 0;
-    chs = nch;
-    while (chs > 0) {
-      const int64_t add = (int64_t)cmp_active_blocks(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, chs - 1) * nbh;
-      if (tail + add > slots) break;
-      tail += add;
-      --chs;
-    }
-    spl = chs < nch ? kCmpSplit : 1;
-    grid = ((int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, 0, chs) +
-            (int64_t)cmp_blocks_range(T, Lk, kCmpChunk, NW, cmp_block, cmp_stride, chs, nch) * spl) * nbh;
-  } else {
-    grid = (int64_t)((Lk + 32 * NW - 1) / (32 * NW)) * nbh;
+  int64_t grid = 0;
+  if (T > 0 && Lk > 0)
+    grid = mode == NSA_MODE_COMPRESS ? cmp_grid(T, Lk, cmp_block, cmp_stride, nbh, s, &chs, &spl)
+                                     : (int64_t)((Lk + 32 * NW - 1) / (32 * NW)) * nbh;
+  // compression partials: the workgroups write their rows, k_cmp_dkdv_reduce
+  // sums them in a fixed order and writes every key
+  const bool partial = mode == NSA_MODE_COMPRESS && dkdv_part != nullptr && grid > 0;
+  NSA_CHECK(!partial || part_bytes >= (size_t)grid * 64 * D * 2 * sizeof(float), NSA_ERR_WORKSPACE);
+  if ((mode == NSA_MODE_COMPRESS && !partial) || T == 0) {
+    int rc = zero_f32(dk, nel, s);
+    if (rc == NSA_OK) rc = zero_f32(dv, nel, s);
+    if (rc != NSA_OK) return rc;
   }
   if (grid == 0) return NSA_OK;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
+  const float scale = 1.0f / sqrtf((float)D);
+  const float sl2 = scale * kLog2e;
+  float* part = partial ? dkdv_part : nullptr;
+  const int64_t part_half = grid * 32 * NW * D;
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16) {
       // groups of G < 16 heads: query tiles of 32 consecutive (query, head) rows
       auto kern = Hq / Hkv < 16 ? k_range_dkdv_split<bf16, DD, NW, true> : k_range_dkdv_split<bf16, DD, NW, false>;
       kern<<<(unsigned)grid, 128 * NW, 0, s>>>(mode, (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k,
-                                               (const bf16*)v, dk, dv, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block,
-                                               cmp_stride, nbh, chs, spl, sl2, scale);
+                                               (const bf16*)v, dk, dv, part, part_half, Hq, Hkv, T, Lk, kCmpChunk,
+                                               window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
     } else
       k_range_dkdv32<float, DD, NW><<<(unsigned)grid, 64 * NW, 0, s>>>(
-          mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, Hq, Hkv,
-          T, Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
+          mode, (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, dk, dv, part,
+          part_half, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
+    if (partial) {
+      if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
+      const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
+      k_cmp_dkdv_reduce<DD, NW><<<(unsigned)((int64_t)nkb * nbh), 256, 0, s>>>(
+          part, part_half, dk, dv, T, Lk, kCmpChunk, cmp_block, cmp_stride, nbh, chs, spl);
+    }
   });
   return nsa_launch_status();
 }
 
 size_t nsa_sel_dkdv_workspace(int B, int Hkv, int T, int S, int block_size, int chunk) {
   if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || block_size <= 0 || chunk <= 0) return 0;
-  return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sizeof(int4) + 256;
+  const size_t nb = (size_t)B * Hkv * sel_csr_blocks(T, block_size);
+  return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sizeof(int4) + 256 + (nb + 1) * sizeof(int32_t);
+}
+
+size_t nsa_sel_dkdv_partial_bytes(int B, int Hkv, int T, int S, int D, int block_size, int chunk) {
+  if (B <= 0 || Hkv <= 0 || T < 0 || S < 0 || D <= 0 || block_size <= 0 || chunk <= 0) return 0;
+  return sel_items_cap(B, Hkv, T, S, block_size, chunk) * sel_passes(block_size) * kSelPass * (size_t)D * 2 *
+         sizeof(float);
 }
 
 int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, const void* dout, const float* coff,
                  const float* dot, const int32_t* q_of_block, int packed, const int32_t* block_offsets, const int32_t* pair_count,
-                 float* dk, float* dv, void* dq_part, void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv,
-                 int T, int D, int S, int block_size, int chunk, int dtype, void* stream) {
+                 float* dk, float* dv, float* dkdv_part, size_t part_bytes, void* dq_part, void* workspace,
+                 size_t workspace_bytes, int B, int Hq, int Hkv, int T, int D, int S, int block_size, int chunk,
+                 int dtype, void* stream) {
   (void)pair_count;
   NSA_CHECK(B > 0 && Hkv > 0 && Hq % Hkv == 0 && T >= 0 && S >= 0, NSA_ERR_SHAPE);
   NSA_CHECK(D == 16 || D == 32 || D == 64 || D == 128, NSA_ERR_SHAPE);
   NSA_CHECK(block_size >= 16 && block_size % 16 == 0 && chunk >= 2 && chunk <= kSelItemMax, NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(workspace_bytes >= nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, chunk), NSA_ERR_WORKSPACE);
+  NSA_CHECK(dkdv_part == nullptr || part_bytes >= nsa_sel_dkdv_partial_bytes(B, Hkv, T, S, D, block_size, chunk),
+            NSA_ERR_WORKSPACE);
   NSA_CHECK(dq_part == nullptr || (packed && kt != nullptr), NSA_ERR_ARG);
   NSA_CHECK(!packed || ((int64_t)T << sel_slot_bits(S)) < (1ll << 31), NSA_ERR_SHAPE);
   // the tile loads address a group's Q / dO rows with 32-bit byte offsets
   NSA_CHECK((int64_t)(Hq / Hkv) * T * D * (dtype == NSA_BF16 ? 2 : 4) < (1ll << 32), NSA_ERR_SHAPE);
   hipStream_t s = (hipStream_t)stream;
   const int64_t nel = (int64_t)B * Hkv * T * D;
-  {
+  const int n_blk = sel_csr_blocks(T, block_size);
+  const bool empty = T == 0 || S == 0 || n_blk == 0;
+  if (dkdv_part == nullptr || empty) {
+    // atomics add into zeroed outputs (the partial reduce writes every key)
     int rc = zero_f32(dk, nel, s);
     if (rc == NSA_OK) rc = zero_f32(dv, nel, s);
     if (rc != NSA_OK) return rc;
   }
-  const int n_blk = sel_csr_blocks(T, block_size);
-  if (T == 0 || S == 0 || n_blk == 0) return NSA_OK;
+  if (empty) return NSA_OK;
   const size_t cap = sel_items_cap(B, Hkv, T, S, block_size, chunk);
   int4* items = (int4*)workspace;
   int32_t* n_items = (int32_t*)((char*)workspace + cap * sizeof(int4));
-  k_sel_items<<<1, 1024, 0, s>>>(block_offsets, B * Hkv * n_blk, n_blk, chunk, items, n_items);
+  int32_t* first = (int32_t*)((char*)workspace + cap * sizeof(int4) + 256);
+  const int nb = B * Hkv * n_blk;
+  k_sel_items<<<1, 1024, 0, s>>>(block_offsets, nb, n_blk, chunk, items, n_items, first);
   if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
+  const int64_t part_half = (int64_t)cap * sel_passes(block_size) * kSelPass * D;
   // one workgroup per resident slot (two per CU); next_item hands out the rest
-  const size_t slots = 2 * (size_t)device_cu_count();
+  const size_t slots = 2 * (size_t)device_cu_count(s);
   const size_t grid_cap = cap * sel_passes(block_size) < slots ? cap * sel_passes(block_size) : slots;
   const float scale = 1.0f / sqrtf((float)D);
   const float sl2 = scale * kLog2e;
@@ -1585,13 +1755,20 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
       auto kern = gp ? k_sel_dkdv32<bf16, DD, true> : k_sel_dkdv32<bf16, DD, false>;
       kern<<<(unsigned)grid_cap, 128, 0, s>>>(
           (const bf16*)q, (const bf16*)dout, coff, dot, (const bf16*)k, (const bf16*)v, (const bf16*)kt, q_of_block,
-          items, n_items, dk, dv, (bf16*)dq_part, Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2, scale);
+          items, n_items, dk, dv, dkdv_part, part_half, (bf16*)dq_part, Hq, Hkv, T, S, packed, n_blk, block_size,
+          Lp, sl2, scale);
     } else {
       auto kern = gp ? k_sel_dkdv32<float, DD, true> : k_sel_dkdv32<float, DD, false>;
       kern<<<(unsigned)grid_cap, 128, 0, s>>>(
           (const float*)q, (const float*)dout, coff, dot, (const float*)k, (const float*)v, (const float*)kt,
-          q_of_block, items, n_items, dk, dv, (float*)dq_part, Hq, Hkv, T, S, packed, n_blk, block_size, Lp, sl2,
-          scale);
+          q_of_block, items, n_items, dk, dv, dkdv_part, part_half, (float*)dq_part, Hq, Hkv, T, S, packed, n_blk,
+          block_size, Lp, sl2, scale);
+    }
+    if (dkdv_part != nullptr) {
+      if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
+      const int npass = sel_passes(block_size);
+      k_sel_dkdv_reduce<DD><<<(unsigned)((int64_t)nb * npass), 256, 0, s>>>(dkdv_part, part_half, first, dk, dv,
+                                                                               T, n_blk, block_size, npass);
     }
   });
   return nsa_launch_status();
@@ -1616,14 +1793,20 @@ constexpr int kMaxDevices = 64;
 void* g_scratch_ptr[kMaxDevices] = {};
 std::mutex g_scratch_mu;
 
-// Device address of the current device's `scratch`, looked up on first use.
-int scratch_on_current_device(void** out) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return NSA_ERR_LAUNCH;
+// Device address of `scratch` on the device of stream `s`, looked up on first
+// use with that device current (the caller's current device is restored).
+int scratch_on_stream_device(hipStream_t s, void** out) {
+  const int dev = stream_device(s);
+  if (dev < 0 || dev >= kMaxDevices) return NSA_ERR_LAUNCH;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return NSA_ERR_LAUNCH;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return NSA_ERR_LAUNCH;
     void* p = nullptr;
-    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return NSA_ERR_LAUNCH;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return NSA_ERR_LAUNCH;
+    if (e != hipSuccess || p == nullptr) return NSA_ERR_LAUNCH;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -1643,10 +1826,10 @@ int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void
   NSA_CHECK(need > 0, NSA_ERR_SHAPE);
   NSA_CHECK(need <= kSelScratchBytes, NSA_ERR_WORKSPACE);
   void* ws = nullptr;
-  const int rc = scratch_on_current_device(&ws);
+  const int rc = scratch_on_stream_device((hipStream_t)stream, &ws);
   if (rc != NSA_OK) return rc;
-  return nsa_sel_dkdv(q, k, v, kt, dout, coff, dot, q_of_block, packed, block_offsets, pair_count, dk, dv, dq_part,
-                      ws, kSelScratchBytes, B, Hq, Hkv, T, D, S, block_size, chunk, dtype, stream);
+  return nsa_sel_dkdv(q, k, v, kt, dout, coff, dot, q_of_block, packed, block_offsets, pair_count, dk, dv, nullptr,
+                      0, dq_part, ws, kSelScratchBytes, B, Hq, Hkv, T, D, S, block_size, chunk, dtype, stream);
 }
 
 }  // extern "C"

@@ -9,10 +9,13 @@
 namespace nsa {
 
 // items[i] = {bh * n_blk + j, begin, end, 0}: pair range [begin, end) of q_of_block;
-// n_items[0] = item count, n_items[1] = 0 (the work counter of next_item)
+// n_items[0] = item count, n_items[1] = 0 (the work counter of next_item).
+// The items of block e are items[first[e] .. first[e + 1]), in query order
+// (first: nb + 1 ints, optional).
 static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __restrict__ offsets, int nb, int n_blk,
                                                            int chunk, int4* __restrict__ items,
-                                                           int32_t* __restrict__ n_items) {
+                                                           int32_t* __restrict__ n_items,
+                                                           int32_t* __restrict__ first = nullptr) {
   __shared__ int part[1024];
   const int tid = threadIdx.x;
   const int per = (nb + 1023) / 1024;
@@ -37,6 +40,7 @@ static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __rest
     const int bh = e / n_blk, j = e % n_blk;
     const int beg = offsets[bh * (n_blk + 1) + j];
     const int end = offsets[bh * (n_blk + 1) + j + 1];
+    if (first != nullptr) first[e] = pos;
     for (int s = beg; s < end; s += chunk) {
       const int se = s + chunk < end ? s + chunk : end;
       items[pos++] = make_int4(e, s, se, 0);
@@ -45,6 +49,7 @@ static __global__ __launch_bounds__(1024) void k_sel_items(const int32_t* __rest
   if (tid == 1023) {
     n_items[0] = part[1023];
     n_items[1] = 0;
+    if (first != nullptr) first[nb] = part[1023];
   }
 }
 

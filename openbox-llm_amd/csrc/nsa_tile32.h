@@ -339,6 +339,23 @@ __device__ __forceinline__ void dma_tile_uniform(void* lds, SrcFn src, int tid) 
 template <int NTH, int NCHUNK>
 constexpr int dma_uniform_loads() { return (NCHUNK + NTH - 1) / NTH; }
 
+// The source row a row-tile request starts from and the last tile row inside
+// the source (nrows >= 1).  A tile that starts at or past the end (r0 >=
+// nrows) reads row nrows - 1 for all its rows: with its start clamped, the
+// per-lane clamp below subtracts at most a lane's own row, so no unsigned
+// offset can wrap below the base.  Unclamped, such a tile's `last` was
+// negative and the subtraction wrapped to about 4 GB past the base.
+struct TileRows {
+  int base, last;
+};
+__host__ __device__ constexpr TileRows tile_rows(int r0, int nrows) {
+  const int b = r0 < nrows ? r0 : nrows - 1;
+  return TileRows{b, nrows - 1 - b};
+}
+static_assert(tile_rows(96, 95).base == 94 && tile_rows(96, 95).last == 0, "a tile past the end reads the last row");
+static_assert(tile_rows(64, 95).base == 64 && tile_rows(64, 95).last == 30, "a tile crossing the end");
+static_assert(tile_rows(0, 95).last == 94, "a tile inside the source");
+
 // dma_tile_uniform for [32][D] row tiles of a [rows][D] source, with the
 // per-thread part of every address (row and chunk inside the tile) computed
 // once by init: a request is a wave-uniform base plus constant per-lane
@@ -365,11 +382,13 @@ struct RowTileDma {
       off[j] = (uint32_t)((r * D + c * C::EPC) * (int)sizeof(T));
     }
   }
-  // rows r0 .. r0 + 31 of src -> lds (r0 < nrows)
+  // rows r0 .. r0 + 31 of src -> lds (nrows >= 1; a tile from r0 >= nrows
+  // reads row nrows - 1 throughout)
   __device__ __forceinline__ void request(void* lds, const T* src, int r0, int nrows, int tid) const {
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const T* base = src + (int64_t)r0 * D;
-    const int last = nrows - 1 - r0;   // last row of the tile inside the source
+    const TileRows tr = tile_rows(r0, nrows);
+    const T* base = src + (int64_t)tr.base * D;
+    const int last = tr.last;   // last row of the tile inside the source
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
       const int first = (j * NTH + 64 * w) % C::ROW_CHUNKS;

@@ -2,9 +2,11 @@
 
 ``build_block_to_query_csr`` keeps the reference contract (nsa_fsa.py:14-64):
 pairs (t, j) with j >= 0 and j*block_size <= t, grouped by (b, hkv, block)
-with queries ascending, global offsets.  It runs as a stable radix sort on the
-GPU (``nsa_csr_build``); the exact pair count is read back once to size the
-returned tensors, as the reference's ``nonzero`` does.
+with queries ascending, global offsets.  It runs as a counting build on the
+GPU (``nsa_csr_build``: per-(block, query chunk) counts, an exclusive scan,
+then placement in query order; a radix sort only past the counting build's LDS
+budget); the exact pair count is read back once to size the returned tensors,
+as the reference's ``nonzero`` does.
 """
 
 import torch

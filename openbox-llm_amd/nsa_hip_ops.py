@@ -157,8 +157,11 @@ OVERLAP_SEL_BWD = False
 
 # True: the fused backward computes the compression and window dQ in one launch
 # (nsa_range_dq_cw) that also finishes the rows; False: one launch per branch
-# through a float32 dQ buffer.
+# through a float32 dQ buffer (the compression dQ finishing the rows, or, with
+# SEPARATE_SEL_DQ, a third launch summing the selection partials), so that
+# each branch's dQ can be timed on its own.
 FUSE_RANGE_DQ = True
+SEPARATE_SEL_DQ = False
 
 
 def _side_stream(device):
@@ -602,14 +605,27 @@ def range_dq_cw(q, do, kc, vc, ktc, lse_c, dot_c, rs_c, kw, vw, ktw, lse_w, dot_
     return out
 
 
+# True (default): the chunks of the compression dK/dV and the work items of
+# the selection dK/dV write partial rows that a second launch sums in a fixed
+# order, so every gradient is bit-identical run to run.  False: they merge
+# with float atomics (no partial buffers; the last bits may differ run to run).
+DETERMINISTIC_DKDV = True
+
+
 def range_dkdv(mode, q, k, v, do, coff, dot, window=0, cmp_block=1, cmp_stride=1):
     B, Hq, T, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     dk = torch.empty(B, Hkv, Lk, D, device=q.device, dtype=torch.float32)
     dv = torch.empty_like(dk)
+    part, part_bytes = None, 0
+    if DETERMINISTIC_DKDV and mode == MODE_COMPRESS:
+        part_bytes = int(_lib().nsa_range_dkdv_partial_bytes(mode, B, Hkv, T, Lk, D, int(cmp_block),
+                                                             int(cmp_stride), _stream(q)))
+        if part_bytes > 0:
+            part = torch.empty(part_bytes // 4, device=q.device, dtype=torch.float32)
     _call(_span_name("dkdv", mode), _lib().nsa_range_dkdv, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(do),
-          L.ptr(coff), L.ptr(dot), L.ptr(dk), L.ptr(dv), B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block),
-          int(cmp_stride), L.dtype_code(q), _stream(q))
+          L.ptr(coff), L.ptr(dot), L.ptr(dk), L.ptr(dv), L.ptr(part), part_bytes, B, Hq, Hkv, T, Lk, D,
+          int(window), int(cmp_block), int(cmp_stride), L.dtype_code(q), _stream(q))
     return dk, dv
 
 
@@ -685,10 +701,14 @@ def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, w
         dq_part = torch.empty(B, Hkv, T, ns, Hq // Hkv, D, device=q.device, dtype=q.dtype)
     ws_bytes = int(_lib().nsa_sel_dkdv_workspace(B, Hkv, T, S, block_size, SEL_DKDV_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    part, part_bytes = None, 0
+    if DETERMINISTIC_DKDV:
+        part_bytes = int(_lib().nsa_sel_dkdv_partial_bytes(B, Hkv, T, S, D, block_size, SEL_DKDV_CHUNK))
+        part = torch.empty(max(part_bytes // 4, 1), device=q.device, dtype=torch.float32)
     _call("dkdv[sel]", _lib().nsa_sel_dkdv, L.ptr(qp), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(dop), L.ptr(coff),
           L.ptr(dot), L.ptr(q_of_block), int(want_dq), L.ptr(offsets),
-          L.ptr(count), L.ptr(dk), L.ptr(dv), L.ptr(dq_part), L.ptr(ws), ws_bytes, B, Hq, Hkv, T, D, S, block_size,
-          SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
+          L.ptr(count), L.ptr(dk), L.ptr(dv), L.ptr(part), part_bytes, L.ptr(dq_part), L.ptr(ws), ws_bytes, B, Hq,
+          Hkv, T, D, S, block_size, SEL_DKDV_CHUNK, L.dtype_code(q), _stream(q))
     return dk, dv, dq_part
 
 
@@ -709,14 +729,22 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
     """Block-outer selection forward -> (o, lse[f32], csr); ``csr`` is the
     packed block -> query CSR (built here when not given), ``qp`` the
     ``pack_heads`` copy of q (made here when not given)."""
-    (o_part, ml_part), csr = sel_fwd_partials(q, k, v, block_idx, block_size, csr, vt, qp)
-    B, Hq, T, D = q.shape
-    idx = block_idx.to(torch.int32).contiguous()
-    o = torch.empty_like(q)
-    lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
-    _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
-          Hq, k.shape[1], T, D, idx.shape[-1], block_size, L.dtype_code(q), _stream(q))
+    parts, csr = sel_fwd_partials(q, k, v, block_idx, block_size, csr, vt, qp)
+    o, lse = sel_merge(block_idx, parts, q.shape, k.shape[1], block_size)
     return o, lse, csr
+
+
+def sel_merge(block_idx, parts, q_shape, Hkv, block_size):
+    """The selection output and lse of every row from the partials of
+    ``sel_fwd_partials`` (in the partials' dtype)."""
+    o_part, ml_part = parts
+    B, Hq, T, D = q_shape
+    idx = block_idx.to(torch.int32).contiguous()
+    o = torch.empty(q_shape, device=o_part.device, dtype=o_part.dtype)
+    lse = torch.empty(B, Hq, T, device=o_part.device, dtype=torch.float32)
+    _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
+          Hq, Hkv, T, D, idx.shape[-1], block_size, L.dtype_code(o_part), _stream(o_part))
+    return o, lse
 
 
 def sel_fwd_partials(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
@@ -977,6 +1005,10 @@ class NSAFusedHIP(torch.autograd.Function):
             if fused_dq:
                 dq_out = range_dq_cw(q, dout, k_cmp, v_cmp, kt_c, lse_c, dot[0], rs[0], kw, vw, kt_w, lse_w, dot[2],
                                      rs[2], geom, dq_part, idx)
+            elif dq_part is not None and SEPARATE_SEL_DQ:
+                range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                         geom.cmp_block, geom.cmp_stride)
+                dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
             elif dq_part is not None:
                 dq_out = range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
                                   geom.cmp_block, geom.cmp_stride, sel_part=dq_part, sel_idx=idx,

@@ -49,6 +49,13 @@ def test_size_queries():
     assert lib.nsa_padded_len(1) % 64 == 0
     assert lib.nsa_sel_dkdv_workspace(1, 4, 32768, 16, 64, 256) > 0
     assert lib.nsa_csr_workspace(1, 4, 32768, 16, 512) > 4 * 32768 * 16 * 4
+    # the deterministic selection dK/dV: one 64-key float row pair per work item
+    cap_items = 4 * 512 + (4 * 32768 * 16 + 1023) // 1024 + 1
+    assert lib.nsa_sel_dkdv_partial_bytes(1, 4, 32768, 16, 128, 64, 1024) == cap_items * 64 * 128 * 2 * 4
+    # the window dK/dV has one writer per key: no partial buffer (answered
+    # before any device query)
+    assert lib.nsa_range_dkdv_partial_bytes(0, 1, 4, 32768, 32768, 128, 1, 1, None) == 0
+    assert lib.nsa_range_dkdv_partial_bytes(1, 1, 4, 0, 2047, 128, 32, 16, None) == 0
 
 
 def test_bad_shapes_are_rejected_without_launching():
@@ -60,7 +67,8 @@ def test_bad_shapes_are_rejected_without_launching():
     # branch outputs are the input type or float32
     assert lib.nsa_range_fwd(0, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 0, 1, None) == -2
     # the selection chunk is capped at 1024 queries (staged in LDS)
-    assert lib.nsa_sel_dkdv(*([None] * 8), 1, *([None] * 6), 1 << 30, 1, 4, 1, 64, 64, 2, 16, 2048, 1, None) == -1
+    assert lib.nsa_sel_dkdv(*([None] * 8), 1, *([None] * 5), 0, None, None, 1 << 30, 1, 4, 1, 64, 64, 2, 16, 2048,
+                            1, None) == -1
     assert lib.nsa_pool_fwd(None, None, 1, 1, 64, 64, 16, 16, 5, None) == -2
 
 

@@ -346,16 +346,10 @@ def test_selection_trailing_partial_block(dtype):
     assert float(xs[1].grad[:, :, 96:].abs().max()) > 0
 
 
-def test_run_to_run_gradient_difference_is_bounded():
-    """Two identical fwd+bwd steps: block indices, the output and every
-    gradient without float atomics (dq, dgate, window dK/dV) are bit-identical;
-    the compression and selection dK/dV, which merge work-item partials with
-    float atomics, differ at most by float32 rounding of their sums."""
-    dev = require_gpu()
+def _two_runs(dev, shape, geom, seed):
     import nsa_fused_kernel as nfk
-    import nsa_hip_ops as ops
-    geom = ops.NSAGeometry(**dict(BASELINE_GEOM, force_init=False, n_local=0))
-    ins, do = _fused_inputs(1, 16, 1, 4096, 128, torch.bfloat16, seed=21, head_scale=True)
+    B, Hq, Hkv, T, D = shape
+    ins, do = _fused_inputs(B, Hq, Hkv, T, D, torch.bfloat16, seed=seed, head_scale=True)
     runs = []
     for _ in range(2):
         xs = [t.to(dev).requires_grad_() for t in ins]
@@ -363,7 +357,42 @@ def test_run_to_run_gradient_difference_is_bounded():
         out.backward(do.to(dev))
         torch.cuda.synchronize()
         runs.append((out.detach().cpu(), idx.cpu(), [x.grad.float().cpu() for x in xs]))
-    (o1, i1, g1), (o2, i2, g2) = runs
+    return runs
+
+
+@pytest.mark.parametrize("shape", [(1, 16, 1, 4096, 128), (2, 12, 2, 4096, 64)], ids=["G16", "G6"])
+def test_run_to_run_gradients_are_bit_identical(shape):
+    """Two identical fwd+bwd steps give bit-identical block indices, output
+    and every gradient.  The compression and selection dK/dV split a key's
+    queries over several workgroups (at T = 4096: two 2048-query chunks and
+    their split tails; selection blocks with more than 1024 pairs); their
+    partial rows are summed in a fixed order, as the reference's block-outer
+    dK/dV writes each block once (nsa_selection_backward.py:207-275)."""
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    assert ops.DETERMINISTIC_DKDV
+    geom = ops.NSAGeometry(**dict(BASELINE_GEOM, force_init=False, n_local=0))
+    (o1, i1, g1), (o2, i2, g2) = _two_runs(dev, shape, geom, seed=21)
+    assert torch.equal(i1, i2) and torch.equal(o1, o2)
+    for nm, a, b in zip(NAMES, g1, g2):
+        d = float((a - b).abs().max())
+        log(f"  d{nm}: run-to-run max |diff| {d:.3e}")
+        assert torch.equal(a, b), f"d{nm} differs between identical runs"
+        assert float(a.abs().max()) > 0, f"d{nm} is all zero"
+
+
+def test_atomic_dkdv_merge_is_bounded():
+    """With DETERMINISTIC_DKDV off the compression and selection dK/dV merge
+    their partials with float atomics: the other gradients stay bit-identical,
+    those differ at most by float32 rounding of their sums."""
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    geom = ops.NSAGeometry(**dict(BASELINE_GEOM, force_init=False, n_local=0))
+    ops.DETERMINISTIC_DKDV = False
+    try:
+        (o1, i1, g1), (o2, i2, g2) = _two_runs(dev, (1, 16, 1, 4096, 128), geom, seed=21)
+    finally:
+        ops.DETERMINISTIC_DKDV = True
     assert torch.equal(i1, i2) and torch.equal(o1, o2)
     for nm, a, b in zip(NAMES, g1, g2):
         d = float((a - b).abs().max())

@@ -7,6 +7,9 @@
 * The two query rows of a selection tile (pair_rows): addressed upward from
   the lower query, so a CSR whose entries do not ascend cannot wrap an
   unsigned offset (tests/host/check_pair_rows.hip).
+* A row-tile request that starts at or past the end of its source reads the
+  last row instead of wrapping an unsigned offset (tile_rows,
+  tests/host/check_tile_rows.hip).
 * M0: the inline-asm DMA helpers of nsa_tile32.h write M0 (the LDS address
   of global_load_lds) behind the compiler's back.  That is safe only while
   no compiler-generated instruction keeps a value in M0 across them.  The
@@ -47,6 +50,18 @@ def test_pair_rows_addressing(tmp_path):
     exe = tmp_path / "check_pair_rows"
     subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", f"-I{ROOT}/include", f"-I{PKG}/csrc",
                     os.path.join(ROOT, "tests", "host", "check_pair_rows.hip"), "-o", str(exe)],
+                   check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout
+
+
+def test_tile_rows_clamp(tmp_path):
+    """Row-tile requests from any start row, also past the end of the source,
+    address only rows of the source (tests/host/check_tile_rows.hip)."""
+    exe = tmp_path / "check_tile_rows"
+    subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", f"-I{ROOT}/include", f"-I{PKG}/csrc",
+                    os.path.join(ROOT, "tests", "host", "check_tile_rows.hip"), "-o", str(exe)],
                    check=True, capture_output=True)
     r = subprocess.run([str(exe)], capture_output=True, text=True)
     print(r.stdout)
