@@ -124,11 +124,11 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
  * and T queries per row block (rows = B Hq T); the selection branch's dot,
  * rowscale and coff (nbr == 1: the only branch, nbr == 3: branch 1) are then
  * written in the same packed row order [B][Hkv][T][G], the layout
- * nsa_sel_dkdv reads. */
+ * nsa_sel_dkdv reads.  dgate_dtype: dtype, or NSA_F32 for dgate unrounded. */
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
-                 int dtype, int o_dtype, void* stream);
+                 int dtype, int o_dtype, int dgate_dtype, void* stream);
 
 /* float32 accumulator -> dtype. */
 int nsa_cast_f32(const float* x, void* y, int64_t n, int dtype, void* stream);
@@ -244,9 +244,10 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
 
 /* Merge of the forward partials (the log-sum-exp combine of
  * nsa_selection_kernel.py:336-364): o and lse per row over the valid slots of
- * block_idx; rows with none get o = 0 and lse = -1e9. */
+ * block_idx; rows with none get o = 0 and lse = -1e9.  o in o_dtype: dtype
+ * (the partials'), or NSA_F32 unrounded. */
 int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_part, void* o, float* lse, int B,
-                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream);
+                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, int o_dtype, void* stream);
 
 /* dq_out = dq_acc (float32, nullable) + sum of the dQ partials of the valid
  * slots, written in the input dtype (the dQ reduce of
@@ -274,20 +275,21 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
  * merges the selection partials of nsa_sel_fwd_bo (o_part, ml_part, with the
  * [B][Hkv][T][S] block_idx of block size sel_block) into o_sel / lse_sel
  * and writes out = sigmoid(g0) o_cmp + sigmoid(g1) o_sel + sigmoid(g2) o from
- * the gate logits [B][Hq][T][3] (out in dtype).  o, o_sel and o_cmp are in
- * o_dtype (dtype, or NSA_F32 unrounded); the blend uses each branch as
- * stored. */
+ * the gate logits [B][Hq][T][3] (out in out_dtype: dtype, or NSA_F32
+ * unrounded).  o, o_sel and o_cmp are in o_dtype (dtype, or NSA_F32
+ * unrounded); the blend uses each branch as stored. */
 int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                          int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                          const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
                          void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
-                         int o_dtype, void* stream);
+                         int o_dtype, int out_dtype, void* stream);
 
 /* Backward dQ of the range branches (query-side half of
  * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426): dq (float32)
  * receives this branch's dQ, added to its contents when `accumulate`.
  * With sel_part (nullable) the call instead finishes the rows and writes
- * dq_out in the input dtype: dq_out = (dq if accumulate) + this branch's dQ +
+ * dq_out in dq_out_dtype (dtype, or NSA_F32 unrounded): dq_out = (dq if
+ * accumulate) + this branch's dQ +
  * the selection dQ partials of nsa_sel_dkdv for the valid slots of sel_idx
  * ([B][Hkv][T][S] block indices of block size sel_block) -- the role of
  * nsa_sel_dq_reduce folded into this kernel; dq is then only read. */
@@ -295,7 +297,7 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
                  const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
                  int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                  const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
-                 void* stream);
+                 int dq_out_dtype, void* stream);
 
 /* Backward dQ of the compression and window branches in one launch, rows
  * finished with the selection dQ partials: equal to nsa_range_dq(window,
@@ -305,13 +307,13 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
  * query length (kw, vw, ktw); lse / dot / rowscale per branch as in
  * nsa_range_dq.  No counterpart in the reference (its two launches are
  * _range_attn_bwd_qtiled_kernel, nsa_fused_kernel.py:321-426, once per
- * branch); sel_part, sel_idx and dq_out are required. */
+ * branch); sel_part, sel_idx and dq_out (in dq_out_dtype) are required. */
 int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void* vc, const void* ktc,
                     const float* lse_c, const float* dot_c, const float* rowscale_c, int Lk, int cmp_block,
                     int cmp_stride, const void* kw, const void* vw, const void* ktw, const float* lse_w,
                     const float* dot_w, const float* rowscale_w, int window, int B, int Hq, int Hkv, int T, int D,
                     const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
-                    void* stream);
+                    int dq_out_dtype, void* stream);
 
 /* Backward dK/dV of the range branches (key-outer; the key-side half of
  * _range_attn_bwd_qtiled_kernel).  coff / dot: row offsets and deltas from

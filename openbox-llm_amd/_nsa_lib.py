@@ -45,7 +45,7 @@ SIGNATURES = {
     "nsa_heads_merge_grad": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
     "nsa_pool_bwd": (_I, [_P, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_gate_fwd": (_I, [_P, _P, _P, _P, _P, _L, _I, _I, _P]),
-    "nsa_bwd_prep": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _I, _P]),
+    "nsa_bwd_prep": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _L, _I, _I, _I, _I, _I, _P]),
     "nsa_cast_f32": (_I, [_P, _P, _L, _I, _P]),
     "nsa_pack_heads": (_I, [_P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_fwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
@@ -62,15 +62,15 @@ SIGNATURES = {
     "nsa_sel_partial_slots": (_I, [_I, _I]),
     "nsa_sel_fwd_bo_workspace": (_Z, [_I, _I, _I, _I, _I, _I]),
     "nsa_sel_fwd_bo": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _Z, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
-    "nsa_sel_merge": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_sel_merge": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_sel_dq_reduce": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_fwd": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _I, _I, _P]),
     "nsa_range_fwd_finish": (_I, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I,
-                                  _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
+                                  _P, _P, _P, _I, _I, _P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "nsa_range_dq": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
-                          _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
+                          _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _I, _P]),
     "nsa_range_dq_cw": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I,
-                             _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _P]),
+                             _I, _I, _I, _I, _I, _P, _P, _I, _I, _P, _I, _I, _P]),
     "nsa_range_dkdv_partial_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z,
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),

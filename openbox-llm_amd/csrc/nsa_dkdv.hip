@@ -544,10 +544,14 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
 // ---------------------------------------------------------------------------
 constexpr int kSplitStages = 4;   // query tiles in flight + 1 (74 KB: two workgroups per CU)
 
-// P of one tile for the dS-wave, as the two 16-bit operand fragments of the
-// P-wave's dV product: fragment f of lane L at 16-byte slot f 64 + L (each
-// store / load one 16-byte access per lane, the lanes' pieces consecutive)
+// P of one tile for the dS-wave, in the lane order of the P-wave's two
+// 16-bit dV operand fragments: fragment f of lane L at 16-byte slot f 64 + L
+// (each store / load one 16-byte access per lane, the lanes' pieces
+// consecutive).  The values go as fp16, not as the bf16 operand: in the
+// backward P = exp(s - lse) * sigmoid(g) <= 1, and fp16 keeps 11 significant
+// bits of it where bf16 keeps 8 -- dS = P (dP - delta) is formed from them.
 typedef uint32_t PTile[4 * 64 * 2];
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 template <typename T, int D> struct PWave {
   using C = Tile32<T, D>;
@@ -593,10 +597,16 @@ template <typename T, int D> struct PWave {
     pf[0].set(P);
     pf[1].set(P + 8);
     {
+      static_assert(sizeof(T) == 2, "the role-split walk hands P over as 16-bit values");
       typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
-      const u32x4_ a = __builtin_bit_cast(u32x4_, pf[0].v), bb = __builtin_bit_cast(u32x4_, pf[1].v);
-      *reinterpret_cast<u32x4_*>(pb + 4 * lane) = a;
-      *reinterpret_cast<u32x4_*>(pb + 256 + 4 * lane) = bb;
+      f16x8 h0, h1;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        h0[r] = (_Float16)P[r];
+        h1[r] = (_Float16)P[8 + r];
+      }
+      *reinterpret_cast<u32x4_*>(pb + 4 * lane) = __builtin_bit_cast(u32x4_, h0);
+      *reinterpret_cast<u32x4_*>(pb + 256 + 4 * lane) = __builtin_bit_cast(u32x4_, h1);
     }
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
@@ -647,11 +657,11 @@ template <typename T, int D> struct SWave {
                                        const float (&dlt)[16], int lane, Frag<T> (&sf)[2]) {
     float dS[16];
     typedef uint32_t u32x4_ __attribute__((ext_vector_type(4)));
-    Frag<T> pf[2];
-    pf[0].v = __builtin_bit_cast(decltype(pf[0].v), *reinterpret_cast<const u32x4_*>(pb + 4 * lane));
-    pf[1].v = __builtin_bit_cast(decltype(pf[1].v), *reinterpret_cast<const u32x4_*>(pb + 256 + 4 * lane));
+    f16x8 ph[2];
+    ph[0] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4_*>(pb + 4 * lane));
+    ph[1] = __builtin_bit_cast(f16x8, *reinterpret_cast<const u32x4_*>(pb + 256 + 4 * lane));
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dS[r] = to_f32(pf[r >> 3].elem(r & 7)) * (pacc[r] - dlt[r]);
+    for (int r = 0; r < 16; ++r) dS[r] = (float)ph[r >> 3][r & 7] * (pacc[r] - dlt[r]);
     sf[0].set(dS);
     sf[1].set(dS + 8);
     Frag<T> sl[2];

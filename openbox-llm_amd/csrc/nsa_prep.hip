@@ -554,7 +554,7 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
                                                   const float* __restrict__ lse2, float* __restrict__ dot,
                                                   float* __restrict__ rowscale, float* __restrict__ coff,
                                                   T* __restrict__ dout_packed, int G, int T_, int64_t rows, int D,
-                                                  int nbr) {
+                                                  int nbr, float* __restrict__ dgate32) {
   constexpr int N = Vec16<T>::N;
   const int gs = D / N;                         // lanes per row, a power of two <= 64
   const int lane = threadIdx.x & 63;
@@ -601,7 +601,8 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
     dot[(int64_t)c * rows + sr] = acc[c];
     rowscale[(int64_t)c * rows + sr] = s;
     if (coff) coff[(int64_t)c * rows + sr] = lse[c][row] * kLog2e - __log2f(s);
-    if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
+    if (dgate32) dgate32[row * 3 + c] = s * (1.0f - s) * acc[c];
+    else if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
   }
 }
 
@@ -909,9 +910,12 @@ int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const v
 int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o2, const void* gate,
                  void* dgate, const float* lse0, const float* lse1, const float* lse2, float* dot,
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
-                 int dtype, int o_dtype, void* stream) {
+                 int dtype, int o_dtype, int dgate_dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
+  NSA_CHECK(dgate_dtype == dtype || dgate_dtype == NSA_F32, NSA_ERR_DTYPE);
+  float* dgate32 = dgate_dtype == NSA_F32 && dtype != NSA_F32 ? (float*)dgate : nullptr;
+  if (dgate32 != nullptr) dgate = nullptr;
   const int vec = dtype == NSA_BF16 ? 8 : 4;
   NSA_CHECK(rows >= 0 && D > 0 && D % vec == 0 && (nbr == 1 || nbr == 3), NSA_ERR_SHAPE);
   const int gs = D / vec;
@@ -928,16 +932,17 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
     k_bwd_prep<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1,
                                                 (const bf16*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2,
-                                                dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr);
+                                                dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr, dgate32);
   else if (dtype == NSA_BF16)
     k_bwd_prep<bf16, float><<<grid, 256, 0, s>>>((const bf16*)dout, (const float*)o0, (const float*)o1,
                                                  (const float*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1,
-                                                 lse2, dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr);
+                                                 lse2, dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr,
+                                                 dgate32);
   else
     k_bwd_prep<float, float><<<grid, 256, 0, s>>>((const float*)dout, (const float*)o0, (const float*)o1,
                                                   (const float*)o2, (const float*)gate, (float*)dgate, lse0, lse1,
                                                   lse2, dot, rowscale, coff, (float*)dout_packed, G, T, rows, D,
-                                                  nbr);
+                                                  nbr, nullptr);
   return nsa_launch_status();
 }
 

@@ -178,6 +178,7 @@ template <typename T, typename TO> struct FwdExtras {
   const T* gate;           // [B][Hq][T][3] gate logits
   T* out;                  // [B][Hq][T][D]
   int S, sel_L;
+  float* out32;            // nullable: out in float32 (unrounded), written instead of `out`
 };
 
 // The wave's own output rows (this branch, unnormalised acc with the row
@@ -284,13 +285,22 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     float y[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * to_f32(from_f32<TO>(acc_s[i])) + g2 * ow[i];
-    store8(f.out + orow * D + 8 * c8, y);
+    if (f.out32 != nullptr)
+      store8(f.out32 + orow * D + 8 * c8, y);
+    else
+      store8(f.out + orow * D + 8 * c8, y);
   }
 }
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kRescale = 8.0f;   // log2 growth of a row maximum that forces a rescale
 
-// One 32-key tile of the forward for NT row tiles.  MASK = false: every key
+// One 32-key tile of the forward for NT row tiles.  pv_split (16-bit
+// operands): P enters the PV product as two operands, its bf16 rounding and
+// the remainder (about 16 significant bits instead of 8), so the stored o
+// (and the backward's row dot dO . o, whose error dS = P (dP - dot) passes on
+// whole to dQ and dK) carries no P rounding; the window forward uses it (at
+// config 4 its dQ error fell from 1.8e-2 to 1.2e-2 for 0.06 ms a step), the
+// compression forward does not (0.29 ms for no measurable gain).  MASK = false: every key
 // of the tile is visible to every valid row of the wave (no per-element test).
 // The row maximum m is only moved when the tile's maximum exceeds it by more
 // than kRescale (wave-uniform branch); p = exp2(s - m) <= 2^kRescale keeps the
@@ -298,7 +308,8 @@ constexpr float kRescale = 8.0f;   // log2 growth of a row maximum that forces a
 template <typename T, int D, int NT, int DT = Tile32<T, D>::DT, int KS = Tile32<T, D>::KS>
 __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT], float (&l_)[NT],
                                          const Frag<T> (&qf)[NT][KS], const T* tK, const T* tV, int kb, bool mask,
-                                         const int (&lo)[NT], const int (&hi)[NT], float sl2, int n, int h) {
+                                         const int (&lo)[NT], const int (&hi)[NT], float sl2, int n, int h,
+                                         bool pv_split) {
   // all K fragments of the tile first, so the LDS reads are in flight together
   Frag<T> ka[KS];
 #pragma unroll
@@ -348,7 +359,7 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
       for (int dt = 0; dt < DT; ++dt) acc[dt][nt] *= alpha;
     }
   }
-  Frag<T> pf[NT][2];
+  Frag<T> pf[NT][2], pl[NT][2];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float p[16];
@@ -361,6 +372,14 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
     l_[nt] += ps;
     pf[nt][0].set(p);
     pf[nt][1].set(p + 8);
+    if constexpr (sizeof(T) == 2) {
+      if (pv_split) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] -= to_f32(from_f32<T>(p[r]));
+        pl[nt][0].set(p);
+        pl[nt][1].set(p + 8);
+      }
+    }
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -368,6 +387,16 @@ __device__ __forceinline__ void fwd_tile(f32x16 (&acc)[DT][NT], float (&m_)[NT],
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], va[dt][s], pf[nt][s]);
+  if constexpr (sizeof(T) == 2) {
+    if (pv_split) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) mma32(acc[dt][nt], va[dt][s], pl[nt][s]);
+    }
+  }
 }
 
 template <typename T, int D, int NT, typename TO, bool FLAT>
@@ -459,7 +488,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // span skip the per-element mask
     const bool mask = !(kb >= fs.lo && kb + 31 <= fs.hi);
     fwd_tile<T, D, NT>(acc, m_, l_, qf, sK[decltype(st)::value], sV[decltype(st)::value], kb, mask, lo, hi, sl2, n,
-                       h);
+                       h, mode == NSA_MODE_WINDOW);
   });
 
   if (fin_args.opart != nullptr) {
@@ -571,7 +600,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                                                     int accumulate, int Hq, int Hkv, int T_, int Lk, int Lp, int nqt,
                                                     int window, int cl, int cd, float sl2, float scale,
                                                     const T* __restrict__ sel_part, const int32_t* __restrict__ sel_idx,
-                                                    T* __restrict__ dq_out, int S, int sel_L, DqWindow<T> w2) {
+                                                    T* __restrict__ dq_out, float* __restrict__ dq_out32, int S,
+                                                    int sel_L, DqWindow<T> w2) {
   using C = Tile32<T, D>;
   constexpr int NST = 3;   // key tiles in flight + 1
   // one LDS buffer: the key stages during the walk, then (finishing rows)
@@ -727,7 +757,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int i = 0; i < 8; ++i) v[i] += x[k2].get(i);
         }
       }
-      store8(dq_out + orow * D + 8 * c8, v);
+      if (dq_out32 != nullptr)
+        store8(dq_out32 + orow * D + 8 * c8, v);
+      else
+        store8(dq_out + orow * D + 8 * c8, v);
     }
     return;
   }
@@ -804,7 +837,7 @@ static int range_dq_launch(int mode, const void* q, const void* k, const void* v
                            const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate,
                            int B, int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                            const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out,
-                           const DqWindow<E>& w2, hipStream_t s) {
+                           bool out_f32, const DqWindow<E>& w2, hipStream_t s) {
   const int NHC = (Hq / Hkv + 15) / 16;
   const int Lp = padded_len(Lk);
   const float scale = 1.0f / sqrtf((float)D);
@@ -819,8 +852,9 @@ static int range_dq_launch(int mode, const void* q, const void* k, const void* v
     auto kern = flat ? k_range_dq32<E, DD, NT, true> : k_range_dq32<E, DD, NT, false>;
     kern<<<(unsigned)grid, 256, 0, s>>>(mode, (const E*)q, (const E*)k, (const E*)v, (const E*)kt, (const E*)dout,
                                         lse, dot, rowscale, dq, accumulate, Hq, Hkv, T, Lk, Lp, nqt, window,
-                                        cmp_block, cmp_stride, sl2, scale, (const E*)sel_part, sel_idx, (E*)dq_out,
-                                        S, sel_block, w2);
+                                        cmp_block, cmp_stride, sl2, scale, (const E*)sel_part, sel_idx,
+                                        out_f32 ? nullptr : (E*)dq_out, out_f32 ? (float*)dq_out : nullptr, S,
+                                        sel_block, w2);
   });
   return nsa_launch_status();
 }
@@ -859,31 +893,37 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
                          int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                          const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,
                          void* o_sel, float* lse_sel, const void* o_cmp, const void* gate, void* out, int dtype,
-                         int o_dtype, void* stream) {
+                         int o_dtype, int out_dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
   NSA_CHECK(o_part && ml_part && block_idx && o_sel && lse_sel && o_cmp && gate && out, NSA_ERR_ARG);
   NSA_CHECK(S >= 1 && sel_block >= 16 && sel_block % 16 == 0, NSA_ERR_SHAPE);
+  NSA_CHECK(out_dtype == dtype || out_dtype == NSA_F32, NSA_ERR_DTYPE);
   if (T == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
+  float* out32 = out_dtype == NSA_F32 && dtype != NSA_F32 ? (float*)out : nullptr;
+  if (out32 != nullptr) out = nullptr;
   if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
     return range_fwd_launch<bf16, bf16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
         FwdExtras<bf16, bf16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel,
-                              lse_sel, (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
+                              lse_sel, (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block,
+                              out32},
         s);
   if (dtype == NSA_BF16)
     return range_fwd_launch<bf16, float>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
         FwdExtras<bf16, float>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
-                               lse_sel, (const float*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block},
+                               lse_sel, (const float*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block,
+                               out32},
         s);
   return range_fwd_launch<float, float>(
       mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
       FwdExtras<float, float>{nullptr, (const float*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
-                              lse_sel, (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block},
+                              lse_sel, (const float*)o_cmp, (const float*)gate, (float*)out, S, sel_block,
+                              nullptr},
       s);
 }
 
@@ -891,8 +931,9 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
                  const float* lse, const float* dot, const float* rowscale, float* dq, int accumulate, int B,
                  int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                  const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
-                 void* stream) {
+                 int dq_out_dtype, void* stream) {
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
+  NSA_CHECK(dq_out_dtype == dtype || dq_out_dtype == NSA_F32, NSA_ERR_DTYPE);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
   NSA_CHECK(sel_part == nullptr || (sel_idx != nullptr && dq_out != nullptr && S >= 1 && sel_block >= 16 &&
@@ -903,9 +944,9 @@ int nsa_range_dq(int mode, const void* q, const void* k, const void* v, const vo
   if (dtype == NSA_BF16)
     return range_dq_launch<bf16>(mode, q, k, v, kt, dout, lse, dot, rowscale, dq, accumulate, B, Hq, Hkv, T, Lk,
                                  D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block, dq_out,
-                                 DqWindow<bf16>{}, s);
+                                 dq_out_dtype == NSA_F32, DqWindow<bf16>{}, s);
   return range_dq_launch<float>(mode, q, k, v, kt, dout, lse, dot, rowscale, dq, accumulate, B, Hq, Hkv, T, Lk, D,
-                                window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block, dq_out,
+                                window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block, dq_out, false,
                                 DqWindow<float>{}, s);
 }
 
@@ -914,7 +955,8 @@ int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void*
                     int cmp_stride, const void* kw, const void* vw, const void* ktw, const float* lse_w,
                     const float* dot_w, const float* rowscale_w, int window, int B, int Hq, int Hkv, int T, int D,
                     const void* sel_part, const int32_t* sel_idx, int S, int sel_block, void* dq_out, int dtype,
-                    void* stream) {
+                    int dq_out_dtype, void* stream) {
+  NSA_CHECK(dq_out_dtype == dtype || dq_out_dtype == NSA_F32, NSA_ERR_DTYPE);
   NSA_CHECK(range_args_ok(NSA_MODE_COMPRESS, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride) &&
                 range_args_ok(NSA_MODE_WINDOW, B, Hq, Hkv, T, T, D, window, cmp_block, cmp_stride),
             NSA_ERR_SHAPE);
@@ -929,13 +971,13 @@ int nsa_range_dq_cw(const void* q, const void* dout, const void* kc, const void*
   if (dtype == NSA_BF16)
     return range_dq_launch<bf16>(NSA_MODE_COMPRESS, q, kc, vc, ktc, dout, lse_c, dot_c, rowscale_c, nullptr, 0, B,
                                  Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block,
-                                 dq_out,
+                                 dq_out, dq_out_dtype == NSA_F32,
                                  DqWindow<bf16>{(const bf16*)kw, (const bf16*)vw, (const bf16*)ktw, lse_w, dot_w,
                                                 rowscale_w, Lpw},
                                  s);
   return range_dq_launch<float>(NSA_MODE_COMPRESS, q, kc, vc, ktc, dout, lse_c, dot_c, rowscale_c, nullptr, 0, B,
                                 Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride, sel_part, sel_idx, S, sel_block,
-                                dq_out,
+                                dq_out, false,
                                 DqWindow<float>{(const float*)kw, (const float*)vw, (const float*)ktw, lse_w, dot_w,
                                                 rowscale_w, Lpw},
                                 s);

@@ -438,7 +438,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const T* __restrict__ opart,
                                                    const float2* __restrict__ mlpart, T* __restrict__ o,
                                                    float* __restrict__ lse, int Hq, int Hkv, int T_, int S, int n_csr,
-                                                   int L, int nsub, int64_t total) {
+                                                   int L, int nsub, int64_t total, float* __restrict__ o32) {
   constexpr int NC = D / 8;
   const int G = Hq / Hkv, NS = S * nsub;
   for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
@@ -492,7 +492,10 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
     const float inv = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] *= inv;
-    store8(o + orow * D + 8 * c, acc);
+    if (o32 != nullptr)
+      store8(o32 + orow * D + 8 * c, acc);
+    else
+      store8(o + orow * D + 8 * c, acc);
     if (c == 0) lse[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
   }
 }
@@ -610,9 +613,11 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
 }
 
 int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_part, void* o, float* lse, int B,
-                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream) {
+                  int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, int o_dtype, void* stream) {
   NSA_CHECK(sel_args_ok(B, Hq, Hkv, T, D, S, block_size), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
+  float* o32 = o_dtype == NSA_F32 && dtype != NSA_F32 ? (float*)o : nullptr;
   const int64_t total = (int64_t)B * Hq * T * (D / 8);
   if (total == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -620,12 +625,12 @@ int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16)
       k_sel_merge<bf16, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const bf16*)o_part, (const float2*)ml_part,
-                                                            (bf16*)o, lse, Hq, Hkv, T, S, n_csr, block_size, nsub,
-                                                            total);
+                                                            o32 ? nullptr : (bf16*)o, lse, Hq, Hkv, T, S, n_csr,
+                                                            block_size, nsub, total, o32);
     else
       k_sel_merge<float, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const float*)o_part,
                                                              (const float2*)ml_part, (float*)o, lse, Hq, Hkv, T, S,
-                                                             n_csr, block_size, nsub, total);
+                                                             n_csr, block_size, nsub, total, nullptr);
   });
   return nsa_launch_status();
 }

@@ -457,12 +457,13 @@ def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_pac
     return o, lse
 
 
-def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=None):
+def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=None, out_f32=False):
     """Window forward that also finishes the gated layer's rows: returns
     (o_w, lse_w, o_s, lse_s, out), with the selection partials ``sel_parts``
     = (o_part, ml_part) of ``sel_fwd_partials`` merged into o_s / lse_s and
     out = sum_c sigmoid(gate_c) o_c over the three branches.  o_w and o_s
-    take o_c's dtype (q's, or float32 unrounded); out is in q's dtype."""
+    take o_c's dtype (q's, or float32 unrounded); out is in q's dtype, or
+    float32 (unrounded) with ``out_f32``."""
     check_qkv(q, k, v)
     q, k, gate, o_c = _contig(q), _contig(k), _contig(gate), _contig(o_c)
     B, Hq, T, D = q.shape
@@ -476,11 +477,11 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     lse_w = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
     o_s = torch.empty_like(o_w)
     lse_s = torch.empty_like(lse_w)
-    out = torch.empty_like(q)
+    out = torch.empty(q.shape, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
     _call("fwd[win]", _lib().nsa_range_fwd_finish, MODE_WINDOW, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o_w),
           L.ptr(lse_w), B, Hq, Hkv, T, T, D, int(window), 1, 1, L.ptr(o_part), L.ptr(ml_part), L.ptr(idx),
           idx.shape[-1], int(sel_block), L.ptr(o_s), L.ptr(lse_s), L.ptr(o_c), L.ptr(gate), L.ptr(out),
-          L.dtype_code(q), L.dtype_code(o_c), _stream(q))
+          L.dtype_code(q), L.dtype_code(o_c), L.dtype_code(out), _stream(q))
     return o_w, lse_w, o_s, lse_s, out
 
 
@@ -537,18 +538,19 @@ def delta_of(do, o, lse, pack_hkv=0):
     coff = torch.empty_like(dot)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o), None, None, None, None, L.ptr(lse), None, None,
           L.ptr(dot), None, L.ptr(coff), L.ptr(dop), G, T, rows, D, 1, L.dtype_code(do), L.dtype_code(o),
-          _stream(o))
+          L.dtype_code(do), _stream(o))
     return (dot, coff) if pack_hkv <= 0 else (dot, coff, dop)
 
 
-def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
+def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0, dgate_f32=False):
     """-> (dot, rowscale, coff [3,B,Hq,T] each, dgate [B,Hq,T,3], dop); branch
     order compression, selection, window; coff = lse * log2(e) -
     log2(rowscale).  With ``pack_hkv`` > 0, dop is dO packed for that many KV
     heads (the ``pack_heads`` layout), else None, and the selection branch's
     dot[1] / rowscale[1] / coff[1] hold their values in the packed row order
     [B, Hkv, T, G] (what ``sel_dkdv`` reads with ``stats_packed``).  The
-    branch outputs share one dtype: dO's, or float32 (unrounded)."""
+    branch outputs share one dtype: dO's, or float32 (unrounded).  dgate is
+    in the gate's dtype, or float32 (unrounded) with ``dgate_f32``."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
     assert o_s.dtype == o_c.dtype and o_w.dtype == o_c.dtype, "branch outputs must share one dtype"
     lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
@@ -557,7 +559,7 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
     dot = torch.empty(3, B, Hq, T, device=o_c.device, dtype=torch.float32)
     rs = torch.empty_like(dot)
     coff = torch.empty_like(dot)
-    dgate = torch.empty_like(gate)
+    dgate = torch.empty(gate.shape, device=gate.device, dtype=torch.float32 if dgate_f32 else gate.dtype)
     dop = None
     G = 1
     if pack_hkv > 0:
@@ -565,43 +567,45 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0):
         dop = torch.empty(B, pack_hkv, T, G, D, device=do.device, dtype=do.dtype)
     _call("nsa_bwd_prep", _lib().nsa_bwd_prep, L.ptr(do), L.ptr(o_c), L.ptr(o_s), L.ptr(o_w), L.ptr(gate), L.ptr(dgate),
           L.ptr(lse_c), L.ptr(lse_s), L.ptr(lse_w), L.ptr(dot), L.ptr(rs), L.ptr(coff), L.ptr(dop), G, T, rows, D, 3,
-          L.dtype_code(do), L.dtype_code(o_c), _stream(o_c))
+          L.dtype_code(do), L.dtype_code(o_c), L.dtype_code(dgate), _stream(o_c))
     return dot, rs, coff, dgate, dop
 
 
 def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0, cmp_block=1,
-             cmp_stride=1, sel_part=None, sel_idx=None, sel_block=0):
+             cmp_stride=1, sel_part=None, sel_idx=None, sel_block=0, out_f32=False):
     """dQ of a range branch into the float32 ``dq`` (added when
     ``accumulate``).  With ``sel_part`` (the selection dQ partials of
     ``sel_dkdv``) and ``sel_idx`` the rows are finished instead: returns
     dq_out in q's dtype = (dq if accumulate) + this branch + the selection
-    partials of the valid slots."""
+    partials of the valid slots (float32 unrounded with ``out_f32``)."""
     B, Hq, T, D = q.shape
     Hkv, Lk = k.shape[1], k.shape[2]
     out = None
     S = 0
     if sel_part is not None:
-        out = torch.empty(B, Hq, T, D, device=q.device, dtype=q.dtype)
+        out = torch.empty(B, Hq, T, D, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
         S = sel_idx.shape[-1]
     _call(_span_name("dq", mode), _lib().nsa_range_dq, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do),
           L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
           int(window), int(cmp_block), int(cmp_stride), L.ptr(sel_part), L.ptr(sel_idx), S, int(sel_block),
-          L.ptr(out), L.dtype_code(q), _stream(q))
+          L.ptr(out), L.dtype_code(q), L.dtype_code(out) if out is not None else L.dtype_code(q), _stream(q))
     return out
 
 
-def range_dq_cw(q, do, kc, vc, ktc, lse_c, dot_c, rs_c, kw, vw, ktw, lse_w, dot_w, rs_w, geom, sel_part, sel_idx):
+def range_dq_cw(q, do, kc, vc, ktc, lse_c, dot_c, rs_c, kw, vw, ktw, lse_w, dot_w, rs_w, geom, sel_part, sel_idx,
+                out_f32=False):
     """dQ of the compression and window branches in one launch, rows finished
-    with the selection dQ partials: returns dq_out in q's dtype = compression
-    + window dQ + the partials of the valid slots of ``sel_idx``."""
+    with the selection dQ partials: returns dq_out in q's dtype (float32
+    unrounded with ``out_f32``) = compression + window dQ + the partials of
+    the valid slots of ``sel_idx``."""
     B, Hq, T, D = q.shape
     Hkv, Lk = kc.shape[1], kc.shape[2]
-    out = torch.empty(B, Hq, T, D, device=q.device, dtype=q.dtype)
+    out = torch.empty(B, Hq, T, D, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
     _call("dq[cmp+win]", _lib().nsa_range_dq_cw, L.ptr(q), L.ptr(do), L.ptr(kc), L.ptr(vc), L.ptr(ktc),
           L.ptr(lse_c), L.ptr(dot_c), L.ptr(rs_c), Lk, int(geom.cmp_block), int(geom.cmp_stride), L.ptr(kw),
           L.ptr(vw), L.ptr(ktw), L.ptr(lse_w), L.ptr(dot_w), L.ptr(rs_w), int(geom.window), B, Hq, Hkv, T, D,
           L.ptr(sel_part), L.ptr(sel_idx), sel_idx.shape[-1], int(geom.sel_block), L.ptr(out), L.dtype_code(q),
-          _stream(q))
+          L.dtype_code(out), _stream(q))
     return out
 
 
@@ -725,25 +729,26 @@ def sel_dq_reduce(block_idx, dq_part, dq_acc, block_size, dtype):
     return out
 
 
-def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
+def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None, o_f32=False):
     """Block-outer selection forward -> (o, lse[f32], csr); ``csr`` is the
     packed block -> query CSR (built here when not given), ``qp`` the
-    ``pack_heads`` copy of q (made here when not given)."""
+    ``pack_heads`` copy of q (made here when not given).  ``o_f32``: o in
+    float32 (unrounded), else in q's dtype."""
     parts, csr = sel_fwd_partials(q, k, v, block_idx, block_size, csr, vt, qp)
-    o, lse = sel_merge(block_idx, parts, q.shape, k.shape[1], block_size)
+    o, lse = sel_merge(block_idx, parts, q.shape, k.shape[1], block_size, o_f32=o_f32)
     return o, lse, csr
 
 
-def sel_merge(block_idx, parts, q_shape, Hkv, block_size):
+def sel_merge(block_idx, parts, q_shape, Hkv, block_size, o_f32=False):
     """The selection output and lse of every row from the partials of
-    ``sel_fwd_partials`` (in the partials' dtype)."""
+    ``sel_fwd_partials`` (o in the partials' dtype, or float32 unrounded)."""
     o_part, ml_part = parts
     B, Hq, T, D = q_shape
     idx = block_idx.to(torch.int32).contiguous()
-    o = torch.empty(q_shape, device=o_part.device, dtype=o_part.dtype)
+    o = torch.empty(q_shape, device=o_part.device, dtype=torch.float32 if o_f32 else o_part.dtype)
     lse = torch.empty(B, Hq, T, device=o_part.device, dtype=torch.float32)
     _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
-          Hq, Hkv, T, D, idx.shape[-1], block_size, L.dtype_code(o_part), _stream(o_part))
+          Hq, Hkv, T, D, idx.shape[-1], block_size, L.dtype_code(o_part), L.dtype_code(o), _stream(o_part))
     return o, lse
 
 
@@ -793,8 +798,12 @@ class SelectionAttnHIP(torch.autograd.Function):
     def forward(ctx, q, k, v, block_idx, block_size):
         q, k, v = _contig(q), _contig(k), _contig(v)
         idx = block_idx.to(torch.int32).contiguous()
-        o, lse, csr = sel_fwd_fsa(q, k, v, idx, block_size)
-        ctx.save_for_backward(q, k, v, idx, o, lse, *csr)
+        # the backward's row dots dO . o read o unrounded (float32): with the
+        # returned bf16 o, a peaked softmax row passes that rounding on to dS
+        # and dK (the same choice as the fused layer's branch outputs)
+        o32, lse, csr = sel_fwd_fsa(q, k, v, idx, block_size, o_f32=q.dtype != torch.float32)
+        o = cast_f32(o32, q.dtype)
+        ctx.save_for_backward(q, k, v, idx, o32, lse, *csr)
         ctx.block_size = block_size
         return o
 
@@ -822,10 +831,11 @@ def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
     return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
-def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None):
+def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None, grads_f32=False):
     """dq, dk, dv of the selection branch (input dtypes), all block-outer
     (the roles of selection_backward_fsa, nsa_selection_backward.py:278-334):
-    one kernel writes dK/dV and the dQ partials, a reduce sums the partials."""
+    one kernel writes dK/dV and the dQ partials, a reduce sums the partials.
+    ``grads_f32``: dk, dv as the float32 sums the kernel forms (not cast)."""
     check_qkv(q, k, v)
     q, k, v, do = (_contig(t) for t in (q, k, v, do))
     idx = block_idx.to(torch.int32).contiguous()
@@ -833,6 +843,8 @@ def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None)
     dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True, dop=dop,
                                stats_packed=True)
     dq = sel_dq_reduce(idx, dq_part, None, block_size, q.dtype)
+    if grads_f32:
+        return dq, dk, dv
     return dq, cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
@@ -890,14 +902,144 @@ class CompressionWithLse(torch.autograd.Function):
         return dq, dk, dv, None, None
 
 
-class NSAFusedHIP(torch.autograd.Function):
-    """All three gated branches in one boundary.
+def fused_forward(q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled=False, out_f32=False):
+    """The gated three-branch layer's forward (nsa_fused_kernel.py:560-573):
+    pool -> compression -> (importance / top-n when block_idx is None) ->
+    selection -> window -> gate.  Returns (out, idx, saved): out in q's dtype
+    (float32 unrounded with ``out_f32``), the int32 block indices, and the
+    tensors ``fused_backward`` needs.  ``pooled``: kc / vc are already the
+    pooled compression tokens [B,Hkv,n_cmp,D]."""
+    check_qkv(q, kc, vc)
+    check_qkv(q, ks, vs)
+    check_qkv(q, kw, vw)
+    q, kc, vc, ks, vs, kw, vw, gate = (_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate))
+    T = q.shape[2]
+    assert ks.shape[2] == T and kw.shape[2] == T, "selection / window keys must have the query length"
+    if pooled:
+        assert kc.shape[2] == n_cmp_tokens(T, geom.cmp_block, geom.cmp_stride), \
+            "pooled compression keys must have (T - l) // d + 1 tokens"
+        k_cmp, v_cmp = kc, vc
+    else:
+        assert kc.shape[2] == T, "compression keys must have the query length"
+        k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
+        v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
+    S = min(geom.n_sel, T // geom.sel_block) if block_idx is None else block_idx.shape[-1]
+    want_sel = S > 0
+    qp = (torch.empty(q.shape[0], ks.shape[1], T, q.shape[1] // ks.shape[1], q.shape[3], device=q.device,
+                      dtype=q.dtype) if want_sel else torch.empty(0, device=q.device, dtype=q.dtype))
+    # the branch outputs stay internal (only their gated sum is returned):
+    # they are kept in float32 so that the backward's row dots dO . o_c
+    # see them unrounded -- with bf16-rounded outputs that dot carries an
+    # error that a peaked softmax row passes on to dS, dQ and dK whole
+    o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride,
+                           q_packed=qp if want_sel else None, o_f32=want_sel)
+    if block_idx is None:
+        block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
+    idx = block_idx.to(torch.int32).contiguous()
+    if idx.shape[-1] > 0:
+        # selection partials; the window forward merges them and applies the gate
+        parts, csr = sel_fwd_partials(q, ks, vs, idx, geom.sel_block, qp=qp)
+        o_w, lse_w, o_s, lse_s, out = range_fwd_finish(q, kw, vw, geom.window, parts, idx, geom.sel_block,
+                                                       o_c, gate, out_f32=out_f32)
+    else:
+        o_s = torch.zeros_like(q)
+        lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
+        csr = ()
+        o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
+        out = gate_fwd(gate, o_c, o_s, o_w)
+        if out_f32:
+            out = out.float()
+    saved = (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, qp, *csr)
+    return out, idx, saved
 
-    Forward: pool -> compression -> (importance / top-n when block_idx is None)
-    -> selection -> window -> gate.  Backward: gate prep, dQ of the three
-    branches accumulated into one float32 buffer, key-side dK/dV per branch,
-    pool backward.  Same outputs and gradients as composing the per-branch
-    Functions (nsa_fused_kernel.py:560-573).
+
+def fused_backward(saved, dout, geom, T, pooled=False, grads_f32=False):
+    """The backward of ``fused_forward`` from its ``saved`` tensors ->
+    (dq, dkc, dvc, dks, dvs, dkw, dvw, dgate): gate prep, the dQ of the three
+    branches, key-side dK/dV per branch, pool backward.  Gradients in the
+    input dtype, or float32 (the unrounded values the kernels form) with
+    ``grads_f32``."""
+    (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w,
+     lse_c, lse_s, lse_w, qp, *csr) = saved
+    dout = _contig(dout)
+    dtype = torch.float32 if grads_f32 else q.dtype
+    dot, rs, coff, dgate, dop = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w,
+                                              pack_hkv=ks.shape[1] if idx.shape[-1] > 0 else 0,
+                                              dgate_f32=grads_f32)
+    # one launch walks the compression and window keys of every query and
+    # finishes its rows with the selection partials (no float32 dQ buffer)
+    fused_dq = FUSE_RANGE_DQ and idx.shape[-1] > 0 and k_cmp.shape[2] > 0
+    dq = None if fused_dq else torch.empty(q.shape, device=q.device, dtype=torch.float32)
+    # selection dK/dV and dQ partials (block-outer, bound by memory traffic),
+    # optionally on a side stream beside the window and compression key-side
+    # kernels (bound by MFMA issue) on the current stream
+    main = torch.cuda.current_stream(q.device)
+    dq_part = None
+    side = main
+    if idx.shape[-1] > 0:
+        side = _side_stream(q.device) if OVERLAP_SEL_BWD else main
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
+                                         csr=tuple(csr), want_dq=True, qp=qp, dop=dop, stats_packed=True)
+        # inputs read on the side stream keep their memory until its work is done
+        for t in (q, ks, vs, dout, coff, dot, idx, qp, dop, *csr):
+            t.record_stream(side)
+    else:
+        dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
+        dvs = torch.zeros_like(dks)
+    # window
+    kt_w = transpose_kv(kw)
+    if not fused_dq:
+        range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
+    dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
+    # compression dK/dV
+    if k_cmp.shape[2] > 0:
+        dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
+                              geom.cmp_block, geom.cmp_stride)
+    else:
+        dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
+        dvp = torch.zeros_like(dkp)
+    if dq_part is not None and side is not main:
+        main.wait_stream(side)
+        for t in (dks, dvs, dq_part):
+            t.record_stream(main)
+    # compression dQ; it finishes the rows: window dQ + its own + the
+    # selection partials, written in the output dtype
+    if k_cmp.shape[2] > 0:
+        kt_c = transpose_kv(k_cmp)
+        if fused_dq:
+            dq_out = range_dq_cw(q, dout, k_cmp, v_cmp, kt_c, lse_c, dot[0], rs[0], kw, vw, kt_w, lse_w, dot[2],
+                                 rs[2], geom, dq_part, idx, out_f32=grads_f32)
+        elif dq_part is not None and SEPARATE_SEL_DQ:
+            range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                     geom.cmp_block, geom.cmp_stride)
+            dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, q.dtype).to(dtype)
+        elif dq_part is not None:
+            dq_out = range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                              geom.cmp_block, geom.cmp_stride, sel_part=dq_part, sel_idx=idx,
+                              sel_block=geom.sel_block, out_f32=grads_f32)
+        else:
+            range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
+                     geom.cmp_block, geom.cmp_stride)
+            dq_out = cast_f32(dq, dtype)
+    else:
+        # (the reduce writes the partials' dtype)
+        dq_out = (sel_dq_reduce(idx, dq_part, dq, geom.sel_block, q.dtype).to(dtype) if dq_part is not None
+                  else cast_f32(dq, dtype))
+    if pooled:
+        dkc, dvc = cast_f32(dkp, dtype), cast_f32(dvp, dtype)
+    else:
+        dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
+        dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
+    return (dq_out, dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
+            cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate)
+
+
+class NSAFusedHIP(torch.autograd.Function):
+    """All three gated branches in one boundary (nsa_fused_kernel.py:560-573):
+    ``fused_forward`` and ``fused_backward``.  Same outputs and gradients as
+    composing the per-branch Functions.
 
     With ``pooled=True`` the compression inputs ``kc``/``vc`` are already the
     pooled tokens ``[B,Hkv,n_cmp,D]`` (the learned BlockCompressor of the
@@ -906,127 +1048,18 @@ class NSAFusedHIP(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled=False):
-        check_qkv(q, kc, vc)
-        check_qkv(q, ks, vs)
-        check_qkv(q, kw, vw)
-        q, kc, vc, ks, vs, kw, vw, gate = (_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate))
-        T = q.shape[2]
-        assert ks.shape[2] == T and kw.shape[2] == T, "selection / window keys must have the query length"
-        if pooled:
-            assert kc.shape[2] == n_cmp_tokens(T, geom.cmp_block, geom.cmp_stride), \
-                "pooled compression keys must have (T - l) // d + 1 tokens"
-            k_cmp, v_cmp = kc, vc
-        else:
-            assert kc.shape[2] == T, "compression keys must have the query length"
-            k_cmp = pool_fwd(kc, geom.cmp_block, geom.cmp_stride)
-            v_cmp = pool_fwd(vc, geom.cmp_block, geom.cmp_stride)
-        S = min(geom.n_sel, T // geom.sel_block) if block_idx is None else block_idx.shape[-1]
-        want_sel = S > 0
-        qp = (torch.empty(q.shape[0], ks.shape[1], T, q.shape[1] // ks.shape[1], q.shape[3], device=q.device,
-                          dtype=q.dtype) if want_sel else torch.empty(0, device=q.device, dtype=q.dtype))
-        # the branch outputs stay internal (only their gated sum is returned):
-        # they are kept in float32 so that the backward's row dots dO . o_c
-        # see them unrounded -- with bf16-rounded outputs that dot carries an
-        # error that a peaked softmax row passes on to dS, dQ and dK whole
-        o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride,
-                               q_packed=qp if want_sel else None, o_f32=want_sel)
-        if block_idx is None:
-            block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
-        idx = block_idx.to(torch.int32).contiguous()
-        if idx.shape[-1] > 0:
-            # selection partials; the window forward merges them and applies the gate
-            parts, csr = sel_fwd_partials(q, ks, vs, idx, geom.sel_block, qp=qp)
-            o_w, lse_w, o_s, lse_s, out = range_fwd_finish(q, kw, vw, geom.window, parts, idx, geom.sel_block,
-                                                           o_c, gate)
-        else:
-            o_s = torch.zeros_like(q)
-            lse_s = torch.full(q.shape[:3], -1e9, device=q.device, dtype=torch.float32)
-            csr = ()
-            o_w, lse_w = range_fwd(MODE_WINDOW, q, kw, vw, geom.window)
-            out = gate_fwd(gate, o_c, o_s, o_w)
-        ctx.save_for_backward(q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w, lse_c, lse_s, lse_w, qp,
-                              *csr)
+        out, idx, saved = fused_forward(q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled)
+        ctx.save_for_backward(*saved)
         ctx.geom = geom
-        ctx.T = T
+        ctx.T = q.shape[2]
         ctx.pooled = pooled
         ctx.mark_non_differentiable(idx)
         return out, idx
 
     @staticmethod
     def backward(ctx, dout, _didx):
-        (q, ks, vs, kw, vw, gate, idx, k_cmp, v_cmp, o_c, o_s, o_w,
-         lse_c, lse_s, lse_w, qp, *csr) = ctx.saved_tensors
-        geom, T = ctx.geom, ctx.T
-        dout = _contig(dout)
-        dtype = q.dtype
-        dot, rs, coff, dgate, dop = gate_bwd_prep(dout, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w,
-                                                  pack_hkv=ks.shape[1] if idx.shape[-1] > 0 else 0)
-        # one launch walks the compression and window keys of every query and
-        # finishes its rows with the selection partials (no float32 dQ buffer)
-        fused_dq = FUSE_RANGE_DQ and idx.shape[-1] > 0 and k_cmp.shape[2] > 0
-        dq = None if fused_dq else torch.empty(q.shape, device=q.device, dtype=torch.float32)
-        # selection dK/dV and dQ partials (block-outer, bound by memory traffic)
-        # run on a side stream beside the window and compression key-side
-        # kernels (bound by MFMA issue) on the current stream
-        main = torch.cuda.current_stream(q.device)
-        dq_part = None
-        if idx.shape[-1] > 0:
-            side = _side_stream(q.device) if OVERLAP_SEL_BWD else main
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                dks, dvs, dq_part = sel_dkdv(q, ks, vs, dout, coff[1], dot[1], idx, geom.sel_block,
-                                             csr=tuple(csr), want_dq=True, qp=qp, dop=dop, stats_packed=True)
-            # inputs read on the side stream keep their memory until its work is done
-            for t in (q, ks, vs, dout, coff, dot, idx, qp, dop, *csr):
-                t.record_stream(side)
-        else:
-            dks = torch.zeros(ks.shape, device=q.device, dtype=torch.float32)
-            dvs = torch.zeros_like(dks)
-        # window
-        kt_w = transpose_kv(kw)
-        if not fused_dq:
-            range_dq(MODE_WINDOW, q, kw, vw, kt_w, dout, lse_w, dot[2], rs[2], dq, False, geom.window)
-        dkw, dvw = range_dkdv(MODE_WINDOW, q, kw, vw, dout, coff[2], dot[2], geom.window)
-        # compression dK/dV
-        if k_cmp.shape[2] > 0:
-            dkp, dvp = range_dkdv(MODE_COMPRESS, q, k_cmp, v_cmp, dout, coff[0], dot[0], 0,
-                                  geom.cmp_block, geom.cmp_stride)
-        else:
-            dkp = torch.zeros(k_cmp.shape, device=q.device, dtype=torch.float32)
-            dvp = torch.zeros_like(dkp)
-        if dq_part is not None and side is not main:
-            main.wait_stream(side)
-            for t in (dks, dvs, dq_part):
-                t.record_stream(main)
-        # compression dQ; it finishes the rows: window dQ + its own + the
-        # selection partials, written in the input dtype
-        if k_cmp.shape[2] > 0:
-            kt_c = transpose_kv(k_cmp)
-            if fused_dq:
-                dq_out = range_dq_cw(q, dout, k_cmp, v_cmp, kt_c, lse_c, dot[0], rs[0], kw, vw, kt_w, lse_w, dot[2],
-                                     rs[2], geom, dq_part, idx)
-            elif dq_part is not None and SEPARATE_SEL_DQ:
-                range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
-                         geom.cmp_block, geom.cmp_stride)
-                dq_out = sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype)
-            elif dq_part is not None:
-                dq_out = range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
-                                  geom.cmp_block, geom.cmp_stride, sel_part=dq_part, sel_idx=idx,
-                                  sel_block=geom.sel_block)
-            else:
-                range_dq(MODE_COMPRESS, q, k_cmp, v_cmp, kt_c, dout, lse_c, dot[0], rs[0], dq, True, 0,
-                         geom.cmp_block, geom.cmp_stride)
-                dq_out = cast_f32(dq, dtype)
-        else:
-            dq_out = (sel_dq_reduce(idx, dq_part, dq, geom.sel_block, dtype) if dq_part is not None
-                      else cast_f32(dq, dtype))
-        if ctx.pooled:
-            dkc, dvc = cast_f32(dkp, dtype), cast_f32(dvp, dtype)
-        else:
-            dkc = pool_bwd(dkp, T, geom.cmp_block, geom.cmp_stride, dtype)
-            dvc = pool_bwd(dvp, T, geom.cmp_block, geom.cmp_stride, dtype)
-        return (dq_out, dkc, dvc, cast_f32(dks, dtype), cast_f32(dvs, dtype),
-                cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate, None, None, None)
+        grads = fused_backward(ctx.saved_tensors, dout, ctx.geom, ctx.T, ctx.pooled)
+        return (*grads, None, None, None)
 
 
 def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None, pooled=False):
