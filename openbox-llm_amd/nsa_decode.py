@@ -12,11 +12,17 @@ how long the sequence will grow):
   (int32, on the device) -- and runs ``prefill`` / ``append`` / ``attend``.
 * ``attend`` is ``nsa_decode_fwd``: split-K compression and window partials,
   single-query importance + top-n (ties to the lower block), split-K over
-  the picked blocks, then the gated merge; four launches, no host sync.
+  the picked blocks, then the gated merge: five launches (four when the
+  pooled sequence fits two token-sum chunks, up to 2048 pooled tokens), no
+  host sync.
 * ``append`` is ``nsa_decode_append``: the new rows go to position ``len``
   and a pooled token is written when the new length completes a span, bit
   for bit what ``block_mean_pool`` (``nsa_pool_fwd``) gives over the whole
-  sequence.
+  sequence (the kernel-level NSA, nsa_fused_kernel.py:549-554).
+* A model layer pools with learned compressors instead (BlockCompressor,
+  nsa_model.py:100-123, or the MLP phi): a cache built with ``compressor``
+  (``NSAAttention.decode_cache`` passes the layer's own) pools the prompt's
+  spans with it and, after every append, the span the new length completes.
 
 Lengths live on the device, so a generation loop of ``append`` + ``attend``
 never waits for the host.
@@ -36,8 +42,13 @@ class NSADecodeCache:
     ``capacity`` tokens (``n_kv_heads`` x ``head_dim``, ``dtype``)."""
 
     def __init__(self, batch, n_kv_heads, head_dim, capacity, geom: NSAGeometry, dtype=torch.bfloat16,
-                 device="cuda"):
+                 device="cuda", compressor=None):
+        """``compressor`` (optional): ``(k, v) -> (k_pooled, v_pooled)``, the
+        pooled tokens ``[B, Hkv, (T - l) // d + 1, D]`` of the spans ``[i d,
+        i d + l)`` of ``k, v [B, Hkv, T, D]``; without it the caches hold the
+        plain span means."""
         self.geom = geom
+        self.compressor = compressor
         shape = (batch, n_kv_heads, capacity, head_dim)
         self.kc, self.vc, self.ks, self.vs, self.kw, self.vw = [
             torch.zeros(shape, device=device, dtype=dtype) for _ in range(6)]
@@ -67,8 +78,14 @@ class NSADecodeCache:
         if n > 0:
             # pooled tokens whose span runs past a sequence's length are
             # rewritten by append before they become visible
-            self.k_cmp[:, :, :n].copy_(_ops.pool_fwd(self.kc[:, :, :T], self.geom.cmp_block, self.geom.cmp_stride))
-            self.v_cmp[:, :, :n].copy_(_ops.pool_fwd(self.vc[:, :, :T], self.geom.cmp_block, self.geom.cmp_stride))
+            kc_t, vc_t = self.kc[:, :, :T], self.vc[:, :, :T]
+            if self.compressor is not None:
+                kp, vp = self.compressor(kc_t, vc_t)
+            else:
+                kp = _ops.pool_fwd(kc_t, self.geom.cmp_block, self.geom.cmp_stride)
+                vp = _ops.pool_fwd(vc_t, self.geom.cmp_block, self.geom.cmp_stride)
+            self.k_cmp[:, :, :n].copy_(kp)
+            self.v_cmp[:, :, :n].copy_(vp)
         if lens is None:
             self.lens.fill_(T)
         else:
@@ -80,6 +97,27 @@ class NSADecodeCache:
         """Append one token per sequence (rows ``[B, Hkv, D]``)."""
         self.lens = _ops.decode_append(*self.caches(), self.k_cmp, self.v_cmp, (kc, vc, ks, vs, kw, vw),
                                        self.lens, self.geom)
+        if self.compressor is not None:
+            self._recompress_last_span()
+
+    def _recompress_last_span(self):
+        """With a learned compressor: pool the span each sequence's new length
+        completes (span (len - l) / d, when it divides) with it, over the
+        mean the append kernel wrote; sequences whose length completes no span
+        keep their pooled tokens.  All on the device (no host sync)."""
+        l, d = self.geom.cmp_block, self.geom.cmp_stride
+        B = self.kc.shape[0]
+        L = self.lens.long()
+        i = torch.clamp((L - l) // d, min=0)
+        done = (L >= l) & ((L - l) % d == 0)
+        pos = torch.clamp(i[:, None] * d + torch.arange(l, device=L.device)[None, :], max=self.capacity - 1)
+        b = torch.arange(B, device=L.device)
+        ks = self.kc[b[:, None], :, pos].permute(0, 2, 1, 3)          # [B, Hkv, l, D]
+        vs = self.vc[b[:, None], :, pos].permute(0, 2, 1, 3)
+        kp, vp = self.compressor(ks.contiguous(), vs.contiguous())      # [B, Hkv, 1, D]
+        for cache, new in ((self.k_cmp, kp), (self.v_cmp, vp)):
+            old = cache[b, :, i]                                        # [B, Hkv, D]
+            cache[b, :, i] = torch.where(done[:, None, None], new[:, :, 0].to(cache.dtype), old)
 
     def _workspace(self, Hq, D):
         if Hq not in self._ws:

@@ -368,6 +368,24 @@ class NSAAttention(nn.Module):
             vb = vc[:, :, :(n_cmp - 1) * d + l].unfold(2, l, d).transpose(-1, -2)
         return self.comp_k(kb), self.comp_v(vb)
 
+    def decode_cache(self, batch, capacity, dtype=None, device=None):
+        """An ``NSADecodeCache`` for this layer: its geometry, and its own
+        learned compressors pooling the compression caches (the prompt's
+        spans and each span a decode step completes), so that a decode step
+        is row t of ``forward`` (with the candidate blocks of t's whole
+        selection block)."""
+        import nsa_decode
+        import nsa_hip_ops as ops
+        p = next(self.parameters())
+        geom = ops.NSAGeometry(self.block_size, self.cmp_stride, self.sel_block, self.n_sel, self.window,
+                               self.force_init, self.n_local)
+
+        def compress(k, v):
+            kp, vp = self._pooled(k, v, self._n_cmp(k.shape[2]))
+            return kp.to(k.dtype), vp.to(v.dtype)
+        return nsa_decode.NSADecodeCache(batch, self.Hkv, self.dh, capacity, geom, dtype or p.dtype,
+                                         device or p.device, compressor=compress)
+
     def _gate_logits(self, x):
         B, T, _ = x.shape
         return self.gate(x).view(B, T, self.Hq, 3).permute(0, 2, 1, 3)      # [B,Hq,T,3]
@@ -375,18 +393,6 @@ class NSAAttention(nn.Module):
     def _stacked_weights(self):
         return (self.q_proj.weight, self.k_cmp.weight, self.v_cmp.weight, self.k_slc.weight, self.v_slc.weight,
                 self.k_win.weight, self.v_win.weight, self.gate.weight)
-
-    def _projections(self, x):
-        """q, kc, vc, ks, vs, kw, vw and the gate logits of ``x`` ([B, T, .]
-        each) from one GEMM over the eight weights stacked: one launch, one
-        weight cast under autocast, and in the backward one dX GEMM instead of
-        eight plus their sum.  The parameters stay the separate modules of the
-        reference's layout (its state_dict names)."""
-        ws = self._stacked_weights()
-        *ys, yg = torch.split(F.linear(x, torch.cat(ws, dim=0)), [t.shape[0] for t in ws], dim=-1)
-        # the gate's bias on its own columns only (its gradient then sums 3 Hq
-        # columns, not the whole stacked width)
-        return (*ys, yg + self.gate.bias.to(yg.dtype))
 
     def _split_fused(self, x):
         """The fused path's inputs from the stacked projection of ``x`` in one

@@ -248,3 +248,56 @@ def test_decode_generation_loop_matches_oracle():
                                        gs[sl, :, t:t + 1].double(), idx[sl, :, None, :S], cfg, [t], t + 1)
             outs.append(o[0, :, 0])
         assert_strict(out, torch.stack(outs), BF, f"step t={t}")
+
+
+@pytest.mark.parametrize("compressor", ["mean", "mlp"])
+def test_model_decode_is_the_layer_row(compressor):
+    """NSAAttention.decode_cache pools with the layer's own compressor (the
+    learned weighted mean + projection, or the MLP phi): a prompt prefill then
+    token-by-token appends, and each step's attend equals row t of the layer's
+    fused forward over the whole sequence (head-major output before the output
+    projection), float32, where the two choose the same blocks.  The same
+    cache without the compressor (plain span means) gives other outputs."""
+    import nsa_decode
+    import nsa_hip_ops as ops
+    import nsa_model
+    dev = require_gpu()
+    torch.manual_seed(0)
+    Hq, Hkv, dh, T, P = 8, 2, 64, 640, 200   # head dim 64: the phi kernels take 64 or 128
+    att = nsa_model.NSAAttention(Hq * dh, Hq, Hkv, block_size=32, n_selected_blocks=4, window=96,
+                                 attn_impl="fused", cmp_stride=16, sel_block=64, compressor=compressor,
+                                 rope=nsa_model.Rotary(dh)).to(dev)
+    with torch.no_grad():
+        for p in att.parameters():
+            p.add_(0.05 * torch.randn_like(p))   # pooling weights and biases away from their init
+        x = torch.randn(2, T, Hq * dh, device=dev)
+        q, kc, vc, ks, vs, kw, vw, gate = att._split_fused(x)
+        k_cmp, v_cmp = att._pooled(kc, vc, att._n_cmp(T))
+        geom = ops.NSAGeometry(32, 16, 64, 4, 96, False, 0)
+        out, idx = ops.nsa_attention(q, k_cmp.to(q.dtype).contiguous(), v_cmp.to(q.dtype).contiguous(), ks, vs, kw,
+                                     vw, gate, geom, pooled=True)
+        cache = att.decode_cache(2, T)
+        plain = nsa_decode.NSADecodeCache(2, Hkv, dh, T, geom, q.dtype, dev)
+        rows = (kc, vc, ks, vs, kw, vw)
+        for c in (cache, plain):
+            c.prefill(*[r[:, :, :P] for r in rows])
+        checked, differs = 0, 0
+        for t in range(P, T):
+            for c in (cache, plain):
+                c.append(*[r[:, :, t] for r in rows])
+            if t % 64 != 63:   # block ends: t's own block is complete for both
+                continue
+            o, pick = cache.attend(q[:, :, t].contiguous(), gate[:, :, t].contiguous())
+            o_plain, _ = plain.attend(q[:, :, t].contiguous(), gate[:, :, t].contiguous())
+            S = min(4, t // 64 + 1)
+            same = torch.equal(torch.sort(pick[:, :, :S].long(), -1).values,
+                               torch.sort(idx[:, :, t, :S].long(), -1).values)
+            if not same:
+                log(f"  t={t}: picks differ (near tie), skipped")
+                continue
+            err = float((o - out[:, :, t]).abs().max())
+            assert err <= 1e-4, f"t={t}: decode vs the layer's row: {err:.3e}"
+            differs += int(float((o_plain - out[:, :, t]).abs().max()) > 1e-3)
+            checked += 1
+        log(f"  {compressor}: {checked} decode rows equal the layer's rows; the plain-mean cache differs on {differs}")
+        assert checked >= 6 and differs >= checked // 2

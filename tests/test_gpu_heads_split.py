@@ -121,3 +121,52 @@ def test_heads_split_rejects_a_table_wider_than_the_row():
     rc = L.load().nsa_heads_split(L.ptr(y), ops._addr(ptrs), None, ops._addr(heads), ops._addr(dims),
                                   ops._addr(rots), 1, None, None, 1, 4, 96, L.dtype_code(y), L.stream_of(y))
     assert rc == L.NSA_ERR_SHAPE
+
+
+@pytest.mark.parametrize("rope", [False, True], ids=["norope", "rope"])
+def test_split_fused_matches_the_modules(rope):
+    """The fused layer's inputs (NSAAttention._split_fused: one GEMM over the
+    eight weights stacked and zero-padded, then the head split with RoPE and
+    the gate bias) against each module applied on its own, split into heads
+    and rotated in float64; gradients of x and of every parameter (the gate
+    bias included) from the same cotangents, float32 on the GPU."""
+    import nsa_model
+    torch.manual_seed(0)
+    Hq, Hkv, dh = 6, 2, 16
+    att = nsa_model.NSAAttention(Hq * dh, Hq, Hkv, block_size=16, n_selected_blocks=2, window=32,
+                                 attn_impl="fused", rope=nsa_model.Rotary(dh) if rope else None).cuda()
+    with torch.no_grad():
+        att.gate.bias.normal_()
+    B, T = 2, 40
+    x = torch.randn(B, T, Hq * dh, device="cuda", requires_grad=True)
+    outs = att._split_fused(x)
+    mods = (att.q_proj, att.k_cmp, att.v_cmp, att.k_slc, att.v_slc, att.k_win, att.v_win, att.gate)
+    heads = (Hq, Hkv, Hkv, Hkv, Hkv, Hkv, Hkv, Hq)
+    rot = (True, True, False, True, False, True, False, False)
+    x64 = x.detach().double().requires_grad_()
+    params64 = {n: p.detach().double().requires_grad_() for n, p in att.named_parameters()}
+    cos, sin = (nsa_model.Rotary(dh).tables(T, "cpu", torch.float64) if rope else (None, None))
+    refs = []
+    for m, H, r in zip(mods, heads, rot):
+        name = [n for n, mm in att.named_modules() if mm is m][0]
+        w, b = params64[name + ".weight"], params64.get(name + ".bias")
+        y = torch.nn.functional.linear(x64.cpu(), w.cpu(), None if b is None else b.cpu())
+        hd = y.shape[-1] // H
+        y = y.view(B, T, H, hd).transpose(1, 2)
+        if r and rope:
+            h2 = hd // 2
+            a, c = y[..., :h2], y[..., h2:]
+            y = torch.cat([a * cos - c * sin, c * cos + a * sin], dim=-1)
+        refs.append(y)
+    assert len(outs) == len(refs)
+    for o, r in zip(outs, refs):
+        assert o.shape == r.shape
+        torch.testing.assert_close(o.detach().double().cpu(), r.detach(), rtol=1e-5, atol=1e-5)
+    cot = [torch.randn(r.shape, dtype=torch.float64) for r in refs]
+    sum((o * c.to(o.device, o.dtype)).sum() for o, c in zip(outs, cot)).backward()
+    sum((r * c).sum() for r, c in zip(refs, cot)).backward()
+    torch.testing.assert_close(x.grad.double().cpu(), x64.grad.cpu(), rtol=1e-5, atol=1e-5)
+    for n, p in att.named_parameters():
+        if n in params64 and params64[n].grad is not None:
+            assert p.grad is not None, f"{n}: no gradient"
+            torch.testing.assert_close(p.grad.double().cpu(), params64[n].grad.cpu(), rtol=1e-4, atol=1e-4)

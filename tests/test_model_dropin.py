@@ -136,31 +136,3 @@ def test_rotary_is_a_rotation():
     d1 = float(qs[5] @ ks[2])
     d2 = float(qs[9] @ ks[6])
     assert abs(d1 - d2) < 1e-4
-
-
-def test_stacked_projections_match_the_modules():
-    """The fused path's one-GEMM projections give each module's output, and
-    the same gradients for x and every parameter (float64, CPU)."""
-    import nsa_model
-    torch.manual_seed(0)
-    att = nsa_model.NSAAttention(96, 6, 2, block_size=16, n_selected_blocks=2, window=32,
-                                 attn_impl="fused").double()
-    with torch.no_grad():
-        att.gate.bias.normal_()
-    x = torch.randn(2, 40, 96, dtype=torch.float64, requires_grad=True)
-    mods = (att.q_proj, att.k_cmp, att.v_cmp, att.k_slc, att.v_slc, att.k_win, att.v_win, att.gate)
-    outs = att._projections(x)
-    assert len(outs) == len(mods)
-    refs = [m(x) for m in mods]
-    for o, r in zip(outs, refs):
-        assert o.shape == r.shape
-        torch.testing.assert_close(o, r, rtol=1e-12, atol=1e-12)
-    cot = [torch.randn_like(r) for r in refs]
-    g1 = torch.autograd.grad(sum((o * c).sum() for o, c in zip(outs, cot)), [x] + list(att.parameters()),
-                             allow_unused=True)
-    g2 = torch.autograd.grad(sum((r * c).sum() for r, c in zip(refs, cot)), [x] + list(att.parameters()),
-                             allow_unused=True)
-    for a, b in zip(g1, g2):
-        assert (a is None) == (b is None)
-        if a is not None:
-            torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
