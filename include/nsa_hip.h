@@ -329,6 +329,41 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
                    const float* dot, float* dk, float* dv, float* dkdv_part, size_t part_bytes, int B, int Hq,
                    int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, int dtype, void* stream);
 
+/* ---- the gated three-branch layer in two calls -------------------------------
+ * nsa_fused_fwd / nsa_fused_bwd replace nsa_fused_forward and its autograd
+ * (nsa_fused_kernel.py:560-573; with block_idx chosen here, the pooling /
+ * importance / top-n of NSAAttention._forward_fused, nsa_model.py:306-370)
+ * for callers without Python: every launch of the layer, in the order and
+ * with the arguments of the Python boundary (bit-identical results).
+ * q [B][Hq][T][D]; kc, vc [B][Hkv][T][D] (pooled = 0: mean-pooled here over
+ * spans [i d, i d + l)) or the pooled tokens [B][Hkv][(T - l) / d + 1][D]
+ * (pooled = 1: a learned compressor's output); ks, vs, kw, vw [B][Hkv][T][D];
+ * gate logits [B][Hq][T][3]; all in dtype.  block_idx [B][Hkv][T][S] int32,
+ * S = min(n_sel, T / sel_block): read when idx_given, else written (top-S
+ * of the importance, ties to the lower block).  out [B][Hq][T][D] in dtype.
+ * Requires T >= cmp_block and T >= sel_block.  Two caller buffers: ctx
+ * (nsa_fused_ctx_bytes) is written by the forward and read by the backward
+ * (pooled keys, packed q, the float32 branch outputs, their lse, the block ->
+ * query CSR); scratch (nsa_fused_scratch_bytes, for the stream's device) is
+ * transient and may be shared by both calls.  The backward takes the
+ * forward's inputs again, dO, and writes every gradient in dtype: dq, dkc /
+ * dvc (shaped like kc / vc), dks, dvs, dkw, dvw, dgate [B][Hq][T][3]; the
+ * compression and selection dK/dV use the deterministic partial merge. */
+size_t nsa_fused_ctx_bytes(int B, int Hq, int Hkv, int T, int D, int cmp_block, int cmp_stride, int sel_block,
+                           int n_sel, int window, int pooled, int dtype);
+size_t nsa_fused_scratch_bytes(int B, int Hq, int Hkv, int T, int D, int cmp_block, int cmp_stride, int sel_block,
+                               int n_sel, int window, int pooled, int dtype, void* stream);
+int nsa_fused_fwd(const void* q, const void* kc, const void* vc, const void* ks, const void* vs, const void* kw,
+                  const void* vw, const void* gate, int32_t* block_idx, int idx_given, void* out, void* ctx,
+                  size_t ctx_bytes, void* scratch, size_t scratch_bytes, int B, int Hq, int Hkv, int T, int D,
+                  int cmp_block, int cmp_stride, int sel_block, int n_sel, int window, int force_init, int n_local,
+                  int pooled, int dtype, void* stream);
+int nsa_fused_bwd(const void* dout, const void* q, const void* kc, const void* vc, const void* ks, const void* vs,
+                  const void* kw, const void* vw, const void* gate, const int32_t* block_idx, const void* ctx,
+                  size_t ctx_bytes, void* scratch, size_t scratch_bytes, void* dq, void* dkc, void* dvc, void* dks,
+                  void* dvs, void* dkw, void* dvw, void* dgate, int B, int Hq, int Hkv, int T, int D, int cmp_block,
+                  int cmp_stride, int sel_block, int n_sel, int window, int pooled, int dtype, void* stream);
+
 /* ---- block importance + top-n ----------------------------------------------
  * Replaces the importance / topk block of NSAAttention._forward_fused
  * (nsa_model.py:343-355): p_cmp = exp(q.k_cmp*scale - lse_cmp) summed over

@@ -74,6 +74,10 @@ SIGNATURES = {
     "nsa_range_dkdv_partial_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "nsa_range_dkdv": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _Z,
                             _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "nsa_fused_ctx_bytes": (_Z, [_I] * 12),
+    "nsa_fused_scratch_bytes": (_Z, [_I] * 12 + [_P]),
+    "nsa_fused_fwd": (_I, [_P] * 8 + [_P, _I, _P, _P, _Z, _P, _Z] + [_I] * 14 + [_P]),
+    "nsa_fused_bwd": (_I, [_P] * 11 + [_Z, _P, _Z] + [_P] * 8 + [_I] * 12 + [_P]),
     "nsa_importance_topn": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _P]),
     "nsa_phi_fwd": (_I, [_P] * 7 + [_I] * 7 + [_P]),

@@ -1036,6 +1036,35 @@ def fused_backward(saved, dout, geom, T, pooled=False, grads_f32=False):
             cast_f32(dkw, dtype), cast_f32(dvw, dtype), dgate)
 
 
+def fused_capi(q, kc, vc, ks, vs, kw, vw, gate, geom, dout, block_idx=None, pooled=False):
+    """The layer through the two C entry points a C caller runs,
+    ``nsa_fused_fwd`` and ``nsa_fused_bwd`` (one call each, caller-owned ctx
+    and scratch buffers) -> (out, block_idx, (dq, dkc, dvc, dks, dvs, dkw,
+    dvw, dgate))."""
+    q, kc, vc, ks, vs, kw, vw, gate, dout = (_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate, dout))
+    B, Hq, T, D = q.shape
+    Hkv = ks.shape[1]
+    dt = L.dtype_code(q)
+    dims = (B, Hq, Hkv, T, D, geom.cmp_block, geom.cmp_stride, geom.sel_block, geom.n_sel, geom.window)
+    ctx_bytes = int(_lib().nsa_fused_ctx_bytes(*dims, int(pooled), dt))
+    scr_bytes = int(_lib().nsa_fused_scratch_bytes(*dims, int(pooled), dt, _stream(q)))
+    assert ctx_bytes > 0 and scr_bytes > 0, "nsa_fused: unsupported shape (T must reach cmp_block and sel_block)"
+    ctx = torch.empty(ctx_bytes, device=q.device, dtype=torch.uint8)
+    scratch = torch.empty(scr_bytes, device=q.device, dtype=torch.uint8)
+    S = min(geom.n_sel, T // geom.sel_block)
+    given = block_idx is not None
+    idx = (block_idx.to(torch.int32).contiguous() if given
+           else torch.empty(B, Hkv, T, S, device=q.device, dtype=torch.int32))
+    out = torch.empty_like(q)
+    _call("nsa_fused_fwd", _lib().nsa_fused_fwd, *map(L.ptr, (q, kc, vc, ks, vs, kw, vw, gate)), L.ptr(idx),
+          int(given), L.ptr(out), L.ptr(ctx), ctx_bytes, L.ptr(scratch), scr_bytes, *dims, int(geom.force_init),
+          int(geom.n_local), int(pooled), dt, _stream(q))
+    grads = [torch.empty_like(t) for t in (q, kc, vc, ks, vs, kw, vw, gate)]
+    _call("nsa_fused_bwd", _lib().nsa_fused_bwd, *map(L.ptr, (dout, q, kc, vc, ks, vs, kw, vw, gate)), L.ptr(idx),
+          L.ptr(ctx), ctx_bytes, L.ptr(scratch), scr_bytes, *map(L.ptr, grads), *dims, int(pooled), dt, _stream(q))
+    return out, idx, tuple(grads)
+
+
 class NSAFusedHIP(torch.autograd.Function):
     """All three gated branches in one boundary (nsa_fused_kernel.py:560-573):
     ``fused_forward`` and ``fused_backward``.  Same outputs and gradients as
