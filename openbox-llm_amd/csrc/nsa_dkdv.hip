@@ -1492,81 +1492,81 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
 }
 
 // dK / dV of every key of the selection blocks from the work items'
-// partials: one workgroup per (block, pass), each output element summed by
-// one thread over the block's items in item order (the items of a block are
-// consecutive and ascend in query order), so the result does not depend on
-// which workgroup finished first.  A block no query selected gets zeros.
+// partials: one thread per 4 floats of a key row, each summed over the
+// block's items in item order (the items of a block are consecutive and
+// ascend in query order), so the result does not depend on which workgroup
+// finished first.  A block no query selected gets zeros.
 template <int D>
 __global__ __launch_bounds__(256) void k_sel_dkdv_reduce(const float* __restrict__ part, int64_t part_half,
                                                          const int32_t* __restrict__ first, float* __restrict__ dk,
-                                                         float* __restrict__ dv, int T_, int n_blk, int L,
-                                                         int npass) {
-  const int e = blockIdx.x / npass, pass = blockIdx.x % npass;   // e = bh * n_blk + j
-  const int bh = e / n_blk, j = e % n_blk;
-  const int k0 = j * L + kSelPass * pass;
-  const int kend = j * L + L < T_ ? j * L + L : T_;
-  const int nk = kend - k0 < kSelPass ? kend - k0 : kSelPass;   // keys of this pass
-  if (nk <= 0) return;
-  const int i0 = first[e], i1 = first[e + 1];
+                                                         float* __restrict__ dv, int T_, int n_blk, int L, int npass,
+                                                         int64_t total) {
   constexpr int V4 = D / 4;   // float4 per key row
-  for (int f = threadIdx.x; f < nk * V4; f += 256) {
-    const int kk = f / V4, c = f % V4;
-    f32x4 a = zero4(), b = zero4();
-    for (int i = i0; i < i1; ++i) {
-      const int64_t row = ((int64_t)i * npass + pass) * kSelPass + kk;
-      a += reinterpret_cast<const f32x4*>(part + row * D)[c];
-      b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
-    }
-    const int64_t orow = ((int64_t)bh * T_ + k0 + kk) * D;
-    reinterpret_cast<f32x4*>(dk + orow)[c] = a;
-    reinterpret_cast<f32x4*>(dv + orow)[c] = b;
+  const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (f >= total) return;
+  const int c = (int)(f % V4);
+  const int kk = (int)((f / V4) % kSelPass);
+  const int64_t ep = f / ((int64_t)V4 * kSelPass);   // (block, pass)
+  const int e = (int)(ep / npass), pass = (int)(ep % npass);   // e = bh * n_blk + j
+  const int bh = e / n_blk, j = e % n_blk;
+  const int key = j * L + kSelPass * pass + kk;
+  const int kend = j * L + L < T_ ? j * L + L : T_;
+  if (kSelPass * pass + kk >= L || key >= kend) return;
+  const int i0 = first[e], i1 = first[e + 1];
+  f32x4 a = zero4(), b = zero4();
+  for (int i = i0; i < i1; ++i) {
+    const int64_t row = ((int64_t)i * npass + pass) * kSelPass + kk;
+    a += reinterpret_cast<const f32x4*>(part + row * D)[c];
+    b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
   }
+  const int64_t orow = ((int64_t)bh * T_ + key) * D;
+  reinterpret_cast<f32x4*>(dk + orow)[c] = a;
+  reinterpret_cast<f32x4*>(dv + orow)[c] = b;
 }
 
 // dK / dV of the pooled keys from the compression workgroups' partial rows:
-// one workgroup per (bh, block of 32 NW keys), each output element summed by
-// one thread over the block's chunks in chunk (then sub-chunk) order -- the
-// logical workgroup numbering of k_range_dkdv32 / k_range_dkdv_split -- so the
-// result does not depend on which workgroup finished first.
+// one thread per 4 floats of a key row, summed over the key block's chunks in
+// chunk (then sub-chunk) order -- the logical workgroup numbering of
+// k_range_dkdv32 / k_range_dkdv_split -- so the result does not depend on
+// which workgroup finished first.
 template <int D, int NW>
 __global__ __launch_bounds__(256) void k_cmp_dkdv_reduce(const float* __restrict__ part, int64_t part_half,
                                                          float* __restrict__ dk, float* __restrict__ dv, int T_,
                                                          int Lk, int chunk, int cl, int cd, int nbh, int chs,
                                                          int spl) {
   constexpr int KB = 32 * NW;
-  const int nkb = (Lk + KB - 1) / KB;
-  const int bh = blockIdx.x / nkb, kblk = blockIdx.x % nkb;
+  constexpr int V4 = D / 4;   // float4 per key row
+  const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (f >= (int64_t)nbh * Lk * V4) return;
+  const int c = (int)(f % V4);
+  const int key = (int)((f / V4) % Lk);
+  const int bh = (int)(f / ((int64_t)V4 * Lk));
+  const int kblk = key / KB, kk = key % KB;
   const int nch = (T_ + chunk - 1) / chunk;
   const int big = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, 0, chs);
   const int per = cmp_blocks_range(T_, Lk, chunk, NW, cl, cd, chs, nch) * spl;
-  const int k0 = kblk * KB;
-  const int nk = Lk - k0 < KB ? Lk - k0 : KB;
-  constexpr int V4 = D / 4;   // float4 per key row
-  for (int f = threadIdx.x; f < nk * V4; f += 256) {
-    const int kk = f / V4, c = f % V4;
-    f32x4 a = zero4(), b = zero4();
-    auto add = [&](int64_t wgi) {
-      const int64_t row = wgi * KB + kk;
-      a += reinterpret_cast<const f32x4*>(part + row * D)[c];
-      b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
-    };
-    int64_t base = (int64_t)bh * big;   // chunks < chs: per bh, chunk-major
-    for (int ch = 0; ch < chs; ++ch) {
-      const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
-      if (kblk < na) add(base + kblk);
-      base += na;
-    }
-    base = (int64_t)big * nbh + (int64_t)bh * per;   // the split chunks: (chunk, sub-chunk)-major
-    for (int ch = chs; ch < nch; ++ch) {
-      const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
-      if (kblk < na)
-        for (int sub = 0; sub < spl; ++sub) add(base + (int64_t)sub * na + kblk);
-      base += (int64_t)na * spl;
-    }
-    const int64_t orow = ((int64_t)bh * Lk + k0 + kk) * D;
-    reinterpret_cast<f32x4*>(dk + orow)[c] = a;
-    reinterpret_cast<f32x4*>(dv + orow)[c] = b;
+  f32x4 a = zero4(), b = zero4();
+  auto add = [&](int64_t wgi) {
+    const int64_t row = wgi * KB + kk;
+    a += reinterpret_cast<const f32x4*>(part + row * D)[c];
+    b += reinterpret_cast<const f32x4*>(part + part_half + row * D)[c];
+  };
+  int64_t base = (int64_t)bh * big;   // chunks < chs: per bh, chunk-major
+  for (int ch = 0; ch < chs; ++ch) {
+    const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+    if (kblk < na) add(base + kblk);
+    base += na;
   }
+  base = (int64_t)big * nbh + (int64_t)bh * per;   // the split chunks: (chunk, sub-chunk)-major
+  for (int ch = chs; ch < nch; ++ch) {
+    const int na = cmp_active_blocks(T_, Lk, chunk, NW, cl, cd, ch);
+    if (kblk < na)
+      for (int sub = 0; sub < spl; ++sub) add(base + (int64_t)sub * na + kblk);
+    base += (int64_t)na * spl;
+  }
+  const int64_t orow = ((int64_t)bh * Lk + key) * D;
+  reinterpret_cast<f32x4*>(dk + orow)[c] = a;
+  reinterpret_cast<f32x4*>(dv + orow)[c] = b;
 }
 
 }  // namespace nsa
@@ -1696,8 +1696,8 @@ int nsa_range_dkdv(int mode, const void* q, const void* k, const void* v, const 
           part_half, Hq, Hkv, T, Lk, kCmpChunk, window, cmp_block, cmp_stride, nbh, chs, spl, sl2, scale);
     if (partial) {
       if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
-      const int nkb = (Lk + 32 * NW - 1) / (32 * NW);
-      k_cmp_dkdv_reduce<DD, NW><<<(unsigned)((int64_t)nkb * nbh), 256, 0, s>>>(
+      const int64_t total = (int64_t)nbh * Lk * (DD / 4);
+      k_cmp_dkdv_reduce<DD, NW><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(
           part, part_half, dk, dv, T, Lk, kCmpChunk, cmp_block, cmp_stride, nbh, chs, spl);
     }
   });
@@ -1777,8 +1777,9 @@ int nsa_sel_dkdv(const void* q, const void* k, const void* v, const void* kt, co
     if (dkdv_part != nullptr) {
       if (hipGetLastError() != hipSuccess) return NSA_ERR_LAUNCH;
       const int npass = sel_passes(block_size);
-      k_sel_dkdv_reduce<DD><<<(unsigned)((int64_t)nb * npass), 256, 0, s>>>(dkdv_part, part_half, first, dk, dv,
-                                                                               T, n_blk, block_size, npass);
+      const int64_t total = (int64_t)nb * npass * kSelPass * (DD / 4);
+      k_sel_dkdv_reduce<DD><<<(unsigned)((total + 255) / 256), 256, 0, s>>>(dkdv_part, part_half, first, dk, dv, T,
+                                                                              n_blk, block_size, npass, total);
     }
   });
   return nsa_launch_status();
