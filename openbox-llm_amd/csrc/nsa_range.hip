@@ -300,8 +300,9 @@ constexpr float kRescale = 8.0f;   // log2 growth of a row maximum that forces a
 // (and the backward's row dot dO . o, whose error dS = P (dP - dot) passes on
 // whole to dQ and dK) carries no P rounding; the window forward uses it (at
 // config 4 its dQ error fell from 1.8e-2 to 1.2e-2 for 0.06 ms a step), the
-// compression forward does not (0.29 ms for no measurable gain).  MASK = false: every key
-// of the tile is visible to every valid row of the wave (no per-element test).
+// compression forward does not (0.29 ms for no measurable gain).  mask =
+// false: every key of the tile is visible to every valid row of the wave (no
+// per-element test).
 // The row maximum m is only moved when the tile's maximum exceeds it by more
 // than kRescale (wave-uniform branch); p = exp2(s - m) <= 2^kRescale keeps the
 // sum and the bf16 P operand in range, and the final 1/l normalises exactly.
