@@ -398,6 +398,20 @@ int nsa_phi_dpre(const void* dout, const void* w2t, const float* pre, float* dpr
  * [BH][L][D] in dx_dtype. */
 int nsa_phi_fold(const void* dspan, int dspan_dtype, void* dx, int BH, int L, int D, int l, int d, int dx_dtype,
                  void* stream);
+/* Parameter gradients of phi (the reference trains its pooler's weights by
+ * autograd, nsa_model.py:100-123), over the n pooled tokens of every
+ * sequence: dW1 = sum dpre^T vec(span + P) [H][l D], dW2 = sum dout^T
+ * silu(pre) [D][H], db1 / db2 the column sums of dpre / dout, dpos = db1^T W1
+ * as [l][D]; all float.  x [BH][L][D] and dout [BH][n][D] in dtype, dpre / pre
+ * float [BH][n][H], pos float [l][D], w1 float [H][l D].  The spans are read
+ * in place.  The tokens are summed in ranges fixed by the shape, then the
+ * ranges in order: the same bits on every run.  workspace: at least
+ * nsa_phi_wgrad_workspace(BH, n, D, H, l) bytes (0: unsupported shape).
+ * D in {64, 128}, H in {32, 64, 128}. */
+size_t nsa_phi_wgrad_workspace(int BH, int n, int D, int H, int l);
+int nsa_phi_wgrad(const void* x, const void* dout, const float* dpre, const float* pre, const float* pos,
+                  const float* w1, float* dw1, float* db1, float* dw2, float* db2, float* dpos, void* workspace,
+                  size_t workspace_bytes, int BH, int L, int D, int H, int l, int d, int dtype, void* stream);
 
 /* ---- decode: one new query per sequence against its KV caches ---------------
  * No reference counterpart as an entry point: the reference runs whole

@@ -83,6 +83,8 @@ SIGNATURES = {
     "nsa_phi_fwd": (_I, [_P] * 7 + [_I] * 7 + [_P]),
     "nsa_phi_dpre": (_I, [_P] * 4 + [_I] * 5 + [_P]),
     "nsa_phi_fold": (_I, [_P, _I, _P] + [_I] * 6 + [_P]),
+    "nsa_phi_wgrad_workspace": (_Z, [_I] * 5),
+    "nsa_phi_wgrad": (_I, [_P] * 12 + [_Z] + [_I] * 7 + [_P]),
     "nsa_decode_workspace": (_Z, [_I] * 11),
     "nsa_decode_fwd": (_I, [_P] * 15 + [_Z] + [_I] * 14 + [_P]),
     "nsa_decode_append": (_I, [_P] * 16 + [_I] * 8 + [_P]),

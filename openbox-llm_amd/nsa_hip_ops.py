@@ -1108,10 +1108,10 @@ def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, blo
 
 class PhiCompressHIP(torch.autograd.Function):
     """``out[b,h,i] = W2 silu(W1 vec(x[b,h,i d : i d + l] + P) + b1) + b2``
-    for ``x [B,H,T,D]``: the forward and the hidden-layer backward on HIP
-    kernels that read the overlapping spans in place; the weight gradients are
-    plain float32 GEMMs.  Parameters may be float32 (autocast): the kernels
-    take W1 / W2 in x's dtype, biases in float32."""
+    for ``x [B,H,T,D]``: the forward, the hidden-layer backward and the
+    parameter gradients (float32 sums in a fixed order) on HIP kernels that
+    read the overlapping spans in place.  Parameters may be float32
+    (autocast): the kernels take W1 / W2 in x's dtype, biases in float32."""
 
     @staticmethod
     def forward(ctx, x, pos, w1, b1, w2, b2, l, d):
@@ -1152,51 +1152,26 @@ class PhiCompressHIP(torch.autograd.Function):
         dpre = torch.empty(M, Hd, device=x.device, dtype=torch.float32)
         _call("nsa_phi_dpre", _lib().nsa_phi_dpre, L.ptr(dout), L.ptr(w2t), L.ptr(pre), L.ptr(dpre), BH, n, D, Hd,
               L.dtype_code(x), _stream(x))
-        # weight gradients in float32 (a bf16 result would round each entry of
-        # a sum over every span); the span gradient, which the fold adds at
-        # most ceil(l / d) at a time in float, runs in x's dtype
+        # parameter gradients summed in float32 (a bf16 result would round
+        # each entry of a sum over every span), in a fixed order; the span
+        # gradient, which the fold adds at most ceil(l / d) at a time in
+        # float, runs in x's dtype
+        f32 = dict(device=x.device, dtype=torch.float32)
+        dw1, db1 = torch.empty(Hd, l * D, **f32), torch.empty(Hd, **f32)
+        dw2, db2, dpos = torch.empty(D, Hd, **f32), torch.empty(D, **f32), torch.empty(l, D, **f32)
+        ws_bytes = int(_lib().nsa_phi_wgrad_workspace(BH, n, D, Hd, l))
+        assert ws_bytes > 0, "phi: unsupported shape for the weight gradients"
+        ws = torch.empty(ws_bytes, device=x.device, dtype=torch.uint8)
+        pos32, w132 = _contig(pos.float()), _contig(w1.float())
+        _call("nsa_phi_wgrad", _lib().nsa_phi_wgrad, L.ptr(x), L.ptr(dout), L.ptr(dpre), L.ptr(pre), L.ptr(pos32),
+              L.ptr(w132), L.ptr(dw1), L.ptr(db1), L.ptr(dw2), L.ptr(db2), L.ptr(dpos), L.ptr(ws), ws_bytes, BH, T,
+              D, Hd, l, d, L.dtype_code(x), _stream(x))
         with torch.autocast("cuda", enabled=False):
-            d2 = dout.reshape(M, D).float()
-            dw2 = _sum_of_products(d2, torch.nn.functional.silu(pre), parts=64)
-            db2 = d2.sum(0)
-            db1 = dpre.sum(0)
-            dw1 = _phi_dw1(x, dpre, BH, n, l, d) + db1[:, None] * pos.float().reshape(1, -1)
             dspan = dpre.to(x.dtype) @ w1.to(x.dtype)
-            dpos = (db1 @ w1.float()).view(l, D)   # sum over the spans of dspan, in float
         _call("nsa_phi_fold", _lib().nsa_phi_fold, L.ptr(dspan), L.dtype_code(dspan), L.ptr(dx), BH, T, D, l, d,
               L.dtype_code(x), _stream(x))
         return (dx, dpos.to(pos.dtype), dw1.to(w1.dtype), db1.to(b1.dtype), dw2.to(w2.dtype), db2.to(b2.dtype),
                 None, None)
-
-
-def _sum_of_products(a, b, parts=16):
-    """a^T b for tall a [M, p], b [M, q] (float32): the M rows in ``parts``
-    batched products, summed, so that a small output still spreads over the
-    GPU."""
-    M = a.shape[0]
-    mc = -(-M // parts)
-    if mc * parts != M:
-        a = torch.nn.functional.pad(a, (0, 0, 0, mc * parts - M))
-        b = torch.nn.functional.pad(b, (0, 0, 0, mc * parts - M))
-    a3 = a.view(parts, mc, a.shape[1]).transpose(1, 2).contiguous()
-    return torch.bmm(a3, b.view(parts, mc, b.shape[1])).sum(0)
-
-
-def _phi_dw1(x, dpre, BH, n, l, d):
-    """dW1 = sum over spans of dpre_i^T vec(span_i), float32 ([H, l D]).  When
-    d divides l, span i is the l / d consecutive d-row chunks i .. i + l/d - 1
-    of the sequence, so the product splits into l / d products over shifted
-    views of the sequence's chunk rows (no unfolded copy of the spans)."""
-    T, D = x.shape[2], x.shape[3]
-    H = dpre.shape[1]
-    if l % d == 0:
-        m = l // d
-        rows = (n - 1 + m) * d                   # the sequence rows the spans cover
-        X = x.reshape(BH, T, D)[:, :rows].to(dpre.dtype).reshape(BH, n - 1 + m, d * D)
-        P = dpre.view(BH, n, H).transpose(1, 2).contiguous()   # [BH, H, n]
-        return torch.cat([torch.bmm(P, X[:, j:j + n]).sum(0) for j in range(m)], dim=1)
-    spans = x.as_strided((BH, n, l * D), (T * D, d * D, 1)).reshape(BH * n, l * D).to(dpre.dtype)
-    return dpre.t() @ spans
 
 
 def phi_compress(x, pos, w1, b1, w2, b2, l, d):

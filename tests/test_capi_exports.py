@@ -42,6 +42,25 @@ def test_library_exports_every_declared_symbol():
     assert sorted(mod.SIGNATURES) == _declared()
 
 
+def _declared_arity():
+    """Parameter count of every declaration in the header."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^\s*(?:int|size_t)\s+(nsa_\w+)\s*\(([^)]*)\)", text, flags=re.M):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_ctypes_signatures_match_the_header_arity():
+    """A wrong argument count in the ctypes table would only surface as a
+    TypeError on the first call on a GPU box."""
+    import _nsa_lib
+    arity = _declared_arity()
+    for name, (_, args) in _nsa_lib.SIGNATURES.items():
+        assert len(args) == arity[name], f"{name}: ctypes has {len(args)} arguments, the header {arity[name]}"
+
+
 def test_size_queries():
     _, lib = _lib()
     assert lib.nsa_version() >= 100
@@ -56,6 +75,13 @@ def test_size_queries():
     # before any device query)
     assert lib.nsa_range_dkdv_partial_bytes(0, 1, 4, 32768, 32768, 128, 1, 1, None) == 0
     assert lib.nsa_range_dkdv_partial_bytes(1, 1, 4, 0, 2047, 128, 32, 16, None) == 0
+    # phi's parameter gradients: float partials of dW1, dW2 and the biases per
+    # token range; unsupported shapes answer 0
+    one = 4 * (128 * 32 * 128 + 128 * 128 + 128 + 128)
+    ws = lib.nsa_phi_wgrad_workspace(4, 2047, 128, 128, 32)
+    assert ws >= one and ws % one == 0
+    assert lib.nsa_phi_wgrad_workspace(4, 2047, 96, 128, 32) == 0
+    assert lib.nsa_phi_wgrad_workspace(4, 0, 128, 128, 32) == 0
 
 
 def test_bad_shapes_are_rejected_without_launching():

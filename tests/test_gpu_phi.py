@@ -27,6 +27,8 @@ CASES = [
     (BF, 2, 1, 500, 128, 64, 8, 4),
     (F32, 1, 2, 300, 128, 128, 32, 16),
     (BF, 1, 2, 401, 64, 128, 16, 20),
+    (BF, 1, 2, 333, 64, 32, 5, 4),      # l D = 320: a partial 128-column group
+    (F32, 2, 1, 260, 64, 64, 3, 2),     # l D = 192
 ]
 
 
@@ -60,6 +62,28 @@ def test_phi_matches_oracle(case):
     for name, got, r in zip(["dx", "dpos", "dW1", "db1", "dW2", "db2"], leaves, ref_leaves):
         assert got.grad.dtype == got.dtype
         assert_strict(got.grad.float().cpu(), r.grad, dtype, name)
+
+
+def test_phi_parameter_gradients_are_run_to_run_identical():
+    """The parameter gradients are sums over every pooled token in a fixed
+    order (token ranges fixed by the shape, then the ranges in order): two
+    backward passes give the same bits."""
+    import nsa_hip_ops as ops
+    dev = require_gpu()
+    B, H, T, D, Hd, l, d = 1, 4, 8192, 128, 128, 32, 16
+    x = randn((B, H, T, D), 1, BF).to(dev)
+    params = [(0.3 * randn((l, D), 2, F32)).to(dev), (randn((Hd, l * D), 3, F32) / 64).to(dev),
+              (0.1 * randn((Hd,), 4, F32)).to(dev), (randn((D, Hd), 5, F32) / 11).to(dev),
+              (0.1 * randn((D,), 6, F32)).to(dev)]
+    dout = randn((B, H, O.n_cmp_tokens(T, l, d), D), 7, BF).to(dev)
+    runs = []
+    for _ in range(2):
+        leaves = [t.clone().requires_grad_() for t in (x, *params)]
+        ops.phi_compress(*leaves, l, d).backward(dout)
+        torch.cuda.synchronize()
+        runs.append([t.grad.clone() for t in leaves])
+    for name, a, b in zip(["dx", "dpos", "dW1", "db1", "dW2", "db2"], *runs):
+        assert torch.equal(a, b), f"{name} differs between two identical backward passes"
 
 
 def test_phi_model_fused_matches_ref():
