@@ -81,13 +81,13 @@ WORKLOADS = {
 # counters read for a plain 1 GiB device copy (x2.0 and x1.0); the commands
 # and counter values are kept under profiles/.  Keyed by (workload, kernel).
 MEASURED_TRAFFIC = {   # profiles/nsa_fused_c3_pmc_traffic.md: bytes read + bytes written per launch
-    ("c3", "dkdv[sel]"): 1.739e10 + 9.315e9,
-    ("c3", "fwd[sel]"): 8.590e9 + 8.729e9,
-    ("c3", "dq[cmp+win]"): 1.173e10 + 5.704e8,
-    ("c3", "fwd[win]"): 1.125e10 + 2.714e9,
-    ("c3", "dkdv[win]"): 9.893e9 + 1.342e8,
-    ("c3", "dkdv[cmp]"): 2.840e9 + 6.630e8,
-    ("c3", "fwd[cmp]"): 6.907e8 + 2.275e9,
+    ("c3", "dkdv[sel]"): 1.737e10 + 8.677e9,
+    ("c3", "fwd[sel]"): 8.588e9 + 8.729e9,
+    ("c3", "dq[cmp+win]"): 1.172e10 + 5.369e8,
+    ("c3", "fwd[win]"): 1.118e10 + 2.714e9,
+    ("c3", "dkdv[win]"): 1.005e10 + 1.384e8,
+    ("c3", "dkdv[cmp]"): 2.733e9 + 1.891e8,
+    ("c3", "fwd[cmp]"): 6.763e8 + 2.226e9,
     ("c3", "nsa_bwd_prep"): 3.834e9 + 8.037e8,
     ("c3", "nsa_importance_topn"): 6.072e8 + 8.389e6,
     ("c3", "nsa_pool_fwd"): 5.873e7 + 2.096e6,
@@ -833,6 +833,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip the forced-block variant and the c1 timings")
     ap.add_argument("--spans", action="store_true", help="print the per-call HIP-event breakdown to stderr")
+    ap.add_argument("--no-branches", action="store_true",
+                    help="skip the per-branch pass (its unfused launches would mix into a profile's per-kernel "
+                         "statistics)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="only run a plain device copy of this many MiB (3 times): the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -905,7 +908,8 @@ def main():
         "selection_pairs": r["pairs"],
         "roofline": roofline,
         "fwd_bwd_split": r["split"],
-        "branches": (measure_branches(w, r["geom"], r["ins"], r["do"], kv) if w["kind"] == "fused" else None),
+        "branches": (measure_branches(w, r["geom"], r["ins"], r["do"], kv)
+                     if w["kind"] == "fused" and not args.no_branches else None),
         "fused_launches_by_branch": branch_fractions(iso_spans, flops_of, PEAK_BF16_TFLOPS),
         "per_kernel": per_kernel_table(iso_spans, flops_of, PEAK_BF16_TFLOPS, name),
         "memory": r["mem"],
