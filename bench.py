@@ -62,7 +62,8 @@ WORKLOADS = {
                vocab=32000, d_model=768, n_layers=12, ffn_hidden=2048,
                desc="BASELINE config 4: 12-layer d768 decoder (12q/2kv heads, hd64, SwiGLU 2048, RMSNorm, RoPE 1e4, "
                     "vocab 32000), NSA l32/d16 l'64 top-16 w512 in every layer, bf16 autocast AdamW step, 8x4096 "
-                    "tokens; dense arm: the same model with causal SDPA attention"),
+                    "tokens; dense arms: the same model with causal SDPA attention, and with the reference's "
+                    "materialised causal score matrix"),
     "dec": dict(kind="decode", B=32, T=32768, Hq=64, Hkv=4, D=128, geom=(32, 16, 64, 16, 512, False, 0),
                 desc="decode step (nsa_decode_fwd): 32 sequences, one new query each at position 32767 of "
                      "32K-token caches, config-3 heads (Hq64 Hkv4 D128) and geometry (l32/d16 l'64 top-16 w512), bf16"),
@@ -497,10 +498,13 @@ def time_gpu_c1(reps=20):
     return res
 
 
-def run_model_bench(args, w):
+def run_model_bench(args, w, arms=("nsa", "dense", "dense_ref")):
     """Config 4: one bf16-autocast AdamW training step of the decoder, NSA
-    (fused HIP attention) against the same model with dense causal SDPA
-    attention; tokens/s and peak device memory per arm."""
+    (fused HIP attention) against the same model with dense causal attention
+    -- through SDPA's flash kernels ("dense"), and as the reference's own
+    control arm computes it, the full causal score matrix materialised
+    (FullAttention, nsa_model.py:377-419: "dense_ref", the arm of the
+    reference's memory claim); tokens/s and peak device memory per arm."""
     import nsa_model
     dev = torch.device("cuda:0")
     B, T = w["B"], w["T"]
@@ -509,14 +513,15 @@ def run_model_bench(args, w):
     x = torch.randint(0, w["vocab"], (B, T), generator=g, device=dev)
     y = torch.randint(0, w["vocab"], (B, T), generator=g, device=dev)
     out = {}
-    for arm in ("nsa", "dense"):
+    for arm in arms:
         torch.cuda.empty_cache()
         base = torch.cuda.memory_allocated()   # other workloads' tensors still held by the caller
         torch.manual_seed(0)
         m = nsa_model.NSATransformer(
             vocab_size=w["vocab"], d_model=w["d_model"], n_layers=w["n_layers"], n_q_heads=w["Hq"],
             n_kv_heads=w["Hkv"], max_seq_len=T, ffn_hidden=w["ffn_hidden"], norm="rms", ffn="swiglu", pos="rope",
-            tie_embeddings=False, attn_type="nsa" if arm == "nsa" else "full", attn_impl="fused", dense_impl="sdpa",
+            tie_embeddings=False, attn_type="nsa" if arm == "nsa" else "full", attn_impl="fused",
+            dense_impl="ref" if arm == "dense_ref" else "sdpa",
             block_size=l, cmp_stride=d, sel_block=ls, n_selected_blocks=n, window=win, force_init=fi,
             n_local=nl).to(dev)
         opt = torch.optim.AdamW(m.parameters(), lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
@@ -533,11 +538,12 @@ def run_model_bench(args, w):
             losses.append(float(step()))
         torch.cuda.synchronize()
         torch.cuda.reset_peak_memory_stats()
+        steps = min(args.steps, 3) if arm == "dense_ref" else args.steps   # ~0.3 s a step
         t0 = time.perf_counter()
-        for _ in range(args.steps):
+        for _ in range(steps):
             loss = step()
         torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        ms = (time.perf_counter() - t0) * 1e3 / steps
         losses.append(float(loss))
         out[arm] = {"ms_per_step": round(ms, 2), "tokens_per_s": round(B * T / (ms / 1e3), 1),
                     "peak_mem_gib": round((torch.cuda.max_memory_allocated() - base) / 2**30, 2),
@@ -686,6 +692,8 @@ def run_other_configs(args):
     c4 = run_model_bench(small, WORKLOADS["c4"])
     c4["nsa_vs_dense_time"] = round(c4["dense"]["ms_per_step"] / c4["nsa"]["ms_per_step"], 4)
     c4["nsa_vs_dense_memory"] = round(c4["nsa"]["peak_mem_gib"] / c4["dense"]["peak_mem_gib"], 4)
+    c4["nsa_vs_dense_ref_time"] = round(c4["dense_ref"]["ms_per_step"] / c4["nsa"]["ms_per_step"], 4)
+    c4["nsa_vs_dense_ref_memory"] = round(c4["nsa"]["peak_mem_gib"] / c4["dense_ref"]["peak_mem_gib"], 4)
     c4["desc"] = WORKLOADS["c4"]["desc"]
     out["c4"] = c4
     torch.cuda.empty_cache()

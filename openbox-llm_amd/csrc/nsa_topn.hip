@@ -1,41 +1,50 @@
 // Block importance + top-n selection (the block choice of NSAAttention,
 // nsa_model.py:245-258 and :343-355).
 //
-// A workgroup of 4 waves takes 8 consecutive queries of one (b, hkv); a wave
-// holds the Q fragments of its 2 queries x 16 heads (a 32-row MFMA operand)
-// and walks the pooled tokens the group's last query sees, 32 per tile, the
-// tiles shared through LDS (direct global -> LDS loads, kImpStages deep):
+// A workgroup of 4 waves takes 4 QPW consecutive queries of one (b, hkv); a
+// wave holds the Q fragments of its QPW queries x P2 heads (P2 = 32 / QPW:
+// the group padded to 16, 8 or 4 rows, a 32-row MFMA operand) and walks the
+// pooled tokens the group's last query sees, 32 per tile, the tiles shared
+// through LDS (direct global -> LDS loads, kImpStages deep).  Small groups
+// (G <= 8, G <= 4) pack 4 or 8 queries into one tile instead of padding
+// their heads to 16 rows:
 //
 //  1. S = Q K_cmp^T on 32x32 MFMAs (rows on M, tokens on N); p_cmp =
 //     exp2(S * scale*log2e - lse_cmp*log2e) with lse_cmp from the compression
 //     forward, tokens the query cannot see set to 0.
-//  2. imp_cmp[q][i] = sum over the group's heads of p_cmp: each lane holds 8
-//     heads of each of its token's 2 rows, summed in order, then the two
-//     lane halves are added (head chunks of groups wider than 16 follow in
-//     chunk order), so every sum has a fixed order.
+//  2. imp_cmp[q][i] = sum over the group's heads of p_cmp: a lane half holds
+//     runs of consecutive rows of one query (8 heads of each of its 2 queries
+//     when QPW = 2, whose two halves are then added; all 8 or 4 heads of its
+//     own 2 or 4 queries when QPW = 4 or 8), summed in order (head chunks of
+//     groups wider than 16 follow in chunk order), so every sum has a fixed
+//     order.
 //  3. every F tiles (and after the last) the tiles' tokens fold into the
 //     selection blocks: imp_slc[j] += imp_cmp[i] * |span_i & block_j| / d,
-//     tokens ascending, one lane per block for both queries; F is the most
-//     tiles whose blocks fit the wave's lanes.  The block sums live in
-//     registers: lane L holds blocks L + 64 k (k < KPL) of both queries, the
+//     tokens ascending, one lane per block for every query of the wave; F is
+//     the most tiles whose blocks fit the wave's lanes.  The block sums live
+//     in registers: lane L holds blocks L + 64 k (k < KPL) of each query, the
 //     same layout the top-S phase reads (no LDS array per query, so long
-//     sequences with thousands of blocks keep several workgroups per CU).
+//     sequences with thousands of blocks keep several workgroups per CU).  A
+//     fold's 64 consecutive blocks fall in two register slots k, the same
+//     for the whole wave, so only those two are updated.
 //  4. per query: score = +inf for forced blocks, -FLT_MAX for blocks not yet
 //     complete, else imp_slc; the order keys of the scores, KPL per lane in
 //     registers (block lane + 64 k), give S picks, each the highest score by
 //     a wave max and, among equal scores, the lowest block index by a wave
-//     min; a picked key is zeroed.  The two queries' picks interleave (two
-//     independent dependency chains) when their keys fit the registers.
+//     min.  With 8 or more keys per lane each lane first orders its 4 best
+//     (ties by block index) and a pick pops the winning lane's head, the list
+//     refilled from the lane's remaining keys when it runs empty; with fewer,
+//     every pick rescans the lane's keys and zeroes the picked one.  Two
+//     queries' picks interleave (two independent dependency chains) when
+//     their keys fit the registers.
 #include "nsa_launch.h"
 #include "nsa_tile32.h"
 
 namespace nsa {
 
-constexpr int kImpQPW = 2;                // queries per wave (2 x 16 heads = 32 rows)
 constexpr int kImpFold = 8;               // tokens read per step of a block's fold
 constexpr int kImpFoldTiles = 8;          // most tiles per fold
 constexpr int kImpStages = 3;             // K tiles in flight + 1
-constexpr int kImpQPB = 4 * kImpQPW;      // queries per workgroup
 
 // last pooled token visible to t (-1: none)
 __device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) {
@@ -47,21 +56,36 @@ __device__ __forceinline__ int imp_last_token(int t, int n_cmp, int cl, int cd) 
 // x / 2^sh when sh >= 0 (x >= 0), else x / d
 __device__ __forceinline__ int div_sh(int x, int d, int sh) { return sh >= 0 ? x >> sh : x / d; }
 
-// LDS: K tiles [kImpStages][32][D] and per-wave token scratch [4][32 F][2]
-// (both queries' values of a token side by side).  cd_sh / ls_sh: log2 of
-// cd / ls when they are powers of two, else -1 (the block fold then
-// divides); rcd = 1 / cd scales the overlap weights; fold_tiles: F above
-// (1 .. kImpFoldTiles).  KPL: blocks per lane (n_slc <= 64 * KPL).
-// a[k] += v for a per-lane k, as KPL masked adds: every slot is touched
-// with a static index, so the array stays in registers (adding 0 leaves the
-// non-negative sums unchanged)
-template <int KPL>
-__device__ __forceinline__ void reg_add(float (&a)[KPL], int k, float v) {
-#pragma unroll
-  for (int i = 0; i < KPL; ++i) a[i] += k == i ? v : 0.0f;
+// Query of register run k (RUN consecutive registers) in lane half h: rows
+// acc_elem(h, r) = 16 (r >> 3) + 8 h + (r & 7), query = row / P2.
+template <int QPW>
+__device__ __forceinline__ int imp_run_query(int k, int h) {
+  if constexpr (QPW == 2) return k;                                // heads 8h..8h+7 of query k
+  else if constexpr (QPW == 4) return 2 * k + h;                   // all 8 rows of query 2k+h
+  else return 4 * (k >> 1) + 2 * h + (k & 1);                      // all 4 rows of query 4(k>>1)+2h+(k&1)
 }
 
-template <typename T, int D, int KPL>
+// Insert key x of slot k into a lane's list of its 4 best keys (m[0] >= m[1]
+// >= ...; 0 = empty), when `take`.  Slots arrive in ascending order and only
+// a strictly greater key moves ahead, so equal keys stay in slot order.
+__device__ __forceinline__ void topn_list_insert(uint32_t (&m)[4], int (&c)[4], uint32_t x, int k, bool take) {
+  const bool b0 = take && x > m[0], b1 = take && x > m[1], b2 = take && x > m[2], b3 = take && x > m[3];
+  m[3] = b2 ? m[2] : (b3 ? x : m[3]);
+  c[3] = b2 ? c[2] : (b3 ? k : c[3]);
+  m[2] = b1 ? m[1] : (b2 ? x : m[2]);
+  c[2] = b1 ? c[1] : (b2 ? k : c[2]);
+  m[1] = b0 ? m[0] : (b1 ? x : m[1]);
+  c[1] = b0 ? c[0] : (b1 ? k : c[1]);
+  m[0] = b0 ? x : m[0];
+  c[0] = b0 ? k : c[0];
+}
+
+// LDS: K tiles [kImpStages][32][D] and per-wave token scratch [4][32 F][QPW]
+// (the wave's queries' values of a token side by side).  cd_sh / ls_sh: log2
+// of cd / ls when they are powers of two, else -1 (the block fold then
+// divides); rcd = 1 / cd scales the overlap weights; fold_tiles: F above
+// (1 .. kImpFoldTiles).  KPL: blocks per lane (n_slc <= 64 * KPL).
+template <typename T, int D, int KPL, int QPW>
 __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
                                                   const float* __restrict__ lse, int32_t* __restrict__ out_idx,
                                                   float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
@@ -69,28 +93,37 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
                                                   int n_local, int nqb, int cd_sh, int ls_sh, int fold_tiles, float rcd, float sl2) {
   using C = Tile32<T, D>;
   constexpr int NST = kImpStages;
+  constexpr int P2 = 32 / QPW;              // rows per query
+  constexpr int RUN = QPW == 8 ? 4 : 8;     // consecutive registers of one query in a lane half
+  constexpr int NRUN = 16 / RUN;            // query partials per lane
+  constexpr int QPB = 4 * QPW;              // queries per workgroup
+  static_assert(QPW == 2 || QPW == 4 || QPW == 8, "2, 4 or 8 queries per wave");
   extern __shared__ __align__(16) char smem[];
   T* sK = reinterpret_cast<T*>(smem);                                   // [NST][ROW_ELEMS]
-  float2* stok = reinterpret_cast<float2*>(sK + NST * C::ROW_ELEMS);    // [4][32 F]
+  float* stok = reinterpret_cast<float*>(sK + NST * C::ROW_ELEMS);      // [4][32 F][QPW]
   const int tid = threadIdx.x, lane = tid & 63, h = lane >> 5, n = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   // long rows first: workgroups go out round-robin, the latest queries first
   const int qb = nqb - 1 - (int)(blockIdx.x % nqb);
   const int bh = (int)(blockIdx.x / nqb);
   const int b = bh / Hkv, hkv = bh % Hkv;
-  const int G = Hq / Hkv, NHC = (G + 15) / 16;
-  const int t0 = qb * kImpQPB;
-  const int tq0 = t0 + kImpQPW * w;   // this wave's queries tq0, tq0 + 1
-  const int tlast = t0 + kImpQPB - 1 < T_ - 1 ? t0 + kImpQPB - 1 : T_ - 1;
+  const int G = Hq / Hkv, NHC = (G + 15) / 16;   // NHC > 1 only with QPW == 2
+  const int t0 = qb * QPB;
+  const int tq0 = t0 + QPW * w;   // this wave's queries tq0 .. tq0 + QPW - 1
+  const int tlast = t0 + QPB - 1 < T_ - 1 ? t0 + QPB - 1 : T_ - 1;
   const int hi_wg = imp_last_token(tlast, n_cmp, cl, cd);
   const int ntile = hi_wg < 0 ? 0 : hi_wg / 32 + 1;
-  int hi_q[kImpQPW];
+  int hi_q[QPW];
 #pragma unroll
-  for (int i = 0; i < kImpQPW; ++i) hi_q[i] = tq0 + i < T_ ? imp_last_token(tq0 + i, n_cmp, cl, cd) : -1;
+  for (int i = 0; i < QPW; ++i) hi_q[i] = tq0 + i < T_ ? imp_last_token(tq0 + i, n_cmp, cl, cd) : -1;
+  // the last visible token of each register run's query (runs of lane half h)
+  int hi_run[NRUN];
+#pragma unroll
+  for (int k = 0; k < NRUN; ++k) hi_run[k] = h ? hi_q[imp_run_query<QPW>(k, 1)] : hi_q[imp_run_query<QPW>(k, 0)];
 
-  float bsum[kImpQPW][KPL];   // block sums of blocks lane + 64 k, both queries
+  float bsum[QPW][KPL];   // block sums of blocks lane + 64 k, every query of the wave
 #pragma unroll
-  for (int i = 0; i < kImpQPW; ++i)
+  for (int i = 0; i < QPW; ++i)
 #pragma unroll
     for (int k = 0; k < KPL; ++k) bsum[i][k] = 0.0f;
   const T* kbase = kc + (int64_t)bh * n_cmp * D;
@@ -98,15 +131,15 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
   kdma.init(tid);
   auto load_tile = [&](int kt) { kdma.request(sK + (kt % NST) * C::ROW_ELEMS, kbase, kt * 32, n_cmp, tid); };
 
-  // this lane's 16 rows: e = acc_elem(h, r) -> query e >> 4, head e & 15
-  float2* my_tok = stok + w * 32 * kImpFoldTiles;
+  // this lane's 16 rows: e = acc_elem(h, r) -> query e / P2, head e % P2
+  float* my_tok = stok + w * 32 * kImpFoldTiles * QPW;
   Frag<T> qf[C::KS];
   float lse2[16];
   auto load_rows = [&](int hc) {
     const int row = perm32(n);            // A operand row this lane supplies
-    const int hd = hc * 16 + (row & 15);
+    const int hd = hc * 16 + row % P2;
     const int hs = hd < G ? hd : G - 1;
-    int tq = tq0 + (row >> 4);
+    int tq = tq0 + row / P2;
     tq = tq < T_ ? tq : T_ - 1;
     const T* qrow = q + (((int64_t)b * Hq + hkv * G + hs) * T_ + tq) * D;
 #pragma unroll
@@ -114,11 +147,11 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int e = acc_elem(h, r);
-      const int he = hc * 16 + (e & 15);
-      int te = tq0 + (e >> 4);
+      const int he = hc * 16 + e % P2;
+      int te = tq0 + e / P2;
       const bool ok = he < G && te < T_;
       te = te < T_ ? te : T_ - 1;
-      // absent rows (heads past the group, queries past T) get p = 0
+      // absent rows (padding heads, queries past T) get p = 0
       lse2[r] = ok ? lse[((int64_t)b * Hq + hkv * G + he) * T_ + te] * kLog2e : __builtin_inff();
     }
     // complete these loads here: the walk's own loads are asm the compiler
@@ -133,6 +166,7 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
   key_pipeline<NST, dma_uniform_loads<256, C::ROW_CHUNKS>()>(ntile, load_tile, [&](int kt) {
     const T* tile = sK + (kt % NST) * C::ROW_ELEMS;
     const int tok = kt * 32 + n;
+    float* slot = my_tok + ((kt % fold_tiles) * 32 + n) * QPW;
     for (int hc = 0; hc < NHC; ++hc) {
       if (NHC > 1) load_rows(hc);   // groups wider than 16 heads: one chunk at a time
       f32x16 sacc = zero16();
@@ -142,33 +176,41 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
         lds_nrow_frag<T, D>(kf, tile, n, h, s);
         mma32(sacc, qf[s], kf);
       }
-      float part[kImpQPW];
+      float part[NRUN];
 #pragma unroll
-      for (int i = 0; i < kImpQPW; ++i) {
-        float acc = fast_exp2(sacc[8 * i] * sl2 - lse2[8 * i]);
+      for (int k = 0; k < NRUN; ++k) {
+        float acc = fast_exp2(sacc[RUN * k] * sl2 - lse2[RUN * k]);
 #pragma unroll
-        for (int j = 1; j < 8; ++j) acc += fast_exp2(sacc[8 * i + j] * sl2 - lse2[8 * i + j]);
-        part[i] = tok <= hi_q[i] ? acc : 0.0f;   // tokens the query cannot see
+        for (int j = 1; j < RUN; ++j) acc += fast_exp2(sacc[RUN * k + j] * sl2 - lse2[RUN * k + j]);
+        part[k] = tok <= hi_run[k] ? acc : 0.0f;   // tokens the query cannot see
       }
-      // heads 8h .. 8h+7 of each row are in lane half h: the half swap gives
-      // both halves part(half 0) and part(half 1); their sum is the same in
-      // every lane
+      if constexpr (QPW == 2) {
+        // heads 8h .. 8h+7 of each query are in lane half h: the half swap
+        // gives both halves part(half 0) and part(half 1); their sum is the
+        // same in every lane, and lane half 0 keeps it
 #pragma unroll
-      for (int i = 0; i < kImpQPW; ++i) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[i]), __float_as_uint(part[i]), false,
-                                                         false);
-        part[i] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      }
-      // lane half 0 keeps both queries' values for token `tok`
-      static_assert(kImpQPW == 2, "a token slot holds two queries");
-      if (h == 0) {
-        float2* slot = my_tok + (kt % fold_tiles) * 32 + n;
-        if (hc == 0) {
-          *slot = make_float2(part[0], part[1]);
-        } else {
-          const float2 o = *slot;
-          *slot = make_float2(o.x + part[0], o.y + part[1]);
+        for (int k = 0; k < 2; ++k) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part[k]), __float_as_uint(part[k]),
+                                                           false, false);
+          part[k] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
         }
+        if (h == 0) {
+          float2* sl2p = reinterpret_cast<float2*>(slot);
+          if (hc == 0) {
+            *sl2p = make_float2(part[0], part[1]);
+          } else {
+            const float2 o = *sl2p;
+            *sl2p = make_float2(o.x + part[0], o.y + part[1]);
+          }
+        }
+      } else if constexpr (QPW == 4) {
+        // lane half h holds queries h and 2 + h whole
+        slot[h] = part[0];
+        slot[2 + h] = part[1];
+      } else {
+        // lane half h holds queries 2h, 2h + 1, 4 + 2h, 5 + 2h whole
+        *reinterpret_cast<float2*>(slot + 2 * h) = make_float2(part[0], part[1]);
+        *reinterpret_cast<float2*>(slot + 4 + 2 * h) = make_float2(part[2], part[3]);
       }
     }
     if (kt % fold_tiles != fold_tiles - 1 && kt != ntile - 1) return;
@@ -191,12 +233,22 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       int b_i = div_sh((j + 1) * ls - 1, cd, cd_sh);
       a_i = a_i > i0 ? a_i : i0;
       b_i = b_i < i1 ? b_i : i1;
-      const float2* tq = my_tok - i0;
-      float s0 = 0.0f, s1 = 0.0f;   // this fold's share of the block's sums
-      for (int ib = a_i; ib <= b_i; ib += kImpFold) {
-        float2 v[kImpFold];
+      const float* tq = my_tok - i0 * QPW;
+      float sq[QPW];   // this fold's share of the block's sums, every query
 #pragma unroll
-        for (int x = 0; x < kImpFold; ++x) v[x] = tq[ib + x <= b_i ? ib + x : b_i];
+      for (int u = 0; u < QPW; ++u) sq[u] = 0.0f;
+      for (int ib = a_i; ib <= b_i; ib += kImpFold) {
+        float v[kImpFold][QPW];
+#pragma unroll
+        for (int x = 0; x < kImpFold; ++x) {
+          const float* src = tq + (ib + x <= b_i ? ib + x : b_i) * QPW;
+#pragma unroll
+          for (int u = 0; u < QPW; u += 2) {
+            const float2 t2 = *reinterpret_cast<const float2*>(src + u);
+            v[x][u] = t2.x;
+            v[x][u + 1] = t2.y;
+          }
+        }
 #pragma unroll
         for (int x = 0; x < kImpFold; ++x) {
           const int i = ib + x;
@@ -204,21 +256,30 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
           const int e = i * cd + cl < (j + 1) * ls ? i * cd + cl : (j + 1) * ls;
           if (i <= b_i && e > a) {
             const float wgt = (float)(e - a) * rcd;
-            s0 += v[x].x * wgt;
-            s1 += v[x].y * wgt;
+#pragma unroll
+            for (int u = 0; u < QPW; ++u) sq[u] += v[x][u] * wgt;
           }
         }
       }
-      reg_add<KPL>(bsum[0], kj, s0);
-      reg_add<KPL>(bsum[1], kj, s1);
+      // the fold's blocks jlo .. jlo + 63 sit in register slots kj0 and
+      // kj0 + 1 of every lane (kj0 is the same for the whole wave): only
+      // those two slots are updated
+      const int kj0 = jlo / kWave;
+#pragma unroll
+      for (int k = 0; k < KPL; ++k) {
+        if (k == kj0 || k == kj0 + 1) {
+#pragma unroll
+          for (int u = 0; u < QPW; ++u) bsum[u][k] += kj == k ? sq[u] : 0.0f;
+        }
+      }
     }
     wave_fence();
   });
 
   // per query of this wave: scores, masking and forcing, then top-S
-  constexpr int QIL = KPL <= 32 ? kImpQPW : 1;   // queries whose picks interleave
+  constexpr int QIL = KPL <= 32 ? 2 : 1;   // queries whose picks interleave
 #pragma unroll
-  for (int q0 = 0; q0 < kImpQPW; q0 += QIL) {
+  for (int q0 = 0; q0 < QPW; q0 += QIL) {
     uint32_t key[QIL][KPL];   // order key of block lane + 64 k; 0 once picked and for absent blocks
     bool live[QIL];
     int32_t* orow[QIL];
@@ -244,29 +305,86 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
         }
       }
     }
-    // pick s lands in lane s % 64 and is stored with the group of 64 it ends
-    for (int s = 0; s < S; ++s) {
+    if constexpr (KPL >= 8) {
+      // each lane keeps its 4 best keys in order (key descending, slot
+      // ascending among equal keys); a pick takes the wave's best list head
+      // and pops it from its lane's list.  A lane's popped keys are always a
+      // prefix of its order, so a list that runs empty is refilled with the
+      // next 4 after the last popped one.
+      uint32_t lm[QIL][4];
+      int lc[QIL][4];
+      uint32_t last_m[QIL];
+      int last_c[QIL];
 #pragma unroll
       for (int u = 0; u < QIL; ++u) {
-        uint32_t m = key[u][0];
 #pragma unroll
-        for (int k = 1; k < KPL; ++k) m = key[u][k] > m ? key[u][k] : m;
-        int kb = 0;   // this lane's lowest k holding m
+        for (int i = 0; i < 4; ++i) {
+          lm[u][i] = 0u;
+          lc[u][i] = KPL;
+        }
+        last_m[u] = 0xFFFFFFFFu;
+        last_c[u] = -1;
 #pragma unroll
-        for (int k = KPL - 1; k > 0; --k) kb = key[u][k] == m ? k : kb;
-        kb = key[u][0] == m ? 0 : kb;
-        const uint32_t top = wave_reduce_u32<true>(m);
-        const int jw = (int)__builtin_amdgcn_readfirstlane(
-            (int)wave_reduce_u32<false>(m == top ? (uint32_t)(lane + kWave * kb) : 0xFFFFFFFFu));
-        pick[u] = lane == (s & (kWave - 1)) ? jw : pick[u];
-        const bool own = lane == (jw & (kWave - 1));
-#pragma unroll
-        for (int k = 0; k < KPL; ++k) key[u][k] = own && k == jw / kWave ? 0u : key[u][k];
+        for (int k = 0; k < KPL; ++k) topn_list_insert(lm[u], lc[u], key[u][k], k, true);
       }
-      if ((s & (kWave - 1)) == kWave - 1 || s == S - 1) {
+      for (int s = 0; s < S; ++s) {
 #pragma unroll
-        for (int u = 0; u < QIL; ++u)
-          if (live[u] && lane <= (s & (kWave - 1))) orow[u][(s & ~(kWave - 1)) + lane] = pick[u];
+        for (int u = 0; u < QIL; ++u) {
+          const uint32_t top = wave_reduce_u32<true>(lm[u][0]);
+          const int jw = (int)__builtin_amdgcn_readfirstlane(
+              (int)wave_reduce_u32<false>(lm[u][0] == top ? (uint32_t)(lane + kWave * lc[u][0]) : 0xFFFFFFFFu));
+          pick[u] = lane == (s & (kWave - 1)) ? jw : pick[u];
+          const bool own = lane == (jw & (kWave - 1));
+          last_m[u] = own ? lm[u][0] : last_m[u];
+          last_c[u] = own ? lc[u][0] : last_c[u];
+#pragma unroll
+          for (int i = 0; i < 3; ++i) {
+            lm[u][i] = own ? lm[u][i + 1] : lm[u][i];
+            lc[u][i] = own ? lc[u][i + 1] : lc[u][i];
+          }
+          lm[u][3] = own ? 0u : lm[u][3];
+          lc[u][3] = own ? KPL : lc[u][3];
+          const bool refill = own && lm[u][0] == 0u;
+          if (__builtin_amdgcn_ballot_w64(refill) != 0) {   // wave-uniform
+#pragma unroll
+            for (int k = 0; k < KPL; ++k) {
+              const uint32_t x = key[u][k];
+              const bool after = x < last_m[u] || (x == last_m[u] && k > last_c[u]);
+              topn_list_insert(lm[u], lc[u], x, k, refill && after);
+            }
+          }
+        }
+        if ((s & (kWave - 1)) == kWave - 1 || s == S - 1) {
+#pragma unroll
+          for (int u = 0; u < QIL; ++u)
+            if (live[u] && lane <= (s & (kWave - 1))) orow[u][(s & ~(kWave - 1)) + lane] = pick[u];
+        }
+      }
+    } else {
+      // few keys per lane: scan them at every pick
+      for (int s = 0; s < S; ++s) {
+#pragma unroll
+        for (int u = 0; u < QIL; ++u) {
+          uint32_t m = key[u][0];
+#pragma unroll
+          for (int k = 1; k < KPL; ++k) m = key[u][k] > m ? key[u][k] : m;
+          int kb = 0;   // this lane's lowest k holding m
+#pragma unroll
+          for (int k = KPL - 1; k > 0; --k) kb = key[u][k] == m ? k : kb;
+          kb = key[u][0] == m ? 0 : kb;
+          const uint32_t top = wave_reduce_u32<true>(m);
+          const int jw = (int)__builtin_amdgcn_readfirstlane(
+              (int)wave_reduce_u32<false>(m == top ? (uint32_t)(lane + kWave * kb) : 0xFFFFFFFFu));
+          pick[u] = lane == (s & (kWave - 1)) ? jw : pick[u];
+          const bool own = lane == (jw & (kWave - 1));
+#pragma unroll
+          for (int k = 0; k < KPL; ++k) key[u][k] = own && k == jw / kWave ? 0u : key[u][k];
+        }
+        if ((s & (kWave - 1)) == kWave - 1 || s == S - 1) {
+#pragma unroll
+          for (int u = 0; u < QIL; ++u)
+            if (live[u] && lane <= (s & (kWave - 1))) orow[u][(s & ~(kWave - 1)) + lane] = pick[u];
+        }
       }
     }
   }
@@ -289,11 +407,18 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const int S = n_sel < n_slc ? n_sel : n_slc;
   NSA_CHECK(n_slc <= 64 * 64, NSA_ERR_SHAPE);
   if (T == 0 || n_slc == 0) return NSA_OK;
+  // blocks per lane (registers: block sums, then order keys)
+  const int kpl = n_slc <= 64 * 2 ? 2 : n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : n_slc <= 64 * 32 ? 32 : 64;
+  // queries per wave: the group's heads padded to 16, 8 or 4 rows of the
+  // 32-row tile, while the block sums (queries x blocks per lane) fit 64
+  // registers (128 at two queries)
+  const int G = Hq / Hkv;
+  int qpw = G > 8 ? 2 : G > 4 ? 4 : 8;
+  while (qpw > 2 && qpw * kpl > 64) qpw /= 2;
   const size_t ksz = (dtype == NSA_BF16 ? 2 : 4) * (size_t)kImpStages * 32 * D;
-  const size_t lds = ksz + sizeof(float) * (4 * kImpQPW * 32 * kImpFoldTiles);
-  static_assert(kImpQPW == 2, "token scratch holds float2 per token");
+  const size_t lds = ksz + sizeof(float) * ((size_t)4 * qpw * 32 * kImpFoldTiles);
   NSA_CHECK(lds <= 160 * 1024, NSA_ERR_SHAPE);
-  const int nqb = (T + kImpQPB - 1) / kImpQPB;
+  const int nqb = (T + 4 * qpw - 1) / (4 * qpw);
   const int64_t grid = (int64_t)B * Hkv * nqb;
   NSA_CHECK(grid < (1ll << 31), NSA_ERR_SHAPE);
   const float sl2 = (1.0f / sqrtf((float)D)) * kLog2e;
@@ -307,8 +432,6 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
     const int64_t span = (int64_t)(32 * f - 1) * cmp_stride + cmp_block;   // positions the tokens cover
     if ((span - 1) / sel_block + 2 <= 64) fold_tiles = f;
   }
-  // blocks per lane (registers: block sums, then order keys)
-  const int kpl = n_slc <= 64 * 8 ? 8 : n_slc <= 64 * 16 ? 16 : n_slc <= 64 * 32 ? 32 : 64;
   hipStream_t s = (hipStream_t)stream;
   // more than 64 KB of dynamic LDS must be allowed per kernel
   auto launch = [&](auto kern, auto qp, auto kp) -> int {
@@ -321,16 +444,17 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
     return NSA_OK;
   };
   int rc = NSA_ERR_SHAPE;
-#define NSA_TOPN_KPL(DD, KK)                                                                          \
-  if (kpl == KK)                                                                                      \
-    rc = dtype == NSA_BF16 ? launch(k_imp_topn<bf16, DD, KK>, (const bf16*)q, (const bf16*)k_cmp)    \
-                           : launch(k_imp_topn<float, DD, KK>, (const float*)q, (const float*)k_cmp);
-#define NSA_TOPN_CASE(DD) \
-  case DD:                \
-    NSA_TOPN_KPL(DD, 8)   \
-    NSA_TOPN_KPL(DD, 16)  \
-    NSA_TOPN_KPL(DD, 32)  \
-    NSA_TOPN_KPL(DD, 64)  \
+#define NSA_TOPN_KQ(DD, KK, QQ)                                                                        \
+  if (kpl == KK && qpw == QQ)                                                                          \
+    rc = dtype == NSA_BF16 ? launch(k_imp_topn<bf16, DD, KK, QQ>, (const bf16*)q, (const bf16*)k_cmp) \
+                           : launch(k_imp_topn<float, DD, KK, QQ>, (const float*)q, (const float*)k_cmp);
+#define NSA_TOPN_CASE(DD)                                                 \
+  case DD:                                                                \
+    NSA_TOPN_KQ(DD, 2, 2) NSA_TOPN_KQ(DD, 2, 4) NSA_TOPN_KQ(DD, 2, 8)     \
+    NSA_TOPN_KQ(DD, 8, 2) NSA_TOPN_KQ(DD, 8, 4) NSA_TOPN_KQ(DD, 8, 8)     \
+    NSA_TOPN_KQ(DD, 16, 2) NSA_TOPN_KQ(DD, 16, 4)                         \
+    NSA_TOPN_KQ(DD, 32, 2)                                                \
+    NSA_TOPN_KQ(DD, 64, 2)                                                \
     break;
   switch (D) {
     NSA_TOPN_CASE(16)
@@ -341,7 +465,7 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
       break;
   }
 #undef NSA_TOPN_CASE
-#undef NSA_TOPN_KPL
+#undef NSA_TOPN_KQ
   if (rc != NSA_OK) return rc;
   return nsa_launch_status();
 }

@@ -86,6 +86,16 @@ SMALL_BASELINE_SHAPES = [
     dict(B=2, Hq=12, Hkv=2, T=1024, D=64),
 ]
 
+# groups of at most 8 (4) heads: the top-n packs 4 (8) queries into a tile,
+# each query's heads padded to 8 (4) rows
+SMALL_GROUP_SHAPES = [
+    dict(B=1, Hq=8, Hkv=1, T=1024, D=64),
+    dict(B=1, Hq=5, Hkv=1, T=1100, D=128),
+    dict(B=2, Hq=6, Hkv=2, T=1024, D=32),
+    dict(B=1, Hq=4, Hkv=4, T=2048, D=128),
+    dict(B=1, Hq=7, Hkv=1, T=777, D=64),
+]
+
 
 def _near_tie_rows(scores, S, eps):
     srt = torch.sort(scores, dim=-1, descending=True).values
@@ -95,13 +105,16 @@ def _near_tie_rows(scores, S, eps):
     return gap <= eps * srt[..., S - 1].abs().clamp(min=1e-30)
 
 
-def _check_topn(B, Hq, Hkv, T, D, dtype, geom_kw):
+def _check_topn(B, Hq, Hkv, T, D, dtype, geom_kw, qk=None):
     dev = require_gpu()
     import nsa_hip_ops as ops
     cfg = O.NSAConfig(**geom_kw)
     geom = ops.NSAGeometry(**geom_kw)
-    ins, _ = _fused_inputs(B, Hq, Hkv, T, D, dtype, seed=5, head_scale=True)
-    q, kc = ins[0], ins[1]
+    if qk is None:
+        ins, _ = _fused_inputs(B, Hq, Hkv, T, D, dtype, seed=5, head_scale=True)
+        q, kc = ins[0], ins[1]
+    else:
+        q, kc = qk
     k_cmp = ops.pool_fwd(kc.to(dev), geom.cmp_block, geom.cmp_stride)
     _, lse_c = ops.range_fwd(ops.MODE_COMPRESS, q.to(dev), k_cmp, k_cmp, 0, geom.cmp_block, geom.cmp_stride)
     idx, scores = ops.importance_topn(q.to(dev), k_cmp, lse_c, geom, return_scores=True)
@@ -134,6 +147,13 @@ def test_topn_indices_bit_exact(shape, dtype):
     _check_topn(*(shape[x] for x in ("B", "Hq", "Hkv", "T", "D")), dtype, BASELINE_GEOM)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SMALL_GROUP_SHAPES, ids=lambda s: "T{T}-Hq{Hq}-Hkv{Hkv}-D{D}".format(**s))
+def test_topn_small_groups_bit_exact(shape, dtype):
+    log(f"topn small group {shape} {dtype}")
+    _check_topn(*(shape[x] for x in ("B", "Hq", "Hkv", "T", "D")), dtype, BASELINE_GEOM)
+
+
 # many selection blocks per query (more than 512 and more than 1024: the
 # top-n phase keeps 16 and 64 block keys per lane), more picks than a wave
 # has lanes, and a group of 24 heads (two 16-head chunks per tile, the
@@ -143,15 +163,38 @@ MANY_BLOCK_CASES = [
      dict(cmp_block=8, cmp_stride=4, sel_block=4, n_sel=80, window=64, force_init=True, n_local=2)),
     (dict(B=1, Hq=24, Hkv=1, T=3072, D=64),
      dict(cmp_block=4, cmp_stride=2, sel_block=2, n_sel=16, window=64, force_init=False, n_local=1)),
+    # 4 heads, 1024 blocks: 4 queries a tile (8 would not fit the block sums)
+    (dict(B=1, Hq=4, Hkv=1, T=4096, D=64),
+     dict(cmp_block=8, cmp_stride=4, sel_block=4, n_sel=40, window=64, force_init=True, n_local=2)),
 ]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("case", MANY_BLOCK_CASES, ids=["nslc1024-S80", "nslc1536-G24"])
+@pytest.mark.parametrize("case", MANY_BLOCK_CASES, ids=["nslc1024-S80", "nslc1536-G24", "nslc1024-G4"])
 def test_topn_many_blocks(case, dtype):
     shape, geom_kw = case
     log(f"topn many blocks {shape} {geom_kw} {dtype}")
     _check_topn(*(shape[x] for x in ("B", "Hq", "Hkv", "T", "D")), dtype, geom_kw)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_topn_one_lane_holds_the_best_blocks(dtype):
+    """Keys zero except the selection blocks j = 5 mod 64, which hold one
+    vector the queries align with: those 16 blocks tie for the best score
+    and all sit in one lane's key registers (block lane + 64 k), their
+    neighbours tie next in the two adjacent lanes.  The picks must take them
+    in ascending block order, popping and refilling those lanes' candidate
+    lists several times."""
+    B, Hq, Hkv, T, D = 1, 4, 1, 4096, 64
+    geom_kw = dict(cmp_block=8, cmp_stride=4, sel_block=4, n_sel=40, window=64, force_init=True, n_local=2)
+    g = torch.Generator().manual_seed(11)
+    v = torch.randn(D, generator=g)
+    v = 4.0 * v / v.norm()
+    kc = torch.zeros(B, Hkv, T, D)
+    for j in range(5, T // 4, 64):
+        kc[0, 0, 4 * j:4 * j + 4] = v
+    q = v.expand(B, Hq, T, D).clone()
+    _check_topn(B, Hq, Hkv, T, D, dtype, geom_kw, qk=(q.to(dtype), kc.to(dtype)))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
