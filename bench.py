@@ -695,6 +695,16 @@ def run_other_configs(args):
     c4["nsa_vs_dense_ref_time"] = round(c4["dense_ref"]["ms_per_step"] / c4["nsa"]["ms_per_step"], 4)
     c4["nsa_vs_dense_ref_memory"] = round(c4["nsa"]["peak_mem_gib"] / c4["dense_ref"]["peak_mem_gib"], 4)
     c4["desc"] = WORKLOADS["c4"]["desc"]
+    # the same model and tokens per step at 4x the sequence length (B2 x
+    # 16384): dense attention's work per token grows with T, NSA's stays near
+    # its top-n and window budget (no materialised arm: its score matrices
+    # would not fit)
+    torch.cuda.empty_cache()
+    c4l = run_model_bench(small, dict(WORKLOADS["c4"], B=2, T=16384), arms=("nsa", "dense"))
+    c4l["nsa_vs_dense_time"] = round(c4l["dense"]["ms_per_step"] / c4l["nsa"]["ms_per_step"], 4)
+    c4l["nsa_vs_dense_memory"] = round(c4l["nsa"]["peak_mem_gib"] / c4l["dense"]["peak_mem_gib"], 4)
+    c4l["desc"] = "config 4's model and step at B2 x T16384 (the same 32768 tokens a step)"
+    c4["long_context"] = c4l
     out["c4"] = c4
     torch.cuda.empty_cache()
     return out
