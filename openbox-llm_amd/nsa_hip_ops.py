@@ -1091,6 +1091,71 @@ class NSAFusedHIP(torch.autograd.Function):
         return (*grads, None, None, None)
 
 
+class NSAFusedCAPI(torch.autograd.Function):
+    """``NSAFusedHIP``'s layer through the two C entry points a C caller runs
+    (``nsa_fused_fwd`` / ``nsa_fused_bwd``): the same kernels with the same
+    arguments (bit-identical outputs and gradients), issued from C++ in one
+    library call per direction instead of the Python sequence of about a dozen
+    calls and their allocations.  Caller-owned buffers: the saved context
+    (branch outputs, lse, packed Q, CSR) lives from the forward to the
+    backward; each call takes its own scratch."""
+
+    @staticmethod
+    def forward(ctx, q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled=False):
+        check_qkv(q, ks, vs)
+        check_qkv(q, kw, vw)
+        ins = tuple(_contig(t) for t in (q, kc, vc, ks, vs, kw, vw, gate))
+        q = ins[0]
+        B, Hq, T, D = q.shape
+        Hkv = ins[3].shape[1]
+        dt = L.dtype_code(q)
+        dims = (B, Hq, Hkv, T, D, geom.cmp_block, geom.cmp_stride, geom.sel_block, geom.n_sel, geom.window)
+        ctx_bytes = int(_lib().nsa_fused_ctx_bytes(*dims, int(pooled), dt))
+        scr_bytes = int(_lib().nsa_fused_scratch_bytes(*dims, int(pooled), dt, _stream(q)))
+        assert ctx_bytes > 0 and scr_bytes > 0, "nsa_fused: unsupported shape (T must reach cmp_block and sel_block)"
+        saved = torch.empty(ctx_bytes, device=q.device, dtype=torch.uint8)
+        scratch = torch.empty(scr_bytes, device=q.device, dtype=torch.uint8)
+        S = min(geom.n_sel, T // geom.sel_block)
+        given = block_idx is not None
+        idx = (block_idx.to(torch.int32).contiguous() if given
+               else torch.empty(B, Hkv, T, S, device=q.device, dtype=torch.int32))
+        out = torch.empty_like(q)
+        _call("nsa_fused_fwd", _lib().nsa_fused_fwd, *map(L.ptr, ins), L.ptr(idx), int(given), L.ptr(out),
+              L.ptr(saved), ctx_bytes, L.ptr(scratch), scr_bytes, *dims, int(geom.force_init), int(geom.n_local),
+              int(pooled), dt, _stream(q))
+        ctx.save_for_backward(*ins, idx, saved)
+        ctx.meta = (dims, scr_bytes, int(pooled), dt)
+        ctx.mark_non_differentiable(idx)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, dout, _didx):
+        *ins, idx, saved = ctx.saved_tensors
+        dims, scr_bytes, pooled, dt = ctx.meta
+        dout = _contig(dout.to(ins[0].dtype))
+        scratch = torch.empty(scr_bytes, device=dout.device, dtype=torch.uint8)
+        grads = [torch.empty_like(t) for t in ins]
+        _call("nsa_fused_bwd", _lib().nsa_fused_bwd, L.ptr(dout), *map(L.ptr, ins), L.ptr(idx), L.ptr(saved),
+              saved.numel(), L.ptr(scratch), scr_bytes, *map(L.ptr, grads), *dims, pooled, dt, _stream(dout))
+        return (*grads, None, None, None)
+
+
+# True: a model layer (nsa_attention_layer) runs through the C entry points
+LAYER_CAPI = True
+
+
+def nsa_attention_layer(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None, pooled=False):
+    """``nsa_attention`` for a model layer: through the C entry points
+    (``NSAFusedCAPI``) where they take the shape, one launch sequence per
+    direction issued from C++; else (``T`` shorter than a compression or
+    selection block, per-call timing wanted, or ``LAYER_CAPI`` off) through
+    ``NSAFusedHIP``."""
+    T = q.shape[2]
+    if LAYER_CAPI and _TIMER is None and T >= geom.cmp_block and T >= geom.sel_block:
+        return NSAFusedCAPI.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom, pooled)
+    return NSAFusedHIP.apply(q, kc, vc, ks, vs, kw, vw, gate_logits, block_idx, geom, pooled)
+
+
 def nsa_attention(q, kc, vc, ks, vs, kw, vw, gate_logits, geom: NSAGeometry, block_idx=None, pooled=False):
     """Full NSA attention (pre out-projection) on the HIP path.
 

@@ -507,8 +507,8 @@ class NSAAttention(nn.Module):
                                self.force_init, self.n_local)
         if block_idx is not None:
             block_idx = block_idx.to(device=q.device, dtype=torch.int32)
-        out, block_idx = ops.nsa_attention(q, k_cmp.contiguous(), v_cmp.contiguous(), ks, vs, kw, vw,
-                                           gate_logits, geom, block_idx=block_idx, pooled=True)
+        out, block_idx = ops.nsa_attention_layer(q, k_cmp.contiguous(), v_cmp.contiguous(), ks, vs, kw, vw,
+                                                 gate_logits, geom, block_idx=block_idx, pooled=True)
         self.last_block_idx = block_idx
         return self._merge(out)
 

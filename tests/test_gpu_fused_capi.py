@@ -55,6 +55,36 @@ def test_fused_capi_equals_the_python_boundary(case):
     log(f"  {name}: out, indices and 8 gradients bit-identical to the Python boundary")
 
 
+@pytest.mark.parametrize("case", [CASES[1], CASES[4]], ids=[CASES[1][0], CASES[4][0]])
+def test_capi_autograd_equals_the_python_boundary(case):
+    """NSAFusedCAPI (the model layer's path: one C call per direction, the
+    context saved between them, scratch per call) against NSAFusedHIP under
+    autograd, twice in a row (the second call reuses the first's freed
+    buffers)."""
+    dev = require_gpu()
+    import nsa_hip_ops as ops
+    name, B, Hq, Hkv, T, D, dtype, gp, _, pooled = case
+    geom = ops.NSAGeometry(*gp)
+    n = ops.n_cmp_tokens(T, geom.cmp_block, geom.cmp_stride)
+    Tc = n if pooled else T
+    for rep in range(2):
+        ins = [randn((B, Hq, T, D), 1 + rep, dtype)] + [randn((B, Hkv, Tc if i < 2 else T, D), 2 + i + rep, dtype)
+                                                        for i in range(6)] + [randn((B, Hq, T, 3), 9 + rep, dtype)]
+        ins = [t.to(dev) for t in ins]
+        do = randn((B, Hq, T, D), 10 + rep, dtype).to(dev)
+        xs = [t.clone().requires_grad_() for t in ins]
+        ys = [t.clone().requires_grad_() for t in ins]
+        out, idx = ops.NSAFusedHIP.apply(*xs, None, geom, pooled)
+        out.backward(do)
+        out_c, idx_c = ops.NSAFusedCAPI.apply(*ys, None, geom, pooled)
+        out_c.backward(do)
+        torch.cuda.synchronize()
+        assert torch.equal(idx_c, idx) and torch.equal(out_c, out), f"{name}: forward differs"
+        for nm, x, y in zip(["q", "kc", "vc", "ks", "vs", "kw", "vw", "gate"], xs, ys):
+            assert torch.equal(y.grad, x.grad), f"{name}: d{nm} differs"
+    log(f"  {name}: the C-ABI autograd path bit-identical, two calls")
+
+
 def test_fused_capi_rejects_bad_calls():
     require_gpu()
     import _nsa_lib as L
