@@ -22,7 +22,7 @@
 namespace {
 
 constexpr int kFwdChunk = 128;    // CSR queries per selection forward work item
-constexpr int kDkdvChunk = 1024;  // CSR queries per selection dK/dV work item
+constexpr int kDkdvChunk = 512;   // CSR queries per selection dK/dV work item
 
 struct Carver {
   size_t off = 0;

@@ -24,7 +24,8 @@ import _nsa_lib as L
 
 MODE_WINDOW = L.MODE_WINDOW
 MODE_COMPRESS = L.MODE_COMPRESS
-SEL_DKDV_CHUNK = 1024         # CSR queries per selection dK/dV work item (c3: 1024 measured 5% faster than 512)
+SEL_DKDV_CHUNK = 512          # CSR queries per selection dK/dV work item (deterministic partials: 512 measured
+                              # 0.1 ms a c3 step and 0.09 ms a c4 layer faster than 1024)
 SEL_FWD_CHUNK = 128           # CSR queries per selection forward work item (c3: 128 measured 0.1 ms faster than 512)
 
 
