@@ -38,6 +38,13 @@ extern "C" {
 
 #define NSA_F32 0
 #define NSA_BF16 1
+/* Only for the branch outputs a forward keeps for its backward (the o_dtype
+ * of nsa_range_fwd, nsa_range_fwd_finish and nsa_bwd_prep, with bf16
+ * inputs): fp16 rows [B][Hq][T][D], each stored divided by a power-of-two
+ * scale s_r (1 unless the row's largest magnitude reaches 2^15), followed in
+ * the same buffer by the float32 scales s_r [B][Hq][T].  Buffer bytes:
+ * B*Hq*T*(2*D + 4).  Eight times finer than bf16 at half float32's size. */
+#define NSA_F16S 2
 
 #define NSA_MODE_WINDOW 0
 #define NSA_MODE_COMPRESS 1
@@ -111,8 +118,9 @@ int nsa_heads_merge_grad(const void* const* douts, void* dy, const int* heads, c
 int nsa_gate_fwd(const void* gate, const void* o_cmp, const void* o_slc, const void* o_win, void* out,
                  int64_t rows, int D, int dtype, void* stream);
 
-/* Backward prep.  o0 / o1 / o2 are in o_dtype: dtype, or NSA_F32 when the
- * forward kept the branch outputs unrounded (nsa_range_fwd's o_dtype).
+/* Backward prep.  o0 / o1 / o2 are in o_dtype: dtype, NSA_F32 when the
+ * forward kept the branch outputs unrounded, or NSA_F16S (bf16 inputs) when
+ * it kept them as scaled fp16 rows (nsa_range_fwd's o_dtype).
  * nbr == 1: dot[r] = dO[r] . o0[r] (the delta of
  * nsa_selection_backward.py:168).  nbr == 3: for each branch c,
  * dot[c*rows + r] = dO . o_c, rowscale[c*rows + r] = sigmoid(g_c) and
@@ -262,9 +270,12 @@ int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float
  * i*cmp_stride + cmp_block - 1 <= t.  k [B][Hkv][Lk][D], vt transposed v with
  * Lp = nsa_padded_len(Lk).  Writes o and lse; q_packed (nullable) also
  * receives q in the nsa_pack_heads layout (the rows are loaded anyway).
- * o_dtype: the type of o -- dtype (the reference's convention), or NSA_F32
- * so that a backward's row dots dO . o see the unrounded output (the fused
- * layer keeps its branch outputs this way; only its gated sum is returned). */
+ * o_dtype: the type of o -- dtype (the reference's convention), NSA_F32 so
+ * that a backward's row dots dO . o see the unrounded output, or NSA_F16S
+ * (bf16 inputs; o then has B*Hq*T*(2*D + 4) bytes) for 11 significant bits
+ * at half float32's size -- the fused layer keeps its branch outputs this
+ * way for bf16 inputs, float32 for float32 inputs; only their gated sum is
+ * returned. */
 int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B, int Hq,
                   int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride, void* q_packed, int dtype,
                   int o_dtype, void* stream);
@@ -276,8 +287,9 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
  * [B][Hkv][T][S] block_idx of block size sel_block) into o_sel / lse_sel
  * and writes out = sigmoid(g0) o_cmp + sigmoid(g1) o_sel + sigmoid(g2) o from
  * the gate logits [B][Hq][T][3] (out in out_dtype: dtype, or NSA_F32
- * unrounded).  o, o_sel and o_cmp are in o_dtype (dtype, or NSA_F32
- * unrounded); the blend uses each branch as stored. */
+ * unrounded).  o, o_sel and o_cmp are in o_dtype (dtype, NSA_F32
+ * unrounded, or NSA_F16S with bf16 inputs); the blend uses each branch as
+ * stored. */
 int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt, void* o, float* lse, int B,
                          int Hq, int Hkv, int T, int Lk, int D, int window, int cmp_block, int cmp_stride,
                          const void* o_part, const float* ml_part, const int32_t* block_idx, int S, int sel_block,

@@ -24,6 +24,7 @@ NSA_ERR_WORKSPACE = -5
 
 NSA_F32 = 0
 NSA_BF16 = 1
+NSA_F16S = 2
 MODE_WINDOW = 0
 MODE_COMPRESS = 1
 
@@ -125,6 +126,14 @@ def dtype_code(t):
         return NSA_F32
     if t.dtype == torch.bfloat16:
         return NSA_BF16
+    if t.dtype == torch.float16:
+        # only as branch outputs in the NSA_F16S form: the rows' halves, then a
+        # float32 scale per row (of D elements) in the same storage
+        rows = t.numel() // t.shape[-1]
+        room = t.untyped_storage().nbytes() - t.storage_offset() * 2
+        assert t.is_contiguous() and room >= rows * (2 * t.shape[-1] + 4), \
+            "float16 tensors are accepted only as NSA_F16S branch outputs (rows followed by their scales)"
+        return NSA_F16S
     raise AssertionError(f"dtype {t.dtype} is not supported (float32 or bfloat16)")
 
 

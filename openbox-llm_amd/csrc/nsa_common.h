@@ -27,6 +27,9 @@ typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16;
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -108,6 +111,7 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
 __device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
 template <typename T> __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
 __device__ __forceinline__ float xor_max(float v, int m) { return fmaxf(v, __shfl_xor(v, m, kWave)); }
@@ -124,6 +128,24 @@ __device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float
 __device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
   *reinterpret_cast<f32x4*>(p) = (f32x4){a, b, c, d};
 }
+__device__ __forceinline__ void store4(f16* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f16x4*>(p) = (f16x4){(f16)a, (f16)b, (f16)c, (f16)d};
+}
+
+// Branch outputs kept for a backward's row dots dO . o in the NSA_F16S form:
+// row r holds o[r] / s_r in fp16 (11 significant bits, eight times finer than
+// bf16) and the float32 scales s_r follow the rows' halves.  s_r is 1 unless
+// the row's largest magnitude amax reaches 2^15 (fp16 ends at 65504); then it
+// is the power of two that brings amax into [2^14, 2^15).  A power of two
+// divides and multiplies back exactly, so the stored value is o[r] rounded
+// once.  Infinite or NaN rows keep s_r = 1 (the values carry them).
+__device__ __forceinline__ float f16s_row_scale(float amax) {
+  if (!(amax >= 32768.0f) || amax == __builtin_inff()) return 1.0f;
+  const int e = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127;   // amax in [2^e, 2^(e+1))
+  return __uint_as_float((uint32_t)(e - 14 + 127) << 23);
+}
+template <typename T> struct IsF16 { static constexpr bool value = false; };
+template <> struct IsF16<f16> { static constexpr bool value = true; };
 
 // float -> u32 with the same order (+inf highest); every float maps above 0
 __device__ __forceinline__ uint32_t order_key(float x) {
@@ -167,5 +189,9 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
 
 // Transposed K/V copies: [B*Hkv][D][Tp] with key-contiguous rows padded to Tp.
 __host__ __device__ inline int padded_len(int n) { return ((n + 32 + 63) / 64) * 64; }
+// The row scales of an NSA_F16S buffer: float32, after its rows * D halves.
+__host__ __device__ inline float* f16s_scales(void* o, int64_t rows, int D) {
+  return reinterpret_cast<float*>(reinterpret_cast<char*>(o) + rows * D * 2);
+}
 
 }  // namespace nsa

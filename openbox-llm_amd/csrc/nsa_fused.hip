@@ -43,6 +43,10 @@ struct Dims {
   int nblk() const { return (T + ls - 1) / ls; }
   size_t es() const { return dtype == NSA_BF16 ? 2 : 4; }
   int64_t rows() const { return (int64_t)B * Hq * T; }
+  // the branch outputs kept for the backward: NSA_F16S for bf16 inputs,
+  // float32 for float32 inputs (unrounded either way but for fp16's 11 bits)
+  int o_dtype() const { return dtype == NSA_BF16 ? NSA_F16S : NSA_F32; }
+  size_t o_bytes() const { return dtype == NSA_BF16 ? (size_t)rows() * (2 * D + 4) : (size_t)rows() * D * 4; }
   int64_t kv(int L) const { return (int64_t)B * Hkv * L * D; }
   bool ok() const {
     return B > 0 && Hkv > 0 && Hq % Hkv == 0 && (D == 16 || D == 32 || D == 64 || D == 128) && l >= 1 && d >= 1 &&
@@ -54,7 +58,8 @@ struct Dims {
 // The state the forward leaves for the backward.
 struct Ctx {
   void *k_cmp, *v_cmp, *qp;
-  float *o_c, *o_s, *o_w, *lse_c, *lse_s, *lse_w;
+  void *o_c, *o_s, *o_w;
+  float *lse_c, *lse_s, *lse_w;
   int32_t *q_of_block, *offsets, *pair_bh, *count;
 };
 
@@ -66,8 +71,8 @@ Ctx carve_ctx(const Dims& m, void* base, size_t* bytes) {
   x.k_cmp = m.pooled ? nullptr : c.take(m.kv(n) * m.es());
   x.v_cmp = m.pooled ? nullptr : c.take(m.kv(n) * m.es());
   x.qp = c.take((size_t)m.rows() * m.D * m.es());
-  float** outs[3] = {&x.o_c, &x.o_s, &x.o_w};
-  for (float** o : outs) *o = (float*)c.take((size_t)m.rows() * m.D * sizeof(float));
+  void** outs[3] = {&x.o_c, &x.o_s, &x.o_w};
+  for (void** o : outs) *o = c.take(m.o_bytes());
   x.lse_c = (float*)c.take(m.rows() * sizeof(float));
   x.lse_s = (float*)c.take(m.rows() * sizeof(float));
   x.lse_w = (float*)c.take(m.rows() * sizeof(float));
@@ -198,7 +203,7 @@ int nsa_fused_fwd(const void* q, const void* kc, const void* vc, const void* ks,
   // compression (its forward also writes the packed q of the selection kernels)
   NSA_TRY(nsa_transpose_kv(v_cmp, w.vt_c, B * Hkv, n, D, Lpn, dtype, stream));
   NSA_TRY(nsa_range_fwd(NSA_MODE_COMPRESS, q, k_cmp, w.vt_c, x.o_c, x.lse_c, B, Hq, Hkv, T, n, D, 0, cmp_block,
-                        cmp_stride, x.qp, dtype, NSA_F32, stream));
+                        cmp_stride, x.qp, dtype, m.o_dtype(), stream));
   if (!idx_given)
     NSA_TRY(nsa_importance_topn(q, k_cmp, x.lse_c, block_idx, nullptr, B, Hq, Hkv, T, n, D, cmp_block, cmp_stride,
                                 sel_block, n_sel, force_init, n_local, dtype, stream));
@@ -212,7 +217,7 @@ int nsa_fused_fwd(const void* q, const void* kc, const void* vc, const void* ks,
   NSA_TRY(nsa_transpose_kv(vw, w.vt_w, B * Hkv, T, D, Lpt, dtype, stream));
   return nsa_range_fwd_finish(NSA_MODE_WINDOW, q, kw, w.vt_w, x.o_w, x.lse_w, B, Hq, Hkv, T, T, D, window, 1, 1,
                               w.o_part, w.ml_part, block_idx, S, sel_block, x.o_s, x.lse_s, x.o_c, gate, out, dtype,
-                              NSA_F32, dtype, stream);
+                              m.o_dtype(), dtype, stream);
 }
 
 int nsa_fused_bwd(const void* dout, const void* q, const void* kc, const void* vc, const void* ks, const void* vs,
@@ -246,7 +251,7 @@ int nsa_fused_bwd(const void* dout, const void* q, const void* kc, const void* v
   float* dvp32 = (f32 && pooled) ? (float*)dvc : w.dvp;
   // gate backward, row dots of the three branches, dO packed for the selection
   NSA_TRY(nsa_bwd_prep(dout, x.o_c, x.o_s, x.o_w, gate, dgate, x.lse_c, x.lse_s, x.lse_w, w.dot, w.rs, w.coff,
-                       w.dop, G, T, R, D, 3, dtype, NSA_F32, dtype, stream));
+                       w.dop, G, T, R, D, 3, dtype, m.o_dtype(), dtype, stream));
   // selection dK/dV and dQ partials (block-outer, deterministic merge)
   NSA_TRY(nsa_transpose_kv(ks, w.kt_s, B * Hkv, T, D, Lpt, dtype, stream));
   NSA_TRY(nsa_sel_dkdv(x.qp, ks, vs, w.kt_s, w.dop, w.coff + R, w.dot + R, x.q_of_block, 1, x.offsets, x.count,

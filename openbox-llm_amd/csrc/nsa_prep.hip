@@ -530,7 +530,12 @@ template <typename T, typename TO> struct BranchRow {
   static constexpr int N = Vec16<T>::N;
   float x[N];
   __device__ __forceinline__ void load(const TO* p) {
-    if constexpr (sizeof(TO) == sizeof(T)) {
+    if constexpr (IsF16<TO>::value) {
+      static_assert(N == 8, "NSA_F16S rows pair with 16-bit inputs");
+      const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+      for (int i = 0; i < N; ++i) x[i] = (float)v[i];
+    } else if constexpr (sizeof(TO) == sizeof(T)) {
       Vec16<T> v;
       v.load(reinterpret_cast<const T*>(p));
 #pragma unroll
@@ -586,6 +591,13 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
   for (int c = 0; c < 3; ++c)
     for (int m = 1; m < gs; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
   if (!ok || sub != 0) return;
+  if constexpr (IsF16<TO>::value) {
+    // NSA_F16S: the rows were stored divided by their power-of-two scales
+    const TO* os[3] = {o0, o1, o2};
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+      if (c < nbr) acc[c] *= f16s_scales(const_cast<TO*>(os[c]), rows, D)[row];
+  }
   // with dout_packed, the statistics of the selection branch (the only
   // branch, or branch 1 of 3) go to the packed row, the layout of the
   // selection dK/dV's query side
@@ -912,7 +924,7 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
                  float* rowscale, float* coff, void* dout_packed, int G, int T, int64_t rows, int D, int nbr,
                  int dtype, int o_dtype, int dgate_dtype, void* stream) {
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32 || (o_dtype == NSA_F16S && dtype == NSA_BF16), NSA_ERR_DTYPE);
   NSA_CHECK(dgate_dtype == dtype || dgate_dtype == NSA_F32, NSA_ERR_DTYPE);
   float* dgate32 = dgate_dtype == NSA_F32 && dtype != NSA_F32 ? (float*)dgate : nullptr;
   if (dgate32 != nullptr) dgate = nullptr;
@@ -929,7 +941,11 @@ int nsa_bwd_prep(const void* dout, const void* o0, const void* o1, const void* o
   NSA_CHECK(grid64 < (1ll << 31), NSA_ERR_SHAPE);
   const int grid = (int)grid64;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
+  if (o_dtype == NSA_F16S)
+    k_bwd_prep<bf16, f16><<<grid, 256, 0, s>>>((const bf16*)dout, (const f16*)o0, (const f16*)o1,
+                                               (const f16*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2,
+                                               dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr, dgate32);
+  else if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
     k_bwd_prep<bf16, bf16><<<grid, 256, 0, s>>>((const bf16*)dout, (const bf16*)o0, (const bf16*)o1,
                                                 (const bf16*)o2, (const bf16*)gate, (bf16*)dgate, lse0, lse1, lse2,
                                                 dot, rowscale, coff, (bf16*)dout_packed, G, T, rows, D, nbr, dgate32);

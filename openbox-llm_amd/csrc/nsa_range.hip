@@ -166,7 +166,9 @@ __host__ __device__ inline int range_qtiles(bool flat, int T, int G, int NT) {
 // the gate into out (the role of nsa_gate_fwd), each from the same rounded
 // branch outputs the separate kernels would read.
 // TO is the type of the branch outputs (o, o_sel, o_cmp): the input type T,
-// or float when the caller keeps them unrounded for the backward's row dots.
+// float when the caller keeps them unrounded for the backward's row dots, or
+// f16 for the NSA_F16S form (fp16 rows, a float32 scale per row after them:
+// o_scale, o_sel_scale, o_cmp_scale).
 template <typename T, typename TO> struct FwdExtras {
   T* q_packed;             // [B][Hkv][T][G][D] (nullable)
   const T* opart;          // [B][Hkv][T][NS][G][D] unnormalised block-local outputs O_j = sum p v
@@ -179,6 +181,9 @@ template <typename T, typename TO> struct FwdExtras {
   T* out;                  // [B][Hq][T][D]
   int S, sel_L;
   float* out32;            // nullable: out in float32 (unrounded), written instead of `out`
+  float* o_scale;          // NSA_F16S row scales of this launch's o, o_sel and o_cmp
+  float* o_sel_scale;
+  const float* o_cmp_scale;
 };
 
 // The wave's own output rows (this branch, unnormalised acc with the row
@@ -226,9 +231,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
       const f32x4 b2 = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8 + 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) ow[i] = a[i], ow[4 + i] = b2[i];
-      store8(o + orow * D + 8 * c8, ow);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ow[i] = to_f32(from_f32<TO>(ow[i]));
+      store_branch8<TO, CPR>(o + orow * D + 8 * c8, ow, f.o_scale + orow, c8 == 0);
     }
     // selection: merge the slot partials (running maximum over batches of 16)
     const int64_t qs = bh * T_ + t;
@@ -274,17 +277,17 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     const float inv_s = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc_s[i] *= inv_s;
-    store8(f.o_sel + orow * D + 8 * c8, acc_s);
+    store_branch8<TO, CPR>(f.o_sel + orow * D + 8 * c8, acc_s, f.o_sel_scale + orow, c8 == 0);
     if (c8 == 0) f.lse_sel[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
     // gate: sigmoid-weighted sum of the three rounded branch outputs
     float oc[8];
-    load8(f.o_cmp + orow * D + 8 * c8, oc);
+    load_branch8(f.o_cmp + orow * D + 8 * c8, oc, f.o_cmp_scale + orow);
     const float g0 = sigmoidf(to_f32(f.gate[orow * 3 + 0]));
     const float g1 = sigmoidf(to_f32(f.gate[orow * 3 + 1]));
     const float g2 = sigmoidf(to_f32(f.gate[orow * 3 + 2]));
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * to_f32(from_f32<TO>(acc_s[i])) + g2 * ow[i];
+    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * acc_s[i] + g2 * ow[i];
     if (f.out32 != nullptr)
       store8(f.out32 + orow * D + 8 * c8, y);
     else
@@ -501,9 +504,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const float lt = l_[nt] + __shfl_xor(l_[nt], 32, kWave);
-    if (!rok[nt]) continue;
     const bool any_key = lo[nt] <= hi[nt];
-    const float inv = any_key ? 1.0f / lt : 0.0f;
+    float inv = any_key ? 1.0f / lt : 0.0f;
+    if constexpr (IsF16<TO>::value) {
+      // NSA_F16S: the row's scale from its largest magnitude (the two lanes
+      // of column n hold the row's halves)
+      float amax = 0.0f;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (D % 32 == 0 || 32 * dt + 8 * (i >> 2) + 4 * h < D) amax = fmaxf(amax, fabsf(acc[dt][nt][i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, kWave)) * inv;
+      const float sc = f16s_row_scale(amax);
+      if (rok[nt] && h == 0) fin_args.o_scale[row[nt]] = sc;
+      inv /= sc;
+    }
+    if (!rok[nt]) continue;
     TO* orow = o + row[nt] * D;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
@@ -868,10 +885,17 @@ int nsa_range_fwd(int mode, const void* q, const void* k, const void* vt, void* 
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32 || (o_dtype == NSA_F16S && dtype == NSA_BF16), NSA_ERR_DTYPE);
   if (T == 0) return NSA_OK;
   hipStream_t s = (hipStream_t)stream;
   NSA_CHECK(q_packed != q, NSA_ERR_ARG);
+  if (o_dtype == NSA_F16S) {
+    FwdExtras<bf16, f16> ex{};
+    ex.q_packed = (bf16*)q_packed;
+    ex.o_scale = f16s_scales(o, (int64_t)B * Hq * T, D);
+    return range_fwd_launch<bf16, f16>(mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block,
+                                       cmp_stride, ex, s);
+  }
   if (dtype == NSA_BF16 && o_dtype == NSA_BF16) {
     FwdExtras<bf16, bf16> ex{};
     ex.q_packed = (bf16*)q_packed;
@@ -898,7 +922,7 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
   NSA_CHECK(mode == NSA_MODE_WINDOW || mode == NSA_MODE_COMPRESS, NSA_ERR_ARG);
   NSA_CHECK(range_args_ok(mode, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride), NSA_ERR_SHAPE);
   NSA_CHECK(dtype == NSA_F32 || dtype == NSA_BF16, NSA_ERR_DTYPE);
-  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32, NSA_ERR_DTYPE);
+  NSA_CHECK(o_dtype == dtype || o_dtype == NSA_F32 || (o_dtype == NSA_F16S && dtype == NSA_BF16), NSA_ERR_DTYPE);
   NSA_CHECK(o_part && ml_part && block_idx && o_sel && lse_sel && o_cmp && gate && out, NSA_ERR_ARG);
   NSA_CHECK(S >= 1 && sel_block >= 16 && sel_block % 16 == 0, NSA_ERR_SHAPE);
   NSA_CHECK(out_dtype == dtype || out_dtype == NSA_F32, NSA_ERR_DTYPE);
@@ -906,6 +930,16 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
   hipStream_t s = (hipStream_t)stream;
   float* out32 = out_dtype == NSA_F32 && dtype != NSA_F32 ? (float*)out : nullptr;
   if (out32 != nullptr) out = nullptr;
+  if (o_dtype == NSA_F16S) {
+    const int64_t rows = (int64_t)B * Hq * T;
+    return range_fwd_launch<bf16, f16>(
+        mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
+        FwdExtras<bf16, f16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (f16*)o_sel,
+                             lse_sel, (const f16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block, out32,
+                             f16s_scales(o, rows, D), f16s_scales(o_sel, rows, D),
+                             f16s_scales(const_cast<void*>(o_cmp), rows, D)},
+        s);
+  }
   if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
     return range_fwd_launch<bf16, bf16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,

@@ -540,6 +540,51 @@ __device__ __forceinline__ void store8(float* p, const float (&x)[8]) {
   *reinterpret_cast<f32x4*>(p) = (f32x4){x[0], x[1], x[2], x[3]};
   *reinterpret_cast<f32x4*>(p + 4) = (f32x4){x[4], x[5], x[6], x[7]};
 }
+__device__ __forceinline__ void load8(const f16* p, float (&x)[8]) {
+  const f16x8 v = *reinterpret_cast<const f16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
+}
+
+// Stores 8 consecutive elements of a branch-output row and leaves in x the
+// values as stored: rounded to TO, or for the NSA_F16S form (TO = f16) scaled
+// by the row's power of two (f16s_row_scale), which the LPR consecutive lanes
+// holding the row agree on through an xor reduction of their maxima; lane
+// `first` of them writes it to *scale.
+template <typename TO, int LPR>
+__device__ __forceinline__ void store_branch8(TO* p, float (&x)[8], float* scale, bool first) {
+  if constexpr (IsF16<TO>::value) {
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(x[i]));
+#pragma unroll
+    for (int k = 1; k < LPR; k <<= 1) m = fmaxf(m, __shfl_xor(m, k, kWave));
+    const float sc = f16s_row_scale(m), inv = 1.0f / sc;
+    f16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[i] = (f16)(x[i] * inv);
+      x[i] = (float)v[i] * sc;
+    }
+    *reinterpret_cast<f16x8*>(p) = v;
+    if (first) *scale = sc;
+  } else {
+    store8(p, x);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = to_f32(from_f32<TO>(x[i]));
+  }
+}
+// Loads 8 consecutive elements of a branch-output row as stored (the row's
+// scale applied for the NSA_F16S form).
+template <typename TO>
+__device__ __forceinline__ void load_branch8(const TO* p, float (&x)[8], const float* scale) {
+  load8(p, x);
+  if constexpr (IsF16<TO>::value) {
+    const float sc = *scale;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] *= sc;
+  }
+}
 
 // 8 consecutive elements of a row as loaded (one 16-byte load for bf16, two
 // for float), converted at use.

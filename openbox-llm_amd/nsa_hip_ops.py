@@ -437,11 +437,34 @@ def sel_fwd(q, k, v, block_idx, block_size, vt=None):
     return o, lse
 
 
-def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_packed=None, o_f32=False):
+def f16s_empty(shape, device):
+    """A branch-output buffer in the library's NSA_F16S form: fp16 rows, each
+    stored divided by a power-of-two scale (1 unless the row's largest
+    magnitude reaches 2^15), followed in the same storage by the float32
+    scales, one per row.  Returns the float16 view of the rows; only the
+    library's kernels read it (``_nsa_lib.dtype_code`` checks the room for
+    the scales)."""
+    rows = shape[0] * shape[1] * shape[2]
+    buf = torch.empty(rows * shape[3] + 2 * rows, device=device, dtype=torch.float16)
+    return buf[:rows * shape[3]].view(shape)
+
+
+def kept_output(shape, like):
+    """The buffer of a branch output kept for the backward's row dots
+    dO . o: NSA_F16S for 16-bit inputs (eight times finer than bf16, half of
+    float32's bytes), float32 for float32 inputs."""
+    if like.dtype == torch.float32:
+        return torch.empty(shape, device=like.device, dtype=torch.float32)
+    return f16s_empty(shape, like.device)
+
+
+def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_packed=None, o_f32=False,
+              o_kept=False):
     """Window (mode 0) or compression (mode 1) forward -> (o, lse[f32]);
     ``q_packed`` (optional, [B, Hkv, T, G, D]) also receives the
-    ``pack_heads`` copy of q.  ``o_f32``: o in float32 (unrounded), else in
-    q's dtype."""
+    ``pack_heads`` copy of q.  ``o_f32``: o in float32 (unrounded);
+    ``o_kept``: o in the form the fused layer keeps for its backward
+    (``kept_output``); else o is in q's dtype."""
     check_qkv(q, k, v)
     q, k = _contig(q), _contig(k)
     B, Hq, T, D = q.shape
@@ -450,7 +473,10 @@ def range_fwd(mode, q, k, v, window=0, cmp_block=1, cmp_stride=1, vt=None, q_pac
         assert Lk == T and window >= 1, "window keys must have the query length, window >= 1"
     if vt is None:
         vt = transpose_kv(v)
-    o = torch.empty(q.shape, device=q.device, dtype=torch.float32 if o_f32 else q.dtype)
+    if o_kept:
+        o = kept_output(q.shape, q)
+    else:
+        o = torch.empty(q.shape, device=q.device, dtype=torch.float32 if o_f32 else q.dtype)
     lse = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
     _call(_span_name("fwd", mode), _lib().nsa_range_fwd, mode, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o), L.ptr(lse),
           B, Hq, Hkv, T, Lk, D, int(window), int(cmp_block), int(cmp_stride), L.ptr(q_packed), L.dtype_code(q),
@@ -463,8 +489,9 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     (o_w, lse_w, o_s, lse_s, out), with the selection partials ``sel_parts``
     = (o_part, ml_part) of ``sel_fwd_partials`` merged into o_s / lse_s and
     out = sum_c sigmoid(gate_c) o_c over the three branches.  o_w and o_s
-    take o_c's dtype (q's, or float32 unrounded); out is in q's dtype, or
-    float32 (unrounded) with ``out_f32``."""
+    take o_c's form (q's dtype, float32 unrounded, or the NSA_F16S form of
+    ``kept_output``); out is in q's dtype, or float32 (unrounded) with
+    ``out_f32``."""
     check_qkv(q, k, v)
     q, k, gate, o_c = _contig(q), _contig(k), _contig(gate), _contig(o_c)
     B, Hq, T, D = q.shape
@@ -473,10 +500,13 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     if vt is None:
         vt = transpose_kv(v)
     o_part, ml_part = sel_parts
-    assert o_c.dtype in (q.dtype, torch.float32), "branch outputs are q's dtype or float32"
-    o_w = torch.empty(q.shape, device=q.device, dtype=o_c.dtype)
+    assert o_c.dtype in (q.dtype, torch.float32, torch.float16), "branch outputs are q's dtype, float32 or NSA_F16S"
+    if o_c.dtype == torch.float16:
+        o_w, o_s = f16s_empty(q.shape, q.device), f16s_empty(q.shape, q.device)
+    else:
+        o_w = torch.empty(q.shape, device=q.device, dtype=o_c.dtype)
+        o_s = torch.empty_like(o_w)
     lse_w = torch.empty(B, Hq, T, device=q.device, dtype=torch.float32)
-    o_s = torch.empty_like(o_w)
     lse_s = torch.empty_like(lse_w)
     out = torch.empty(q.shape, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
     _call("fwd[win]", _lib().nsa_range_fwd_finish, MODE_WINDOW, L.ptr(q), L.ptr(k), L.ptr(vt), L.ptr(o_w),
@@ -550,8 +580,9 @@ def gate_bwd_prep(do, o_c, o_s, o_w, gate, lse_c, lse_s, lse_w, pack_hkv=0, dgat
     heads (the ``pack_heads`` layout), else None, and the selection branch's
     dot[1] / rowscale[1] / coff[1] hold their values in the packed row order
     [B, Hkv, T, G] (what ``sel_dkdv`` reads with ``stats_packed``).  The
-    branch outputs share one dtype: dO's, or float32 (unrounded).  dgate is
-    in the gate's dtype, or float32 (unrounded) with ``dgate_f32``."""
+    branch outputs share one form: dO's dtype, float32 (unrounded) or the
+    NSA_F16S form of ``kept_output``.  dgate is in the gate's dtype, or
+    float32 (unrounded) with ``dgate_f32``."""
     do, o_c, o_s, o_w, gate = (_contig(t) for t in (do, o_c, o_s, o_w, gate))
     assert o_s.dtype == o_c.dtype and o_w.dtype == o_c.dtype, "branch outputs must share one dtype"
     lse_c, lse_s, lse_w = (_contig(t) for t in (lse_c, lse_s, lse_w))
@@ -929,11 +960,13 @@ def fused_forward(q, kc, vc, ks, vs, kw, vw, gate, block_idx, geom, pooled=False
     qp = (torch.empty(q.shape[0], ks.shape[1], T, q.shape[1] // ks.shape[1], q.shape[3], device=q.device,
                       dtype=q.dtype) if want_sel else torch.empty(0, device=q.device, dtype=q.dtype))
     # the branch outputs stay internal (only their gated sum is returned):
-    # they are kept in float32 so that the backward's row dots dO . o_c
-    # see them unrounded -- with bf16-rounded outputs that dot carries an
-    # error that a peaked softmax row passes on to dS, dQ and dK whole
+    # they are kept finer than bf16 (fp16 rows with a power-of-two scale per
+    # row, or float32 for float32 inputs) so that the backward's row dots
+    # dO . o_c see them with 11 significant bits -- with bf16-rounded outputs
+    # that dot carries an error that a peaked softmax row passes on to dS, dQ
+    # and dK whole
     o_c, lse_c = range_fwd(MODE_COMPRESS, q, k_cmp, v_cmp, 0, geom.cmp_block, geom.cmp_stride,
-                           q_packed=qp if want_sel else None, o_f32=want_sel)
+                           q_packed=qp if want_sel else None, o_kept=want_sel)
     if block_idx is None:
         block_idx = importance_topn(q, k_cmp, lse_c, geom, T)
     idx = block_idx.to(torch.int32).contiguous()

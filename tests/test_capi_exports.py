@@ -90,8 +90,10 @@ def test_bad_shapes_are_rejected_without_launching():
     assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 48, 2, 16, 1, None) == -1
     assert lib.nsa_sel_fwd(None, None, None, None, None, None, 1, 4, 1, 64, 64, 2, 8, 1, None) == -1
     assert lib.nsa_range_fwd(7, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 1, 1, None) == -3
-    # branch outputs are the input type or float32
+    # branch outputs are the input type, float32, or NSA_F16S with bf16 inputs
     assert lib.nsa_range_fwd(0, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 0, 1, None) == -2
+    assert lib.nsa_range_fwd(0, None, None, None, None, None, 1, 4, 1, 64, 64, 64, 16, 16, 16, None, 0, 2, None) == -2
+    assert lib.nsa_bwd_prep(*([None] * 12), None, 1, 64, 256, 64, 3, 0, 2, 0, None) == -2
     # the selection chunk is capped at 1024 queries (staged in LDS)
     assert lib.nsa_sel_dkdv(*([None] * 8), 1, *([None] * 5), 0, None, None, 1 << 30, 1, 4, 1, 64, 64, 2, 16, 2048,
                             1, None) == -1
@@ -130,3 +132,19 @@ def test_decode_entry_points_check_before_launching():
     # lens_in and lens_out must differ (the update of one sequence's length
     # would race with the other KV heads' reads)
     assert lib.nsa_decode_append(*([fake] * 14), fake, fake, 1, 1, 64, 128, 7, 32, 16, 1, None) == mod.NSA_ERR_ARG
+
+
+def test_f16s_buffers_carry_their_row_scales():
+    """NSA_F16S branch outputs: the float16 view of the rows must have the
+    float32 row scales after it in the same storage; a plain float16 tensor
+    is refused before any call."""
+    import torch
+    mod, _ = _lib()
+    import nsa_hip_ops as ops
+    o = ops.f16s_empty((2, 3, 5, 64), "cpu")
+    assert o.shape == (2, 3, 5, 64) and o.dtype == torch.float16
+    assert o.untyped_storage().nbytes() == 2 * 3 * 5 * (64 * 2 + 4)
+    assert mod.dtype_code(o) == mod.NSA_F16S
+    assert ops.kept_output((2, 3, 5, 64), torch.empty(0, dtype=torch.float32)).dtype == torch.float32
+    with pytest.raises(AssertionError):
+        mod.dtype_code(torch.empty(2, 3, 5, 64, dtype=torch.float16))
