@@ -43,6 +43,16 @@
 namespace nsa {
 
 constexpr int kImpFold = 8;               // tokens read per step of a block's fold
+constexpr int kFoldTaps = 8;              // most tokens per block of the fixed-weight fold
+
+// The fold's weights when a selection block is a whole number of strides
+// (ls = R cd): token i = j R + r meets block j, for r = rlo .. rlo + n - 1,
+// with the same weight w[r - rlo] = |[r cd, r cd + cl) & [0, ls)| / cd for
+// every block j.  n = 0: other geometries (the fold computes each overlap).
+struct FoldTaps {
+  int n, rlo, R;
+  float w[kFoldTaps];
+};
 constexpr int kImpFoldTiles = 8;          // most tiles per fold
 constexpr int kImpStages = 3;             // K tiles in flight + 1
 
@@ -80,17 +90,29 @@ __device__ __forceinline__ void topn_list_insert(uint32_t (&m)[4], int (&c)[4], 
   c[0] = b0 ? k : c[0];
 }
 
+// Waves per SIMD the register budget is cut to.  The walk's chain of
+// dependent MFMAs, exponentials and per-tile barrier is latency-bound, so a
+// third and fourth wave per SIMD pay even when the block sums they cost in
+// registers (KPL per query) go to scratch: those are touched only by the
+// fold (two slots a fold) and the picks.  16-bit inputs, two queries a wave,
+// 512 to 2048 blocks (c5: 9.7 -> 7.2 ms); measured slower at five.
+template <typename T, int KPL, int QPW>
+constexpr int kImpWaves() {
+  return sizeof(T) == 2 && QPW == 2 && KPL >= 8 && KPL <= 32 ? 4 : 1;
+}
+
 // LDS: K tiles [kImpStages][32][D] and per-wave token scratch [4][32 F][QPW]
 // (the wave's queries' values of a token side by side).  cd_sh / ls_sh: log2
 // of cd / ls when they are powers of two, else -1 (the block fold then
 // divides); rcd = 1 / cd scales the overlap weights; fold_tiles: F above
 // (1 .. kImpFoldTiles).  KPL: blocks per lane (n_slc <= 64 * KPL).
 template <typename T, int D, int KPL, int QPW>
-__global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(kImpWaves<T, KPL, QPW>()))) void k_imp_topn(const T* __restrict__ q, const T* __restrict__ kc,
                                                   const float* __restrict__ lse, int32_t* __restrict__ out_idx,
                                                   float* __restrict__ scores, int Hq, int Hkv, int T_, int n_cmp,
                                                   int n_slc, int S, int cl, int cd, int ls, int force_init,
-                                                  int n_local, int nqb, int cd_sh, int ls_sh, int fold_tiles, float rcd, float sl2) {
+                                                  int n_local, int nqb, int cd_sh, int ls_sh, int fold_tiles, float rcd, float sl2,
+                                                  const FoldTaps taps) {
   using C = Tile32<T, D>;
   constexpr int NST = kImpStages;
   constexpr int P2 = 32 / QPW;              // rows per query
@@ -237,6 +259,31 @@ __global__ __launch_bounds__(256) void k_imp_topn(const T* __restrict__ q, const
       float sq[QPW];   // this fold's share of the block's sums, every query
 #pragma unroll
       for (int u = 0; u < QPW; ++u) sq[u] = 0.0f;
+      if (taps.n > 0) {
+        // the same tokens a_i .. b_i in the same order with the same
+        // weights, without the per-token overlap arithmetic
+        const int ib0 = j * taps.R + taps.rlo;
+        float v[kFoldTaps][QPW];
+#pragma unroll
+        for (int x = 0; x < kFoldTaps; ++x) {
+          const int i = ib0 + x;
+          const float* src = tq + (i >= a_i && i <= b_i ? i : a_i) * QPW;
+#pragma unroll
+          for (int u = 0; u < QPW; u += 2) {
+            const float2 t2 = *reinterpret_cast<const float2*>(src + u);
+            v[x][u] = t2.x;
+            v[x][u + 1] = t2.y;
+          }
+        }
+#pragma unroll
+        for (int x = 0; x < kFoldTaps; ++x) {
+          const int i = ib0 + x;
+          if (x < taps.n && i >= a_i && i <= b_i) {
+#pragma unroll
+            for (int u = 0; u < QPW; ++u) sq[u] += v[x][u] * taps.w[x];
+          }
+        }
+      } else
       for (int ib = a_i; ib <= b_i; ib += kImpFold) {
         float v[kImpFold][QPW];
 #pragma unroll
@@ -427,6 +474,21 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
   const float rcd = 1.0f / (float)cmp_stride;
   // tiles per fold: the most (up to kImpFoldTiles) whose tokens' blocks fit
   // the wave's lanes
+  FoldTaps taps{};
+  if (sel_block % cmp_stride == 0) {
+    const int rlo = -((cmp_block - 1) / cmp_stride), rhi = (sel_block - 1) / cmp_stride;
+    if (rhi - rlo + 1 <= kFoldTaps) {
+      taps.n = rhi - rlo + 1;
+      taps.rlo = rlo;
+      taps.R = sel_block / cmp_stride;
+      for (int x = 0; x < taps.n; ++x) {
+        const int p0 = (rlo + x) * cmp_stride;   // the token's span relative to the block start
+        const int a = p0 > 0 ? p0 : 0;
+        const int e = p0 + cmp_block < sel_block ? p0 + cmp_block : sel_block;
+        taps.w[x] = (float)(e - a) * rcd;
+      }
+    }
+  }
   int fold_tiles = 1;
   for (int f = 2; f <= kImpFoldTiles; ++f) {
     const int64_t span = (int64_t)(32 * f - 1) * cmp_stride + cmp_block;   // positions the tokens cover
@@ -440,7 +502,7 @@ int nsa_importance_topn(const void* q, const void* k_cmp, const float* lse_cmp, 
       return NSA_ERR_LAUNCH;
     kern<<<(unsigned)grid, 256, lds, s>>>(qp, kp, lse_cmp, block_idx, scores, Hq, Hkv, T, n_cmp, n_slc, S,
                                           cmp_block, cmp_stride, sel_block, force_init, n_local, nqb, cd_sh, ls_sh,
-                                          fold_tiles, rcd, sl2);
+                                          fold_tiles, rcd, sl2, taps);
     return NSA_OK;
   };
   int rc = NSA_ERR_SHAPE;
