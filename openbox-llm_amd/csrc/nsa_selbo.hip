@@ -20,7 +20,11 @@ namespace nsa {
 
 constexpr float kNegInfS = -__builtin_inff();
 
-constexpr int kFwdStages = 2;   // query tiles in flight per wave of k_sel_fwd_bo
+// query tiles in flight per wave of k_sel_fwd_bo: three at D = 128 (one wave
+// per SIMD by registers, so the stages are what keeps loads in flight: 1-1.5%
+// faster than two at c3 and c5), two below (more waves fit, and a third stage
+// would cost one of them its LDS)
+template <int D> constexpr int fwd_bo_stages() { return D == 128 ? 3 : 2; }
 
 // Loads of one 2-query Q tile into a natural-order row stage, issued by the
 // one wave of the workgroup.  Q is packed per query, [B, Hkv, T, G, D]: the
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
                                                    int n_blk, int L, int Lp, int nsub, float sl2) {
   using C = Tile32<T, D>;
   constexpr int KS = C::KS, DT = C::DT;
-  constexpr int NST = kFwdStages;
+  constexpr int NST = fwd_bo_stages<D>();
   constexpr int LT = FwdIssuer<T, D>::LPT;
   constexpr int NSW = fwd_bo_stores<T, D>();
   static_assert((NST - 1) * (LT + NSW) < 64, "in-flight operations exceed the vmcnt range");
