@@ -235,14 +235,20 @@ int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void
  * selection_forward_fsa, nsa_selection_kernel.py:232-365): work items as in
  * nsa_sel_dkdv over a CSR built with pack_slot (its entries in any order
  * within a block); for every (query, slot, pass)
- * it writes the unnormalised block-local output O_j = sum_k p_k v_k (input
- * dtype; p_k = exp2(s_k - m_j)) to o_part and (m_j [log2 units], l_j = sum_k
+ * it writes the unnormalised block-local output O_j = sum_k p_k v_k
+ * (p_k = exp2(s_k - m_j)) to o_part and (m_j [log2 units], l_j = sum_k
  * p_k) float pairs to ml_part, as the reference's per-pair partials
  * (nsa_selection_kernel.py:286-290), both laid out
  * [B][Hkv][T][nsa_sel_partial_slots(S, block_size)][G] (x D for o_part).
  * q is in the nsa_pack_heads layout [B][Hkv][T][G][D], vt is the
  * nsa_transpose_kv copy of v; chunk <= 1024.  Workspace from
- * nsa_sel_fwd_bo_workspace. */
+ * nsa_sel_fwd_bo_workspace.  o_part's elements are float32 for NSA_F32
+ * inputs and fp16 for NSA_BF16 inputs (11 significant bits; the merged
+ * output, and the backward's row dot dO . o through it, inherit the
+ * partials' rounding): a partial row whose largest magnitude reaches 2^15 is
+ * stored divided by a power of two s, with m_j + log2 s and l_j / s, which
+ * merge to the same output.  nsa_sel_merge and nsa_range_fwd_finish read them
+ * with the inputs' dtype. */
 int nsa_sel_partial_slots(int S, int block_size);
 size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
 int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* q_of_block,
@@ -252,8 +258,9 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
 
 /* Merge of the forward partials (the log-sum-exp combine of
  * nsa_selection_kernel.py:336-364): o and lse per row over the valid slots of
- * block_idx; rows with none get o = 0 and lse = -1e9.  o in o_dtype: dtype
- * (the partials'), or NSA_F32 unrounded. */
+ * block_idx; rows with none get o = 0 and lse = -1e9.  dtype: the inputs'
+ * of nsa_sel_fwd_bo (its partials fp16 for NSA_BF16); o in o_dtype: dtype,
+ * or NSA_F32 unrounded. */
 int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_part, void* o, float* lse, int B,
                   int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, int o_dtype, void* stream);
 

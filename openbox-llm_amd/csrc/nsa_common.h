@@ -144,6 +144,17 @@ __device__ __forceinline__ float f16s_row_scale(float amax) {
   const int e = (int)((__float_as_uint(amax) >> 23) & 0xffu) - 127;   // amax in [2^e, 2^(e+1))
   return __uint_as_float((uint32_t)(e - 14 + 127) << 23);
 }
+// Element type of the selection forward's partial outputs (the unnormalised
+// block-local O_j = sum_k p_k v_k): fp16 for 16-bit inputs (11 significant
+// bits against bf16's 8; the merged selection output, and through the row
+// dot dO . o the selection dK, inherit the partials' rounding), with a
+// power-of-two scale per partial row folded into its m_j (O_j / s, l_j / s,
+// m_j + log2 s merge to the same output) so that rows past 2^15 stay in
+// fp16's range; the input type otherwise.
+template <typename T> struct PartOf { using type = T; };
+template <> struct PartOf<bf16> { using type = f16; };
+template <typename T> using PartT = typename PartOf<T>::type;
+
 template <typename T> struct IsF16 { static constexpr bool value = false; };
 template <> struct IsF16<f16> { static constexpr bool value = true; };
 

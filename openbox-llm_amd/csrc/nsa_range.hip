@@ -171,7 +171,7 @@ __host__ __device__ inline int range_qtiles(bool flat, int T, int G, int NT) {
 // o_scale, o_sel_scale, o_cmp_scale).
 template <typename T, typename TO> struct FwdExtras {
   T* q_packed;             // [B][Hkv][T][G][D] (nullable)
-  const T* opart;          // [B][Hkv][T][NS][G][D] unnormalised block-local outputs O_j = sum p v
+  const PartT<T>* opart;   // [B][Hkv][T][NS][G][D] unnormalised block-local outputs O_j = sum p v
   const float2* ml;        // [B][Hkv][T][NS][G] (m_j [log2 units], l_j)
   const int32_t* idx;      // [B][Hkv][T][S] selected blocks
   TO* o_sel;               // [B][Hq][T][D]
@@ -239,7 +239,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     float acc_s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float M = -__builtin_inff(), Ls = 0.0f;
     for (int s0 = 0; s0 < NS; s0 += 16) {
-      Raw8<T> x[16];
+      Raw8<PartT<T>> x[16];
       float2 ml[16];
       int jv[16];
 #pragma unroll
@@ -934,7 +934,7 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
     const int64_t rows = (int64_t)B * Hq * T;
     return range_fwd_launch<bf16, f16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-        FwdExtras<bf16, f16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (f16*)o_sel,
+        FwdExtras<bf16, f16>{nullptr, (const f16*)o_part, (const float2*)ml_part, block_idx, (f16*)o_sel,
                              lse_sel, (const f16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block, out32,
                              f16s_scales(o, rows, D), f16s_scales(o_sel, rows, D),
                              f16s_scales(const_cast<void*>(o_cmp), rows, D)},
@@ -943,14 +943,14 @@ int nsa_range_fwd_finish(int mode, const void* q, const void* k, const void* vt,
   if (dtype == NSA_BF16 && o_dtype == NSA_BF16)
     return range_fwd_launch<bf16, bf16>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-        FwdExtras<bf16, bf16>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel,
+        FwdExtras<bf16, bf16>{nullptr, (const f16*)o_part, (const float2*)ml_part, block_idx, (bf16*)o_sel,
                               lse_sel, (const bf16*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block,
                               out32},
         s);
   if (dtype == NSA_BF16)
     return range_fwd_launch<bf16, float>(
         mode, q, k, vt, o, lse, B, Hq, Hkv, T, Lk, D, window, cmp_block, cmp_stride,
-        FwdExtras<bf16, float>{nullptr, (const bf16*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
+        FwdExtras<bf16, float>{nullptr, (const f16*)o_part, (const float2*)ml_part, block_idx, (float*)o_sel,
                                lse_sel, (const float*)o_cmp, (const bf16*)gate, (bf16*)out, S, sel_block,
                                out32},
         s);

@@ -111,7 +111,7 @@ template <typename T, int D, bool GP>
 __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ vt, const int32_t* __restrict__ q_of_block,
                                                    const int4* __restrict__ items,
-                                                   int32_t* __restrict__ n_items, T* __restrict__ opart,
+                                                   int32_t* __restrict__ n_items, PartT<T>* __restrict__ opart,
                                                    float2* __restrict__ mlpart, int Hq, int Hkv, int T_, int S,
                                                    int n_blk, int L, int Lp, int nsub, float sl2) {
   using C = Tile32<T, D>;
@@ -329,6 +329,17 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         // rows of 256 B per instruction.  A row that does not exist takes the
         // place of row 0 (always a real row: query A, first head of the
         // chunk) and rewrites its bytes, so every store instruction issues.
+        static_assert(IsF16<PartT<T>>::value, "16-bit inputs keep fp16 partials");
+        // the row's power-of-two scale (fp16's range; 1 below 2^15), folded
+        // into m_j with l_j scaled alike; lane half h holds half the row, the
+        // partner lane (n, 1 - h) the other half (columns d >= D hold 0)
+        float amax = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(acc[dt][i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
+        const float psc = f16s_row_scale(amax), pinv = 1.0f / psc;
         wave_fence();   // the previous tile's rows are read out
         // GP: each row's partial row; a row that does not exist: -1
         if constexpr (GP)
@@ -339,10 +350,10 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
           for (int hf = 0; hf < 2; ++hf) {
             const int c = 4 * dt + 2 * hf + h;
             if (D % 32 == 0 || c < CPR) {
-              bf16x8 v;
+              f16x8 v;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = (bf16)acc[dt][8 * hf + i];
-              *reinterpret_cast<bf16x8*>(sO + (n * CPR + (c ^ (n % CPR))) * 8) = v;
+              for (int i = 0; i < 8; ++i) v[i] = (f16)(acc[dt][8 * hf + i] * pinv);
+              *reinterpret_cast<f16x8*>(sO + (n * CPR + (c ^ (n % CPR))) * 8) = v;
             }
           }
         wave_fence();
@@ -358,8 +369,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
             const int r = RPI * i + rl;
             const int64_t ro = srow[r];
             const int rr = ro >= 0 ? r : 0;
-            const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
-            *reinterpret_cast<bf16x8*>(opart + (ro >= 0 ? ro : r0) * D + 8 * c) = v;
+            const f16x8 v = *reinterpret_cast<const f16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+            *reinterpret_cast<f16x8*>(opart + (ro >= 0 ? ro : r0) * D + 8 * c) = v;
           }
         } else {
           // rows 0-15: query A, rows 16-31: query B, each 16 heads of G D
@@ -370,18 +381,18 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
           // query's rows, so its base address is uniform.
           const int uA = __builtin_amdgcn_readfirstlane(tA), uB = __builtin_amdgcn_readfirstlane(tB);
           const int usA = __builtin_amdgcn_readfirstlane(sA), usB = __builtin_amdgcn_readfirstlane(sB);
-          const T* baseA = opart + ((((int64_t)bh * T_ + uA) * NS + usA * nsub + pass) * G + hc * 16) * D;
-          const T* baseB = uB >= 0 ? opart + ((((int64_t)bh * T_ + uB) * NS + usB * nsub + pass) * G + hc * 16) * D
-                                   : baseA;
+          PartT<T>* baseA = opart + ((((int64_t)bh * T_ + uA) * NS + usA * nsub + pass) * G + hc * 16) * D;
+          PartT<T>* baseB =
+              uB >= 0 ? opart + ((((int64_t)bh * T_ + uB) * NS + usB * nsub + pass) * G + hc * 16) * D : baseA;
           const int grem = G - hc * 16;   // heads of the chunk that exist
           if (uB >= 0 && grem >= 16) {
             // every row exists: the row and its base are fixed per instruction
 #pragma unroll
             for (int i = 0; i < 32 / RPI; ++i) {
               const int r = RPI * i + rl;
-              const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (r * CPR + (c ^ (r % CPR))) * 8);
-              T* dst = const_cast<T*>(RPI * i < 16 ? baseA : baseB) + ((r & 15) * D + 8 * c);
-              *reinterpret_cast<bf16x8*>(dst) = v;
+              const f16x8 v = *reinterpret_cast<const f16x8*>(sO + (r * CPR + (c ^ (r % CPR))) * 8);
+              PartT<T>* dst = (RPI * i < 16 ? baseA : baseB) + ((r & 15) * D + 8 * c);
+              *reinterpret_cast<f16x8*>(dst) = v;
             }
           } else {
 #pragma unroll
@@ -389,19 +400,21 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
               const int r = RPI * i + rl;
               int rr = uB < 0 && r >= 16 ? r - 16 : r;
               rr = (rr & 15) < grem ? rr : rr & 16;
-              const bf16x8 v = *reinterpret_cast<const bf16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
-              T* dst = const_cast<T*>(r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
-              *reinterpret_cast<bf16x8*>(dst) = v;
+              const f16x8 v = *reinterpret_cast<const f16x8*>(sO + (rr * CPR + (c ^ (rr % CPR))) * 8);
+              PartT<T>* dst = (r < 16 ? baseA : baseB) + ((rr & 15) * D + 8 * c);
+              *reinterpret_cast<f16x8*>(dst) = v;
             }
           }
         }
         if (rok && h == 0) {
           const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
-          mlpart[prow] = make_float2(mx, lt);
+          // O_j / s with m_j + log2 s and l_j / s (exact: s is a power of two)
+          const float lgs = (float)((int)((__float_as_uint(psc) >> 23) & 0xffu) - 127);
+          mlpart[prow] = make_float2(mx == kNegInfS ? mx : mx + lgs, lt * pinv);
         }
       } else if (rok) {
         const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
-        T* orow = opart + prow * D;
+        PartT<T>* orow = opart + prow * D;
         // register r of lane half h holds d = 32 dt + acc_elem(h, r)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
@@ -439,7 +452,7 @@ constexpr int kSlotBatch = 16;
 // o[row] = sum_slots exp2(m - M) O_slot / sum exp2(m - M) l over the valid
 // slots, lse = (M + log2 L) ln 2, with a running maximum M across batches.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const T* __restrict__ opart,
+__global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ idx, const PartT<T>* __restrict__ opart,
                                                    const float2* __restrict__ mlpart, T* __restrict__ o,
                                                    float* __restrict__ lse, int Hq, int Hkv, int T_, int S, int n_csr,
                                                    int L, int nsub, int64_t total, float* __restrict__ o32) {
@@ -458,7 +471,7 @@ __global__ __launch_bounds__(256) void k_sel_merge(const int32_t* __restrict__ i
     float M = kNegInfS, Ls = 0.0f;
     for (int s0 = 0; s0 < NS; s0 += kSlotBatch) {
       float2 ml[kSlotBatch];
-      Raw8<T> x[kSlotBatch];
+      Raw8<PartT<T>> x[kSlotBatch];
       bool ok[kSlotBatch];
       int jv[kSlotBatch];
 #pragma unroll
@@ -604,7 +617,7 @@ int nsa_sel_fwd_bo(const void* q, const void* k, const void* vt, const int32_t* 
     if (dtype == NSA_BF16) {
       auto kern = gp ? k_sel_fwd_bo<bf16, DD, true> : k_sel_fwd_bo<bf16, DD, false>;
       kern<<<(unsigned)grid, 64, 0, s>>>((const bf16*)q, (const bf16*)k, (const bf16*)vt, q_of_block, items,
-                                         n_items, (bf16*)o_part, (float2*)ml_part, Hq, Hkv, T, S, n_blk,
+                                         n_items, (f16*)o_part, (float2*)ml_part, Hq, Hkv, T, S, n_blk,
                                          block_size, Lp, nsub, sl2);
     } else {
       auto kern = gp ? k_sel_fwd_bo<float, DD, true> : k_sel_fwd_bo<float, DD, false>;
@@ -628,7 +641,7 @@ int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_
   const int n_csr = sel_csr_blocks(T, block_size), nsub = sel_passes(block_size);
   NSA_DISPATCH_D(D, {
     if (dtype == NSA_BF16)
-      k_sel_merge<bf16, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const bf16*)o_part, (const float2*)ml_part,
+      k_sel_merge<bf16, DD><<<grid_for(total), 256, 0, s>>>(block_idx, (const f16*)o_part, (const float2*)ml_part,
                                                             o32 ? nullptr : (bf16*)o, lse, Hq, Hkv, T, S, n_csr,
                                                             block_size, nsub, total, o32);
     else

@@ -600,6 +600,17 @@ template <> struct Raw8<bf16> {
     v = __builtin_bit_cast(bf16x8, u);
   }
 };
+template <> struct Raw8<f16> {
+  f16x8 v;
+  __device__ __forceinline__ void load(const f16* p) { v = *reinterpret_cast<const f16x8*>(p); }
+  __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
+  __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
+    u32x4 u = __builtin_bit_cast(u32x4, v);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = ok ? u[i] : 0u;
+    v = __builtin_bit_cast(f16x8, u);
+  }
+};
 template <> struct Raw8<float> {
   f32x4 a, b;
   __device__ __forceinline__ void load(const float* p) {

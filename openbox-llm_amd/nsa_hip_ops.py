@@ -773,15 +773,28 @@ def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None, o_f3
 
 def sel_merge(block_idx, parts, q_shape, Hkv, block_size, o_f32=False):
     """The selection output and lse of every row from the partials of
-    ``sel_fwd_partials`` (o in the partials' dtype, or float32 unrounded)."""
+    ``sel_fwd_partials`` (o in the inputs' dtype, or float32 unrounded)."""
     o_part, ml_part = parts
     B, Hq, T, D = q_shape
     idx = block_idx.to(torch.int32).contiguous()
-    o = torch.empty(q_shape, device=o_part.device, dtype=torch.float32 if o_f32 else o_part.dtype)
+    dt = _partial_input_dtype(o_part)
+    o = torch.empty(q_shape, device=o_part.device, dtype=torch.float32 if o_f32 else dt)
     lse = torch.empty(B, Hq, T, device=o_part.device, dtype=torch.float32)
     _call("nsa_sel_merge", _lib().nsa_sel_merge, L.ptr(idx), L.ptr(o_part), L.ptr(ml_part), L.ptr(o), L.ptr(lse), B,
-          Hq, Hkv, T, D, idx.shape[-1], block_size, L.dtype_code(o_part), L.dtype_code(o), _stream(o_part))
+          Hq, Hkv, T, D, idx.shape[-1], block_size, L.NSA_BF16 if dt == torch.bfloat16 else L.NSA_F32,
+          L.dtype_code(o), _stream(o_part))
     return o, lse
+
+
+def _partial_dtype(dtype):
+    """The selection forward partials' element type for inputs of ``dtype``:
+    fp16 for bf16 inputs (11 significant bits; a power-of-two scale per
+    partial row is folded into its m), the input type otherwise."""
+    return torch.float16 if dtype == torch.bfloat16 else dtype
+
+
+def _partial_input_dtype(o_part):
+    return torch.bfloat16 if o_part.dtype == torch.float16 else o_part.dtype
 
 
 def sel_fwd_partials(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None):
@@ -806,7 +819,7 @@ def sel_fwd_partials(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None)
     q_of_block, offsets, _, _ = csr
     ns = int(_lib().nsa_sel_partial_slots(S, block_size))
     G = Hq // Hkv
-    o_part = torch.empty(B, Hkv, T, ns, G, D, device=q.device, dtype=q.dtype)
+    o_part = torch.empty(B, Hkv, T, ns, G, D, device=q.device, dtype=_partial_dtype(q.dtype))
     ml_part = torch.empty(B, Hkv, T, ns, G, 2, device=q.device, dtype=torch.float32)
     ws_bytes = int(_lib().nsa_sel_fwd_bo_workspace(B, Hkv, T, S, block_size, SEL_FWD_CHUNK))
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
