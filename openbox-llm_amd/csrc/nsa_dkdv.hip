@@ -212,13 +212,10 @@ template <typename T, int D> struct KeyAcc {
   // then P and dS packed as the operands of the second half.  With MASK,
   // vis(r) says whether this lane's key is visible to the row of accumulator
   // register r (VisPair, VisBits); without, every key is.
-  // With SPLIT (16-bit operands only), sl receives the rounding remainder
-  // dS - round(dS) of the dS operand, for a second dK^T product: dS then
-  // enters dK with about twice the significant bits.
-  template <bool MASK, bool SPLIT, typename Vis>
+  template <bool MASK, typename Vis>
   __device__ __forceinline__ void front(const KvStage<T, D>& s, const Rows& q, const Vis& vis, float sl2,
                                         int lane, Frag<T> (&ta)[C::DT][2], Frag<T> (&tb)[C::DT][2],
-                                        Frag<T> (&pf)[2], Frag<T> (&sf)[2], Frag<T> (&sl)[2]) {
+                                        Frag<T> (&pf)[2], Frag<T> (&sf)[2]) {
     const int h = lane >> 5;
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
@@ -257,27 +254,17 @@ template <typename T, int D> struct KeyAcc {
     pf[1].set(P + 8);
     sf[0].set(dS);
     sf[1].set(dS + 8);
-    if constexpr (SPLIT && sizeof(T) == 2) {
-      float lo[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lo[r] = dS[r] - to_f32(from_f32<T>(dS[r]));
-      sl[0].set(lo);
-      sl[1].set(lo + 8);
-    }
   }
 
-  // Second half: dV^T += dO^T P, dK^T += Q^T dS (registers only); with
-  // SPLIT also dK^T += Q^T (dS - round(dS))
-  template <bool SPLIT = false>
+  // Second half: dV^T += dO^T P, dK^T += Q^T dS (registers only)
   __device__ __forceinline__ void back(const Frag<T> (&ta)[C::DT][2], const Frag<T> (&tb)[C::DT][2],
-                                       const Frag<T> (&pf)[2], const Frag<T> (&sf)[2], const Frag<T> (&sl)[2]) {
+                                       const Frag<T> (&pf)[2], const Frag<T> (&sf)[2]) {
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt) {
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
         mma32(dv[dt], ta[dt][k], pf[k]);
         mma32(dk[dt], tb[dt][k], sf[k]);
-        if constexpr (SPLIT && sizeof(T) == 2) mma32(dk[dt], tb[dt][k], sl[k]);
       }
     }
   }
@@ -460,7 +447,7 @@ template <typename T, int D, int NTH> struct GroupTiles {
 // fragment k: accumulator register 8 k + j), and post(info, hc, i) after the
 // back half, so what pre stages in LDS is visible to post without a second
 // barrier.
-template <bool WANT_DS, int NSW, typename T, int D, int NTH, bool SPLIT, typename Tiles, typename Pre,
+template <bool WANT_DS, int NSW, typename T, int D, int NTH, typename Tiles, typename Pre,
           typename Post>
 __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[kKvStages], Tiles& tiles, int nhc,
                                         int ntile, Pre pre, Post post, float sl2, int tid) {
@@ -506,11 +493,11 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
       const auto inf = tiles.info(s, ti);
       bool mask;
       const auto v = tiles.vis(inf, mask);
-      Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2], sl[2];
+      Frag<T> ta[C::DT][2], tb[C::DT][2], pf[2], sf[2];
       if (mask)
-        acc.template front<true, SPLIT>(s, rows, v, sl2, lane, ta, tb, pf, sf, sl);
+        acc.template front<true>(s, rows, v, sl2, lane, ta, tb, pf, sf);
       else
-        acc.template front<false, SPLIT>(s, rows, v, sl2, lane, ta, tb, pf, sf, sl);
+        acc.template front<false>(s, rows, v, sl2, lane, ta, tb, pf, sf);
       if (WANT_DS) pre(sf, p);
       if (it + NST - 1 < total)
         vm_wait_steps<(NST - 2) * LT, WANT_DS ? NSW : 0, NST - 2>(it);
@@ -518,7 +505,7 @@ __device__ __forceinline__ void kv_walk(KeyAcc<T, D>& acc, KvStage<T, D> (&stg)[
         vm_wait<0>();
       __syncthreads();
       if (it + 1 < total) KeyAcc<T, D>::read_rows(rows, stg[(p + 1) % NST], lane);
-      acc.template back<SPLIT>(ta, tb, pf, sf, sl);
+      acc.back(ta, tb, pf, sf);
       if (WANT_DS) post(inf, hc, p);
       if (it + NST < total) request(stg[p]);
       if (++ti == ntile) {
@@ -650,9 +637,8 @@ template <typename T, int D> struct SWave {
 #pragma unroll
     for (int r = 0; r < 16; ++r) dlt[r] = s.dot[acc_elem(h, r)];
   }
-  // after: dS from the P-wave's P; dK^T += Q^T dS (with SPLIT also its
-  // rounding remainder); sf receives dS as operand fragments
-  template <bool SPLIT>
+  // after: dS from the P-wave's P; dK^T += Q^T dS; sf receives dS as
+  // operand fragments
   __device__ __forceinline__ void back(const uint32_t* pb, const f32x16& pacc, const Frag<T> (&tb)[C::DT][2],
                                        const float (&dlt)[16], int lane, Frag<T> (&sf)[2]) {
     float dS[16];
@@ -664,21 +650,10 @@ template <typename T, int D> struct SWave {
     for (int r = 0; r < 16; ++r) dS[r] = (float)ph[r >> 3][r & 7] * (pacc[r] - dlt[r]);
     sf[0].set(dS);
     sf[1].set(dS + 8);
-    Frag<T> sl[2];
-    if constexpr (SPLIT && sizeof(T) == 2) {
-      float lo[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lo[r] = dS[r] - to_f32(from_f32<T>(dS[r]));
-      sl[0].set(lo);
-      sl[1].set(lo + 8);
-    }
 #pragma unroll
     for (int dt = 0; dt < C::DT; ++dt)
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        mma32(dk[dt], tb[dt][k], sf[k]);
-        if constexpr (SPLIT && sizeof(T) == 2) mma32(dk[dt], tb[dt][k], sl[k]);
-      }
+      for (int k = 0; k < 2; ++k) mma32(dk[dt], tb[dt][k], sf[k]);
   }
 };
 
@@ -836,7 +811,7 @@ __device__ __forceinline__ void walk_p(PWave<T, D>& pw, KvStage<T, D> (&stg)[kSp
   }
 }
 
-template <typename T, int D, int NTH, bool SPLIT, typename MakeReq>
+template <typename T, int D, int NTH, typename MakeReq>
 __device__ __forceinline__ void walk_s(SWave<T, D>& sw, KvStage<T, D> (&stg)[kSplitStages], const PTile* pbuf,
                                        MakeReq make_rq, int total, int tid) {
   using C = Tile32<T, D>;
@@ -874,7 +849,7 @@ __device__ __forceinline__ void walk_s(SWave<T, D>& sw, KvStage<T, D> (&stg)[kSp
         vm_wait<0>();
       __syncthreads();
       Frag<T> sf[2];
-      sw.template back<SPLIT>(pbuf[p & 1], pacc, tb, dlt, lane, sf);
+      sw.back(pbuf[p & 1], pacc, tb, dlt, lane, sf);
       if (it + 1 < total) {
 #pragma unroll
         for (int k = 0; k < C::KS; ++k) lds_row_frag<T, D>(da[k], stg[(p + 1) % NST].dr, n, h, k);
@@ -1070,7 +1045,7 @@ void k_range_dkdv32(int mode, const T* __restrict__ q, const T* __restrict__ dou
   auto no_pre = [](const Frag<T>*, int) {};
   auto no_post = [](const auto&, int, int) {};
   auto tiles = pair_tiles<T, D, NTH>(x, b, hkv, qsrc, vis);
-  kv_walk<false, 0, T, D, NTH, false>(acc, stg, tiles, x.NHC, ntile, no_pre, no_post, sl2, tid);
+  kv_walk<false, 0, T, D, NTH>(acc, stg, tiles, x.NHC, ntile, no_pre, no_post, sl2, tid);
   if (key_ok) {
     if (prow != nullptr)
       acc.write(prow, prow + part_half, scale, false, h);
@@ -1205,7 +1180,7 @@ void k_range_dkdv_split(int mode, const T* __restrict__ q, const T* __restrict__
     } else {
       SWave<T, D> sw;
       sw.init(v + kvoff, key_safe, h);
-      walk_s<T, D, NTH, false>(sw, stg, pbuf[w], make_rq, total, tid);
+      walk_s<T, D, NTH>(sw, stg, pbuf[w], make_rq, total, tid);
       if (key_ok) store_rows<T, D>(sw.dk, prow ? prow : dk + kvoff + (int64_t)key * D, scale, atomic, h);
     }
   };
@@ -1436,9 +1411,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
         if (preal && t >= 0) dq_store(dq, t, tiles.entry_s(e) * npass + pass, pg);
       };
       if (dq_part != nullptr)
-        kv_walk<true, NSW, T, D, NTH, true>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
+        kv_walk<true, NSW, T, D, NTH>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
       else
-        kv_walk<false, 0, T, D, NTH, true>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
+        kv_walk<false, 0, T, D, NTH>(acc, stg, tiles, 1, ntile, pre, post, sl2, tid);
     } else {
       const int ntile = (cnt + 1) / 2;
       auto decode = [&](int i, int& t, int& s) {
@@ -1473,9 +1448,9 @@ void k_sel_dkdv32(const T* __restrict__ q, const T* __restrict__ dout, const flo
       };
       auto tiles = pair_tiles<T, D, NTH>(x, b, hkv, qsrc, vis);
       if (dq_part != nullptr)
-        kv_walk<true, NSW, T, D, NTH, true>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
+        kv_walk<true, NSW, T, D, NTH>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
       else
-        kv_walk<false, 0, T, D, NTH, true>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
+        kv_walk<false, 0, T, D, NTH>(acc, stg, tiles, x.NHC, ntile, pre, post, sl2, tid);
     }
     if (key_ok) {
       if (part != nullptr) {
