@@ -148,7 +148,7 @@ __device__ __forceinline__ float f16s_row_scale(float amax) {
 // block-local O_j = sum_k p_k v_k): fp16 for 16-bit inputs (11 significant
 // bits against bf16's 8; the merged selection output, and through the row
 // dot dO . o the selection dK, inherit the partials' rounding), with a
-// power-of-two scale per partial row folded into its m_j (O_j / s, l_j / s,
+// power-of-two scale for each partial folded into its m_j (O_j / s, l_j / s,
 // m_j + log2 s merge to the same output) so that rows past 2^15 stay in
 // fp16's range; the input type otherwise.
 template <typename T> struct PartOf { using type = T; };

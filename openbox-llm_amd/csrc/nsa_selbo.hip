@@ -178,6 +178,29 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) settle(vf[dt][kk]);
+    // 16-bit inputs: one power-of-two scale s for every partial of this wave.
+    // With p <= 1 (each tile's own row maximum) a partial is bounded by
+    // |O_j| <= l_j max|v| <= 64 max|v| over the keys that exist, so s (1
+    // below 2^15) keeps O_j / s in fp16's range.  p is divided by s inside
+    // its exponent: the MFMAs then give O_j / s and l_j / s, and m_j + log2 s
+    // records it.
+    float lgs = 0.0f;
+    if constexpr (sizeof(T) == 2) {
+      float vmax = 0.0f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int c0 = kbase + 16 * kk + 8 * h;   // keys c0 .. c0 + 7 (past Lp - 8 only keys >= kend)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (c0 + i < kend) vmax = fmaxf(vmax, fabsf(to_f32(vf[dt][kk].elem(i))));
+        }
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, o, kWave));
+      const float psc = f16s_row_scale(fminf(64.0f * vmax, 3.0e38f));
+      lgs = (float)((int)((__float_as_uint(psc) >> 23) & 0xffu) - 127);
+    }
     __syncthreads();   // sent written
     const int QPT = GP ? 32 / G : 2;   // entries per tile
     const int ntile = (cnt + QPT - 1) / QPT;
@@ -296,7 +319,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         for (int r = 0; r < 16; ++r) mr = fmaxf(mr, st[mt][r]);
       mr = fmaxf(mr, __shfl_xor(mr, 32, kWave));
       const float mx = mr == kNegInfS ? kNegInfS : mr * sl2;
-      const float ms = mx == kNegInfS ? 0.0f : mx;
+      const float ms = (mx == kNegInfS ? 0.0f : mx) + lgs;
       float ps = 0.0f;
       Frag<T> pf[4];
 #pragma unroll
@@ -330,16 +353,6 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         // place of row 0 (always a real row: query A, first head of the
         // chunk) and rewrites its bytes, so every store instruction issues.
         static_assert(IsF16<PartT<T>>::value, "16-bit inputs keep fp16 partials");
-        // the row's power-of-two scale (fp16's range; 1 below 2^15), folded
-        // into m_j with l_j scaled alike; lane half h holds half the row, the
-        // partner lane (n, 1 - h) the other half (columns d >= D hold 0)
-        float amax = 0.0f;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(acc[dt][i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 32, kWave));
-        const float psc = f16s_row_scale(amax), pinv = 1.0f / psc;
         wave_fence();   // the previous tile's rows are read out
         // GP: each row's partial row; a row that does not exist: -1
         if constexpr (GP)
@@ -352,7 +365,7 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
             if (D % 32 == 0 || c < CPR) {
               f16x8 v;
 #pragma unroll
-              for (int i = 0; i < 8; ++i) v[i] = (f16)(acc[dt][8 * hf + i] * pinv);
+              for (int i = 0; i < 8; ++i) v[i] = (f16)acc[dt][8 * hf + i];
               *reinterpret_cast<f16x8*>(sO + (n * CPR + (c ^ (n % CPR))) * 8) = v;
             }
           }
@@ -408,9 +421,8 @@ __global__ __launch_bounds__(64) void k_sel_fwd_bo(const T* __restrict__ q, cons
         }
         if (rok && h == 0) {
           const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
-          // O_j / s with m_j + log2 s and l_j / s (exact: s is a power of two)
-          const float lgs = (float)((int)((__float_as_uint(psc) >> 23) & 0xffu) - 127);
-          mlpart[prow] = make_float2(mx == kNegInfS ? mx : mx + lgs, lt * pinv);
+          // O_j / s and l_j / s (p came out divided by s) with m_j + log2 s
+          mlpart[prow] = make_float2(mx == kNegInfS ? mx : mx + lgs, lt);
         }
       } else if (rok) {
         const int64_t prow = (((int64_t)bh * T_ + t) * NS + slot) * G + g;
