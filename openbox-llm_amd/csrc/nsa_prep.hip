@@ -573,6 +573,24 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
     const int64_t bhq = row / T_;
     prow = ((bhq / G) * T_ + (row - bhq * T_)) * G + bhq % G;
   }
+  // the tail operands of the branches this lane finishes (c = sub, sub + gs,
+  // ...: one each once gs >= 3), fetched before the rows so that their
+  // latency overlaps the rows'
+  float gv[3], lv[3], sv[3];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int c = sub + k * gs;
+    gv[k] = 0.0f;
+    lv[k] = 0.0f;
+    sv[k] = 1.0f;
+    if (ok && c < nbr) {
+      if (nbr == 3) gv[k] = to_f32(gate[row * 3 + c]);
+      if (coff) lv[k] = (c == 0 ? lse0 : c == 1 ? lse1 : lse2)[row];
+      // NSA_F16S: the rows were stored divided by their power-of-two scales
+      if constexpr (IsF16<TO>::value)
+        sv[k] = f16s_scales(const_cast<TO*>(c == 0 ? o0 : c == 1 ? o1 : o2), rows, D)[row];
+    }
+  }
   if (ok) {
     Vec16<T> d;
     BranchRow<T, TO> x;
@@ -590,31 +608,27 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
 #pragma unroll
   for (int c = 0; c < 3; ++c)
     for (int m = 1; m < gs; m <<= 1) acc[c] += __shfl_xor(acc[c], m, kWave);
-  if (!ok || sub != 0) return;
-  if constexpr (IsF16<TO>::value) {
-    // NSA_F16S: the rows were stored divided by their power-of-two scales
-    const TO* os[3] = {o0, o1, o2};
-#pragma unroll
-    for (int c = 0; c < 3; ++c)
-      if (c < nbr) acc[c] *= f16s_scales(const_cast<TO*>(os[c]), rows, D)[row];
-  }
+  if (!ok || sub >= nbr) return;
   // with dout_packed, the statistics of the selection branch (the only
   // branch, or branch 1 of 3) go to the packed row, the layout of the
   // selection dK/dV's query side
-  if (nbr == 1) {
-    dot[prow] = acc[0];
-    if (coff) coff[prow] = lse0[row] * kLog2e;
-    return;
-  }
-  const float* lse[3] = {lse0, lse1, lse2};
-  for (int c = 0; c < nbr; ++c) {
-    const float s = sigmoidf(to_f32(gate[row * 3 + c]));
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int c = sub + k * gs;
+    if (c >= nbr) break;
+    const float a = (c == 0 ? acc[0] : c == 1 ? acc[1] : acc[2]) * sv[k];
+    if (nbr == 1) {
+      dot[prow] = a;
+      if (coff) coff[prow] = lv[k] * kLog2e;
+      continue;
+    }
+    const float sg = sigmoidf(gv[k]);
     const int64_t sr = c == 1 ? prow : row;
-    dot[(int64_t)c * rows + sr] = acc[c];
-    rowscale[(int64_t)c * rows + sr] = s;
-    if (coff) coff[(int64_t)c * rows + sr] = lse[c][row] * kLog2e - __log2f(s);
-    if (dgate32) dgate32[row * 3 + c] = s * (1.0f - s) * acc[c];
-    else if (dgate) dgate[row * 3 + c] = from_f32<T>(s * (1.0f - s) * acc[c]);
+    dot[(int64_t)c * rows + sr] = a;
+    rowscale[(int64_t)c * rows + sr] = sg;
+    if (coff) coff[(int64_t)c * rows + sr] = lv[k] * kLog2e - __log2f(sg);
+    if (dgate32) dgate32[row * 3 + c] = sg * (1.0f - sg) * a;
+    else if (dgate) dgate[row * 3 + c] = from_f32<T>(sg * (1.0f - sg) * a);
   }
 }
 
