@@ -224,6 +224,12 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     range_row<FLAT>(rr, mp, 0, r, t, gl);
     if (t >= T_ || gl >= G) continue;
     const int64_t orow = ((int64_t)mp.b * Hq + mp.hkv * G + gl) * T_ + t;
+    // the gate's other operands (compression row and logits) are loaded
+    // first: their latency then overlaps the partials', not follows it
+    Raw8<TO> ocr;
+    ocr.load(f.o_cmp + orow * D + 8 * c8);
+    const float ocs = IsF16<TO>::value ? f.o_cmp_scale[orow] : 1.0f;
+    const T gr0 = f.gate[orow * 3 + 0], gr1 = f.gate[orow * 3 + 1], gr2 = f.gate[orow * 3 + 2];
     // this branch's row chunk, rounded as stored
     float ow[8];
     {
@@ -280,14 +286,15 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     store_branch8<TO, CPR>(f.o_sel + orow * D + 8 * c8, acc_s, f.o_sel_scale + orow, c8 == 0);
     if (c8 == 0) f.lse_sel[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
     // gate: sigmoid-weighted sum of the three rounded branch outputs
-    float oc[8];
-    load_branch8(f.o_cmp + orow * D + 8 * c8, oc, f.o_cmp_scale + orow);
-    const float g0 = sigmoidf(to_f32(f.gate[orow * 3 + 0]));
-    const float g1 = sigmoidf(to_f32(f.gate[orow * 3 + 1]));
-    const float g2 = sigmoidf(to_f32(f.gate[orow * 3 + 2]));
+    const float g0 = sigmoidf(to_f32(gr0));
+    const float g1 = sigmoidf(to_f32(gr1));
+    const float g2 = sigmoidf(to_f32(gr2));
     float y[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = g0 * oc[i] + g1 * acc_s[i] + g2 * ow[i];
+    for (int i = 0; i < 8; ++i) {
+      const float oc = IsF16<TO>::value ? ocr.get(i) * ocs : ocr.get(i);
+      y[i] = g0 * oc + g1 * acc_s[i] + g2 * ow[i];
+    }
     if (f.out32 != nullptr)
       store8(f.out32 + orow * D + 8 * c8, y);
     else
