@@ -254,7 +254,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
         const int64_t pr = (qs * NS + sl) * G + gl;
         jv[k2] = irow[sl / nsub];
         ml[k2] = f.ml[pr];
-        x[k2].load(f.opart + pr * D + 8 * c8);
+        x[k2].load_nt(f.opart + pr * D + 8 * c8);
       }
       bool ok[16];
       float bm = M;
@@ -773,7 +773,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int k2 = 0; k2 < 16; ++k2) {
           const int sl = s0 + k2 < NS ? s0 + k2 : NS - 1;
           jv[k2] = irow[sl / nsub];
-          x[k2].load(sel_part + ((qrow_sel * NS + sl) * G + gl) * D + 8 * c8);
+          x[k2].load_nt(sel_part + ((qrow_sel * NS + sl) * G + gl) * D + 8 * c8);
         }
 #pragma unroll
         for (int k2 = 0; k2 < 16; ++k2) {

@@ -587,11 +587,15 @@ __device__ __forceinline__ void load_branch8(const TO* p, float (&x)[8], const f
 }
 
 // 8 consecutive elements of a row as loaded (one 16-byte load for bf16, two
-// for float), converted at use.
+// for float), converted at use.  load_nt: a non-temporal load, for data read
+// once (the selection partials), which then does not displace cached lines.
 template <typename T> struct Raw8;
 template <> struct Raw8<bf16> {
   bf16x8 v;
   __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void load_nt(const bf16* p) {
+    v = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+  }
   __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
   __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
     u32x4 u = __builtin_bit_cast(u32x4, v);
@@ -603,6 +607,9 @@ template <> struct Raw8<bf16> {
 template <> struct Raw8<f16> {
   f16x8 v;
   __device__ __forceinline__ void load(const f16* p) { v = *reinterpret_cast<const f16x8*>(p); }
+  __device__ __forceinline__ void load_nt(const f16* p) {
+    v = __builtin_bit_cast(f16x8, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p)));
+  }
   __device__ __forceinline__ float get(int i) const { return (float)v[i]; }
   __device__ __forceinline__ void keep_if(bool ok) {   // zero, bit for bit, unless ok
     u32x4 u = __builtin_bit_cast(u32x4, v);
@@ -616,6 +623,10 @@ template <> struct Raw8<float> {
   __device__ __forceinline__ void load(const float* p) {
     a = *reinterpret_cast<const f32x4*>(p);
     b = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ void load_nt(const float* p) {
+    a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
   }
   __device__ __forceinline__ float get(int i) const { return i < 4 ? a[i] : b[i - 4]; }
   __device__ __forceinline__ void keep_if(bool ok) {
