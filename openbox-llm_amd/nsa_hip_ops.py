@@ -151,9 +151,12 @@ _SIDE_STREAMS = {}
 
 # True: the fused backward runs the selection dK/dV on a side stream, beside
 # the window and compression key-side kernels.  False (default): everything
-# runs in order on the current stream.  At c3 on MI355X both take the same
-# 25.3 ms per fwd+bwd step (the kernels share the CUs without gaining from it),
-# and in order each kernel's timing describes that kernel alone.
+# runs in order on the current stream.  At c3 on MI355X the overlap is slower:
+# 22.9-23.0 against 22.3 ms per fwd+bwd step, and 23.2 ms with the selection
+# dK/dV's persistent grid halved to one workgroup per CU to leave room beside
+# it (alone, that grid takes 7.5 instead of 5.0 ms: the kernel needs both
+# workgroups per CU for its memory traffic).  In order, each kernel's timing
+# describes that kernel alone.
 OVERLAP_SEL_BWD = False
 
 # True: the fused backward computes the compression and window dQ in one launch
