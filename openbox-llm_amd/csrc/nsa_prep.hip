@@ -488,6 +488,10 @@ template <> struct Vec16<bf16> {
   __device__ __forceinline__ float operator[](int i) const { return (float)v[i]; }
   __device__ __forceinline__ void set(int i, float x) { v[i] = (bf16)x; }
   __device__ __forceinline__ void store(bf16* p) const { *reinterpret_cast<bf16x8*>(p) = v; }
+  __device__ __forceinline__ void store_nt(bf16* p) const {
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(__builtin_bit_cast(u4, v), reinterpret_cast<u4*>(p));
+  }
 };
 template <> struct Vec16<float> {
   static constexpr int N = 4;
@@ -496,6 +500,7 @@ template <> struct Vec16<float> {
   __device__ __forceinline__ float operator[](int i) const { return v[i]; }
   __device__ __forceinline__ void set(int i, float x) { v[i] = x; }
   __device__ __forceinline__ void store(float* p) const { *reinterpret_cast<f32x4*>(p) = v; }
+  __device__ __forceinline__ void store_nt(float* p) const { __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p)); }
 };
 
 // One thread per 16-byte vector of the output (D is a multiple of the vector).
@@ -595,7 +600,8 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
     Vec16<T> d;
     BranchRow<T, TO> x;
     d.load(dout + row * D + sub * N);
-    if (dout_packed != nullptr) d.store(dout_packed + prow * D + sub * N);
+    // the packed copy: whole rows, read by a later launch
+    if (dout_packed != nullptr) d.store_nt(dout_packed + prow * D + sub * N);
     const TO* os[3] = {o0, o1, o2};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {

@@ -545,13 +545,25 @@ __device__ __forceinline__ void load8(const f16* p, float (&x)[8]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) x[i] = (float)v[i];
 }
+// store8 as a non-temporal store, for rows that consecutive lanes write whole
+// (one 16-byte chunk each) and that a later launch reads: they need not stay
+// cached.  Float rows take two stores a lane, each covering every other chunk
+// of the row: those keep the cached store, so that the L2 merges the halves of
+// a line before it goes to memory.
+__device__ __forceinline__ void store8_nt(bf16* p, const float (&x)[8]) {
+  bf16x8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (bf16)x[i];
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+}
+__device__ __forceinline__ void store8_nt(float* p, const float (&x)[8]) { store8(p, x); }
 
 // Stores 8 consecutive elements of a branch-output row and leaves in x the
 // values as stored: rounded to TO, or for the NSA_F16S form (TO = f16) scaled
 // by the row's power of two (f16s_row_scale), which the LPR consecutive lanes
 // holding the row agree on through an xor reduction of their maxima; lane
 // `first` of them writes it to *scale.
-template <typename TO, int LPR>
+template <typename TO, int LPR, bool NT = false>
 __device__ __forceinline__ void store_branch8(TO* p, float (&x)[8], float* scale, bool first) {
   if constexpr (IsF16<TO>::value) {
     float m = 0.0f;
@@ -566,10 +578,16 @@ __device__ __forceinline__ void store_branch8(TO* p, float (&x)[8], float* scale
       v[i] = (f16)(x[i] * inv);
       x[i] = (float)v[i] * sc;
     }
-    *reinterpret_cast<f16x8*>(p) = v;
+    if constexpr (NT)
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+    else
+      *reinterpret_cast<f16x8*>(p) = v;
     if (first) *scale = sc;
   } else {
-    store8(p, x);
+    if constexpr (NT)
+      store8_nt(p, x);
+    else
+      store8(p, x);
 #pragma unroll
     for (int i = 0; i < 8; ++i) x[i] = to_f32(from_f32<TO>(x[i]));
   }
