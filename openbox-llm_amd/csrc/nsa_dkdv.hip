@@ -1258,10 +1258,9 @@ static inline int zero_f32(float* x, int64_t n, hipStream_t s) {
 // before the tile's barrier (double-buffered by tile parity) and dQ^T =
 // K^T dS^T is formed after it for the pass's 64 keys -- each wave covering
 // half of D -- and written, scaled, to the (query, slot, pass) partial that
-// k_sel_dq_reduce sums.  dS enters dK^T twice, rounded and as its rounding
-// remainder: a block that every query selects sums tens of thousands of rows
-// into one key's dK, and a single 16-bit dS would leave that sum with an
-// error near the bf16 gradient tolerance.
+// k_sel_dq_reduce sums.  dS enters dK^T once, as a 16-bit operand: with the
+// row dots formed from fp16 branch outputs and partials, a second product
+// with its rounding remainder no longer paid for its MFMAs.
 // GP: groups of G <= 10 heads take floor(32 / G) entries per row tile
 // (GroupTiles), the others two queries x 16 heads per head chunk (PairTiles).
 template <typename T, int D, bool GP>
