@@ -245,9 +245,10 @@ int nsa_sel_dkdv_noalloc(const void* q, const void* k, const void* v, const void
  * nsa_sel_fwd_bo_workspace.  o_part's elements are float32 for NSA_F32
  * inputs and fp16 for NSA_BF16 inputs (11 significant bits; the merged
  * output, and the backward's row dot dO . o through it, inherit the
- * partials' rounding): a partial row whose largest magnitude reaches 2^15 is
- * stored divided by a power of two s, with m_j + log2 s and l_j / s, which
- * merge to the same output.  nsa_sel_merge and nsa_range_fwd_finish read them
+ * partials' rounding): the partials of one block and 64-key pass are stored
+ * divided by a power of two s, with m_j + log2 s and l_j / s, which merge to
+ * the same output; s is 1 unless 64 max|v| over the pass's keys (a bound on
+ * every such partial) reaches 2^15.  nsa_sel_merge and nsa_range_fwd_finish read them
  * with the inputs' dtype. */
 int nsa_sel_partial_slots(int S, int block_size);
 size_t nsa_sel_fwd_bo_workspace(int B, int Hkv, int T, int S, int block_size, int chunk);
