@@ -495,6 +495,11 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     take o_c's form (q's dtype, float32 unrounded, or the NSA_F16S form of
     ``kept_output``); out is in q's dtype, or float32 (unrounded) with
     ``out_f32``."""
+    o_part, ml_part = sel_parts
+    D = q.shape[-1]
+    _check_sel_partials(o_part, q, _partial_dtype(q.dtype), "o_part", S=idx.shape[-1], block_size=sel_block)
+    if ml_part.dtype != torch.float32 or ml_part.numel() * D != 2 * o_part.numel() or not ml_part.is_contiguous():
+        raise TypeError("ml_part must hold one float32 (m, l) pair per partial row")
     check_qkv(q, k, v)
     q, k, gate, o_c = _contig(q), _contig(k), _contig(gate), _contig(o_c)
     B, Hq, T, D = q.shape
@@ -502,7 +507,6 @@ def range_fwd_finish(q, k, v, window, sel_parts, idx, sel_block, o_c, gate, vt=N
     assert gate.shape == (B, Hq, T, 3) and gate.dtype == q.dtype, "gate logits must be [B, Hq, T, 3] in q's dtype"
     if vt is None:
         vt = transpose_kv(v)
-    o_part, ml_part = sel_parts
     assert o_c.dtype in (q.dtype, torch.float32, torch.float16), "branch outputs are q's dtype, float32 or NSA_F16S"
     if o_c.dtype == torch.float16:
         o_w, o_s = f16s_empty(q.shape, q.device), f16s_empty(q.shape, q.device)
@@ -618,8 +622,9 @@ def range_dq(mode, q, k, v, kt, do, lse, dot, rowscale, dq, accumulate, window=0
     out = None
     S = 0
     if sel_part is not None:
-        out = torch.empty(B, Hq, T, D, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
         S = sel_idx.shape[-1]
+        _check_sel_partials(sel_part, q, q.dtype, "sel_part", S=S, block_size=sel_block)
+        out = torch.empty(B, Hq, T, D, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
     _call(_span_name("dq", mode), _lib().nsa_range_dq, mode, L.ptr(q), L.ptr(k), L.ptr(v), L.ptr(kt), L.ptr(do),
           L.ptr(lse), L.ptr(dot), L.ptr(rowscale), L.ptr(dq), int(accumulate), B, Hq, Hkv, T, Lk, D,
           int(window), int(cmp_block), int(cmp_stride), L.ptr(sel_part), L.ptr(sel_idx), S, int(sel_block),
@@ -635,6 +640,7 @@ def range_dq_cw(q, do, kc, vc, ktc, lse_c, dot_c, rs_c, kw, vw, ktw, lse_w, dot_
     the valid slots of ``sel_idx``."""
     B, Hq, T, D = q.shape
     Hkv, Lk = kc.shape[1], kc.shape[2]
+    _check_sel_partials(sel_part, q, q.dtype, "sel_part", S=sel_idx.shape[-1], block_size=geom.sel_block)
     out = torch.empty(B, Hq, T, D, device=q.device, dtype=torch.float32 if out_f32 else q.dtype)
     _call("dq[cmp+win]", _lib().nsa_range_dq_cw, L.ptr(q), L.ptr(do), L.ptr(kc), L.ptr(vc), L.ptr(ktc),
           L.ptr(lse_c), L.ptr(dot_c), L.ptr(rs_c), Lk, int(geom.cmp_block), int(geom.cmp_stride), L.ptr(kw),
@@ -753,15 +759,25 @@ def sel_dkdv(q, k, v, do, coff, dot, block_idx, block_size, csr=None, kt=None, w
 
 def sel_dq_reduce(block_idx, dq_part, dq_acc, block_size, dtype):
     """dQ of the selection branch (+ the float32 ``dq_acc`` of the other
-    branches, if given) in ``dtype``."""
+    branches, if given) in ``dtype``.  The kernel reads the partials and
+    writes its result in the partials' own dtype (the library cannot see a
+    buffer's type: a dtype code that differs from the buffer's would read past
+    its end); another ``dtype`` is a conversion of that result."""
     idx = block_idx.to(torch.int32).contiguous()
     B, Hkv, T, S = idx.shape
     G, D = dq_part.shape[-2], dq_part.shape[-1]
     Hq = Hkv * G
-    out = torch.empty(B, Hq, T, D, device=dq_part.device, dtype=dtype)
+    if dq_part.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("selection dQ partials are bfloat16 or float32")
+    ns = int(_lib().nsa_sel_partial_slots(S, block_size))
+    if not dq_part.is_contiguous() or dq_part.numel() != B * Hkv * T * ns * G * D:
+        raise ValueError("dq_part must be the contiguous [B, Hkv, T, slots, G, D] partials of block_idx")
+    if dq_acc is not None and (dq_acc.dtype != torch.float32 or dq_acc.numel() != B * Hq * T * D):
+        raise TypeError("dq_acc must be a float32 [B, Hq, T, D] accumulator")
+    out = torch.empty(B, Hq, T, D, device=dq_part.device, dtype=dq_part.dtype)
     _call("dq[sel]", _lib().nsa_sel_dq_reduce, L.ptr(idx), L.ptr(dq_part), L.ptr(dq_acc), L.ptr(out), B, Hq, Hkv,
           T, D, S, block_size, L.dtype_code(out), _stream(dq_part))
-    return out
+    return out if dtype == out.dtype else out.to(dtype)
 
 
 def sel_fwd_fsa(q, k, v, block_idx, block_size, csr=None, vt=None, qp=None, o_f32=False):
@@ -780,6 +796,12 @@ def sel_merge(block_idx, parts, q_shape, Hkv, block_size, o_f32=False):
     o_part, ml_part = parts
     B, Hq, T, D = q_shape
     idx = block_idx.to(torch.int32).contiguous()
+    if o_part.dtype not in (torch.float16, torch.float32) or not o_part.is_contiguous():
+        raise TypeError("o_part must be the contiguous fp16 (bf16 inputs) or float32 partials of sel_fwd_partials")
+    ns = int(_lib().nsa_sel_partial_slots(idx.shape[-1], block_size))
+    if o_part.numel() != B * Hq * T * ns * D or ml_part.numel() != 2 * B * Hq * T * ns \
+            or ml_part.dtype != torch.float32 or not ml_part.is_contiguous():
+        raise ValueError("o_part / ml_part must hold the [B, Hkv, T, slots, G] partials of block_idx")
     dt = _partial_input_dtype(o_part)
     o = torch.empty(q_shape, device=o_part.device, dtype=torch.float32 if o_f32 else dt)
     lse = torch.empty(B, Hq, T, device=o_part.device, dtype=torch.float32)
@@ -791,9 +813,26 @@ def sel_merge(block_idx, parts, q_shape, Hkv, block_size, o_f32=False):
 
 def _partial_dtype(dtype):
     """The selection forward partials' element type for inputs of ``dtype``:
-    fp16 for bf16 inputs (11 significant bits; a power-of-two scale per
-    partial row is folded into its m), the input type otherwise."""
+    fp16 for bf16 inputs (11 significant bits; a power-of-two scale per block
+    and 64-key pass is folded into each partial's m), the input type
+    otherwise."""
     return torch.float16 if dtype == torch.bfloat16 else dtype
+
+
+def _check_sel_partials(part, q, dtype, what, S=None, block_size=None):
+    """A selection partial buffer read by a kernel that takes its element type
+    from q: it must be that type, contiguous, and (given S and block_size) of
+    the [B, Hkv, T, slots, G, D] size, or the kernel would read another
+    buffer's bytes or past its end."""
+    if part.dtype != dtype:
+        raise TypeError(f"{what} must be {dtype} for {q.dtype} inputs (got {part.dtype})")
+    if not part.is_contiguous():
+        raise ValueError(f"{what} must be contiguous")
+    if S is not None:
+        B, Hq, T, D = q.shape
+        ns = int(_lib().nsa_sel_partial_slots(S, block_size))
+        if part.numel() != B * Hq * T * ns * D:
+            raise ValueError(f"{what} must hold [B, Hkv, T, {ns}, G, D] partials")
 
 
 def _partial_input_dtype(o_part):
