@@ -6,7 +6,9 @@
 // offers: a decode step equals row t of any prefill whose length covers the
 // end of t's selection block).
 //
-// Five launches on the caller's stream, no host synchronisation:
+// Five launches on the caller's stream, no host synchronisation (four when
+// the pooled sequence fits two token-sum chunks, <= 2048 tokens: k_dec_topn
+// then forms the token sums itself, with k_dec_toksum's arithmetic):
 //  1. k_dec_part (compression + window): split-K over the pooled tokens and
 //     the window keys.  One wave per split (up to 8 tiles of 32 keys; fewer
 //     when the batch is small, so the splits still spread over the CUs).
