@@ -33,12 +33,14 @@ def test_dq_reduce_sums_valid_slots_in_the_partials_dtype(heads):
     torch.cuda.synchronize()
     assert part.dtype == torch.bfloat16 and r16.dtype == torch.bfloat16 and r32.dtype == torch.float32
     assert torch.equal(r32, r16.float()), "the float32 request is not the reduce's result converted"
-    # the valid slots (a block that starts at or before the query) summed in float32
+    # the valid slots (a block that starts at or before the query) summed in
+    # float32; the partials of the other slots are never written (selected,
+    # not multiplied by 0: their bytes may be anything)
     t = torch.arange(T, device=dev)[None, None, :, None]
-    valid = ((idx >= 0) & (idx.long() * bs <= t)).float()                     # [B, Hkv, T, S]
+    valid = (idx >= 0) & (idx.long() * bs <= t)                                # [B, Hkv, T, S]
     ns = part.shape[3]
     assert ns == S, "one pass per slot at block size 64"
-    ref = (part.float() * valid[..., None, None]).sum(3)                        # [B, Hkv, T, G, D]
+    ref = torch.where(valid[..., None, None], part.float(), 0.0).sum(3)         # [B, Hkv, T, G, D]
     ref = ref.permute(0, 1, 3, 2, 4).reshape(B, Hq, T, D)
     err = float(((r32 - ref).abs() / ref.abs().clamp_min(1.0)).max())
     log(f"  reduce vs float32 sum of the valid partials: {err:.2e}")
