@@ -600,8 +600,15 @@ __global__ __launch_bounds__(256) void k_bwd_prep(const T* __restrict__ dout, co
     Vec16<T> d;
     BranchRow<T, TO> x;
     d.load(dout + row * D + sub * N);
-    // the packed copy: whole rows, read by a later launch
-    if (dout_packed != nullptr) d.store_nt(dout_packed + prow * D + sub * N);
+    // the packed copy, read by a later launch: rows of 128 bytes or more
+    // fill whole lines and skip the cache (shorter ones share lines with rows
+    // that other instructions write, so they keep the cached store)
+    if (dout_packed != nullptr) {
+      if (D * (int)sizeof(T) >= 128)
+        d.store_nt(dout_packed + prow * D + sub * N);
+      else
+        d.store(dout_packed + prow * D + sub * N);
+    }
     const TO* os[3] = {o0, o1, o2};
 #pragma unroll
     for (int c = 0; c < 3; ++c) {

@@ -237,7 +237,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
       const f32x4 b2 = *reinterpret_cast<const f32x4*>(fin + r * FIN_PITCH + 8 * c8 + 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) ow[i] = a[i], ow[4 + i] = b2[i];
-      store_branch8<TO, CPR, true>(o + orow * D + 8 * c8, ow, f.o_scale + orow, c8 == 0);
+      store_branch8<TO, CPR, kWholeLines<D>>(o + orow * D + 8 * c8, ow, f.o_scale + orow, c8 == 0);
     }
     // selection: merge the slot partials (running maximum over batches of 16)
     const int64_t qs = bh * T_ + t;
@@ -283,7 +283,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     const float inv_s = Ls > 0.0f ? 1.0f / Ls : 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc_s[i] *= inv_s;
-    store_branch8<TO, CPR, true>(f.o_sel + orow * D + 8 * c8, acc_s, f.o_sel_scale + orow, c8 == 0);
+    store_branch8<TO, CPR, kWholeLines<D>>(f.o_sel + orow * D + 8 * c8, acc_s, f.o_sel_scale + orow, c8 == 0);
     if (c8 == 0) f.lse_sel[orow] = Ls > 0.0f ? (M + __log2f(Ls)) * kLn2 : kLseEmpty;
     // gate: sigmoid-weighted sum of the three rounded branch outputs
     const float g0 = sigmoidf(to_f32(gr0));
@@ -298,7 +298,7 @@ __device__ __forceinline__ void finish_rows(const FwdExtras<T, TO>& f, const f32
     if (f.out32 != nullptr)
       store8(f.out32 + orow * D + 8 * c8, y);
     else
-      store8_nt(f.out + orow * D + 8 * c8, y);
+      store8_as<kWholeLines<D>>(f.out + orow * D + 8 * c8, y);
   }
 }
 constexpr float kNegInf = -__builtin_inff();
@@ -785,7 +785,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if (dq_out32 != nullptr)
         store8(dq_out32 + orow * D + 8 * c8, v);
       else
-        store8_nt(dq_out + orow * D + 8 * c8, v);
+        store8_as<kWholeLines<D>>(dq_out + orow * D + 8 * c8, v);
     }
     return;
   }

@@ -22,7 +22,7 @@ constexpr float kNegInfS = -__builtin_inff();
 
 // one 16-byte chunk of a partial row, as a non-temporal store: the rows are
 // written whole (16 lanes a row) and read once by a later launch, so they
-// need not stay cached (fwd 3.23 -> 3.09 ms at c3).  The dK/dV's dQ partial
+// need not stay cached (fwd 3.17 -> 3.06 ms at c3).  The dK/dV's dQ partial
 // stores are not whole rows per instruction: non-temporal there, their
 // partial lines reach memory unmerged (7.4 instead of 5.1 ms).
 __device__ __forceinline__ void part_store(f16* p, const f16x8& v) {

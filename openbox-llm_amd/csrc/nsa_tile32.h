@@ -557,6 +557,16 @@ __device__ __forceinline__ void store8_nt(bf16* p, const float (&x)[8]) {
   __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
 }
 __device__ __forceinline__ void store8_nt(float* p, const float (&x)[8]) { store8(p, x); }
+// 16-bit rows of D >= 64 elements fill whole 128-byte lines; shorter rows
+// share lines with rows that other instructions write, so they keep the cached
+// store
+template <int D> constexpr bool kWholeLines = D >= 64;
+template <bool NT, typename T> __device__ __forceinline__ void store8_as(T* p, const float (&x)[8]) {
+  if constexpr (NT)
+    store8_nt(p, x);
+  else
+    store8(p, x);
+}
 
 // Stores 8 consecutive elements of a branch-output row and leaves in x the
 // values as stored: rounded to TO, or for the NSA_F16S form (TO = f16) scaled
