@@ -888,16 +888,18 @@ class SelectionAttnHIP(torch.autograd.Function):
         # the backward's row dots dO . o read o unrounded (float32): with the
         # returned bf16 o, a peaked softmax row passes that rounding on to dS
         # and dK (the same choice as the fused layer's branch outputs)
-        o32, lse, csr = sel_fwd_fsa(q, k, v, idx, block_size, o_f32=q.dtype != torch.float32)
+        # the packed Q copy both block-outer kernels read, made once
+        qp = pack_heads(q, k.shape[1])
+        o32, lse, csr = sel_fwd_fsa(q, k, v, idx, block_size, qp=qp, o_f32=q.dtype != torch.float32)
         o = cast_f32(o32, q.dtype)
-        ctx.save_for_backward(q, k, v, idx, o32, lse, *csr)
+        ctx.save_for_backward(q, k, v, idx, o32, lse, qp, *csr)
         ctx.block_size = block_size
         return o
 
     @staticmethod
     def backward(ctx, do):
-        q, k, v, idx, o, lse, *csr = ctx.saved_tensors
-        dq, dk, dv = selection_backward_fsa(q, k, v, idx, ctx.block_size, do, o, lse, csr=tuple(csr))
+        q, k, v, idx, o, lse, qp, *csr = ctx.saved_tensors
+        dq, dk, dv = selection_backward_fsa(q, k, v, idx, ctx.block_size, do, o, lse, csr=tuple(csr), qp=qp)
         return dq, dk, dv, None, None
 
 
@@ -918,16 +920,17 @@ def selection_backward(q, k, v, block_idx, block_size, do, o, lse=None):
     return cast_f32(dq, q.dtype), cast_f32(dk, k.dtype), cast_f32(dv, v.dtype)
 
 
-def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None, grads_f32=False):
+def selection_backward_fsa(q, k, v, block_idx, block_size, do, o, lse, csr=None, grads_f32=False, qp=None):
     """dq, dk, dv of the selection branch (input dtypes), all block-outer
     (the roles of selection_backward_fsa, nsa_selection_backward.py:278-334):
     one kernel writes dK/dV and the dQ partials, a reduce sums the partials.
-    ``grads_f32``: dk, dv as the float32 sums the kernel forms (not cast)."""
+    ``grads_f32``: dk, dv as the float32 sums the kernel forms (not cast).
+    ``qp``: the ``pack_heads`` copy of q, if the caller kept it."""
     check_qkv(q, k, v)
     q, k, v, do = (_contig(t) for t in (q, k, v, do))
     idx = block_idx.to(torch.int32).contiguous()
     dot, coff, dop = delta_of(do, o, lse, pack_hkv=k.shape[1])
-    dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True, dop=dop,
+    dk, dv, dq_part = sel_dkdv(q, k, v, do, coff, dot, idx, block_size, csr=csr, want_dq=True, qp=qp, dop=dop,
                                stats_packed=True)
     dq = sel_dq_reduce(idx, dq_part, None, block_size, q.dtype)
     if grads_f32:
