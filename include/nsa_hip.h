@@ -267,7 +267,10 @@ int nsa_sel_merge(const int32_t* block_idx, const void* o_part, const float* ml_
 
 /* dq_out = dq_acc (float32, nullable) + sum of the dQ partials of the valid
  * slots, written in the input dtype (the dQ reduce of
- * nsa_selection_backward.py:322-334). */
+ * nsa_selection_backward.py:322-334).  dtype is the partials' and dq_out's
+ * element type: the partial buffer is read as that type, so a code that
+ * differs from the buffer's reads another size (a float32 code on a bf16
+ * buffer reads past its end). */
 int nsa_sel_dq_reduce(const int32_t* block_idx, const void* dq_part, const float* dq_acc, void* dq_out, int B,
                       int Hq, int Hkv, int T, int D, int S, int block_size, int dtype, void* stream);
 
