@@ -869,7 +869,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the NSA layer shards over (B, Hkv) with no communication; see DESIGN.md)", file=sys.stderr)
+              "(the NSA layer shards over (B, Hkv) with no communication)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
