@@ -83,15 +83,15 @@ WORKLOADS = {
 # and counter values are kept under profiles/.  Keyed by (workload, kernel).
 MEASURED_TRAFFIC = {   # profiles/nsa_fused_c3_pmc_traffic.md: bytes read + bytes written per launch
     ("c3", "dkdv[sel]"): 1.740e10 + 8.803e9,
-    ("c3", "fwd[sel]"): 8.587e9 + 8.729e9,
-    ("c3", "dq[cmp+win]"): 1.128e10 + 5.369e8,
-    ("c3", "fwd[win]"): 1.007e10 + 1.671e9,
+    ("c3", "fwd[sel]"): 8.435e9 + 8.733e9,
+    ("c3", "dq[cmp+win]"): 1.131e10 + 5.369e8,
+    ("c3", "fwd[win]"): 1.003e10 + 1.663e9,
     ("c3", "dkdv[win]"): 1.007e10 + 1.384e8,
-    ("c3", "dkdv[cmp]"): 2.761e9 + 1.890e8,
-    ("c3", "fwd[cmp]"): 6.536e8 + 1.419e9,
+    ("c3", "dkdv[cmp]"): 2.739e9 + 1.892e8,
+    ("c3", "fwd[cmp]"): 6.543e8 + 1.420e9,
     ("c3", "nsa_bwd_prep"): 2.273e9 + 8.012e8,
-    ("c3", "nsa_importance_topn"): 6.021e8 + 2.503e8,
-    ("c3", "nsa_pool_fwd"): 5.850e7 + 2.096e6,
+    ("c3", "nsa_importance_topn"): 6.019e8 + 2.509e8,
+    ("c3", "nsa_pool_fwd"): 5.853e7 + 2.096e6,
 }
 
 ISO_STEPS = 2   # untimed steps with every call timed (per-kernel spans, dominant kernel)
